@@ -1,0 +1,108 @@
+/*
+ * trellis_sparse.h -- C ABI of the MI355X (gfx950) sparse-voxel convolution library.
+ *
+ * This is the drop-in boundary for trellis.cpp's sparse path (include/sparse.h,
+ * src/sparse.cpp). Every entry point takes plain device pointers, sizes and a HIP stream
+ * passed as void* (a hipStream_t; NULL = the null stream), never allocates on the caller's
+ * behalf unless its comment says so, and is stream-ordered: it enqueues work and returns.
+ *
+ * Memory layouts are the reference's own, so buffers interoperate without transposes:
+ *   coords  int32 [N][3]        (x, y, z) as std::vector<std::array<int,3>> (sparse.h:17)
+ *   feats   [N][C] row-major    = ggml [C, N] (sparse.h:19; test_sparse_conv.cpp:42-44)
+ *   nbr     int32 [27][N]       tap-major neighbour table, sentinel N (sparse.h:14-16)
+ *                               tap t = kd*9 + kh*3 + kw reads the voxel at
+ *                               (x+kd-1, y+kh-1, z+kw-1)
+ *   weight  [Co][27][Ci]        = ggml ne [Ci, 27, Co] (sparse.h:20; convert.py:143-146)
+ *   bias    float [Co]
+ *
+ * Coordinates must lie in [0, 2^21 - 3] on every axis (the reference's own key is exact on
+ * [0, 4094], sparse.cpp:25). Errors are reported as a tsp_status with a message readable
+ * through tsp_last_error(); nothing throws across this boundary.
+ */
+#ifndef TRELLIS_SPARSE_ABI_H
+#define TRELLIS_SPARSE_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    TSP_OK = 0,
+    TSP_ERR_INVALID = 1,      /* bad argument (null pointer, negative size, ...)          */
+    TSP_ERR_HIP = 2,          /* a HIP runtime call failed                                  */
+    TSP_ERR_RANGE = 3,        /* a coordinate outside [0, 2^21-3]                           */
+    TSP_ERR_UNSUPPORTED = 4,  /* dtype / channel combination no kernel implements           */
+    TSP_ERR_WORKSPACE = 5     /* workspace smaller than the matching *_workspace_bytes()    */
+} tsp_status;
+
+typedef enum { TSP_F32 = 0, TSP_F16 = 1, TSP_BF16 = 2 } tsp_dtype;
+
+/* Conv kernel selection. AUTO picks MFMA for 16-bit features with Ci % 32 == 0 and
+ * Co % 64 == 0, and the VALU kernel otherwise. */
+typedef enum { TSP_ALGO_AUTO = 0, TSP_ALGO_MFMA = 1, TSP_ALGO_NARROW = 2 } tsp_algo;
+
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char* tsp_last_error(void);
+
+/* Library version: major*10000 + minor*100 + patch. */
+int tsp_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * Coordinate hash and neighbour table.
+ * Replaces trellis::build_neighbor_table (include/sparse.h:17, src/sparse.cpp:21-39),
+ * which builds a std::unordered_map on the host; here the map is an open-addressing table in
+ * device memory and the 27 probes per voxel run on the GPU. The table is bit-identical to
+ * the reference's: row of the voxel at each offset, N when absent, and for duplicate
+ * coordinates the largest row index (the reference's last insert wins, sparse.cpp:26).
+ * ------------------------------------------------------------------------------------- */
+
+/* Device workspace (bytes) tsp_rulebook_build needs for n voxels. */
+size_t tsp_rulebook_workspace_bytes(int64_t n);
+
+/* d_coords int32 [n][3] -> d_nbr int32 [27*n]. d_status, if not NULL, is a device int32 that
+ * the kernels OR with 1 when a coordinate is out of range (the caller zeroes it and reads it
+ * back when it wants to check). */
+int tsp_rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d_nbr,
+                       void* d_workspace, size_t workspace_bytes, int32_t* d_status,
+                       void* stream);
+
+/* Adds the number of active (voxel, tap) pairs #{(t,i): nbr[t*n+i] != n} to *d_count
+ * (device uint64). */
+int tsp_rulebook_count_pairs(const int32_t* d_nbr, int64_t n, unsigned long long* d_count,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Submanifold 3x3x3 convolution.
+ * Replaces trellis::sparse_submconv (include/sparse.h:20-22, src/sparse.cpp:61-92):
+ *   out[i] = bias + sum_t W_t . feats[nbr[t*n+i]]   (absent taps contribute nothing)
+ * computed in one fused gather-GEMM kernel with fp32 accumulation. feats and weight share a
+ * dtype (f32, f16 or bf16), except that f32 feats may be combined with f16/bf16 weights (the
+ * reference's default of f32 activations and f16 weights, sparse.cpp:17-19). out may be f32
+ * or the feature dtype. d_out must not alias d_feats.
+ * ------------------------------------------------------------------------------------- */
+int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
+                     const int32_t* d_nbr, const void* d_weight, int weight_dtype,
+                     const float* d_bias, int co, void* d_out, int out_dtype, int algo,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * 2x subdivision (channel-to-spatial) index math.
+ * Replaces the host loop of trellis::sparse_c2s (src/sparse.cpp:205-222): parent i keeps
+ * octant o (0..7) when d_mask[o + 8i] != 0; children are emitted parent-major, octant
+ * ascending, at (2x+(o&1), 2y+((o>>1)&1), 2z+((o>>2)&1)) with gidx = o + 8i, and
+ * mstart[i] = index of parent i's first child, mstart[n] = M.
+ * d_child_coords must hold 8*n*3 int32 and d_gidx 8*n int32 (the most M can be); *d_m
+ * (device int64) receives M.
+ * ------------------------------------------------------------------------------------- */
+size_t tsp_subdivide_workspace_bytes(int64_t n);
+int tsp_subdivide(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
+                  int32_t* d_mstart, int32_t* d_child_coords, int32_t* d_gidx, int64_t* d_m,
+                  void* d_workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TRELLIS_SPARSE_ABI_H */

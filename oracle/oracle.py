@@ -1,0 +1,290 @@
+"""CPU oracle for the sparse submanifold conv path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+module. It is the checker the HIP library is compared against, never the thing that is
+measured or shipped.
+
+Integer / index work and the conv itself run in the C restatement (liboracle.so, built
+from oracle.c by oracle/Makefile); the per-voxel block arithmetic (LayerNorm, SiLU,
+linear layers) is restated here in numpy float64.
+
+Layouts match the reference: coords int32 [N,3] (x,y,z); feats [N,C] row-major
+(= ggml [C,N]); nbr int32 [27*N] tap-major with sentinel N (sparse.h:14-16);
+conv weight [Co,27,Ci] (= ggml [Ci,27,Co], convert.py:143-146); bias [Co].
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+
+
+def build() -> str:
+    """Compile liboracle.so with oracle/Makefile (gcc, OpenMP)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.orc_neighbor_table_hash.argtypes = [_i32p, ctypes.c_int64, _i32p]
+        L.orc_neighbor_table_hash.restype = ctypes.c_int
+        L.orc_neighbor_table_grid.argtypes = [_i32p, ctypes.c_int64, _i32p, ctypes.c_int64]
+        L.orc_neighbor_table_grid.restype = ctypes.c_int
+        L.orc_count_pairs.argtypes = [_i32p, ctypes.c_int64]
+        L.orc_count_pairs.restype = ctypes.c_int64
+        L.orc_subm_conv_f32.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _i32p, _f32p, _f32p,
+                                        ctypes.c_int, _f32p, ctypes.c_int]
+        L.orc_subm_conv_f32.restype = None
+        L.orc_subm_conv_f32_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _i32p, _f32p,
+                                             _f32p, ctypes.c_int, _f32p, ctypes.c_int64,
+                                             ctypes.c_int64, ctypes.c_int]
+        L.orc_subm_conv_f32_rows.restype = None
+        L.orc_subm_conv_f64.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _i32p, _f32p, _f32p,
+                                        ctypes.c_int, _f64p, ctypes.c_int]
+        L.orc_subm_conv_f64.restype = None
+        L.orc_subm_conv_f64_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _i32p, _f32p,
+                                             _f32p, ctypes.c_int, _f64p,
+                                             np.ctypeslib.ndpointer(dtype=np.int64,
+                                                                    flags="C_CONTIGUOUS"),
+                                             ctypes.c_int64, ctypes.c_int]
+        L.orc_subm_conv_f64_rows.restype = None
+        L.orc_subdivide.argtypes = [_u8p, _i32p, ctypes.c_int64, _i32p, _i32p, _i32p]
+        L.orc_subdivide.restype = ctypes.c_int64
+        _lib = L
+    return _lib
+
+
+def _coords(coords) -> np.ndarray:
+    c = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 3)
+    return c
+
+
+# ----------------------------------------------------------------------------------------
+# Rulebook (sparse.cpp:21-39)
+# ----------------------------------------------------------------------------------------
+def neighbor_table(coords) -> np.ndarray:
+    """Tap-major int32 [27*N] table via the hash-map restatement of build_neighbor_table."""
+    c = _coords(coords)
+    n = c.shape[0]
+    out = np.empty(27 * n, np.int32)
+    if lib().orc_neighbor_table_hash(c, n, out) != 0:
+        raise ValueError("coordinates outside [-2^20, 2^20)")
+    return out
+
+
+def neighbor_table_grid(coords, max_cells: int = 1 << 31) -> np.ndarray:
+    """The same table by brute force on a dense occupancy grid (independent check)."""
+    c = _coords(coords)
+    n = c.shape[0]
+    out = np.empty(27 * n, np.int32)
+    if lib().orc_neighbor_table_grid(c, n, out, max_cells) != 0:
+        raise ValueError("bounding box too large for the dense-grid brute force")
+    return out
+
+
+def neighbor_table_sorted(coords) -> np.ndarray:
+    """A third, vectorised statement: binary search of packed keys (max row wins on ties)."""
+    c = _coords(coords).astype(np.int64)
+    n = c.shape[0]
+    out = np.full((27, n), n, np.int32)
+    if n == 0:
+        return out.reshape(-1)
+    lo = c.min(0) - 1
+    span = c.max(0) - lo + 2
+    key = lambda p: ((p[:, 0] - lo[0]) * span[1] + (p[:, 1] - lo[1])) * span[2] + (p[:, 2] - lo[2])
+    k = key(c)
+    # stable sort by key; for duplicate keys the last occurrence (largest row) is the one kept
+    order = np.lexsort((np.arange(n), k))
+    ks = k[order]
+    last = np.ones(n, bool)
+    last[:-1] = ks[1:] != ks[:-1]
+    ks, rows = ks[last], order[last]
+    for t in range(27):
+        off = np.array([t // 9 - 1, (t // 3) % 3 - 1, t % 3 - 1])
+        q = key(c + off)
+        pos = np.minimum(np.searchsorted(ks, q), len(ks) - 1)
+        hit = ks[pos] == q
+        out[t, hit] = rows[pos[hit]]
+    return out.reshape(-1)
+
+
+def count_pairs(nbr, n: int) -> int:
+    nb = np.ascontiguousarray(nbr, dtype=np.int32)
+    return int(lib().orc_count_pairs(nb, n))
+
+
+# ----------------------------------------------------------------------------------------
+# Submanifold conv (sparse.cpp:61-92)
+# ----------------------------------------------------------------------------------------
+def subm_conv_f32(feats, nbr, weight, bias, threads: int = 0) -> np.ndarray:
+    """fp32, 27 taps in tap order against the zero sentinel row, bias last (sparse.cpp:64-79)."""
+    f = np.ascontiguousarray(feats, dtype=np.float32)
+    n, ci = f.shape
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    co = w.shape[0]
+    assert w.shape == (co, 27, ci)
+    b = np.ascontiguousarray(bias, dtype=np.float32).reshape(co)
+    nb = np.ascontiguousarray(nbr, dtype=np.int32).reshape(27 * n)
+    out = np.empty((n, co), np.float32)
+    lib().orc_subm_conv_f32(f, n, ci, nb, w, b, co, out, threads)
+    return out
+
+
+def subm_conv_f32_rows(feats, nbr, weight, bias, r0: int, r1: int, threads: int = 0) -> np.ndarray:
+    f = np.ascontiguousarray(feats, dtype=np.float32)
+    n, ci = f.shape
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    co = w.shape[0]
+    b = np.ascontiguousarray(bias, dtype=np.float32).reshape(co)
+    nb = np.ascontiguousarray(nbr, dtype=np.int32).reshape(27 * n)
+    out = np.zeros((n, co), np.float32)
+    lib().orc_subm_conv_f32_rows(f, n, ci, nb, w, b, co, out, r0, r1, threads)
+    return out
+
+
+def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0) -> np.ndarray:
+    """The same sum in fp64 over active taps only: the tolerance judge."""
+    f = np.ascontiguousarray(feats, dtype=np.float32)
+    n, ci = f.shape
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    co = w.shape[0]
+    b = np.ascontiguousarray(bias, dtype=np.float32).reshape(co)
+    nb = np.ascontiguousarray(nbr, dtype=np.int32).reshape(27 * n)
+    out = np.empty((n, co), np.float64)
+    lib().orc_subm_conv_f64(f, n, ci, nb, w, b, co, out, threads)
+    return out
+
+
+def subm_conv_f64_rows(feats, nbr, weight, bias, rows, threads: int = 0) -> np.ndarray:
+    """fp64 conv for the listed output rows only -> [len(rows), Co]."""
+    f = np.ascontiguousarray(feats, dtype=np.float32)
+    n, ci = f.shape
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    co = w.shape[0]
+    b = np.ascontiguousarray(bias, dtype=np.float32).reshape(co)
+    nb = np.ascontiguousarray(nbr, dtype=np.int32).reshape(27 * n)
+    r = np.ascontiguousarray(rows, dtype=np.int64)
+    out = np.empty((len(r), co), np.float64)
+    lib().orc_subm_conv_f64_rows(f, n, ci, nb, w, b, co, out, r, len(r), threads)
+    return out
+
+
+def rel_err(mine, ref) -> float:
+    """max|d| / max|ref| -- the metric of test_sparse_conv.cpp:16-23."""
+    mine = np.asarray(mine, np.float64)
+    ref = np.asarray(ref, np.float64)
+    g = np.abs(ref).max() if ref.size else 0.0
+    d = np.abs(mine - ref).max() if ref.size else 0.0
+    return float(d / g) if g > 0 else float(d)
+
+
+# ----------------------------------------------------------------------------------------
+# C2S subdivision index math (sparse.cpp:205-224)
+# ----------------------------------------------------------------------------------------
+def subdivide(mask, coords):
+    """Returns (child_coords [M,3], gidx [M], mstart [N+1]) in parent-major, octant-ascending
+    order (sparse.cpp:211-222)."""
+    c = _coords(coords)
+    n = c.shape[0]
+    m8 = np.ascontiguousarray(mask, dtype=np.uint8).reshape(8 * n)
+    cc = np.empty((8 * n, 3), np.int32)
+    gi = np.empty(8 * n, np.int32)
+    ms = np.empty(n + 1, np.int32)
+    m = lib().orc_subdivide(m8, c, n, cc, gi, ms)
+    return cc[:m].copy(), gi[:m].copy(), ms
+
+
+def subdivide_vectorised(mask, coords):
+    """Independent statement following the upstream SparseChannel2Spatial formulation
+    (nonzero + repeat_interleave; docs/spec/22-sparse_conv.md section 5)."""
+    c = _coords(coords).astype(np.int64)
+    n = c.shape[0]
+    sub = np.asarray(mask, np.uint8).reshape(n, 8) != 0
+    n_leaf = sub.sum(1)
+    parent, subidx = np.nonzero(sub)            # row-major: parent then octant ascending
+    child = 2 * c[parent]
+    for a in range(3):
+        child[:, a] += (subidx >> a) & 1
+    mstart = np.zeros(n + 1, np.int64)
+    mstart[1:] = np.cumsum(n_leaf)
+    return child.astype(np.int32), (parent * 8 + subidx).astype(np.int32), mstart.astype(np.int32)
+
+
+# ----------------------------------------------------------------------------------------
+# Block arithmetic (float64)
+# ----------------------------------------------------------------------------------------
+def layer_norm(x, weight=None, bias=None, eps: float = 1e-6):
+    """Row LayerNorm over channels with biased variance (ggml_norm, sparse.cpp:124)."""
+    x = np.asarray(x, np.float64)
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    y = (x - mu) / np.sqrt(var + eps)
+    if weight is not None:
+        y = y * np.asarray(weight, np.float64)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return y
+
+
+def silu(x):
+    x = np.asarray(x, np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def linear(x, w, b):
+    """y = x @ w.T + b with w [out, in] (ggml mul_mat of ne [in, out], sparse.cpp:126)."""
+    return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T + np.asarray(b, np.float64)
+
+
+def convnext_block(feats, nbr, p: dict, prefix: str):
+    """SparseConvNeXtBlock3d (sparse.cpp:102-137): conv -> LN(1e-6)+affine -> mlp.0 -> SiLU
+    -> mlp.2 -> + block input. Returns float64 [N, C]."""
+    x = np.asarray(feats, np.float32)
+    h = subm_conv_f64(x, nbr, p[prefix + ".conv.weight"], p[prefix + ".conv.bias"])
+    h = layer_norm(h, p[prefix + ".norm.weight"], p[prefix + ".norm.bias"], 1e-6)
+    h = linear(h, p[prefix + ".mlp.0.weight"], p[prefix + ".mlp.0.bias"])
+    h = silu(h)
+    h = linear(h, p[prefix + ".mlp.2.weight"], p[prefix + ".mlp.2.bias"])
+    return h + x.astype(np.float64)
+
+
+def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None):
+    """SparseResBlockC2S3d (sparse.cpp:172-336). Returns (out float64 [M,Cout],
+    child_coords [M,3], mask_used uint8 [8N])."""
+    x = np.asarray(feats, np.float32)
+    n, cin = x.shape
+    c = _coords(coords)
+    if ext_mask is None:
+        logits = linear(x, p[prefix + ".to_subdiv.weight"], p[prefix + ".to_subdiv.bias"])
+        mask = (logits > 0).astype(np.uint8).reshape(-1)        # sparse.cpp:215
+    else:
+        mask = (np.asarray(ext_mask).reshape(-1) != 0).astype(np.uint8)
+    child, gidx, _ = subdivide(mask, c)
+    k = cin // 8
+    r = cout // k
+    nbr = neighbor_table(c)
+    h = silu(layer_norm(x, p[prefix + ".norm1.weight"], p[prefix + ".norm1.bias"], 1e-6))
+    h = subm_conv_f64(h.astype(np.float32), nbr, p[prefix + ".conv1.weight"], p[prefix + ".conv1.bias"])
+    h = h.reshape(n * 8, cout)[gidx]                              # octant gather, :288
+    h = silu(layer_norm(h, None, None, 1e-6))                     # norm2 without affine, :293
+    nbr2 = neighbor_table(child)
+    h = subm_conv_f64(h.astype(np.float32), nbr2, p[prefix + ".conv2.weight"], p[prefix + ".conv2.bias"])
+    xs = x.reshape(n * 8, k)[gidx].astype(np.float64)             # skip gather, :307
+    skip = np.repeat(xs, r, axis=1)                               # repeat_interleave, :322
+    return h + skip, child, mask

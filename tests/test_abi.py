@@ -1,0 +1,104 @@
+"""CPU tests of the C ABI boundary: the library loads, exports every symbol the header declares
+(unmangled, extern "C"), and rejects bad arguments with a status code and a message before any
+device work -- no GPU needed."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "trellis_sparse.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tsp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_lists_match(pkg):
+    assert header_functions() == sorted(pkg.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    L = pkg.lib()
+    for name in header_functions():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", pkg.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [n for n in header_functions() if n not in exported]
+    assert not missing, missing
+
+
+def test_version_and_error_string(pkg):
+    L = pkg.lib()
+    assert L.tsp_version() >= 100
+    assert isinstance(L.tsp_last_error(), bytes)
+
+
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails validation first
+NULL = ctypes.c_void_p(0)
+
+
+def _err(pkg):
+    return pkg.lib().tsp_last_error().decode()
+
+
+def test_rulebook_validation(pkg):
+    L = pkg.lib()
+    assert L.tsp_rulebook_build(FAKE, -1, FAKE, FAKE, 1 << 20, NULL, NULL) == 1
+    assert "out of range" in _err(pkg)
+    assert L.tsp_rulebook_build(NULL, 0, NULL, NULL, 0, NULL, NULL) == 0       # empty: no-op
+    assert L.tsp_rulebook_build(NULL, 10, FAKE, FAKE, 1 << 20, NULL, NULL) == 1
+    ws = L.tsp_rulebook_workspace_bytes(1000)
+    assert L.tsp_rulebook_build(FAKE, 1000, FAKE, FAKE, ws - 1, NULL, NULL) == 5
+    assert "workspace" in _err(pkg)
+    assert L.tsp_rulebook_count_pairs(FAKE, -3, FAKE, NULL) == 1
+
+
+def test_workspace_sizes(pkg):
+    L = pkg.lib()
+    prev = 0
+    for n in (0, 1, 1000, 10**5, 10**6, 4 * 10**6):
+        b = L.tsp_rulebook_workspace_bytes(n)
+        assert b >= 12 * 2 * n and b >= prev
+        prev = b
+    assert L.tsp_subdivide_workspace_bytes(10**6) >= 4 * (10**6 // 1024)
+
+
+def test_conv_validation(pkg):
+    L = pkg.lib()
+    f = lambda **kw: L.tsp_subm_conv3x3(
+        kw.get("feats", FAKE), kw.get("fdt", 2), kw.get("n", 100), kw.get("ci", 64),
+        kw.get("nbr", FAKE), kw.get("w", FAKE), kw.get("wdt", 2), kw.get("bias", FAKE),
+        kw.get("co", 64), kw.get("out", ctypes.c_void_p(0x2000)), kw.get("odt", 0),
+        kw.get("algo", 0), NULL)
+    assert f(n=-1) == 1
+    assert f(ci=0) == 1 and f(co=-4) == 1
+    assert f(fdt=7) == 1 and f(odt=9) == 1
+    assert f(algo=5) == 1
+    assert f(nbr=NULL) == 1
+    assert f(out=FAKE) == 1 and "alias" in _err(pkg)
+    assert f(n=0) == 0                                              # empty: no-op
+    assert f(algo=1, ci=48) == 4 and "MFMA" in _err(pkg)            # ci % 32 != 0
+    assert f(algo=1, fdt=0, wdt=0) == 4                             # fp32 has no MFMA path here
+    assert f(algo=1, co=96) == 4                                    # co % 64 != 0
+
+
+def test_subdivide_validation(pkg):
+    L = pkg.lib()
+    assert L.tsp_subdivide(FAKE, FAKE, -1, FAKE, FAKE, FAKE, FAKE, FAKE, 64, NULL) == 1
+    assert L.tsp_subdivide(FAKE, FAKE, 1 << 29, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, NULL) == 1
+    ws = L.tsp_subdivide_workspace_bytes(5000)
+    assert L.tsp_subdivide(FAKE, FAKE, 5000, FAKE, FAKE, FAKE, FAKE, FAKE, ws - 1, NULL) == 5
+
+
+def test_python_binding_rejects_host_tensors(pkg):
+    import torch
+    with pytest.raises(ValueError):
+        pkg.rulebook_build(torch.zeros((4, 3), dtype=torch.int32))

@@ -1,0 +1,182 @@
+"""GPU parity of the submanifold conv against the oracle.
+
+Tolerance: max|gpu - ref| / max|ref| (the metric of test_sparse_conv.cpp:16-23) <= 1e-3 for
+16-bit features with fp32 accumulation, against the fp64 oracle on identical (already
+rounded) inputs; fp32 runs are held to 1e-5. bf16/f16 outputs are additionally rounded once,
+so they are held to 4e-3 (2^-8 = one bf16 ulp at the largest element)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL_16 = 1e-3
+TOL_32 = 1e-5
+TOL_16_OUT = 4e-3
+
+
+def _case(name):
+    print(f"[conv] {name}", flush=True)
+
+
+def _dev(a, dtype):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.to(dtype).cuda()
+
+
+def _run(pkg, coords, feats, weight, bias, dtype, wdtype=None, out_dtype=None, algo="auto"):
+    import torch
+    c = torch.from_numpy(np.ascontiguousarray(coords, np.int32)).cuda()
+    nbr = pkg.rulebook_build(c)
+    f = _dev(feats, dtype)
+    w = _dev(weight, wdtype or dtype)
+    b = _dev(bias, torch.float32)
+    out = pkg.subm_conv3x3(f, nbr, w, b, out_dtype=out_dtype or torch.float32, algo=algo)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), nbr
+
+
+def test_golden_fp32(gpu_lib, golden):
+    _case("conv_rand800_c32 f32")
+    import torch
+    g = golden("conv_rand800_c32.npz")
+    out, _ = _run(gpu_lib, g["coords"], g["feats"], g["weight"], g["bias"], torch.float32)
+    assert out.shape == g["out"].shape
+    err = float(np.abs(out - g["out"]).max() / np.abs(g["out"]).max())
+    assert err < TOL_32, err
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_golden_16bit(gpu_lib, golden, orc, shells, dtype_name):
+    _case(f"conv_rand800_c32 {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    g = golden("conv_rand800_c32.npz")
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    f, w = shells.round_to(g["feats"], key), shells.round_to(g["weight"], key)
+    ref = orc.subm_conv_f64(f, orc.neighbor_table(g["coords"]), w, g["bias"])
+    out, _ = _run(gpu_lib, g["coords"], f, w, g["bias"], dt)
+    assert orc.rel_err(out, ref) < TOL_16
+
+
+def _rand_case(shells, rng, n_hint, ci, co, dtype):
+    coords = shells.sphere_shell(48, 24.0, 14.0, 16.0)
+    coords = coords[:n_hint] if n_hint else coords
+    feats = shells.round_to(rng.standard_normal((len(coords), ci)).astype(np.float32), dtype)
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32), dtype)
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    return coords, feats, weight, bias
+
+
+@pytest.mark.parametrize("ci,co,n", [(64, 64, 0), (128, 128, 0), (256, 256, 3000), (32, 64, 257),
+                                     (96, 192, 1000), (128, 320, 511), (64, 128, 1),
+                                     (512, 64, 700)])
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_mfma_vs_oracle(gpu_lib, orc, shells, ci, co, n, dtype_name):
+    _case(f"mfma ci={ci} co={co} n={n} {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(ci * 1000 + co + n)
+    coords, feats, weight, bias = _rand_case(shells, rng, n, ci, co, key)
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    out, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo="mfma")
+    assert orc.rel_err(out, ref) < TOL_16
+    out_n, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo="narrow")
+    assert orc.rel_err(out_n, ref) < TOL_16
+
+
+@pytest.mark.parametrize("ci,co", [(3, 5), (16, 8), (64, 64), (33, 70)])
+def test_narrow_fp32_ragged(gpu_lib, orc, shells, ci, co):
+    _case(f"narrow f32 ci={ci} co={co}")
+    import torch
+    rng = np.random.default_rng(ci + 100 * co)
+    coords, feats, weight, bias = _rand_case(shells, rng, 1500, ci, co, "f32")
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    out, _ = _run(gpu_lib, coords, feats, weight, bias, torch.float32)
+    assert orc.rel_err(out, ref) < TOL_32
+
+
+def test_f32_feats_with_16bit_weights(gpu_lib, orc, shells):
+    """The reference's default: f32 activations with f16 weights (sparse.cpp:17-19)."""
+    _case("f32 feats x f16/bf16 weights")
+    import torch
+    rng = np.random.default_rng(31)
+    for wdt, key in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+        coords, feats, weight, bias = _rand_case(shells, rng, 2000, 64, 64, "f32")
+        weight = shells.round_to(weight, key)
+        ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+        out, _ = _run(gpu_lib, coords, feats, weight, bias, torch.float32, wdtype=wdt)
+        assert orc.rel_err(out, ref) < TOL_32
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_16bit_output(gpu_lib, orc, shells, dtype_name):
+    _case(f"16-bit output {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(41)
+    coords, feats, weight, bias = _rand_case(shells, rng, 4000, 128, 128, key)
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    for algo in ("mfma", "narrow"):
+        out, _ = _run(gpu_lib, coords, feats, weight, bias, dt, out_dtype=dt, algo=algo)
+        assert orc.rel_err(out, ref) < TOL_16_OUT
+
+
+def test_isolated_voxels_and_empty(gpu_lib, orc):
+    _case("isolated + empty")
+    import torch
+    rng = np.random.default_rng(51)
+    coords = (np.arange(300, dtype=np.int32)[:, None] * 3).repeat(3, 1)   # no two adjacent
+    feats = rng.standard_normal((300, 64)).astype(np.float32)
+    weight = rng.standard_normal((64, 27, 64)).astype(np.float32)
+    bias = rng.standard_normal(64).astype(np.float32)
+    out, _ = _run(gpu_lib, coords, feats, weight, bias, torch.float32)
+    ref = feats.astype(np.float64) @ weight[:, 13, :].T.astype(np.float64) + bias   # W_13 f + b
+    assert orc.rel_err(out, ref) < TOL_32
+    empty = gpu_lib.subm_conv3x3(
+        torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda"),
+        torch.zeros(0, dtype=torch.int32, device="cuda"),
+        torch.zeros((64, 27, 64), dtype=torch.bfloat16, device="cuda"),
+        torch.zeros(64, dtype=torch.float32, device="cuda"))
+    assert empty.shape == (0, 64)
+
+
+def test_shell64_fp32_workload(gpu_lib, orc, shells):
+    _case("shell64-c64-f32")
+    import torch
+    w = shells.workload("shell64-c64-f32")
+    ref = orc.subm_conv_f64(w.feats, orc.neighbor_table(w.coords), w.weight, w.bias)
+    out, _ = _run(gpu_lib, w.coords, w.feats, w.weight, w.bias, torch.float32)
+    assert orc.rel_err(out, ref) < TOL_32
+
+
+@pytest.mark.parametrize("name", ["ellipsoids128-c256-bf16", "shells256-c128-bf16"])
+def test_full_size_sampled_rows(gpu_lib, orc, shells, name):
+    """Full-size workloads: every output row of a deterministic sample (the first and last
+    tiles plus 3000 random rows) against the fp64 oracle, MFMA and VALU kernels against each
+    other on all rows, and bitwise reproducibility."""
+    _case(name)
+    import torch
+    w = shells.workload(name)
+    c = torch.from_numpy(w.coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    f = _dev(w.feats, torch.bfloat16)
+    wt = _dev(w.weight, torch.bfloat16)
+    b = _dev(w.bias, torch.float32)
+    out = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma")
+    out2 = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma")
+    outn = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="narrow")
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    rng = np.random.default_rng(0)
+    rows = np.unique(np.concatenate([np.arange(512), np.arange(w.n - 512, w.n),
+                                     rng.integers(0, w.n, 3000)]))
+    nbr_h = nbr.cpu().numpy()
+    ref = orc.subm_conv_f64_rows(w.feats, nbr_h, w.weight, w.bias, rows)
+    got = out.cpu().numpy()
+    assert orc.rel_err(got[rows], ref) < TOL_16
+    assert orc.rel_err(got, outn.cpu().numpy()) < TOL_16

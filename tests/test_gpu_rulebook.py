@@ -1,0 +1,76 @@
+"""GPU parity of the coordinate hash / neighbour table: bit-exact against the oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_table(pkg, coords):
+    import torch
+    c = torch.from_numpy(np.ascontiguousarray(coords, np.int32)).cuda()
+    nbr = pkg.rulebook_build(c)
+    torch.cuda.synchronize()
+    return nbr.cpu().numpy()
+
+
+def _case(name):
+    print(f"[rulebook] {name}", flush=True)
+
+
+@pytest.mark.parametrize("fixture", ["rulebook_rand800.npz", "rulebook_edges.npz"])
+def test_golden(gpu_lib, golden, fixture):
+    _case(fixture)
+    g = golden(fixture)
+    assert np.array_equal(_gpu_table(gpu_lib, g["coords"]), g["nbr"])
+
+
+def test_edge_cases(gpu_lib, orc, shells):
+    rng = np.random.default_rng(21)
+    big = (1 << 21) - 3
+    cases = {
+        "single": np.array([[0, 0, 0]], np.int32),
+        "duplicates": rng.integers(0, 12, size=(3000, 3)).astype(np.int32),
+        "corners": np.array([[0, 0, 0], [big, big, big], [big, 0, big], [1, 0, 0],
+                             [big - 1, big, big]], np.int32),
+        "sparse-huge": rng.integers(0, big + 1, size=(5000, 3)).astype(np.int32),
+        "dense-cube": np.array([(x, y, z) for x in range(10) for y in range(10)
+                                for z in range(10)], np.int32),
+        "shell-255": shells.sphere_shell(40, 20.0, 10.0, 11.0)[:255],
+        "shell-257": shells.sphere_shell(40, 20.0, 10.0, 11.0)[:257],
+        "unsorted": rng.permutation(shells.sphere_shell(40, 20.0, 12.0, 14.0)),
+    }
+    for name, c in cases.items():
+        _case(name)
+        ref = orc.neighbor_table_sorted(c)
+        assert np.array_equal(_gpu_table(gpu_lib, c), ref), name
+
+
+def test_empty(gpu_lib):
+    import torch
+    nbr = gpu_lib.rulebook_build(torch.zeros((0, 3), dtype=torch.int32, device="cuda"))
+    assert nbr.numel() == 0
+
+
+def test_out_of_range_reported(gpu_lib):
+    import torch
+    for bad in ([-1, 0, 0], [0, (1 << 21) - 2, 0]):
+        c = torch.tensor([[1, 1, 1], bad], dtype=torch.int32, device="cuda")
+        with pytest.raises(gpu_lib.TspError):
+            gpu_lib.rulebook_build(c)
+
+
+@pytest.mark.parametrize("name", ["shell64-c64-f32", "shells256-c128-bf16"])
+def test_workload_bit_exact(gpu_lib, orc, shells, name):
+    _case(name)
+    import torch
+    w = shells.workload(name)
+    c = torch.from_numpy(w.coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    again = gpu_lib.rulebook_build(c)
+    got = nbr.cpu().numpy()
+    ref = orc.neighbor_table(w.coords)
+    assert np.array_equal(got, ref)
+    assert torch.equal(nbr, again)                                   # deterministic
+    assert gpu_lib.count_pairs(nbr, w.n) == orc.count_pairs(ref, w.n)

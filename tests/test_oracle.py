@@ -1,0 +1,289 @@
+"""CPU tests that pin the oracle: golden fixtures, independent statements of each result,
+closed forms, library routines and invariants. Each check is chosen so that a plausible
+mistake (wrong tap order, transposed weight, dropped term, off-by-one octant) fails it; the
+`*_planted` tests plant such mistakes in the oracle's inputs and assert the checks notice."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+
+# ------------------------------------------------------------------------------------------
+# Rulebook
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("fixture", ["rulebook_rand800.npz", "rulebook_edges.npz"])
+def test_rulebook_golden(orc, golden, fixture):
+    g = golden(fixture)
+    for fn in (orc.neighbor_table, orc.neighbor_table_grid, orc.neighbor_table_sorted):
+        assert np.array_equal(fn(g["coords"]), g["nbr"])
+
+
+def test_rulebook_three_way_random(orc, shells):
+    rng = np.random.default_rng(11)
+    sets = [
+        shells.sphere_shell(24, 12.0, 7.0, 9.0),
+        rng.integers(0, 12, size=(3000, 3)).astype(np.int32),        # many duplicates
+        rng.integers(0, 1 << 20, size=(2000, 3)).astype(np.int32),   # sparse, huge coords
+        np.zeros((0, 3), np.int32),
+        np.array([[3, 4, 5]], np.int32),
+    ]
+    for c in sets:
+        a = orc.neighbor_table(c)
+        c_small = c if (len(c) == 0 or c.max() < 4096) else None
+        if c_small is not None:
+            assert np.array_equal(a, orc.neighbor_table_grid(c))
+        assert np.array_equal(a, orc.neighbor_table_sorted(c))
+
+
+def test_rulebook_tap_convention(orc):
+    # tap t = kd*9 + kh*3 + kw reads the voxel at (x+kd-1, y+kh-1, z+kw-1) (sparse.h:14-16)
+    c = np.array([[5, 5, 5], [6, 5, 4], [4, 6, 5]], np.int32)
+    nbr = orc.neighbor_table(c).reshape(27, 3)
+    t_b = 2 * 9 + 1 * 3 + 0          # offset (+1, 0, -1) from voxel 0
+    t_c = 0 * 9 + 2 * 3 + 1          # offset (-1, +1, 0) from voxel 0
+    assert nbr[t_b, 0] == 1 and nbr[t_c, 0] == 2
+    assert nbr[26 - t_b, 1] == 0     # the mirror tap sees voxel 0 from voxel 1
+    assert all(nbr[t, 0] == 3 for t in range(27) if t not in (t_b, t_c, 13))
+    assert nbr[13].tolist() == [0, 1, 2]
+
+
+def test_rulebook_special_cases(orc):
+    iso = np.array([[10, 10, 10], [20, 20, 20]], np.int32)
+    nbr = orc.neighbor_table(iso).reshape(27, 2)
+    assert nbr[13].tolist() == [0, 1] and (np.delete(nbr, 13, 0) == 2).all()
+    cube = np.array([(x, y, z) for x in range(3) for y in range(3) for z in range(3)], np.int32)
+    nbr = orc.neighbor_table(cube).reshape(27, 27)
+    centre = 13                     # voxel (1,1,1) is row 13 in x-major order
+    assert nbr[:, centre].tolist() == list(range(27))
+    dup = np.array([[1, 1, 1], [2, 1, 1], [1, 1, 1], [1, 1, 1]], np.int32)
+    nbr = orc.neighbor_table(dup).reshape(27, 4)
+    assert nbr[13].tolist() == [3, 1, 3, 3]          # last insert wins (sparse.cpp:26)
+    assert nbr[9 * 2 + 3 + 1, 0] == 1                 # (+1,0,0) neighbour
+    assert nbr[0 * 9 + 3 + 1, 1] == 3                 # (-1,0,0) from (2,1,1) -> last dup
+    assert orc.neighbor_table(np.zeros((0, 3), np.int32)).size == 0
+
+
+def test_rulebook_planted(orc):
+    """A table built with the z and x offsets swapped must fail the fixture check."""
+    c = np.array([[5, 5, 5], [6, 5, 5], [5, 5, 6]], np.int32)
+    good = orc.neighbor_table(c)
+    swapped = orc.neighbor_table(c[:, ::-1].copy())   # planted: axes reversed
+    assert not np.array_equal(good, swapped)
+
+
+def test_count_pairs(orc, golden):
+    g = golden("rulebook_rand800.npz")
+    n = len(g["coords"])
+    assert orc.count_pairs(g["nbr"], n) == int((g["nbr"] != n).sum())
+
+
+# ------------------------------------------------------------------------------------------
+# Conv
+# ------------------------------------------------------------------------------------------
+def _dense_box(rng, dims, ci):
+    X, Y, Z = dims
+    coords = np.array([(x, y, z) for x in range(X) for y in range(Y) for z in range(Z)],
+                      np.int32)
+    feats = rng.standard_normal((len(coords), ci)).astype(np.float32)
+    return coords, feats
+
+
+def _conv3d_reference(coords, feats, weight, bias, dims):
+    """torch.nn.functional.conv3d with zero padding 1 on the dense box (a textbook routine):
+    on a fully occupied box the submanifold conv is exactly this cross-correlation."""
+    X, Y, Z = dims
+    ci = feats.shape[1]
+    co = weight.shape[0]
+    dense = torch.zeros(1, ci, X, Y, Z, dtype=torch.float64)
+    cc = torch.from_numpy(coords.astype(np.int64))
+    dense[0, :, cc[:, 0], cc[:, 1], cc[:, 2]] = torch.from_numpy(feats).double().T
+    w = torch.from_numpy(weight).double().reshape(co, 3, 3, 3, ci).permute(0, 4, 1, 2, 3)
+    out = F.conv3d(dense, w.contiguous(), torch.from_numpy(bias).double(), padding=1)
+    return out[0, :, cc[:, 0], cc[:, 1], cc[:, 2]].T.numpy()
+
+
+def test_conv_dense_box_equals_conv3d(orc):
+    rng = np.random.default_rng(5)
+    dims = (5, 4, 6)
+    coords, feats = _dense_box(rng, dims, 8)
+    weight = rng.standard_normal((7, 27, 8)).astype(np.float32)
+    bias = rng.standard_normal(7).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    ref = _conv3d_reference(coords, feats, weight, bias, dims)
+    assert np.allclose(orc.subm_conv_f64(feats, nbr, weight, bias), ref, rtol=1e-12, atol=1e-10)
+    assert orc.rel_err(orc.subm_conv_f32(feats, nbr, weight, bias), ref) < 1e-6
+
+
+def test_conv_dense_box_planted(orc):
+    """Weights with the tap axis mirrored (a transposed kernel) must fail the conv3d check."""
+    rng = np.random.default_rng(6)
+    dims = (4, 4, 4)
+    coords, feats = _dense_box(rng, dims, 4)
+    weight = rng.standard_normal((3, 27, 4)).astype(np.float32)
+    bias = np.zeros(3, np.float32)
+    nbr = orc.neighbor_table(coords)
+    ref = _conv3d_reference(coords, feats, weight, bias, dims)
+    planted = weight[:, ::-1, :].copy()
+    assert orc.rel_err(orc.subm_conv_f64(feats, nbr, planted, bias), ref) > 1e-2
+    planted_t = weight.reshape(3, 3, 3, 3, 4).transpose(0, 3, 2, 1, 4).reshape(3, 27, 4).copy()
+    assert orc.rel_err(orc.subm_conv_f64(feats, nbr, planted_t, bias), ref) > 1e-2
+
+
+def test_conv_golden(orc, golden):
+    g = golden("conv_rand800_c32.npz")
+    nbr = orc.neighbor_table(g["coords"])
+    out = orc.subm_conv_f64(g["feats"], nbr, g["weight"], g["bias"])
+    assert np.allclose(out, g["out"], rtol=1e-12, atol=1e-12)
+    assert orc.rel_err(orc.subm_conv_f32(g["feats"], nbr, g["weight"], g["bias"]), g["out"]) < 1e-5
+
+
+def test_conv_invariants(orc, shells):
+    rng = np.random.default_rng(7)
+    coords = shells.sphere_shell(20, 10.0, 5.0, 7.0)
+    n = len(coords)
+    f1 = rng.standard_normal((n, 16)).astype(np.float32)
+    f2 = rng.standard_normal((n, 16)).astype(np.float32)
+    w = rng.standard_normal((8, 27, 16)).astype(np.float32)
+    b0 = np.zeros(8, np.float32)
+    nbr = orc.neighbor_table(coords)
+    y1, y2 = orc.subm_conv_f64(f1, nbr, w, b0), orc.subm_conv_f64(f2, nbr, w, b0)
+    y12 = orc.subm_conv_f64((2 * f1 + f2).astype(np.float32), nbr, w, b0)
+    # (2*f1 + f2 is rounded to f32 before the conv, hence the 1e-5 tolerance)
+    assert np.allclose(y12, 2 * y1 + y2, rtol=1e-5, atol=1e-5)          # linear in features
+    w2 = rng.standard_normal((8, 27, 16)).astype(np.float32)
+    yw = orc.subm_conv_f64(f1, nbr, (w + w2).astype(np.float32), b0)
+    assert np.allclose(yw, y1 + orc.subm_conv_f64(f1, nbr, w2, b0), rtol=1e-5, atol=1e-5)
+    shifted = coords + np.array([7, 3, 11], np.int32)                  # translation invariance
+    assert np.array_equal(orc.neighbor_table(shifted), nbr)
+    perm = rng.permutation(n)                                           # row relabelling
+    nbr_p = orc.neighbor_table(coords[perm])
+    yp = orc.subm_conv_f64(f1[perm], nbr_p, w, b0)
+    assert np.allclose(yp, y1[perm], atol=1e-12)
+    bias = rng.standard_normal(8).astype(np.float32)                    # bias added once
+    assert np.allclose(orc.subm_conv_f64(f1, nbr, w, bias), y1 + bias, atol=1e-12)
+
+
+def test_conv_rows_variants(orc, golden):
+    g = golden("conv_rand800_c32.npz")
+    nbr = orc.neighbor_table(g["coords"])
+    rows = np.array([0, 5, 799, 400], np.int64)
+    r64 = orc.subm_conv_f64_rows(g["feats"], nbr, g["weight"], g["bias"], rows)
+    assert np.allclose(r64, g["out"][rows], rtol=0, atol=1e-12)
+    r32 = orc.subm_conv_f32_rows(g["feats"], nbr, g["weight"], g["bias"], 100, 200)
+    full = orc.subm_conv_f32(g["feats"], nbr, g["weight"], g["bias"])
+    assert np.array_equal(r32[100:200], full[100:200])
+
+
+# ------------------------------------------------------------------------------------------
+# Subdivision
+# ------------------------------------------------------------------------------------------
+def test_subdivide_golden(orc, golden):
+    g = golden("subdivide_rand600.npz")
+    ch, gi, ms = orc.subdivide(g["mask"], g["coords"])
+    assert np.array_equal(ch, g["child"]) and np.array_equal(gi, g["gidx"])
+    assert np.array_equal(ms, g["mstart"])
+
+
+def test_subdivide_properties(orc, shells):
+    rng = np.random.default_rng(8)
+    coords = shells.random_distinct_voxels(300, 12, 8)
+    for p in (0.0, 0.2, 1.0):
+        mask = (rng.random(8 * 300) < p).astype(np.uint8) * rng.integers(1, 255, 8 * 300).astype(np.uint8)
+        ch, gi, ms = orc.subdivide(mask, coords)
+        ch2, gi2, ms2 = orc.subdivide_vectorised(mask, coords)
+        assert np.array_equal(ch, ch2) and np.array_equal(gi, gi2) and np.array_equal(ms, ms2)
+        m = len(ch)
+        assert m == int((mask != 0).sum()) and ms[-1] == m
+        parent, octant = gi // 8, gi % 8
+        assert np.array_equal(ch >> 1, coords[parent])                   # child / 2 = parent
+        bits = np.stack([(octant >> a) & 1 for a in range(3)], 1)
+        assert np.array_equal(ch & 1, bits)                              # bit0->x,1->y,2->z
+        assert np.all(np.diff(gi) > 0)                                   # parent-major order
+        assert len(np.unique(ch, axis=0)) == m                           # children distinct
+
+
+def test_subdivide_planted(orc, golden):
+    g = golden("subdivide_rand600.npz")
+    ch, _, _ = orc.subdivide(g["mask"], g["coords"])
+    planted = orc.subdivide(g["mask"].reshape(-1, 8)[:, ::-1].reshape(-1).copy(), g["coords"])[0]
+    assert not np.array_equal(ch, planted)     # reversed octant bit order is caught
+
+
+# ------------------------------------------------------------------------------------------
+# Block arithmetic against torch library routines
+# ------------------------------------------------------------------------------------------
+def test_layer_norm_and_silu(orc):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((50, 24))
+    w, b = rng.standard_normal(24), rng.standard_normal(24)
+    ref = F.layer_norm(torch.from_numpy(x), (24,), torch.from_numpy(w), torch.from_numpy(b), 1e-6)
+    assert np.allclose(orc.layer_norm(x, w, b, 1e-6), ref.numpy(), atol=1e-12)
+    assert np.allclose(orc.silu(x), F.silu(torch.from_numpy(x)).numpy(), atol=1e-14)
+
+
+def _block_params(rng, c, cout=None):
+    p = {}
+    s = lambda *shape: (rng.standard_normal(shape) * 0.05).astype(np.float32)
+    pre = "blk"
+    p[pre + ".conv.weight"], p[pre + ".conv.bias"] = s(c, 27, c), s(c)
+    p[pre + ".norm.weight"], p[pre + ".norm.bias"] = (1 + s(c)), s(c)
+    p[pre + ".mlp.0.weight"], p[pre + ".mlp.0.bias"] = s(4 * c, c), s(4 * c)
+    p[pre + ".mlp.2.weight"], p[pre + ".mlp.2.bias"] = s(c, 4 * c), s(c)
+    if cout:
+        p["c2s.to_subdiv.weight"], p["c2s.to_subdiv.bias"] = s(8, c) * 20, s(8)
+        p["c2s.norm1.weight"], p["c2s.norm1.bias"] = (1 + s(c)), s(c)
+        p["c2s.conv1.weight"], p["c2s.conv1.bias"] = s(8 * cout, 27, c), s(8 * cout)
+        p["c2s.conv2.weight"], p["c2s.conv2.bias"] = s(cout, 27, cout), s(cout)
+    return p
+
+
+def test_convnext_block_vs_torch(orc, shells):
+    """sparse.cpp:102-137 restated with torch's layer_norm / linear / silu."""
+    rng = np.random.default_rng(10)
+    coords = shells.random_distinct_voxels(200, 8, 10)
+    c = 16
+    x = rng.standard_normal((200, c)).astype(np.float32)
+    p = _block_params(rng, c)
+    nbr = orc.neighbor_table(coords)
+    out = orc.convnext_block(x, nbr, p, "blk")
+    T = lambda a: torch.from_numpy(np.asarray(a)).double()
+    h = T(orc.subm_conv_f64(x, nbr, p["blk.conv.weight"], p["blk.conv.bias"]))
+    h = F.layer_norm(h, (c,), T(p["blk.norm.weight"]), T(p["blk.norm.bias"]), 1e-6)
+    h = F.silu(F.linear(h, T(p["blk.mlp.0.weight"]), T(p["blk.mlp.0.bias"])))
+    h = F.linear(h, T(p["blk.mlp.2.weight"]), T(p["blk.mlp.2.bias"])) + T(x)
+    assert np.allclose(out, h.numpy(), atol=1e-10)
+
+
+def test_c2s_block_vs_loops(orc, shells):
+    """sparse.cpp:172-336 against a per-(parent, octant) loop statement of SparseResBlockC2S3d
+    (the formulation of tools/ref_c2s.py:59-79)."""
+    rng = np.random.default_rng(12)
+    n, cin, cout = 120, 16, 8
+    coords = shells.random_distinct_voxels(n, 8, 12)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    p = _block_params(rng, cin, cout)
+    out, child, mask = orc.c2s_block(x, coords, p, "c2s", cout)
+    T = lambda a: torch.from_numpy(np.asarray(a)).double()
+    logits = F.linear(T(x), T(p["c2s.to_subdiv.weight"]), T(p["c2s.to_subdiv.bias"]))
+    sub = (logits > 0).numpy()
+    assert np.array_equal(mask.reshape(n, 8) != 0, sub)
+    h = F.silu(F.layer_norm(T(x), (cin,), T(p["c2s.norm1.weight"]), T(p["c2s.norm1.bias"]), 1e-6))
+    nbr = orc.neighbor_table(coords)
+    h = orc.subm_conv_f64(h.numpy().astype(np.float32), nbr, p["c2s.conv1.weight"], p["c2s.conv1.bias"])
+    rows, kids, skips = [], [], []
+    k = cin // 8
+    for i in range(n):
+        for o in range(8):
+            if sub[i, o]:
+                xx, yy, zz = coords[i]
+                kids.append((2 * xx + (o & 1), 2 * yy + ((o >> 1) & 1), 2 * zz + ((o >> 2) & 1)))
+                rows.append(h[i, o * cout:(o + 1) * cout])
+                skips.append(np.repeat(x[i, o * k:(o + 1) * k].astype(np.float64), cout // k))
+    kids = np.array(kids, np.int32)
+    assert np.array_equal(kids, child)
+    hn = F.silu(F.layer_norm(T(np.array(rows)), (cout,), None, None, 1e-6)).numpy()
+    nbr2 = orc.neighbor_table(kids)
+    h2 = orc.subm_conv_f64(hn.astype(np.float32), nbr2, p["c2s.conv2.weight"], p["c2s.conv2.bias"])
+    assert np.allclose(out, h2 + np.array(skips), atol=1e-9)

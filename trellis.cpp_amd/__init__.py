@@ -1,0 +1,183 @@
+"""Python binding of libtrellis_sparse.so, the MI355X sparse-voxel conv library.
+
+The library's interface is the C ABI declared in include/trellis_sparse.h; this module loads
+it with ctypes and wraps each entry point for torch device tensors (torch supplies device
+memory and the current HIP stream; all compute happens in the library's HIP kernels).
+
+There is no fallback: if the shared library is missing or a call fails, an exception is
+raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtrellis_sparse.so")
+
+TSP_F32, TSP_F16, TSP_BF16 = 0, 1, 2
+ALGO = {"auto": 0, "mfma": 1, "narrow": 2}
+STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "RANGE", 4: "UNSUPPORTED", 5: "WORKSPACE"}
+
+# Every extern "C" entry point the header declares (checked by the CPU test suite).
+EXPORTS = (
+    "tsp_last_error", "tsp_version",
+    "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
+    "tsp_subm_conv3x3",
+    "tsp_subdivide_workspace_bytes", "tsp_subdivide",
+)
+
+
+class TspError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} -> {STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def build(jobs: int = 8) -> str:
+    """Compile libtrellis_sparse.so for gfx950 (hipcc through trellis.cpp_amd/Makefile)."""
+    subprocess.run(["make", "-s", "-C", HERE, f"-j{jobs}"], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(
+            f"{LIB_PATH} is not built; run `make -C {HERE}` (or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    c_i64, c_int, c_sz, c_vp = ctypes.c_int64, ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
+    L.tsp_last_error.restype = ctypes.c_char_p
+    L.tsp_last_error.argtypes = []
+    L.tsp_version.restype = c_int
+    L.tsp_rulebook_workspace_bytes.restype = c_sz
+    L.tsp_rulebook_workspace_bytes.argtypes = [c_i64]
+    L.tsp_rulebook_build.restype = c_int
+    L.tsp_rulebook_build.argtypes = [c_vp, c_i64, c_vp, c_vp, c_sz, c_vp, c_vp]
+    L.tsp_rulebook_count_pairs.restype = c_int
+    L.tsp_rulebook_count_pairs.argtypes = [c_vp, c_i64, c_vp, c_vp]
+    L.tsp_subm_conv3x3.restype = c_int
+    L.tsp_subm_conv3x3.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int,
+                                   c_vp, c_int, c_int, c_vp]
+    L.tsp_subdivide_workspace_bytes.restype = c_sz
+    L.tsp_subdivide_workspace_bytes.argtypes = [c_i64]
+    L.tsp_subdivide.restype = c_int
+    L.tsp_subdivide.argtypes = [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]
+    _lib = L
+    return L
+
+
+def _check(fn: str, code: int) -> None:
+    if code != 0:
+        raise TspError(fn, code, lib().tsp_last_error().decode(errors="replace"))
+
+
+# --------------------------------------------------------------------------------------------
+# torch conveniences (device memory + stream plumbing only)
+# --------------------------------------------------------------------------------------------
+def _torch():
+    import torch
+    return torch
+
+
+def dtype_code(dt) -> int:
+    torch = _torch()
+    return {torch.float32: TSP_F32, torch.float16: TSP_F16, torch.bfloat16: TSP_BF16}[dt]
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensors must live on the GPU")
+
+
+def rulebook_build(coords, check: bool = True, stream=None):
+    """coords int32 [N,3] on the GPU -> tap-major int32 neighbour table [27*N] (sentinel N)."""
+    torch = _torch()
+    _require_cuda(coords)
+    c = coords.contiguous()
+    if c.dtype != torch.int32 or c.dim() != 2 or c.shape[1] != 3:
+        raise ValueError("coords must be int32 [N, 3]")
+    n = c.shape[0]
+    nbr = torch.empty(27 * n, dtype=torch.int32, device=c.device)
+    ws_bytes = lib().tsp_rulebook_workspace_bytes(n)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c.device)
+    status = torch.zeros(1, dtype=torch.int32, device=c.device)
+    _check("tsp_rulebook_build",
+           lib().tsp_rulebook_build(_ptr(c), n, _ptr(nbr), _ptr(ws), ws_bytes, _ptr(status),
+                                    _stream(stream)))
+    if check and n and int(status.item()) != 0:
+        raise TspError("tsp_rulebook_build", 3, "coordinate outside [0, 2^21-3]")
+    return nbr
+
+
+def count_pairs(nbr, n: int, stream=None) -> int:
+    torch = _torch()
+    _require_cuda(nbr)
+    cnt = torch.zeros(1, dtype=torch.int64, device=nbr.device)
+    _check("tsp_rulebook_count_pairs",
+           lib().tsp_rulebook_count_pairs(_ptr(nbr), n, _ptr(cnt), _stream(stream)))
+    return int(cnt.item())
+
+
+def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", out=None,
+                 stream=None):
+    """feats [N,Ci], nbr int32 [27*N], weight [Co,27,Ci], bias f32 [Co] -> out [N,Co]."""
+    torch = _torch()
+    _require_cuda(feats, nbr, weight, bias)
+    n, ci = feats.shape
+    co = weight.shape[0]
+    if weight.shape != (co, 27, ci):
+        raise ValueError(f"weight must be [Co,27,Ci]=[{co},27,{ci}], got {tuple(weight.shape)}")
+    if nbr.numel() != 27 * n or nbr.dtype != torch.int32:
+        raise ValueError("nbr must be int32 [27*N]")
+    if bias.dtype != torch.float32 or bias.numel() != co:
+        raise ValueError("bias must be float32 [Co]")
+    odt = out_dtype or feats.dtype
+    if out is None:
+        out = torch.empty((n, co), dtype=odt, device=feats.device)
+    f, w, b = feats.contiguous(), weight.contiguous(), bias.contiguous()
+    _check("tsp_subm_conv3x3",
+           lib().tsp_subm_conv3x3(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr), _ptr(w),
+                                  dtype_code(w.dtype), _ptr(b), co, _ptr(out),
+                                  dtype_code(out.dtype), ALGO[algo], _stream(stream)))
+    return out
+
+
+def subdivide(mask, coords, stream=None):
+    """mask uint8 [8N] (or [N,8]), coords int32 [N,3] -> (child coords [M,3], gidx [M],
+    mstart [N+1])."""
+    torch = _torch()
+    _require_cuda(mask, coords)
+    c = coords.contiguous()
+    n = c.shape[0]
+    m8 = mask.reshape(-1).contiguous()
+    if m8.dtype != torch.uint8 or m8.numel() != 8 * n:
+        raise ValueError("mask must be uint8 with 8*N entries")
+    mstart = torch.empty(n + 1, dtype=torch.int32, device=c.device)
+    child = torch.empty((max(8 * n, 1), 3), dtype=torch.int32, device=c.device)
+    gidx = torch.empty(max(8 * n, 1), dtype=torch.int32, device=c.device)
+    m_dev = torch.empty(1, dtype=torch.int64, device=c.device)
+    ws_bytes = lib().tsp_subdivide_workspace_bytes(n)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c.device)
+    _check("tsp_subdivide",
+           lib().tsp_subdivide(_ptr(m8), _ptr(c), n, _ptr(mstart), _ptr(child), _ptr(gidx),
+                               _ptr(m_dev), _ptr(ws), ws_bytes, _stream(stream)))
+    m = int(m_dev.item())
+    return child[:m], gidx[:m], mstart

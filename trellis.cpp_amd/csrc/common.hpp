@@ -1,0 +1,94 @@
+// Shared helpers for the sparse-voxel HIP library (gfx950 / CDNA4 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "trellis_sparse.h"
+
+namespace tsp {
+
+// ---- status ------------------------------------------------------------------------------
+// The C ABI never throws: every entry point returns a tsp_status and leaves a message in a
+// thread-local buffer readable through tsp_last_error().
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define TSP_CHECK_HIP(expr)                                                                 \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) {                                                             \
+            ::tsp::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),        \
+                             __FILE__, __LINE__);                                           \
+            return TSP_ERR_HIP;                                                             \
+        }                                                                                   \
+    } while (0)
+
+#define TSP_REQUIRE(cond, code, ...)                                                        \
+    do {                                                                                    \
+        if (!(cond)) {                                                                      \
+            ::tsp::set_error(__VA_ARGS__);                                                  \
+            return (code);                                                                  \
+        }                                                                                   \
+    } while (0)
+
+// Checks the launch that was just issued.
+#define TSP_CHECK_LAUNCH() TSP_CHECK_HIP(hipGetLastError())
+
+inline size_t dtype_size(int dt) { return dt == TSP_F32 ? 4 : 2; }
+inline bool dtype_valid(int dt) { return dt == TSP_F32 || dt == TSP_F16 || dt == TSP_BF16; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- element conversions -------------------------------------------------------------------
+// bf16 and fp16 values are handled as raw 16-bit patterns in memory.
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// Round to nearest even; NaN stays NaN (quiet bit forced).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return __half2float(__ushort_as_half(b));
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+template <int DT> struct Elem;
+template <> struct Elem<TSP_F32> {
+    using storage = float;
+    __device__ __forceinline__ static float load(const storage* p, int64_t i) { return p[i]; }
+    __device__ __forceinline__ static void store(storage* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Elem<TSP_BF16> {
+    using storage = uint16_t;
+    __device__ __forceinline__ static float load(const storage* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+    __device__ __forceinline__ static void store(storage* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+};
+template <> struct Elem<TSP_F16> {
+    using storage = uint16_t;
+    __device__ __forceinline__ static float load(const storage* p, int64_t i) { return f16_bits_to_f32(p[i]); }
+    __device__ __forceinline__ static void store(storage* p, int64_t i, float v) { p[i] = f32_to_f16_bits(v); }
+};
+
+// ---- MFMA operand types (gfx950) ----------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kTaps = 27;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tsp

@@ -1,0 +1,436 @@
+// Submanifold 3x3x3 convolution: one fused gather-GEMM kernel per conv.
+//
+// Replaces sparse_submconv / submconv_range (src/sparse.cpp:61-92). The reference builds, per
+// tap, a materialised get_rows gather of the zero-padded input, a mul_mat with W_t and an add
+// into the accumulator (27 x 3 graph nodes, sparse.cpp:68-77). Here every output voxel tile
+// keeps its accumulator in registers for all 27 taps; the gather reads input rows straight
+// from HBM/L2 by the neighbour table, absent taps (table value N) contribute nothing, and the
+// bias is added in the epilogue. Nothing is materialised.
+//
+// Two kernels:
+//   * k_conv_mfma  -- bf16/fp16 features and weights, fp32 accumulation on CDNA4 matrix cores
+//                     (v_mfma_f32_32x32x16_{bf16,f16}). A workgroup owns 64*WAVES output
+//                     voxels x BN output channels; each wave owns 64 voxels x BN channels. The
+//                     weight slice of the current (tap, 32-channel chunk) is staged in LDS
+//                     (double-buffered) and shared by all waves; each wave gathers its own
+//                     neighbour rows straight into MFMA operand registers, prefetching the
+//                     next chunk while the current one multiplies.
+//   * k_conv_narrow -- VALU fp32 FMA, any dtype mix and any channel count. LDS-tiled 64 voxels
+//                     x 64 channels, each thread a 4x4 register block.
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace tsp {
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// VALU kernel
+// ---------------------------------------------------------------------------------------------
+constexpr int NB_M = 64, NB_N = 64, NB_K = 32, NB_THREADS = 256;
+
+template <int FDT, int WDT, int ODT>
+__global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
+    const typename Elem<FDT>::storage* __restrict__ feats, int64_t n, int ci,
+    const int32_t* __restrict__ nbr, const typename Elem<WDT>::storage* __restrict__ weight,
+    const float* __restrict__ bias, int co, typename Elem<ODT>::storage* __restrict__ out) {
+    __shared__ float sA[NB_K][NB_M + 4];
+    __shared__ float sB[NB_K][NB_N + 4];
+    __shared__ int32_t sRow[NB_M];
+
+    const int tid = threadIdx.x;
+    const int ty = tid / 16, tx = tid % 16;
+    const int64_t row0 = (int64_t)blockIdx.x * NB_M;
+    const int co0 = blockIdx.y * NB_N;
+    const int32_t sentinel = (int32_t)n;
+
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = 0.f;
+
+    for (int t = 0; t < kTaps; ++t) {
+        int valid = 0;
+        if (tid < NB_M) {
+            const int64_t i = row0 + tid;
+            const int32_t r = (i < n) ? nbr[(int64_t)t * n + i] : sentinel;
+            sRow[tid] = r;
+            valid = r != sentinel;
+        }
+        if (!__syncthreads_or(valid)) continue;   // no voxel of the tile has this neighbour
+
+        for (int kc = 0; kc < ci; kc += NB_K) {
+            {   // gathered input rows -> sA[k][row]
+                const int r = tid / 4, kk = (tid % 4) * 8;
+                const int32_t src = sRow[r];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int k = kc + kk + j;
+                    float v = 0.f;
+                    // unsigned compare: the sentinel N (and any value outside [0,N)) reads zero
+                    if ((uint32_t)src < (uint32_t)n && k < ci)
+                        v = Elem<FDT>::load(feats, (int64_t)src * ci + k);
+                    sA[kk + j][r] = v;
+                }
+            }
+            {   // W[co][t][k] -> sB[k][co]
+                const int c = tid / 4, kk = (tid % 4) * 8;
+                const int oc = co0 + c;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int k = kc + kk + j;
+                    float v = 0.f;
+                    if (oc < co && k < ci)
+                        v = Elem<WDT>::load(weight, ((int64_t)oc * kTaps + t) * ci + k);
+                    sB[kk + j][c] = v;
+                }
+            }
+            __syncthreads();
+#pragma unroll 8
+            for (int k = 0; k < NB_K; ++k) {
+                const float4 a = *reinterpret_cast<const float4*>(&sA[k][ty * 4]);
+                const float4 b = *reinterpret_cast<const float4*>(&sB[k][tx * 4]);
+                const float av[4] = {a.x, a.y, a.z, a.w};
+                const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[p][q] = fmaf(av[p], bv[q], acc[p][q]);
+            }
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int64_t i = row0 + ty * 4 + p;
+        if (i >= n) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int oc = co0 + tx * 4 + q;
+            if (oc < co) Elem<ODT>::store(out, i * co + oc, acc[p][q] + bias[oc]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// MFMA kernel
+// ---------------------------------------------------------------------------------------------
+// Operand layout of v_mfma_f32_32x32x16_{bf16,f16} (64 lanes, l = lane):
+//   A (32 x 16): lane l holds A[l % 32][8*(l/32) .. 8*(l/32)+7]
+//   B (16 x 32): lane l holds B[8*(l/32) .. 8*(l/32)+7][l % 32]
+//   D (32 x 32): lane l, element j holds D[8*(j/4) + 4*(l/32) + (j%4)][l % 32]
+// A 16-channel k-step s of a 32-channel chunk uses channels 16*s + 8*(l/32) .. +7 for both A
+// and B, so every lane's operand is one contiguous 16-byte load.
+constexpr int MK = 32;            // channels per pipeline stage
+constexpr int MPAD = 8;           // LDS row padding (elements) of the staged weight slice
+
+template <bool BF16>
+__device__ __forceinline__ f32x16_t mfma32x32x16(const u32x4_t& a, const u32x4_t& b,
+                                                 const f32x16_t& c) {
+    if constexpr (BF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+}
+
+template <int ODT>
+__device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
+    Elem<ODT>::store(reinterpret_cast<typename Elem<ODT>::storage*>(out), idx, v);
+}
+
+template <bool BF16, int BN, int WAVES, int ODT>
+__global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd) {
+    constexpr int NT = WAVES * 64;
+    constexpr int BM = 64 * WAVES;
+    constexpr int CB = BN / 32;                       // 32-wide column blocks per wave
+    constexpr int PIECES = BN * (MK / 8);             // 16-byte pieces of one weight stage
+    constexpr int PPT = (PIECES + NT - 1) / NT;       // pieces per thread
+    static_assert(PIECES % NT == 0 || PIECES < NT, "weight stage must split evenly");
+
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN][MK + MPAD];
+    __shared__ uint32_t sMask;
+    __shared__ int8_t sTaps[kTaps];
+    __shared__ int sNTaps;
+
+    // XCD-aware tile order: consecutive workgroup ids go round-robin over the 8 XCDs, so give
+    // each XCD one contiguous range of (tile, column-tile) pairs; neighbouring tiles then
+    // gather from rows already resident in that XCD's L2.
+    const int64_t b = blockIdx.x;
+    const int64_t lin = (b % 8) * per_xcd + b / 8;
+    if (lin >= n_tiles * n_ctiles) return;
+    const int64_t tile = lin / n_ctiles;
+    const int co0 = (int)(lin % n_ctiles) * BN;
+
+    const int tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64;
+    const int lr = lane & 31, g = lane >> 5;
+    const int64_t wrow0 = tile * BM + (int64_t)wave * 64;   // this wave's first voxel
+    const int32_t sentinel = (int32_t)n;
+
+    // Taps that some voxel of the workgroup has (wave ballots, OR in LDS).
+    if (tid == 0) sMask = 0;
+    __syncthreads();
+    {
+        uint32_t wm = 0;
+        const int64_t i = wrow0 + lane;
+        for (int t = 0; t < kTaps; ++t) {
+            const bool v = (i < n) && nbr[(int64_t)t * n + i] != sentinel;
+            if (__ballot(v)) wm |= 1u << t;
+        }
+        if (lane == 0 && wm) atomicOr(&sMask, wm);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t m = sMask;
+        int k = 0;
+        while (m) {
+            const int t = __builtin_ctz(m);
+            sTaps[k++] = (int8_t)t;
+            m &= m - 1;
+        }
+        sNTaps = k;
+    }
+    __syncthreads();
+    const int ntaps = sNTaps;
+    const int nkc = ci / MK;
+    const int iters = ntaps * nkc;
+
+    f32x16_t acc[2][CB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[rb][cb][j] = 0.f;
+
+    if (iters == 0) goto epilogue;
+    {
+        // neighbour rows of this wave for the current tap: lanes l and l+32 share row l%32
+        int32_t rowsA[2];
+        auto load_rows = [&](int t, int32_t* r) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                const int64_t i = wrow0 + rb * 32 + lr;
+                r[rb] = (i < n) ? nbr[(int64_t)t * n + i] : sentinel;
+            }
+        };
+        auto load_a = [&](const int32_t* r, int kc, u32x4_t (*a)[2]) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    if ((uint32_t)r[rb] < (uint32_t)n) {   // sentinel N -> zero operand
+                        a[rb][s] = *reinterpret_cast<const u32x4_t*>(
+                            feats + (int64_t)r[rb] * ci + kc + s * 16 + g * 8);
+                    } else {
+                        a[rb][s] = u32x4_t{0u, 0u, 0u, 0u};
+                    }
+                }
+        };
+        auto load_b = [&](int t, int kc, u32x4_t* regs) {
+#pragma unroll
+            for (int p = 0; p < PPT; ++p) {
+                const int piece = tid + p * NT;
+                if (piece < PIECES) {
+                    const int c = piece / (MK / 8), kq = piece % (MK / 8);
+                    regs[p] = *reinterpret_cast<const u32x4_t*>(
+                        weight + ((int64_t)(co0 + c) * kTaps + t) * ci + kc + kq * 8);
+                }
+            }
+        };
+        auto store_b = [&](int buf, const u32x4_t* regs) {
+#pragma unroll
+            for (int p = 0; p < PPT; ++p) {
+                const int piece = tid + p * NT;
+                if (piece < PIECES) {
+                    const int c = piece / (MK / 8), kq = piece % (MK / 8);
+                    *reinterpret_cast<u32x4_t*>(&sB[buf][c][kq * 8]) = regs[p];
+                }
+            }
+        };
+
+        u32x4_t aCur[2][2], aNext[2][2];
+        u32x4_t bRegs[PPT];
+        int t = sTaps[0];
+        load_rows(t, rowsA);
+        load_a(rowsA, 0, aCur);
+        load_b(t, 0, bRegs);
+        store_b(0, bRegs);
+        __syncthreads();
+
+        for (int it = 0; it < iters; ++it) {
+            const int buf = it & 1;
+            const bool more = it + 1 < iters;
+            if (more) {
+                const int nt = sTaps[(it + 1) / nkc];
+                const int nkcoff = ((it + 1) % nkc) * MK;
+                if (nkcoff == 0) load_rows(nt, rowsA);
+                load_a(rowsA, nkcoff, aNext);
+                load_b(nt, nkcoff, bRegs);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const u32x4_t bf =
+                        *reinterpret_cast<const u32x4_t*>(&sB[buf][cb * 32 + lr][s * 16 + g * 8]);
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+                        acc[rb][cb] = mfma32x32x16<BF16>(aCur[rb][s], bf, acc[rb][cb]);
+                }
+            }
+            if (more) {
+                store_b(buf ^ 1, bRegs);
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) aCur[rb][s] = aNext[rb][s];
+            }
+            __syncthreads();
+        }
+    }
+
+epilogue:
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const int oc = co0 + cb * 32 + lr;
+        const float bv = bias[oc];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int64_t i = wrow0 + rb * 32 + 8 * (j / 4) + 4 * g + (j % 4);
+                if (i < n) store_out<ODT>(out, i * co + oc, acc[rb][cb][j] + bv);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dispatch
+// ---------------------------------------------------------------------------------------------
+template <int FDT, int WDT, int ODT>
+int launch_narrow(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
+                  const float* bias, int co, void* out, hipStream_t s) {
+    dim3 grid((unsigned)ceil_div(n, NB_M), (unsigned)ceil_div(co, NB_N));
+    hipLaunchKernelGGL((k_conv_narrow<FDT, WDT, ODT>), grid, dim3(NB_THREADS), 0, s,
+                       reinterpret_cast<const typename Elem<FDT>::storage*>(feats), n, ci, nbr,
+                       reinterpret_cast<const typename Elem<WDT>::storage*>(weight), bias, co,
+                       reinterpret_cast<typename Elem<ODT>::storage*>(out));
+    TSP_CHECK_LAUNCH();
+    return TSP_OK;
+}
+
+template <int FDT, int WDT>
+int narrow_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+               const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+    switch (odt) {
+        case TSP_F32: return launch_narrow<FDT, WDT, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s);
+        case TSP_F16: return launch_narrow<FDT, WDT, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s);
+        case TSP_BF16: return launch_narrow<FDT, WDT, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s);
+    }
+    set_error("tsp_subm_conv3x3: bad out dtype %d", odt);
+    return TSP_ERR_INVALID;
+}
+
+int dispatch_narrow(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci,
+                    const int32_t* nbr, const void* weight, const float* bias, int co, void* out,
+                    hipStream_t s) {
+    if (fdt == TSP_F32 && wdt == TSP_F32) return narrow_out<TSP_F32, TSP_F32>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    if (fdt == TSP_F32 && wdt == TSP_F16) return narrow_out<TSP_F32, TSP_F16>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    if (fdt == TSP_F32 && wdt == TSP_BF16) return narrow_out<TSP_F32, TSP_BF16>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    if (fdt == TSP_F16 && wdt == TSP_F16) return narrow_out<TSP_F16, TSP_F16>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    if (fdt == TSP_BF16 && wdt == TSP_BF16) return narrow_out<TSP_BF16, TSP_BF16>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    set_error("tsp_subm_conv3x3: unsupported dtype pair feats=%d weight=%d", fdt, wdt);
+    return TSP_ERR_UNSUPPORTED;
+}
+
+template <bool BF16, int BN, int WAVES, int ODT>
+int launch_mfma(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
+                const float* bias, int co, void* out, hipStream_t s) {
+    constexpr int BM = 64 * WAVES;
+    const int64_t n_tiles = ceil_div(n, BM);
+    const int n_ctiles = co / BN;
+    const int64_t total = n_tiles * n_ctiles;
+    const int64_t per_xcd = ceil_div(total, 8);
+    hipLaunchKernelGGL((k_conv_mfma<BF16, BN, WAVES, ODT>), dim3((unsigned)(per_xcd * 8)),
+                       dim3(WAVES * 64), 0, s, reinterpret_cast<const uint16_t*>(feats), n, ci,
+                       nbr, reinterpret_cast<const uint16_t*>(weight), bias, co, out, n_tiles,
+                       n_ctiles, per_xcd);
+    TSP_CHECK_LAUNCH();
+    return TSP_OK;
+}
+
+template <bool BF16, int BN>
+int mfma_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+             const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+    constexpr int WAVES = 4;
+    if (odt == TSP_F32) return launch_mfma<BF16, BN, WAVES, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s);
+    if (BF16 && odt == TSP_BF16) return launch_mfma<BF16, BN, WAVES, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s);
+    if (!BF16 && odt == TSP_F16) return launch_mfma<BF16, BN, WAVES, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s);
+    set_error("tsp_subm_conv3x3: MFMA path writes f32 or the feature dtype, not %d", odt);
+    return TSP_ERR_UNSUPPORTED;
+}
+
+bool mfma_eligible(int fdt, int wdt, int odt, int ci, int co) {
+    if (fdt != wdt || fdt == TSP_F32) return false;
+    if (odt != TSP_F32 && odt != fdt) return false;
+    return ci % MK == 0 && co % 64 == 0;
+}
+
+int dispatch_mfma(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+                  const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+    const bool bn128 = co % 128 == 0;
+    if (fdt == TSP_BF16)
+        return bn128 ? mfma_out<true, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
+                     : mfma_out<true, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    return bn128 ? mfma_out<false, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
+                 : mfma_out<false, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+}
+
+}  // namespace
+}  // namespace tsp
+
+using namespace tsp;
+
+extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
+                                const int32_t* d_nbr, const void* d_weight, int weight_dtype,
+                                const float* d_bias, int co, void* d_out, int out_dtype, int algo,
+                                void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3: n=%lld out of range", (long long)n);
+    TSP_REQUIRE(ci > 0 && co > 0, TSP_ERR_INVALID, "tsp_subm_conv3x3: ci=%d co=%d", ci, co);
+    TSP_REQUIRE(dtype_valid(feat_dtype) && dtype_valid(weight_dtype) && dtype_valid(out_dtype),
+                TSP_ERR_INVALID, "tsp_subm_conv3x3: bad dtype");
+    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_NARROW, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3: bad algo %d", algo);
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_feats && d_nbr && d_weight && d_bias && d_out, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3: null pointer");
+    TSP_REQUIRE(d_out != d_feats, TSP_ERR_INVALID, "tsp_subm_conv3x3: out aliases feats");
+    TSP_REQUIRE((int64_t)ci * kTaps * co < (int64_t)1 << 40, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3: weight too large");
+    hipStream_t s = as_stream(stream);
+    const bool eligible = mfma_eligible(feat_dtype, weight_dtype, out_dtype, ci, co) &&
+                          (reinterpret_cast<uintptr_t>(d_feats) % 16 == 0) &&
+                          (reinterpret_cast<uintptr_t>(d_weight) % 16 == 0);
+    if (algo == TSP_ALGO_MFMA) {
+        TSP_REQUIRE(eligible, TSP_ERR_UNSUPPORTED,
+                    "tsp_subm_conv3x3: MFMA path needs f16/bf16 feats and weights of one dtype, "
+                    "16-byte aligned buffers, ci %% 32 == 0 and co %% 64 == 0 (got ci=%d co=%d)",
+                    ci, co);
+    }
+    if (algo == TSP_ALGO_MFMA || (algo == TSP_ALGO_AUTO && eligible))
+        return dispatch_mfma(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight, d_bias, co,
+                             d_out, s);
+    return dispatch_narrow(feat_dtype, weight_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight,
+                           d_bias, co, d_out, s);
+}
