@@ -87,7 +87,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="shells256-c128-bf16")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -126,14 +126,36 @@ def main():
     rulebook_ms = rb_ev[0].elapsed_time(rb_ev[1]) / 5
     pairs = pkg.count_pairs(nbr, w.n)
 
+    # The MFMA path runs with a conv plan of the table and packed weights, both built once
+    # (like the table, a plan serves every conv of a stage; weights are packed at model load).
+    planned = (args.algo in ("auto", "mfma") and w.dtype in ("bf16", "f16")
+               and w.ci % 16 == 0 and w.co % 64 == 0)
+    plan_ms = None
+    if planned:
+        plan = pkg.conv_plan_build(nbr, w.n)
+        packed = pkg.conv_weight_pack(weight)
+        torch.cuda.synchronize()
+        rb_ev[0].record(stream)
+        for _ in range(5):
+            plan = pkg.conv_plan_build(nbr, w.n)
+        rb_ev[1].record(stream)
+        torch.cuda.synchronize()
+        plan_ms = rb_ev[0].elapsed_time(rb_ev[1]) / 5
+
+        def step():
+            pkg.subm_conv3x3_planned(feats, nbr, plan, packed, bias, w.co, out=out)
+    else:
+        def step():
+            pkg.subm_conv3x3(feats, nbr, weight, bias, out=out, algo=args.algo)
+
     for _ in range(args.warmup):
-        pkg.subm_conv3x3(feats, nbr, weight, bias, out=out, algo=args.algo)
+        step()
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     t0 = time.perf_counter()
     ev[0].record(stream)
     for _ in range(args.steps):
-        pkg.subm_conv3x3(feats, nbr, weight, bias, out=out, algo=args.algo)
+        step()
     ev[1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -177,12 +199,14 @@ def main():
         "config": {
             "workload": w.name, "grid": w.grid, "n_voxels": w.n, "active_pairs": pairs,
             "pairs_per_voxel": pairs / max(w.n, 1), "c_in": w.ci, "c_out": w.co,
-            "accumulate": "f32", "out_dtype": w.dtype, "algo": args.algo,
+            "accumulate": "f32", "out_dtype": w.dtype,
+            "algo": "mfma-planned" if planned else args.algo,
             "parallelism": "single-gpu",
         },
         "tflops": tflops,
         "tflops_dense27_equivalent": flops_dense / (ms * 1e-3) / 1e12,
         "rulebook_ms": rulebook_ms,
+        "plan_ms": plan_ms,
         "wall_s_timed_region": wall,
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -41,8 +41,14 @@ typedef enum {
 typedef enum { TSP_F32 = 0, TSP_F16 = 1, TSP_BF16 = 2 } tsp_dtype;
 
 /* Conv kernel selection. AUTO picks MFMA for 16-bit features with Ci % 32 == 0 and
- * Co % 64 == 0, and the VALU kernel otherwise. */
-typedef enum { TSP_ALGO_AUTO = 0, TSP_ALGO_MFMA = 1, TSP_ALGO_NARROW = 2 } tsp_algo;
+ * Co % 64 == 0, and the VALU kernel otherwise.
+ *   MFMA         matrix-core kernel that stages each tile's distinct neighbour rows in LDS
+ *   NARROW       VALU fp32-FMA kernel, any dtype mix and channel count
+ *   MFMA_GATHER  matrix-core kernel that gathers neighbour rows straight from L2/HBM (no LDS
+ *                staging; same eligibility as MFMA) */
+typedef enum {
+    TSP_ALGO_AUTO = 0, TSP_ALGO_MFMA = 1, TSP_ALGO_NARROW = 2, TSP_ALGO_MFMA_GATHER = 3
+} tsp_algo;
 
 /* Thread-local message for the last failing call on this thread ("" if none). */
 const char* tsp_last_error(void);
@@ -87,6 +93,33 @@ int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
                      const int32_t* d_nbr, const void* d_weight, int weight_dtype,
                      const float* d_bias, int co, void* d_out, int out_dtype, int algo,
                      void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Reusable conv plan and packed weights (no counterpart call in the reference: they split
+ * the work sparse_submconv repeats on every call, sparse.cpp:61-92, into what depends only on
+ * the neighbour table -- shared by every conv of a decoder stage, shape_decoder.cpp:93-103 --
+ * and what depends only on the weights, loaded once per model, trellis_model.cpp:96-142).
+ *
+ * A plan holds, for every tile of 512 consecutive voxels, the sorted set of input rows the
+ * tile's table entries reference and each entry's rank in that set; the planned conv stages
+ * those rows in LDS once per tile. Packed weights hold W [Co][27][Ci] in the order the
+ * matrix-core operands are read. Both are plain device buffers owned by the caller.
+ * ------------------------------------------------------------------------------------- */
+size_t tsp_conv_plan_bytes(int64_t n);
+int tsp_conv_plan_build(const int32_t* d_nbr, int64_t n, void* d_plan, size_t plan_bytes,
+                        void* stream);
+
+/* W [co][27][ci] (f16 or bf16; ci % 16 == 0, co % 32 == 0) -> d_packed, same byte size. */
+int tsp_conv_weight_pack(const void* d_weight, int dtype, int ci, int co, void* d_packed,
+                         void* stream);
+
+/* The conv of tsp_subm_conv3x3 (MFMA kernel) with a plan of d_nbr and packed weights:
+ * f16/bf16 features, ci % 16 == 0, co % 64 == 0, out f32 or the feature dtype. d_nbr is still
+ * read for the tiles whose rows do not fit the LDS stage. */
+int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t n, int ci,
+                             const int32_t* d_nbr, const void* d_plan,
+                             const void* d_packed_weight, const float* d_bias, int co,
+                             void* d_out, int out_dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 2x subdivision (channel-to-spatial) index math.

@@ -90,6 +90,25 @@ def test_conv_validation(pkg):
     assert f(algo=1, co=96) == 4                                    # co % 64 != 0
 
 
+def test_plan_and_pack_validation(pkg):
+    L = pkg.lib()
+    assert L.tsp_conv_plan_build(FAKE, -1, FAKE, 1 << 30, NULL) == 1
+    assert L.tsp_conv_plan_build(NULL, 0, NULL, 0, NULL) == 0
+    pb = L.tsp_conv_plan_bytes(100000)
+    assert pb > 27 * 2 * 100000
+    assert L.tsp_conv_plan_build(FAKE, 100000, FAKE, pb - 1, NULL) == 5
+    assert L.tsp_conv_weight_pack(FAKE, 0, 64, 64, ctypes.c_void_p(0x2000), NULL) == 4   # f32
+    assert L.tsp_conv_weight_pack(FAKE, 2, 40, 64, ctypes.c_void_p(0x2000), NULL) == 4   # ci%16
+    assert L.tsp_conv_weight_pack(FAKE, 2, 64, 48, ctypes.c_void_p(0x2000), NULL) == 4   # co%32
+    assert L.tsp_conv_weight_pack(FAKE, 2, 64, 64, FAKE, NULL) == 1                      # aliased
+    p = lambda **kw: L.tsp_subm_conv3x3_planned(
+        kw.get("feats", FAKE), kw.get("dt", 2), kw.get("n", 100), kw.get("ci", 64), FAKE,
+        FAKE, FAKE, FAKE, kw.get("co", 64), kw.get("out", ctypes.c_void_p(0x2000)),
+        kw.get("odt", 0), NULL)
+    assert p(dt=0) == 4 and p(odt=1) == 4 and p(ci=40) == 4 and p(co=96) == 4
+    assert p(n=-5) == 1 and p(out=FAKE) == 1 and p(n=0) == 0
+
+
 def test_subdivide_validation(pkg):
     L = pkg.lib()
     assert L.tsp_subdivide(FAKE, FAKE, -1, FAKE, FAKE, FAKE, FAKE, FAKE, 64, NULL) == 1

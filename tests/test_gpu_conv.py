@@ -82,10 +82,73 @@ def test_mfma_vs_oracle(gpu_lib, orc, shells, ci, co, n, dtype_name):
     rng = np.random.default_rng(ci * 1000 + co + n)
     coords, feats, weight, bias = _rand_case(shells, rng, n, ci, co, key)
     ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
-    out, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo="mfma")
-    assert orc.rel_err(out, ref) < TOL_16
-    out_n, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo="narrow")
-    assert orc.rel_err(out_n, ref) < TOL_16
+    for algo in ("mfma", "mfma_gather", "narrow"):
+        out, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo=algo)
+        assert orc.rel_err(out, ref) < TOL_16, algo
+
+
+def _run_planned(pkg, coords, feats, weight, bias, dtype, out_dtype=None):
+    import torch
+    c = torch.from_numpy(np.ascontiguousarray(coords, np.int32)).cuda()
+    nbr = pkg.rulebook_build(c)
+    plan = pkg.conv_plan_build(nbr, len(coords))
+    pw = pkg.conv_weight_pack(_dev(weight, dtype))
+    out = pkg.subm_conv3x3_planned(_dev(feats, dtype), nbr, plan, pw, _dev(bias, torch.float32),
+                                   weight.shape[0], out_dtype=out_dtype or torch.float32)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("ci,co,n", [(64, 64, 0), (128, 128, 0), (48, 64, 900), (256, 256, 2100),
+                                     (32, 192, 513), (16, 128, 1)])
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_planned_vs_oracle(gpu_lib, orc, shells, ci, co, n, dtype_name):
+    _case(f"planned ci={ci} co={co} n={n} {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(ci * 7 + co + n)
+    coords, feats, weight, bias = _rand_case(shells, rng, n, ci, co, key)
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    assert orc.rel_err(_run_planned(gpu_lib, coords, feats, weight, bias, dt), ref) < TOL_16
+    out16 = _run_planned(gpu_lib, coords, feats, weight, bias, dt, out_dtype=dt)
+    assert orc.rel_err(out16, ref) < TOL_16_OUT
+
+
+def test_weight_pack_layout(gpu_lib):
+    """packed[((c32*nkc + kc)*27 + t)*64 + lane][e] = W[32*c32 + lane%32][t][16*kc + 8*(lane//32) + e]"""
+    _case("weight pack layout")
+    import torch
+    ci, co = 48, 96
+    w = torch.arange(co * 27 * ci, dtype=torch.float32).reshape(co, 27, ci)
+    w16 = (w % 2048).to(torch.float16)        # exactly representable, all distinct per 2048
+    packed = gpu_lib.conv_weight_pack(w16.cuda()).cpu().reshape(co // 32, ci // 16, 27, 2, 32, 8)
+    ref = w16.reshape(co // 32, 32, 27, ci // 16, 2, 8).permute(0, 3, 2, 4, 1, 5)
+    assert torch.equal(packed, ref)
+
+
+@pytest.mark.parametrize("n_shell", ["r14", "r22"])
+def test_mfma_unsorted_inputs(gpu_lib, orc, shells, n_shell):
+    """Row order scattered at random: a 512-voxel tile then references far more distinct rows
+    than LDS holds (r14: ~23K voxels, span fits but the set does not) or a row range wider
+    than the bitmap (r22: ~92K voxels), so the MFMA kernel's direct path runs."""
+    _case(f"unsorted {n_shell}")
+    import torch
+    rng = np.random.default_rng(61)
+    r = 14.0 if n_shell == "r14" else 22.0
+    coords = rng.permutation(shells.sphere_shell(64, 32.0, r, r + 2.0))
+    n = len(coords)
+    feats = shells.round_to(rng.standard_normal((n, 64)).astype(np.float32), "bf16")
+    weight = shells.round_to((rng.standard_normal((128, 27, 64)) / 40).astype(np.float32), "bf16")
+    bias = (rng.standard_normal(128) * 0.1).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    rows = np.unique(np.concatenate([np.arange(600), rng.integers(0, n, 2000)]))
+    ref = orc.subm_conv_f64_rows(feats, nbr, weight, bias, rows)
+    for algo in ("mfma", "mfma_gather"):
+        out, _ = _run(gpu_lib, coords, feats, weight, bias, torch.bfloat16, algo=algo)
+        assert orc.rel_err(out[rows], ref) < TOL_16, algo
+    out = _run_planned(gpu_lib, coords, feats, weight, bias, torch.bfloat16)
+    assert orc.rel_err(out[rows], ref) < TOL_16
 
 
 @pytest.mark.parametrize("ci,co", [(3, 5), (16, 8), (64, 64), (33, 70)])
@@ -169,9 +232,15 @@ def test_full_size_sampled_rows(gpu_lib, orc, shells, name):
     b = _dev(w.bias, torch.float32)
     out = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma")
     out2 = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma")
+    outg = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma_gather")
     outn = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="narrow")
+    plan = gpu_lib.conv_plan_build(nbr, w.n)
+    outp = gpu_lib.subm_conv3x3_planned(f, nbr, plan, gpu_lib.conv_weight_pack(wt), b, w.co,
+                                        out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
+    assert torch.equal(outp, out)        # same MFMA order: the stored plan changes nothing
+    assert orc.rel_err(outg.cpu().numpy(), out.cpu().numpy()) < TOL_16
     rng = np.random.default_rng(0)
     rows = np.unique(np.concatenate([np.arange(512), np.arange(w.n - 512, w.n),
                                      rng.integers(0, w.n, 3000)]))

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtrellis_sparse.so")
 
 TSP_F32, TSP_F16, TSP_BF16 = 0, 1, 2
-ALGO = {"auto": 0, "mfma": 1, "narrow": 2}
+ALGO = {"auto": 0, "mfma": 1, "narrow": 2, "mfma_gather": 3}
 STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "RANGE", 4: "UNSUPPORTED", 5: "WORKSPACE"}
 
 # Every extern "C" entry point the header declares (checked by the CPU test suite).
@@ -25,6 +25,8 @@ EXPORTS = (
     "tsp_last_error", "tsp_version",
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
     "tsp_subm_conv3x3",
+    "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
+    "tsp_subm_conv3x3_planned",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
 )
 
@@ -65,6 +67,15 @@ def lib() -> ctypes.CDLL:
     L.tsp_subm_conv3x3.restype = c_int
     L.tsp_subm_conv3x3.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int,
                                    c_vp, c_int, c_int, c_vp]
+    L.tsp_conv_plan_bytes.restype = c_sz
+    L.tsp_conv_plan_bytes.argtypes = [c_i64]
+    L.tsp_conv_plan_build.restype = c_int
+    L.tsp_conv_plan_build.argtypes = [c_vp, c_i64, c_vp, c_sz, c_vp]
+    L.tsp_conv_weight_pack.restype = c_int
+    L.tsp_conv_weight_pack.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
+    L.tsp_subm_conv3x3_planned.restype = c_int
+    L.tsp_subm_conv3x3_planned.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
+                                           c_int, c_vp, c_int, c_vp]
     L.tsp_subdivide_workspace_bytes.restype = c_sz
     L.tsp_subdivide_workspace_bytes.argtypes = [c_i64]
     L.tsp_subdivide.restype = c_int
@@ -157,6 +168,51 @@ def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", o
            lib().tsp_subm_conv3x3(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr), _ptr(w),
                                   dtype_code(w.dtype), _ptr(b), co, _ptr(out),
                                   dtype_code(out.dtype), ALGO[algo], _stream(stream)))
+    return out
+
+
+def conv_plan_build(nbr, n: int, stream=None):
+    """Plan of neighbour table nbr (int32 [27*N]) for tsp_subm_conv3x3_planned -> uint8 buffer."""
+    torch = _torch()
+    _require_cuda(nbr)
+    nb = lib().tsp_conv_plan_bytes(n)
+    plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=nbr.device)
+    _check("tsp_conv_plan_build",
+           lib().tsp_conv_plan_build(_ptr(nbr), n, _ptr(plan), nb, _stream(stream)))
+    return plan
+
+
+def conv_weight_pack(weight, stream=None):
+    """W [Co,27,Ci] f16/bf16 -> packed copy (same dtype and byte size, flat)."""
+    torch = _torch()
+    _require_cuda(weight)
+    w = weight.contiguous()
+    co, _, ci = w.shape
+    packed = torch.empty(w.numel(), dtype=w.dtype, device=w.device)
+    _check("tsp_conv_weight_pack",
+           lib().tsp_conv_weight_pack(_ptr(w), dtype_code(w.dtype), ci, co, _ptr(packed),
+                                      _stream(stream)))
+    return packed
+
+
+def subm_conv3x3_planned(feats, nbr, plan, packed_weight, bias, co: int, out_dtype=None, out=None,
+                         stream=None):
+    """The MFMA conv with a plan (conv_plan_build) and packed weights (conv_weight_pack)."""
+    torch = _torch()
+    _require_cuda(feats, nbr, plan, packed_weight, bias)
+    n, ci = feats.shape
+    if packed_weight.numel() != co * 27 * ci:
+        raise ValueError("packed weight size does not match [Co,27,Ci]")
+    if bias.dtype != torch.float32 or bias.numel() != co:
+        raise ValueError("bias must be float32 [Co]")
+    odt = out_dtype or feats.dtype
+    if out is None:
+        out = torch.empty((n, co), dtype=odt, device=feats.device)
+    f = feats.contiguous()
+    _check("tsp_subm_conv3x3_planned",
+           lib().tsp_subm_conv3x3_planned(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr),
+                                          _ptr(plan), _ptr(packed_weight), _ptr(bias), co,
+                                          _ptr(out), dtype_code(out.dtype), _stream(stream)))
     return out
 
 

@@ -7,19 +7,20 @@
 // from HBM/L2 by the neighbour table, absent taps (table value N) contribute nothing, and the
 // bias is added in the epilogue. Nothing is materialised.
 //
-// Two kernels:
-//   * k_conv_mfma  -- bf16/fp16 features and weights, fp32 accumulation on CDNA4 matrix cores
-//                     (v_mfma_f32_32x32x16_{bf16,f16}). A workgroup owns 64*WAVES output
-//                     voxels x BN output channels; each wave owns 64 voxels x BN channels. The
-//                     weight slice of the current (tap, 32-channel chunk) is staged in LDS
-//                     (double-buffered) and shared by all waves; each wave gathers its own
-//                     neighbour rows straight into MFMA operand registers, prefetching the
-//                     next chunk while the current one multiplies.
+// Three kernels:
+//   * k_conv_halo (conv_halo.hip) -- the MFMA kernel: bf16/fp16 features and weights, fp32
+//                     accumulation, each tile's distinct neighbour rows staged in LDS.
+//   * k_conv_mfma  -- MFMA kernel that gathers straight from L2/HBM: a workgroup owns 64*WAVES
+//                     output voxels x BN output channels; each wave owns 64 voxels x BN
+//                     channels. The weight slice of the current (tap, 32-channel chunk) is
+//                     staged in LDS (double-buffered) and shared by all waves; each wave
+//                     gathers its own neighbour rows straight into MFMA operand registers,
+//                     prefetching the next chunk while the current one multiplies.
 //   * k_conv_narrow -- VALU fp32 FMA, any dtype mix and any channel count. LDS-tiled 64 voxels
 //                     x 64 channels, each thread a 4x4 register block.
 #include <algorithm>
 
-#include "common.hpp"
+#include "conv_internal.hpp"
 
 namespace tsp {
 namespace {
@@ -115,33 +116,10 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
 }
 
 // ---------------------------------------------------------------------------------------------
-// MFMA kernel
+// MFMA kernel gathering from L2/HBM
 // ---------------------------------------------------------------------------------------------
-// Operand layout of v_mfma_f32_32x32x16_{bf16,f16} (64 lanes, l = lane):
-//   A (32 x 16): lane l holds A[l % 32][8*(l/32) .. 8*(l/32)+7]
-//   B (16 x 32): lane l holds B[8*(l/32) .. 8*(l/32)+7][l % 32]
-//   D (32 x 32): lane l, element j holds D[8*(j/4) + 4*(l/32) + (j%4)][l % 32]
-// A 16-channel k-step s of a 32-channel chunk uses channels 16*s + 8*(l/32) .. +7 for both A
-// and B, so every lane's operand is one contiguous 16-byte load.
 constexpr int MK = 32;            // channels per pipeline stage
 constexpr int MPAD = 8;           // LDS row padding (elements) of the staged weight slice
-
-template <bool BF16>
-__device__ __forceinline__ f32x16_t mfma32x32x16(const u32x4_t& a, const u32x4_t& b,
-                                                 const f32x16_t& c) {
-    if constexpr (BF16) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-    } else {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-    }
-}
-
-template <int ODT>
-__device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
-    Elem<ODT>::store(reinterpret_cast<typename Elem<ODT>::storage*>(out), idx, v);
-}
 
 template <bool BF16, int BN, int WAVES, int ODT>
 __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
@@ -313,6 +291,7 @@ epilogue:
     }
 }
 
+
 // ---------------------------------------------------------------------------------------------
 // Dispatch
 // ---------------------------------------------------------------------------------------------
@@ -353,8 +332,8 @@ int dispatch_narrow(int fdt, int wdt, int odt, const void* feats, int64_t n, int
 }
 
 template <bool BF16, int BN, int WAVES, int ODT>
-int launch_mfma(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
-                const float* bias, int co, void* out, hipStream_t s) {
+int launch_gather(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
+                  const float* bias, int co, void* out, hipStream_t s) {
     constexpr int BM = 64 * WAVES;
     const int64_t n_tiles = ceil_div(n, BM);
     const int n_ctiles = co / BN;
@@ -369,30 +348,35 @@ int launch_mfma(const void* feats, int64_t n, int ci, const int32_t* nbr, const 
 }
 
 template <bool BF16, int BN>
-int mfma_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
-             const void* weight, const float* bias, int co, void* out, hipStream_t s) {
-    constexpr int WAVES = 4;
-    if (odt == TSP_F32) return launch_mfma<BF16, BN, WAVES, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s);
-    if (BF16 && odt == TSP_BF16) return launch_mfma<BF16, BN, WAVES, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s);
-    if (!BF16 && odt == TSP_F16) return launch_mfma<BF16, BN, WAVES, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s);
+int gather_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+               const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+    if (odt == TSP_F32) return launch_gather<BF16, BN, 4, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s);
+    if (BF16 && odt == TSP_BF16) return launch_gather<BF16, BN, 4, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s);
+    if (!BF16 && odt == TSP_F16) return launch_gather<BF16, BN, 4, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s);
     set_error("tsp_subm_conv3x3: MFMA path writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
 
-bool mfma_eligible(int fdt, int wdt, int odt, int ci, int co) {
-    if (fdt != wdt || fdt == TSP_F32) return false;
-    if (odt != TSP_F32 && odt != fdt) return false;
-    return ci % MK == 0 && co % 64 == 0;
-}
-
-int dispatch_mfma(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
-                  const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+int dispatch_gather(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+                    const void* weight, const float* bias, int co, void* out, hipStream_t s) {
     const bool bn128 = co % 128 == 0;
     if (fdt == TSP_BF16)
-        return bn128 ? mfma_out<true, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
-                     : mfma_out<true, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
-    return bn128 ? mfma_out<false, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
-                 : mfma_out<false, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+        return bn128 ? gather_out<true, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
+                     : gather_out<true, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+    return bn128 ? gather_out<false, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
+                 : gather_out<false, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+}
+
+// MFMA kernels: 16-bit feats and weights of one dtype, out f32 or that dtype, ci % 32 == 0,
+// co % 64 == 0, 16-byte aligned operands, and a weight below 4 GiB (32-bit offsets).
+bool mfma_eligible(int fdt, int wdt, int odt, int ci, int co, const void* f, const void* w,
+                   const void* o) {
+    if (fdt != wdt || fdt == TSP_F32) return false;
+    if (odt != TSP_F32 && odt != fdt) return false;
+    if (reinterpret_cast<uintptr_t>(f) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
+        reinterpret_cast<uintptr_t>(o) % 16)
+        return false;
+    return ci % MK == 0 && co % 64 == 0 && (int64_t)kTaps * ci * co * 2 < ((int64_t)1 << 32);
 }
 
 }  // namespace
@@ -400,37 +384,101 @@ int dispatch_mfma(int fdt, int odt, const void* feats, int64_t n, int ci, const 
 
 using namespace tsp;
 
+#define TSP_CONV_COMMON_CHECKS(fn)                                                             \
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX, TSP_ERR_INVALID, fn ": n=%lld out of range", \
+                (long long)n);                                                                \
+    TSP_REQUIRE(ci > 0 && co > 0, TSP_ERR_INVALID, fn ": ci=%d co=%d", ci, co);               \
+    TSP_REQUIRE((int64_t)ci * kTaps * co < (int64_t)1 << 40, TSP_ERR_INVALID,                 \
+                fn ": weight too large")
+
 extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
                                 const int32_t* d_nbr, const void* d_weight, int weight_dtype,
                                 const float* d_bias, int co, void* d_out, int out_dtype, int algo,
                                 void* stream) {
     clear_error();
-    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX, TSP_ERR_INVALID,
-                "tsp_subm_conv3x3: n=%lld out of range", (long long)n);
-    TSP_REQUIRE(ci > 0 && co > 0, TSP_ERR_INVALID, "tsp_subm_conv3x3: ci=%d co=%d", ci, co);
+    TSP_CONV_COMMON_CHECKS("tsp_subm_conv3x3");
     TSP_REQUIRE(dtype_valid(feat_dtype) && dtype_valid(weight_dtype) && dtype_valid(out_dtype),
                 TSP_ERR_INVALID, "tsp_subm_conv3x3: bad dtype");
-    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_NARROW, TSP_ERR_INVALID,
+    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_MFMA_GATHER, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3: bad algo %d", algo);
     if (n == 0) return TSP_OK;
     TSP_REQUIRE(d_feats && d_nbr && d_weight && d_bias && d_out, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3: null pointer");
     TSP_REQUIRE(d_out != d_feats, TSP_ERR_INVALID, "tsp_subm_conv3x3: out aliases feats");
-    TSP_REQUIRE((int64_t)ci * kTaps * co < (int64_t)1 << 40, TSP_ERR_INVALID,
-                "tsp_subm_conv3x3: weight too large");
     hipStream_t s = as_stream(stream);
-    const bool eligible = mfma_eligible(feat_dtype, weight_dtype, out_dtype, ci, co) &&
-                          (reinterpret_cast<uintptr_t>(d_feats) % 16 == 0) &&
-                          (reinterpret_cast<uintptr_t>(d_weight) % 16 == 0);
-    if (algo == TSP_ALGO_MFMA) {
+    const bool eligible =
+        mfma_eligible(feat_dtype, weight_dtype, out_dtype, ci, co, d_feats, d_weight, d_out);
+    if (algo == TSP_ALGO_MFMA || algo == TSP_ALGO_MFMA_GATHER) {
         TSP_REQUIRE(eligible, TSP_ERR_UNSUPPORTED,
                     "tsp_subm_conv3x3: MFMA path needs f16/bf16 feats and weights of one dtype, "
                     "16-byte aligned buffers, ci %% 32 == 0 and co %% 64 == 0 (got ci=%d co=%d)",
                     ci, co);
     }
+    if (algo == TSP_ALGO_MFMA_GATHER)
+        return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight, d_bias, co,
+                               d_out, s);
     if (algo == TSP_ALGO_MFMA || (algo == TSP_ALGO_AUTO && eligible))
-        return dispatch_mfma(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight, d_bias, co,
-                             d_out, s);
+        return halo_conv_launch(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, nullptr, d_weight,
+                                d_bias, co, d_out, s);
     return dispatch_narrow(feat_dtype, weight_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight,
                            d_bias, co, d_out, s);
+}
+
+extern "C" size_t tsp_conv_plan_bytes(int64_t n) { return n < 0 ? 0 : halo_plan_bytes(n); }
+
+extern "C" int tsp_conv_plan_build(const int32_t* d_nbr, int64_t n, void* d_plan,
+                                   size_t plan_bytes, void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX, TSP_ERR_INVALID,
+                "tsp_conv_plan_build: n=%lld out of range", (long long)n);
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_nbr && d_plan, TSP_ERR_INVALID, "tsp_conv_plan_build: null pointer");
+    TSP_REQUIRE(plan_bytes >= halo_plan_bytes(n), TSP_ERR_WORKSPACE,
+                "tsp_conv_plan_build: plan buffer %zu < %zu bytes", plan_bytes,
+                halo_plan_bytes(n));
+    return halo_plan_build(d_nbr, n, d_plan, as_stream(stream));
+}
+
+extern "C" int tsp_conv_weight_pack(const void* d_weight, int dtype, int ci, int co,
+                                    void* d_packed, void* stream) {
+    clear_error();
+    TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
+                "tsp_conv_weight_pack: packed weights are f16 or bf16, not dtype %d", dtype);
+    TSP_REQUIRE(ci > 0 && co > 0 && ci % 16 == 0 && co % 32 == 0, TSP_ERR_UNSUPPORTED,
+                "tsp_conv_weight_pack: needs ci %% 16 == 0 and co %% 32 == 0 (ci=%d co=%d)", ci, co);
+    TSP_REQUIRE((int64_t)kTaps * ci * co * 2 < ((int64_t)1 << 32), TSP_ERR_UNSUPPORTED,
+                "tsp_conv_weight_pack: weight of 4 GiB or more");
+    TSP_REQUIRE(d_weight && d_packed && d_weight != d_packed, TSP_ERR_INVALID,
+                "tsp_conv_weight_pack: null or aliased pointer");
+    TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_weight) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_packed) % 16 == 0,
+                TSP_ERR_INVALID, "tsp_conv_weight_pack: buffers must be 16-byte aligned");
+    return halo_weight_pack(d_weight, ci, co, d_packed, as_stream(stream));
+}
+
+extern "C" int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t n, int ci,
+                                        const int32_t* d_nbr, const void* d_plan,
+                                        const void* d_packed_weight, const float* d_bias, int co,
+                                        void* d_out, int out_dtype, void* stream) {
+    clear_error();
+    TSP_CONV_COMMON_CHECKS("tsp_subm_conv3x3_planned");
+    TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned: features are f16 or bf16, not dtype %d", dtype);
+    TSP_REQUIRE(out_dtype == TSP_F32 || out_dtype == dtype, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned: out is f32 or the feature dtype");
+    TSP_REQUIRE(ci % 16 == 0 && co % 64 == 0, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned: needs ci %% 16 == 0 and co %% 64 == 0 (ci=%d co=%d)",
+                ci, co);
+    TSP_REQUIRE((int64_t)kTaps * ci * co * 2 < ((int64_t)1 << 32), TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned: weight of 4 GiB or more");
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_feats && d_nbr && d_plan && d_packed_weight && d_bias && d_out,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned: null pointer");
+    TSP_REQUIRE(d_out != d_feats, TSP_ERR_INVALID, "tsp_subm_conv3x3_planned: out aliases feats");
+    TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_feats) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_packed_weight) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_out) % 16 == 0,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned: buffers must be 16-byte aligned");
+    return halo_conv_launch(dtype, out_dtype, d_feats, n, ci, d_nbr, d_plan, d_packed_weight,
+                            d_bias, co, d_out, as_stream(stream));
 }

@@ -1,0 +1,45 @@
+// Pieces shared by the conv translation units (conv.hip, conv_halo.hip).
+#pragma once
+#include "common.hpp"
+
+namespace tsp {
+
+// Operand layout of v_mfma_f32_32x32x16_{bf16,f16} (64 lanes, l = lane):
+//   A (32 x 16): lane l holds A[l % 32][8*(l/32) .. 8*(l/32)+7]
+//   B (16 x 32): lane l holds B[8*(l/32) .. 8*(l/32)+7][l % 32]
+//   D (32 x 32): lane l, element j holds D[8*(j/4) + 4*(l/32) + (j%4)][l % 32]
+// A 16-channel k-step uses channels 8*(l/32) .. +7 of lane l for both A and B, so every lane's
+// operand is one contiguous 16-byte load.
+template <bool BF16>
+__device__ __forceinline__ f32x16_t mfma32x32x16(const u32x4_t& a, const u32x4_t& b,
+                                                 const f32x16_t& c) {
+    if constexpr (BF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+}
+
+template <int ODT>
+__device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
+    Elem<ODT>::store(reinterpret_cast<typename Elem<ODT>::storage*>(out), idx, v);
+}
+
+// ---- LDS-staged ("halo") MFMA conv, conv_halo.hip --------------------------------------------
+constexpr int HB_M = 512;   // output voxels per workgroup (and per plan tile)
+
+// Bytes of a conv plan for n voxels (see tsp_conv_plan_bytes).
+size_t halo_plan_bytes(int64_t n);
+// Builds the plan of neighbour table `nbr` into `plan`.
+int halo_plan_build(const int32_t* nbr, int64_t n, void* plan, hipStream_t s);
+// Packs [co][27][ci] 16-bit weights into the MFMA operand order (ci % 16 == 0, co % 32 == 0).
+int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s);
+// The conv. With plan == nullptr the tile plan is built inside the kernel and `weight` is in
+// the [co][27][ci] layout; with a plan, `weight` must be packed by halo_weight_pack.
+int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+                     const void* plan, const void* weight, const float* bias, int co, void* out,
+                     hipStream_t s);
+
+}  // namespace tsp
