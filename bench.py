@@ -44,26 +44,34 @@ def load_package():
 
 
 def cpu_baseline(w, nbr, budget_s: float):
-    """Times the oracle's fp32 conv (all 27 taps against the zero row, tap-sequential
-    accumulation -- the reference's algorithm) on a contiguous output-row sample sized to take
-    about `budget_s` seconds on all host threads, then the same sample size/8 on one thread."""
-    import numpy as np
+    """The CPU oracle (a C restatement of the reference's algorithm: all 27 taps against the
+    zero row, fp32, tap-sequential accumulation, bias last, OpenMP over output rows) timed on
+    this host: one warm-up, then the median of >= 3 timed runs over a contiguous output-row
+    range sized so the timed runs take about budget_s (the whole conv when it is fast enough);
+    a 1-thread run over a smaller range; and the neighbour-table build (hash restatement,
+    single-threaded like the reference's build_neighbor_table)."""
+    import statistics
     orc = _load("trellis_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     n = w.n
-    r0 = n // 3
-    probe = min(n - r0, 2000)
+
+    def timed(r0, r1, th):
+        t = time.perf_counter()
+        orc.subm_conv_f32_rows(w.feats, nbr, w.weight, w.bias, r0, r1, th)
+        return time.perf_counter() - t
+
+    probe = min(n, 4000)
+    per_row = timed(0, probe, threads) / probe                     # also the warm-up
+    rows = int(min(n, max(probe, budget_s / 3 / max(per_row, 1e-12))))
+    r0 = (n - rows) // 2
+    reps = int(min(20, max(3, budget_s / max(rows * per_row, 1e-12))))
+    runs = [timed(r0, r0 + rows, threads) for _ in range(reps)]
+    dt = statistics.median(runs)
+    rows1 = max(1, min(rows, int(max(budget_s / 4, 1.0) / max(per_row * threads, 1e-12))))
+    dt1 = timed(r0, r0 + rows1, 1)
     t = time.perf_counter()
-    orc.subm_conv_f32_rows(w.feats, nbr, w.weight, w.bias, r0, r0 + probe, threads)
-    per_row = (time.perf_counter() - t) / probe
-    rows = int(min(n - r0, max(probe, budget_s / max(per_row, 1e-9))))
-    t = time.perf_counter()
-    orc.subm_conv_f32_rows(w.feats, nbr, w.weight, w.bias, r0, r0 + rows, threads)
-    dt = time.perf_counter() - t
-    rows1 = max(1, min(rows // max(threads, 1), 20000))
-    t = time.perf_counter()
-    orc.subm_conv_f32_rows(w.feats, nbr, w.weight, w.bias, r0, r0 + rows1, 1)
-    dt1 = time.perf_counter() - t
+    orc.neighbor_table(w.coords)
+    rb_s = time.perf_counter() - t
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -74,9 +82,12 @@ def cpu_baseline(w, nbr, budget_s: float):
         pass
     return {
         "value": rows / dt, "unit": "voxels/s", "cores": threads, "kind": "port",
-        "sample": f"output rows [{r0}, {r0 + rows}) of {n} ({rows} rows, {dt:.1f} s), fp32, "
-                  f"27 dense taps, tap-sequential accumulation",
-        "value_1core": rows1 / dt1, "sample_1core": f"{rows1} rows, {dt1:.1f} s",
+        "sample": f"output rows [{r0}, {r0 + rows}) of {n}: median of {reps} runs "
+                  f"({', '.join(f'{x:.2f}' for x in runs)} s) after a warm-up; fp32, all 27 "
+                  f"taps against the zero row, tap-sequential accumulation "
+                  f"(CPU restatement of sparse.cpp; ggml unavailable)",
+        "value_1core": rows1 / dt1, "sample_1core": f"{rows1} rows in {dt1:.2f} s on 1 thread",
+        "rulebook_s_1thread": rb_s,
         "cpu_model": cpu_model,
     }
 
@@ -188,7 +199,15 @@ def main():
         gbs = compulsory / (ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": gbs / PEAK_HBM_GBS}
+    # HBM bytes per launch of the conv kernel, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # passes scaled by a copy kernel of known size (profiles/traffic_<workload>.md)
     roof["traffic"] = None
+    tj = os.path.join(ROOT, "profiles", "traffic.json")
+    if planned and os.path.exists(tj):
+        rec = json.load(open(tj)).get(w.name)
+        if rec:
+            roof["traffic"] = rec["bytes_per_launch"]
+            roof["traffic_source"] = rec["source"]
     roof["algorithmic_flops_per_launch"] = flops
     roof["compulsory_bytes_per_launch"] = compulsory
 
