@@ -135,6 +135,37 @@ int tsp_subdivide(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
                   int32_t* d_mstart, int32_t* d_child_coords, int32_t* d_gidx, int64_t* d_m,
                   void* d_workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Per-voxel pieces of the ConvNeXt and C2S blocks (sparse_convnext, sparse.cpp:94-137;
+ * sparse_c2s, sparse.cpp:172-336). Rows are voxels, row-major [N][C].
+ * ------------------------------------------------------------------------------------- */
+
+/* out[i] = x[i] . W^T + bias for W [co][ci] (ggml_mul_mat of ne [ci, co] plus ggml_add,
+ * sparse.cpp:126-128, 188). Any dtype mix; fp32 accumulation; d_bias may be NULL. */
+int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
+               int weight_dtype, const float* d_bias, int co, void* d_out, int out_dtype,
+               void* stream);
+
+/* Row LayerNorm over c channels with biased variance and eps (ggml_norm, sparse.cpp:124,
+ * 259, 293), then * gamma + beta when those are not NULL, then x * sigmoid(x) when silu != 0.
+ * d_out may equal d_x. */
+int tsp_layer_norm(const void* d_x, int x_dtype, int64_t n, int c, const float* d_gamma,
+                   const float* d_beta, float eps, int silu, void* d_out, int out_dtype,
+                   void* stream);
+
+/* Channel-to-spatial gather (sparse.cpp:263-291): out[m][k] = h[gidx[m]/8][(gidx[m]%8)*cout + k]
+ * for h [N][8*cout]; gidx from tsp_subdivide. */
+int tsp_c2s_gather(const void* d_h, int dtype, const int32_t* d_gidx, int64_t m, int cout,
+                   void* d_out, void* stream);
+
+/* C2S skip connection (sparse.cpp:302-323): with K = cin/8 and R = cout/K,
+ * acc[m][k*R + r] += x[gidx[m]/8][(gidx[m]%8)*K + k] for every r < R. */
+int tsp_c2s_skip_add(const void* d_x, int x_dtype, const int32_t* d_gidx, int64_t m, int cin,
+                     int cout, void* d_acc, int acc_dtype, void* stream);
+
+/* mask[e] = logits[e] > 0 (the predicted subdivision, sparse.cpp:215). */
+int tsp_mask_positive(const float* d_logits, int64_t n, uint8_t* d_mask, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

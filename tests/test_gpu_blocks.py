@@ -1,0 +1,153 @@
+"""GPU parity of the per-voxel block pieces (linear, LayerNorm, C2S gather / skip, mask) and of
+whole ConvNeXt / C2S blocks composed from the C ABI, against the oracle (fp64).
+
+Tolerance: max|d| / max|ref| <= 1e-5 for fp32 paths; gather, skip and mask are copies, sums
+and comparisons and must be exact."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL_32 = 1e-5
+
+
+def _case(name):
+    print(f"[blocks] {name}", flush=True)
+
+
+def _t(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.to(dtype) if dtype is not None else t
+
+
+@pytest.mark.parametrize("n,ci,co", [(1, 8, 3), (300, 64, 256), (1000, 256, 64), (777, 33, 17)])
+def test_linear(gpu_lib, orc, n, ci, co):
+    _case(f"linear n={n} ci={ci} co={co}")
+    import torch
+    rng = np.random.default_rng(n + ci + co)
+    x = rng.standard_normal((n, ci)).astype(np.float32)
+    w = rng.standard_normal((co, ci)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32)
+    ref = orc.linear(x, w, b)
+    out = gpu_lib.linear(_t(x), _t(w), _t(b)).cpu().numpy()
+    assert orc.rel_err(out, ref) < TOL_32
+    out_nb = gpu_lib.linear(_t(x), _t(w)).cpu().numpy()      # no bias
+    assert orc.rel_err(out_nb, x.astype(np.float64) @ w.T.astype(np.float64)) < TOL_32
+    # f32 activations x f16 weights (the reference's default weight dtype)
+    w16 = w.astype(np.float16)
+    out16 = gpu_lib.linear(_t(x), _t(w16), _t(b)).cpu().numpy()
+    assert orc.rel_err(out16, orc.linear(x, w16.astype(np.float32), b)) < TOL_32
+
+
+@pytest.mark.parametrize("c", [7, 64, 1024, 4096])
+def test_layer_norm(gpu_lib, orc, c):
+    _case(f"layer_norm c={c}")
+    rng = np.random.default_rng(c)
+    x = (rng.standard_normal((333, c)) * 3 + 1).astype(np.float32)
+    g = rng.standard_normal(c).astype(np.float32)
+    b = rng.standard_normal(c).astype(np.float32)
+    for affine in (False, True):
+        for silu in (False, True):
+            ref = orc.layer_norm(x, g if affine else None, b if affine else None, 1e-6)
+            if silu:
+                ref = orc.silu(ref)
+            out = gpu_lib.layer_norm(_t(x), _t(g) if affine else None, _t(b) if affine else None,
+                                     1e-6, silu).cpu().numpy()
+            assert orc.rel_err(out, ref) < TOL_32, (affine, silu)
+
+
+def test_c2s_gather_and_skip(gpu_lib, golden):
+    _case("c2s gather / skip")
+    import torch
+    g = golden("subdivide_rand600.npz")
+    n = len(g["coords"])
+    gidx = g["gidx"]
+    m = len(gidx)
+    rng = np.random.default_rng(2)
+    cout, cin = 24, 32
+    h = rng.standard_normal((n, 8 * cout)).astype(np.float32)
+    out = gpu_lib.c2s_gather(_t(h), _t(gidx), cout).cpu().numpy()
+    assert np.array_equal(out, h.reshape(n * 8, cout)[gidx])
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    acc0 = rng.standard_normal((m, cout)).astype(np.float32)
+    acc = _t(acc0.copy())
+    gpu_lib.c2s_skip_add(_t(x), _t(gidx), acc)
+    k = cin // 8
+    skip = np.repeat(x.reshape(n * 8, k)[gidx], cout // k, axis=1)
+    assert np.array_equal(acc.cpu().numpy(), acc0 + skip)
+
+
+def test_mask_positive(gpu_lib):
+    _case("mask")
+    x = np.array([[-1.0, 0.0, 2.0, -0.0, 1e-30, -1e-30, np.inf, -np.inf]], np.float32)
+    assert gpu_lib.mask_positive(_t(x)).cpu().numpy().tolist() == [[0, 0, 1, 0, 1, 0, 1, 0]]
+
+
+def _params(rng, c, cout=None, scale=0.05):
+    s = lambda *shape: (rng.standard_normal(shape) * scale).astype(np.float32)
+    p = {"blk.conv.weight": s(c, 27, c), "blk.conv.bias": s(c),
+         "blk.norm.weight": 1 + s(c), "blk.norm.bias": s(c),
+         "blk.mlp.0.weight": s(4 * c, c), "blk.mlp.0.bias": s(4 * c),
+         "blk.mlp.2.weight": s(c, 4 * c), "blk.mlp.2.bias": s(c)}
+    if cout:
+        p.update({"c2s.to_subdiv.weight": s(8, c) * 20, "c2s.to_subdiv.bias": s(8),
+                  "c2s.norm1.weight": 1 + s(c), "c2s.norm1.bias": s(c),
+                  "c2s.conv1.weight": s(8 * cout, 27, c), "c2s.conv1.bias": s(8 * cout),
+                  "c2s.conv2.weight": s(cout, 27, cout), "c2s.conv2.bias": s(cout)})
+    return p
+
+
+def test_convnext_block_composed(gpu_lib, orc, shells):
+    """conv -> LN(1e-6)+affine -> mlp.0 -> SiLU -> mlp.2 -> + x (sparse.cpp:102-137), fp32."""
+    _case("convnext block")
+    import torch
+    rng = np.random.default_rng(4)
+    coords = shells.sphere_shell(40, 20.0, 12.0, 14.0)
+    c = 32
+    x = rng.standard_normal((len(coords), c)).astype(np.float32)
+    p = _params(rng, c)
+    nbr = gpu_lib.rulebook_build(_t(coords))
+    P = {k: _t(v) for k, v in p.items()}
+    h = gpu_lib.subm_conv3x3(_t(x), nbr, P["blk.conv.weight"], P["blk.conv.bias"])
+    h = gpu_lib.layer_norm(h, P["blk.norm.weight"], P["blk.norm.bias"], 1e-6)
+    h = gpu_lib.linear(h, P["blk.mlp.0.weight"], P["blk.mlp.0.bias"])
+    h = h * torch.sigmoid(h)           # SiLU in torch (test composition only)
+    h = gpu_lib.linear(h, P["blk.mlp.2.weight"], P["blk.mlp.2.bias"]) + _t(x)
+    ref = orc.convnext_block(x, orc.neighbor_table(coords), p, "blk")
+    assert orc.rel_err(h.cpu().numpy(), ref) < 1e-4
+
+
+@pytest.mark.parametrize("ext", [False, True])
+def test_c2s_block_composed(gpu_lib, orc, shells, ext):
+    """to_subdiv -> mask -> subdivide; LN+SiLU -> conv1 -> octant gather -> LN+SiLU -> conv2 on
+    the children -> + repeat_interleave skip (sparse.cpp:172-336), fp32."""
+    _case(f"c2s block ext={ext}")
+    import torch
+    rng = np.random.default_rng(5)
+    coords = shells.random_distinct_voxels(500, 12, 5)
+    n, cin, cout = len(coords), 32, 16
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    p = _params(rng, cin, cout)
+    P = {k: _t(v) for k, v in p.items()}
+    ext_mask = (rng.random(8 * n) < 0.3).astype(np.uint8) if ext else None
+    xc, cc = _t(x), _t(coords)
+    if ext:
+        mask = _t(ext_mask)
+    else:
+        mask = gpu_lib.mask_positive(gpu_lib.linear(xc, P["c2s.to_subdiv.weight"],
+                                                    P["c2s.to_subdiv.bias"])).reshape(-1)
+    child, gidx, _ = gpu_lib.subdivide(mask, cc)
+    h = gpu_lib.layer_norm(xc, P["c2s.norm1.weight"], P["c2s.norm1.bias"], 1e-6, silu=True)
+    h = gpu_lib.subm_conv3x3(h, gpu_lib.rulebook_build(cc), P["c2s.conv1.weight"],
+                             P["c2s.conv1.bias"])
+    h = gpu_lib.layer_norm(gpu_lib.c2s_gather(h, gidx, cout), None, None, 1e-6, silu=True)
+    out = gpu_lib.subm_conv3x3(h, gpu_lib.rulebook_build(child), P["c2s.conv2.weight"],
+                               P["c2s.conv2.bias"])
+    gpu_lib.c2s_skip_add(xc, gidx, out)
+    ref, rchild, rmask = orc.c2s_block(x, coords, p, "c2s", cout, ext_mask)
+    assert np.array_equal(mask.cpu().numpy().reshape(-1), rmask)
+    assert np.array_equal(child.cpu().numpy(), rchild)
+    assert orc.rel_err(out.cpu().numpy(), ref) < 1e-4

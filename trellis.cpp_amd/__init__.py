@@ -28,6 +28,7 @@ EXPORTS = (
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
     "tsp_subm_conv3x3_planned",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
+    "tsp_linear", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add", "tsp_mask_positive",
 )
 
 
@@ -76,6 +77,18 @@ def lib() -> ctypes.CDLL:
     L.tsp_subm_conv3x3_planned.restype = c_int
     L.tsp_subm_conv3x3_planned.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
                                            c_int, c_vp, c_int, c_vp]
+    L.tsp_linear.restype = c_int
+    L.tsp_linear.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_int, c_vp, c_int, c_vp, c_int,
+                             c_vp]
+    L.tsp_layer_norm.restype = c_int
+    L.tsp_layer_norm.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, ctypes.c_float, c_int,
+                                 c_vp, c_int, c_vp]
+    L.tsp_c2s_gather.restype = c_int
+    L.tsp_c2s_gather.argtypes = [c_vp, c_int, c_vp, c_i64, c_int, c_vp, c_vp]
+    L.tsp_c2s_skip_add.restype = c_int
+    L.tsp_c2s_skip_add.argtypes = [c_vp, c_int, c_vp, c_i64, c_int, c_int, c_vp, c_int, c_vp]
+    L.tsp_mask_positive.restype = c_int
+    L.tsp_mask_positive.argtypes = [c_vp, c_i64, c_vp, c_vp]
     L.tsp_subdivide_workspace_bytes.restype = c_sz
     L.tsp_subdivide_workspace_bytes.argtypes = [c_i64]
     L.tsp_subdivide.restype = c_int
@@ -237,3 +250,69 @@ def subdivide(mask, coords, stream=None):
                                _ptr(m_dev), _ptr(ws), ws_bytes, _stream(stream)))
     m = int(m_dev.item())
     return child[:m], gidx[:m], mstart
+
+
+def linear(x, weight, bias=None, out_dtype=None, stream=None):
+    """x [N,Ci] . W^T + bias for W [Co,Ci] -> [N,Co] (fp32 accumulation)."""
+    torch = _torch()
+    _require_cuda(x, weight, bias)
+    n, ci = x.shape
+    co = weight.shape[0]
+    if weight.shape != (co, ci):
+        raise ValueError("weight must be [Co, Ci]")
+    out = torch.empty((n, co), dtype=out_dtype or x.dtype, device=x.device)
+    xc, wc = x.contiguous(), weight.contiguous()
+    _check("tsp_linear",
+           lib().tsp_linear(_ptr(xc), dtype_code(xc.dtype), n, ci, _ptr(wc), dtype_code(wc.dtype),
+                            _ptr(bias), co, _ptr(out), dtype_code(out.dtype), _stream(stream)))
+    return out
+
+
+def layer_norm(x, gamma=None, beta=None, eps: float = 1e-6, silu: bool = False, out_dtype=None,
+               stream=None):
+    """Row LayerNorm over channels (biased variance) [* gamma + beta] [then SiLU]."""
+    torch = _torch()
+    _require_cuda(x, gamma, beta)
+    xc = x.contiguous()
+    n, c = xc.shape
+    out = torch.empty((n, c), dtype=out_dtype or x.dtype, device=x.device)
+    _check("tsp_layer_norm",
+           lib().tsp_layer_norm(_ptr(xc), dtype_code(xc.dtype), n, c, _ptr(gamma), _ptr(beta),
+                                eps, 1 if silu else 0, _ptr(out), dtype_code(out.dtype),
+                                _stream(stream)))
+    return out
+
+
+def c2s_gather(h, gidx, cout: int, stream=None):
+    """h [N, 8*cout] -> [M, cout]: child m takes block gidx[m] % 8 of parent gidx[m] // 8."""
+    torch = _torch()
+    _require_cuda(h, gidx)
+    m = gidx.numel()
+    out = torch.empty((m, cout), dtype=h.dtype, device=h.device)
+    hc = h.contiguous()
+    _check("tsp_c2s_gather",
+           lib().tsp_c2s_gather(_ptr(hc), dtype_code(hc.dtype), _ptr(gidx), m, cout, _ptr(out),
+                                _stream(stream)))
+    return out
+
+
+def c2s_skip_add(x, gidx, acc, stream=None):
+    """acc [M, Cout] += repeat_interleave(x.reshape(8N, Cin/8)[gidx], Cout/(Cin/8)) in place."""
+    _require_cuda(x, gidx, acc)
+    xc = x.contiguous()
+    m, cout = acc.shape
+    _check("tsp_c2s_skip_add",
+           lib().tsp_c2s_skip_add(_ptr(xc), dtype_code(xc.dtype), _ptr(gidx), m, xc.shape[1],
+                                  cout, _ptr(acc), dtype_code(acc.dtype), _stream(stream)))
+    return acc
+
+
+def mask_positive(logits, stream=None):
+    """uint8 mask of logits > 0 (float32 input, any shape)."""
+    torch = _torch()
+    _require_cuda(logits)
+    lc = logits.contiguous()
+    mask = torch.empty(lc.shape, dtype=torch.uint8, device=lc.device)
+    _check("tsp_mask_positive",
+           lib().tsp_mask_positive(_ptr(lc), lc.numel(), _ptr(mask), _stream(stream)))
+    return mask

@@ -30,11 +30,14 @@ namespace {
 // ---------------------------------------------------------------------------------------------
 constexpr int NB_M = 64, NB_N = 64, NB_K = 32, NB_THREADS = 256;
 
+// taps = 27 with a neighbour table is the conv; taps = 1 with nbr == nullptr (row i reads row
+// i) is a dense linear layer, weight [co][ci]. bias may be null.
 template <int FDT, int WDT, int ODT>
 __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
     const typename Elem<FDT>::storage* __restrict__ feats, int64_t n, int ci,
-    const int32_t* __restrict__ nbr, const typename Elem<WDT>::storage* __restrict__ weight,
-    const float* __restrict__ bias, int co, typename Elem<ODT>::storage* __restrict__ out) {
+    const int32_t* __restrict__ nbr, int taps,
+    const typename Elem<WDT>::storage* __restrict__ weight, const float* __restrict__ bias,
+    int co, typename Elem<ODT>::storage* __restrict__ out) {
     __shared__ float sA[NB_K][NB_M + 4];
     __shared__ float sB[NB_K][NB_N + 4];
     __shared__ int32_t sRow[NB_M];
@@ -51,11 +54,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = 0.f;
 
-    for (int t = 0; t < kTaps; ++t) {
+    for (int t = 0; t < taps; ++t) {
         int valid = 0;
         if (tid < NB_M) {
             const int64_t i = row0 + tid;
-            const int32_t r = (i < n) ? nbr[(int64_t)t * n + i] : sentinel;
+            const int32_t r = (i < n) ? (nbr ? nbr[(int64_t)t * n + i] : (int32_t)i) : sentinel;
             sRow[tid] = r;
             valid = r != sentinel;
         }
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
                     const int k = kc + kk + j;
                     float v = 0.f;
                     if (oc < co && k < ci)
-                        v = Elem<WDT>::load(weight, ((int64_t)oc * kTaps + t) * ci + k);
+                        v = Elem<WDT>::load(weight, ((int64_t)oc * taps + t) * ci + k);
                     sB[kk + j][c] = v;
                 }
             }
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int oc = co0 + tx * 4 + q;
-            if (oc < co) Elem<ODT>::store(out, i * co + oc, acc[p][q] + bias[oc]);
+            if (oc < co) Elem<ODT>::store(out, i * co + oc, acc[p][q] + (bias ? bias[oc] : 0.f));
         }
     }
 }
@@ -301,8 +304,8 @@ int launch_narrow(const void* feats, int64_t n, int ci, const int32_t* nbr, cons
     dim3 grid((unsigned)ceil_div(n, NB_M), (unsigned)ceil_div(co, NB_N));
     hipLaunchKernelGGL((k_conv_narrow<FDT, WDT, ODT>), grid, dim3(NB_THREADS), 0, s,
                        reinterpret_cast<const typename Elem<FDT>::storage*>(feats), n, ci, nbr,
-                       reinterpret_cast<const typename Elem<WDT>::storage*>(weight), bias, co,
-                       reinterpret_cast<typename Elem<ODT>::storage*>(out));
+                       nbr ? kTaps : 1, reinterpret_cast<const typename Elem<WDT>::storage*>(weight),
+                       bias, co, reinterpret_cast<typename Elem<ODT>::storage*>(out));
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
@@ -481,4 +484,19 @@ extern "C" int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t 
                 TSP_ERR_INVALID, "tsp_subm_conv3x3_planned: buffers must be 16-byte aligned");
     return halo_conv_launch(dtype, out_dtype, d_feats, n, ci, d_nbr, d_plan, d_packed_weight,
                             d_bias, co, d_out, as_stream(stream));
+}
+
+extern "C" int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
+                          int weight_dtype, const float* d_bias, int co, void* d_out,
+                          int out_dtype, void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && ci > 0 && co > 0, TSP_ERR_INVALID, "tsp_linear: n=%lld ci=%d co=%d",
+                (long long)n, ci, co);
+    TSP_REQUIRE(dtype_valid(x_dtype) && dtype_valid(weight_dtype) && dtype_valid(out_dtype),
+                TSP_ERR_INVALID, "tsp_linear: bad dtype");
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_x && d_weight && d_out, TSP_ERR_INVALID, "tsp_linear: null pointer");
+    TSP_REQUIRE(d_out != d_x, TSP_ERR_INVALID, "tsp_linear: out aliases x");
+    return dispatch_narrow(x_dtype, weight_dtype, out_dtype, d_x, n, ci, nullptr, d_weight,
+                           d_bias, co, d_out, as_stream(stream));
 }
