@@ -1,0 +1,83 @@
+"""GPU parity of the C++ host side: the check programs (tests/host/*.cpp) load a GGUF of
+synthetic weights through Model::load and run trellis::build_neighbor_table, sparse_submconv and
+sparse_convnext in a ggml graph, and sparse_c2s, against the oracle's outputs.
+
+Bars: table, children and masks exact. Features max|d|/max|ref|: <= 1e-3 on the matrix-core
+path (F32 activations rounded to F16 as ggml's F16 mul_mat does, fp32 accumulation); <= 2e-5
+for that conv against the oracle fed the same F16-rounded features; <= 1e-5 on the fp32 path
+(--f32, the reference's g_sparse_cast_f32)."""
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from host_cases import write_c2s_case, write_conv_case
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "trellis.cpp_amd", "host", "bin")
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    for b in ("sparse_conv_check", "c2s_check"):
+        if not os.path.exists(os.path.join(BIN, b)):
+            pytest.fail(f"{b} is not built")
+
+
+def _run(args):
+    print("[host]", " ".join(os.path.basename(a) for a in args), flush=True)
+    r = subprocess.run(args, capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0, r.stderr
+    return r.stdout
+
+
+def _val(out, key):
+    m = re.search(rf"{key}\s*(?:rel=)?([-+0-9.eE]+)", out)
+    assert m, (key, out)
+    return float(m.group(1))
+
+
+@pytest.mark.parametrize("c,f32", [(64, False), (64, True), (128, False), (48, False)])
+def test_conv_and_convnext(gpu, orc, shells, tmp_path, c, f32):
+    coords = shells.sphere_shell(40, 20.0, 12.0, 14.0)
+    write_conv_case(str(tmp_path), orc, coords, c, seed=c)
+    args = [os.path.join(BIN, "sparse_conv_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0"]
+    out = _run(args + (["--f32"] if f32 else []))
+    assert _val(out, "nbr_exact") == 1
+    conv, block = _val(out, "conv_out"), _val(out, "block_out")
+    mfma = not f32 and c % 64 == 0
+    tol = 1e-3 if mfma else 1e-5
+    assert conv < tol and block < tol, (conv, block)
+
+
+def test_conv_matches_rounded_features(gpu, orc, shells, tmp_path):
+    """On the matrix-core path the only difference from the closed form is the features'
+    rounding to F16: against the oracle fed F16-rounded features it agrees to fp32 accumulation."""
+    coords = shells.sphere_shell(40, 20.0, 12.0, 14.0)
+    write_conv_case(str(tmp_path), orc, coords, 64, seed=7)
+    os.replace(tmp_path / "conv_out16.npy", tmp_path / "conv_out.npy")
+    out = _run([os.path.join(BIN, "sparse_conv_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0"])
+    assert _val(out, "conv_out") < 2e-5
+
+
+@pytest.mark.parametrize("cin,cout,ext,f32", [(64, 32, False, False), (64, 32, True, False),
+                                              (128, 64, False, False), (128, 64, True, True)])
+def test_c2s(gpu, orc, shells, tmp_path, cin, cout, ext, f32):
+    coords = shells.random_distinct_voxels(700, 14, cin + cout)
+    write_c2s_case(str(tmp_path), orc, coords, cin, cout, seed=cin + cout, ext=ext)
+    args = [os.path.join(BIN, "c2s_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0"]
+    out = _run(args + (["--ext"] if ext else []) + (["--f32"] if f32 else []))
+    assert _val(out, "coords_exact") == 1
+    assert _val(out, "mask_exact") == 1
+    tol = 1e-5 if f32 else 1e-3
+    assert _val(out, "feats") < tol

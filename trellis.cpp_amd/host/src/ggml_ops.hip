@@ -1,0 +1,221 @@
+// Elementwise kernels of the graph runtime: broadcast add / mul, SiLU, dtype conversion and
+// row gather. All are grid-stride loops over contiguous tensors; they are memory-bound and
+// sized for HBM streaming (256 threads, at most 64K workgroups).
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+
+#include "runtime.hpp"
+
+namespace tgr {
+namespace {
+
+constexpr int kThreads = 256;
+
+inline unsigned grid_for(int64_t total) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((total + kThreads - 1) / kThreads, 65536));
+}
+
+template <int DT> struct Io;
+template <> struct Io<TSP_F32> {
+    static __device__ float ld(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
+    static __device__ void st(void* p, int64_t i, float v) { static_cast<float*>(p)[i] = v; }
+};
+template <> struct Io<TSP_F16> {
+    static __device__ float ld(const void* p, int64_t i) {
+        return __half2float(static_cast<const __half*>(p)[i]);
+    }
+    static __device__ void st(void* p, int64_t i, float v) {
+        static_cast<__half*>(p)[i] = __float2half_rn(v);
+    }
+};
+template <> struct Io<TSP_BF16> {
+    static __device__ float ld(const void* p, int64_t i) {
+        const uint32_t b = (uint32_t)static_cast<const uint16_t*>(p)[i] << 16;
+        return __uint_as_float(b);
+    }
+    static __device__ void st(void* p, int64_t i, float v) {
+        // round to nearest even; NaN stays a quiet NaN
+        const uint32_t u = __float_as_uint(v);
+        uint16_t r;
+        if ((u & 0x7fffffffu) > 0x7f800000u) r = (uint16_t)((u >> 16) | 0x40u);
+        else r = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        static_cast<uint16_t*>(p)[i] = r;
+    }
+};
+
+struct Shape4 {
+    int64_t ne[4];
+};
+
+// out[i] = a[i] (op) b[broadcast(i)]
+template <int ADT, int BDT, bool MUL>
+__global__ void k_binary(const void* __restrict__ a, const void* __restrict__ b,
+                         float* __restrict__ out, Shape4 sa, Shape4 sb, int64_t total) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = i, bi = 0, stride = 1;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int64_t c = r % sa.ne[d];
+            r /= sa.ne[d];
+            bi += (c % sb.ne[d]) * stride;
+            stride *= sb.ne[d];
+        }
+        const float x = Io<ADT>::ld(a, i), y = Io<BDT>::ld(b, bi);
+        out[i] = MUL ? x * y : x + y;
+    }
+}
+
+// b broadcast along rows only (b has a->ne[0] elements): the common bias / scale case
+template <int ADT, int BDT, bool MUL>
+__global__ void k_binary_row(const void* __restrict__ a, const void* __restrict__ b,
+                             float* __restrict__ out, int64_t ne0, int64_t total) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = Io<ADT>::ld(a, i), y = Io<BDT>::ld(b, i % ne0);
+        out[i] = MUL ? x * y : x + y;
+    }
+}
+
+__global__ void k_silu(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = x[i];
+        y[i] = v / (1.0f + expf(-v));
+    }
+}
+
+template <int XDT>
+__global__ void k_add_inplace(float* __restrict__ y, const void* __restrict__ x, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] += Io<XDT>::ld(x, i);
+}
+
+template <int XDT, int YDT>
+__global__ void k_convert(const void* __restrict__ x, void* __restrict__ y, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        Io<YDT>::st(y, i, Io<XDT>::ld(x, i));
+}
+
+template <int DT>
+__global__ void k_get_rows(const void* __restrict__ a, int64_t rows, const int32_t* __restrict__ idx,
+                           int64_t n_idx, int64_t k, float* __restrict__ out) {
+    const int64_t total = n_idx * k;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / k, c = e % k;
+        const int64_t src = idx[r];
+        out[e] = (src >= 0 && src < rows) ? Io<DT>::ld(a, src * k + c) : 0.0f;
+    }
+}
+
+__global__ void k_get_rows_i32(const int32_t* __restrict__ a, int64_t rows,
+                               const int32_t* __restrict__ idx, int64_t n_idx, int64_t k,
+                               int32_t* __restrict__ out) {
+    const int64_t total = n_idx * k;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / k, c = e % k;
+        const int64_t src = idx[r];
+        out[e] = (src >= 0 && src < rows) ? a[src * k + c] : 0;
+    }
+}
+
+template <bool MUL>
+hipError_t binary_typed(const ggml_tensor* a, const ggml_tensor* b, float* out, hipStream_t s) {
+    const int64_t total = ggml_nelements(a);
+    const bool row = ggml_nelements(b) == b->ne[0] && b->ne[0] == a->ne[0];
+    const int ad = tsp_dtype_of(a->type), bd = tsp_dtype_of(b->type);
+    Shape4 sa{{a->ne[0], a->ne[1], a->ne[2], a->ne[3]}}, sb{{b->ne[0], b->ne[1], b->ne[2], b->ne[3]}};
+    const dim3 g(grid_for(total)), blk(kThreads);
+#define TGR_BIN(AD, BD)                                                                        \
+    if (ad == AD && bd == BD) {                                                                \
+        if (row)                                                                               \
+            hipLaunchKernelGGL((k_binary_row<AD, BD, MUL>), g, blk, 0, s, a->data, b->data, out, \
+                               a->ne[0], total);                                               \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_binary<AD, BD, MUL>), g, blk, 0, s, a->data, b->data, out, sa, \
+                               sb, total);                                                     \
+        return hipGetLastError();                                                              \
+    }
+    TGR_BIN(TSP_F32, TSP_F32)
+    TGR_BIN(TSP_F32, TSP_F16)
+    TGR_BIN(TSP_F16, TSP_F32)
+    TGR_BIN(TSP_F16, TSP_F16)
+#undef TGR_BIN
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_binary(int op_mul, const ggml_tensor* a, const ggml_tensor* b, float* out,
+                         hipStream_t s) {
+    if (ggml_nelements(a) == 0) return hipSuccess;
+    return op_mul ? binary_typed<true>(a, b, out, s) : binary_typed<false>(a, b, out, s);
+}
+
+hipError_t launch_silu(const float* x, float* y, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu, dim3(grid_for(n)), dim3(kThreads), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_inplace(float* y, const void* x, int xd, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const dim3 g(grid_for(n)), blk(kThreads);
+    switch (xd) {
+        case TSP_F32: hipLaunchKernelGGL((k_add_inplace<TSP_F32>), g, blk, 0, s, y, x, n); break;
+        case TSP_F16: hipLaunchKernelGGL((k_add_inplace<TSP_F16>), g, blk, 0, s, y, x, n); break;
+        case TSP_BF16: hipLaunchKernelGGL((k_add_inplace<TSP_BF16>), g, blk, 0, s, y, x, n); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_convert(const void* x, int xd, void* y, int yd, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const dim3 g(grid_for(n)), blk(kThreads);
+#define TGR_CVT(XD, YD)                                                                   \
+    if (xd == XD && yd == YD) {                                                           \
+        hipLaunchKernelGGL((k_convert<XD, YD>), g, blk, 0, s, x, y, n);                   \
+        return hipGetLastError();                                                         \
+    }
+    TGR_CVT(TSP_F32, TSP_F16)
+    TGR_CVT(TSP_F32, TSP_BF16)
+    TGR_CVT(TSP_F16, TSP_F32)
+    TGR_CVT(TSP_BF16, TSP_F32)
+#undef TGR_CVT
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_get_rows(const ggml_tensor* a, const int32_t* idx, int64_t n_idx, void* out,
+                           hipStream_t s) {
+    const int64_t k = a->ne[0], rows = a->ne[1];
+    if (n_idx * k == 0) return hipSuccess;
+    const dim3 g(grid_for(n_idx * k)), blk(kThreads);
+    switch (a->type) {
+        case GGML_TYPE_F32:
+            hipLaunchKernelGGL((k_get_rows<TSP_F32>), g, blk, 0, s, a->data, rows, idx, n_idx, k,
+                               static_cast<float*>(out));
+            break;
+        case GGML_TYPE_F16:
+            hipLaunchKernelGGL((k_get_rows<TSP_F16>), g, blk, 0, s, a->data, rows, idx, n_idx, k,
+                               static_cast<float*>(out));
+            break;
+        case GGML_TYPE_BF16:
+            hipLaunchKernelGGL((k_get_rows<TSP_BF16>), g, blk, 0, s, a->data, rows, idx, n_idx, k,
+                               static_cast<float*>(out));
+            break;
+        case GGML_TYPE_I32:
+            hipLaunchKernelGGL(k_get_rows_i32, g, blk, 0, s, static_cast<const int32_t*>(a->data),
+                               rows, idx, n_idx, k, static_cast<int32_t*>(out));
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace tgr

@@ -1,0 +1,72 @@
+// Internal interface of the HIP graph runtime behind the ggml-compatible headers: device memory
+// RAII, ggml <-> library dtype mapping, the elementwise kernels' launchers (ggml_ops.hip) and
+// the context hooks the sparse adapter uses to keep per-graph state alive.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+
+#include "ggml-backend.h"
+#include "ggml.h"
+#include "trellis_sparse.h"
+
+namespace tgr {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
+
+[[noreturn]] void fail(const std::string& msg);   // throws std::runtime_error
+void hip_check(hipError_t e, const char* what);    // throws on error
+
+// Owning device allocation on the current device.
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr; o.n_ = 0; }
+    void* get() const { return p_; }
+    template <class T> T* as() const { return static_cast<T*>(p_); }
+    size_t size() const { return n_; }
+
+private:
+    void* p_ = nullptr;
+    size_t n_ = 0;
+};
+
+// HIP device and stream of a backend made by ggml_backend_hip_init.
+int backend_device(ggml_backend_t backend);
+hipStream_t backend_stream(ggml_backend_t backend);
+
+// Library dtype of a floating ggml type; -1 for the others.
+int tsp_dtype_of(enum ggml_type t);
+bool is_contiguous(const ggml_tensor* t);
+
+// The context owns `obj` until ggml_free.
+void context_keep(ggml_context* ctx, std::shared_ptr<void> obj);
+// Per-context memo (e.g. the conv plan node of a neighbour table).
+ggml_tensor* context_memo_get(ggml_context* ctx, const ggml_tensor* key, int kind);
+void context_memo_put(ggml_context* ctx, const ggml_tensor* key, int kind, ggml_tensor* value);
+
+// Elementwise kernels (ggml_ops.hip); all return hipSuccess or the launch error.
+// out = a (op) b with b broadcast over a (ggml_can_repeat); a/b f32 or f16, out f32.
+hipError_t launch_binary(int op_mul, const ggml_tensor* a, const ggml_tensor* b, float* out,
+                         hipStream_t s);
+hipError_t launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
+// y[i] += x[i] (x f32 / f16 / bf16)
+hipError_t launch_add_inplace(float* y, const void* x, int x_dtype, int64_t n, hipStream_t s);
+// y[i] = (dtype) x[i]: f32 -> f16 / bf16 (round to nearest even), and f16 / bf16 -> f32.
+hipError_t launch_convert(const void* x, int x_dtype, void* y, int y_dtype, int64_t n,
+                          hipStream_t s);
+// out[r][k] = a[idx[r]][k] for a [rows][k] (f32/f16/i32 -> f32, i32 -> i32).
+hipError_t launch_get_rows(const ggml_tensor* a, const int32_t* idx, int64_t n_idx, void* out,
+                           hipStream_t s);
+
+}  // namespace tgr
