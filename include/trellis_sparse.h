@@ -141,7 +141,9 @@ int tsp_subdivide(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
  * ------------------------------------------------------------------------------------- */
 
 /* out[i] = x[i] . W^T + bias for W [co][ci] (ggml_mul_mat of ne [ci, co] plus ggml_add,
- * sparse.cpp:126-128, 188). Any dtype mix; fp32 accumulation; d_bias may be NULL. */
+ * sparse.cpp:126-128, 188). Any dtype mix; fp32 accumulation; d_bias may be NULL. f16/bf16 x and
+ * weights of one dtype with ci % 32 == 0, co % 64 == 0 and 16-byte aligned buffers run on the
+ * matrix cores, the rest on the VALU kernel. */
 int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
                int weight_dtype, const float* d_bias, int co, void* d_out, int out_dtype,
                void* stream);

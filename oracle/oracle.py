@@ -288,3 +288,24 @@ def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None):
     xs = x.reshape(n * 8, k)[gidx].astype(np.float64)             # skip gather, :307
     skip = np.repeat(xs, r, axis=1)                               # repeat_interleave, :322
     return h + skip, child, mask
+
+
+def decode_unet(latent, coords, p: dict, stages, out_ch: int, guide=None):
+    """SparseUnetVaeDecoder (shape_decoder.cpp:79-117): from_latent -> per stage, its ConvNeXt
+    blocks on the stage's table then its C2S block (masks from `guide` when given, else
+    predicted) -> LayerNorm(eps 1e-5, no affine, :116) -> output_layer. `stages` lists
+    (block prefixes, (c2s prefix, cin, cout)). Returns (out float64 [M, out_ch], coords [M,3],
+    masks used per stage)."""
+    c = _coords(coords)
+    h = linear(np.asarray(latent, np.float32), p["from_latent.weight"], p["from_latent.bias"])
+    masks = []
+    for si, (blocks, (c2s, _cin, cout)) in enumerate(stages):
+        nbr = neighbor_table(c)
+        for b in blocks:
+            h = convnext_block(h.astype(np.float32), nbr, p, b)
+        h, c, m = c2s_block(h.astype(np.float32), c, p, c2s, cout,
+                            None if guide is None else guide[si])
+        masks.append(m)
+    h = layer_norm(h, None, None, 1e-5)
+    out = linear(h, p["output_layer.weight"], p["output_layer.bias"])
+    return out, c, masks

@@ -39,6 +39,27 @@ def c2s_params(rng, cin, cout, prefix="blocks.3.4"):
             f"{prefix}.conv2.bias": s(0.1, cout)}
 
 
+def decoder_params(rng, channels=(128, 64, 32, 16), blocks=(1, 1, 1), latent=32, out_ch=7):
+    """A small SparseUnetVaeDecoder under the reference's key names (shape_decoder.cpp:79-117):
+    from_latent, per stage `blocks` ConvNeXt blocks then a C2S block, output_layer. Returns the
+    parameters and the stage list the oracle decoder takes."""
+    s = lambda scale, *shape: (rng.standard_normal(shape) * scale).astype(np.float32)
+    p = {"from_latent.weight": s(1 / np.sqrt(latent), channels[0], latent),
+         "from_latent.bias": s(0.1, channels[0])}
+    stages = []
+    for si, (cin, cout) in enumerate(zip(channels[:-1], channels[1:])):
+        names = []
+        for j in range(blocks[si]):
+            p.update(convnext_params(rng, cin, f"blocks.{si}.{j}"))
+            names.append(f"blocks.{si}.{j}")
+        c2s = f"blocks.{si}.{blocks[si]}"
+        p.update(c2s_params(rng, cin, cout, c2s))
+        stages.append((names, (c2s, cin, cout)))
+    p["output_layer.weight"] = s(1 / np.sqrt(channels[-1]), out_ch, channels[-1])
+    p["output_layer.bias"] = s(0.1, out_ch)
+    return p, stages
+
+
 def stored(params):
     """The parameters as the host program will see them: 2-D+ weights through F16."""
     return {k: (_f16(v) if v.ndim >= 2 else v) for k, v in params.items()}

@@ -40,6 +40,14 @@ def test_linear(gpu_lib, orc, n, ci, co):
     w16 = w.astype(np.float16)
     out16 = gpu_lib.linear(_t(x), _t(w16), _t(b)).cpu().numpy()
     assert orc.rel_err(out16, orc.linear(x, w16.astype(np.float32), b)) < TOL_32
+    # 16-bit x and weights of one dtype: the matrix-core path when ci % 32 == 0 and co % 64 == 0
+    for tdt in (torch.float16, torch.bfloat16):
+        xr, wr = _t(x).to(tdt), _t(w).to(tdt)
+        ref = orc.linear(xr.float().cpu().numpy(), wr.float().cpu().numpy(), b)
+        out = gpu_lib.linear(xr, wr, _t(b), out_dtype=torch.float32).cpu().numpy()
+        assert orc.rel_err(out, ref) < TOL_32, tdt
+        out_nb = gpu_lib.linear(xr, wr, out_dtype=torch.float32).cpu().numpy()
+        assert orc.rel_err(out_nb, ref - b.astype(np.float64)) < TOL_32, tdt
 
 
 @pytest.mark.parametrize("c", [7, 64, 1024, 4096])

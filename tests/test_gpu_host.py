@@ -1,6 +1,7 @@
 """GPU parity of the C++ host side: the check programs (tests/host/*.cpp) load a GGUF of
 synthetic weights through Model::load and run trellis::build_neighbor_table, sparse_submconv and
-sparse_convnext in a ggml graph, and sparse_c2s, against the oracle's outputs.
+sparse_convnext in a ggml graph, sparse_c2s, and the device-resident decoders (shape_decode,
+shape_upsample, tex_decode), against the oracle's outputs.
 
 Bars: table, children and masks exact. Features max|d|/max|ref|: <= 1e-3 on the matrix-core
 path (F32 activations rounded to F16 as ggml's F16 mul_mat does, fp32 accumulation); <= 2e-5
@@ -81,3 +82,53 @@ def test_c2s(gpu, orc, shells, tmp_path, cin, cout, ext, f32):
     assert _val(out, "mask_exact") == 1
     tol = 1e-5 if f32 else 1e-3
     assert _val(out, "feats") < tol
+
+
+# ---- the device-resident decoders (shape_decode, shape_upsample, tex_decode) ----------------------
+def _decoder_case(tmp_path, orc, shells, out_ch, seed):
+    from gguf_writer import write as write_gguf
+    from host_cases import decoder_params, stored
+    rng = np.random.default_rng(seed)
+    coords = shells.random_distinct_voxels(200, 10, seed)
+    latent = rng.standard_normal((len(coords), 32)).astype(np.float32)
+    p, stages = decoder_params(rng, out_ch=out_ch)
+    write_gguf(str(tmp_path / f"model{out_ch}.gguf"), p)
+    np.save(tmp_path / "latent.npy", latent)
+    np.save(tmp_path / "coords.npy", np.ascontiguousarray(coords, np.int32))
+    return coords, latent, stored(p), stages
+
+
+def test_shape_decode_fp32(gpu, orc, shells, tmp_path):
+    """Predicted masks, fp32 paths: masks, children and output against the oracle decoder."""
+    coords, latent, q, stages = _decoder_case(tmp_path, orc, shells, 7, seed=11)
+    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model7.gguf"), str(tmp_path), "0", "--f32"])
+    ref, rcoords, rmasks = orc.decode_unet(latent, coords, q, stages, 7)
+    assert np.array_equal(np.load(tmp_path / "coords_out.npy"), rcoords)
+    for s, m in enumerate(rmasks):
+        assert np.array_equal(np.load(tmp_path / f"subs_out_{s}.npy"), m), s
+    err = orc.rel_err(np.load(tmp_path / "out.npy"), ref)
+    print(f"shape_decode fp32 rel={err:.3e} M={len(rcoords)}", flush=True)
+    assert err < 1e-5
+    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model7.gguf"), str(tmp_path), "0", "--f32",
+          "--upsample"])
+    assert np.array_equal(np.load(tmp_path / "coords_out.npy"), rcoords)
+
+
+def test_tex_decode_guided(gpu, orc, shells, tmp_path):
+    """Masks given (the texture decoder's route), matrix-core paths with 16-bit activations."""
+    coords, latent, q, stages = _decoder_case(tmp_path, orc, shells, 6, seed=12)
+    rng = np.random.default_rng(5)
+    guide, n = [], len(coords)
+    for _ in stages:
+        guide.append((rng.random(8 * n) < 0.4).astype(np.uint8))
+        n = int(guide[-1].sum())
+    for s, g in enumerate(guide):
+        np.save(tmp_path / f"subs_{s}.npy", g)
+    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model6.gguf"), str(tmp_path), "0", "--tex"])
+    ref, rcoords, _ = orc.decode_unet(latent, coords, q, stages, 6, guide)
+    out = np.load(tmp_path / "out.npy")
+    assert out.shape == ref.shape
+    err = orc.rel_err(out, ref)
+    print(f"tex_decode 16-bit rel={err:.3e} M={len(rcoords)}", flush=True)
+    # every conv and linear of 3 stages rounds its input to F16 (measured 1.1e-3)
+    assert err < 3e-3

@@ -128,7 +128,7 @@ template <bool BF16, int BN, int WAVES, int ODT>
 __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, int taps) {
     constexpr int NT = WAVES * 64;
     constexpr int BM = 64 * WAVES;
     constexpr int CB = BN / 32;                       // 32-wide column blocks per wave
@@ -162,8 +162,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
     {
         uint32_t wm = 0;
         const int64_t i = wrow0 + lane;
-        for (int t = 0; t < kTaps; ++t) {
-            const bool v = (i < n) && nbr[(int64_t)t * n + i] != sentinel;
+        for (int t = 0; t < taps; ++t) {
+            const bool v = (i < n) && (!nbr || nbr[(int64_t)t * n + i] != sentinel);
             if (__ballot(v)) wm |= 1u << t;
         }
         if (lane == 0 && wm) atomicOr(&sMask, wm);
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 const int64_t i = wrow0 + rb * 32 + lr;
-                r[rb] = (i < n) ? nbr[(int64_t)t * n + i] : sentinel;
+                r[rb] = (i < n) ? (nbr ? nbr[(int64_t)t * n + i] : (int32_t)i) : sentinel;
             }
         };
         auto load_a = [&](const int32_t* r, int kc, u32x4_t (*a)[2]) {
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
                 if (piece < PIECES) {
                     const int c = piece / (MK / 8), kq = piece % (MK / 8);
                     regs[p] = *reinterpret_cast<const u32x4_t*>(
-                        weight + ((int64_t)(co0 + c) * kTaps + t) * ci + kc + kq * 8);
+                        weight + ((int64_t)(co0 + c) * taps + t) * ci + kc + kq * 8);
                 }
             }
         };
@@ -283,7 +283,7 @@ epilogue:
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
         const int oc = co0 + cb * 32 + lr;
-        const float bv = bias[oc];
+        const float bv = bias ? bias[oc] : 0.f;
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -335,8 +335,8 @@ int dispatch_narrow(int fdt, int wdt, int odt, const void* feats, int64_t n, int
 }
 
 template <bool BF16, int BN, int WAVES, int ODT>
-int launch_gather(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
-                  const float* bias, int co, void* out, hipStream_t s) {
+int launch_gather(const void* feats, int64_t n, int ci, const int32_t* nbr, int taps,
+                  const void* weight, const float* bias, int co, void* out, hipStream_t s) {
     constexpr int BM = 64 * WAVES;
     const int64_t n_tiles = ceil_div(n, BM);
     const int n_ctiles = co / BN;
@@ -345,29 +345,32 @@ int launch_gather(const void* feats, int64_t n, int ci, const int32_t* nbr, cons
     hipLaunchKernelGGL((k_conv_mfma<BF16, BN, WAVES, ODT>), dim3((unsigned)(per_xcd * 8)),
                        dim3(WAVES * 64), 0, s, reinterpret_cast<const uint16_t*>(feats), n, ci,
                        nbr, reinterpret_cast<const uint16_t*>(weight), bias, co, out, n_tiles,
-                       n_ctiles, per_xcd);
+                       n_ctiles, per_xcd, taps);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
 
 template <bool BF16, int BN>
-int gather_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+int gather_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr, int taps,
                const void* weight, const float* bias, int co, void* out, hipStream_t s) {
-    if (odt == TSP_F32) return launch_gather<BF16, BN, 4, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s);
-    if (BF16 && odt == TSP_BF16) return launch_gather<BF16, BN, 4, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s);
-    if (!BF16 && odt == TSP_F16) return launch_gather<BF16, BN, 4, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s);
+    if (odt == TSP_F32) return launch_gather<BF16, BN, 4, TSP_F32>(feats, n, ci, nbr, taps, weight, bias, co, out, s);
+    if (BF16 && odt == TSP_BF16) return launch_gather<BF16, BN, 4, TSP_BF16>(feats, n, ci, nbr, taps, weight, bias, co, out, s);
+    if (!BF16 && odt == TSP_F16) return launch_gather<BF16, BN, 4, TSP_F16>(feats, n, ci, nbr, taps, weight, bias, co, out, s);
     set_error("tsp_subm_conv3x3: MFMA path writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
 
+// taps = 27 with a neighbour table is the conv; taps = 1 with nbr == nullptr (row i reads row i)
+// is a linear layer.
 int dispatch_gather(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
-                    const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+                    int taps, const void* weight, const float* bias, int co, void* out,
+                    hipStream_t s) {
     const bool bn128 = co % 128 == 0;
     if (fdt == TSP_BF16)
-        return bn128 ? gather_out<true, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
-                     : gather_out<true, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
-    return bn128 ? gather_out<false, 128>(odt, feats, n, ci, nbr, weight, bias, co, out, s)
-                 : gather_out<false, 64>(odt, feats, n, ci, nbr, weight, bias, co, out, s);
+        return bn128 ? gather_out<true, 128>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s)
+                     : gather_out<true, 64>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s);
+    return bn128 ? gather_out<false, 128>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s)
+                 : gather_out<false, 64>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s);
 }
 
 // MFMA kernels: 16-bit feats and weights of one dtype, out f32 or that dtype, ci % 32 == 0,
@@ -418,8 +421,8 @@ extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, 
                     ci, co);
     }
     if (algo == TSP_ALGO_MFMA_GATHER)
-        return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight, d_bias, co,
-                               d_out, s);
+        return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, kTaps, d_weight,
+                               d_bias, co, d_out, s);
     if (algo == TSP_ALGO_MFMA || (algo == TSP_ALGO_AUTO && eligible))
         return halo_conv_launch(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, nullptr, d_weight,
                                 d_bias, co, d_out, s);
@@ -497,6 +500,12 @@ extern "C" int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const
     if (n == 0) return TSP_OK;
     TSP_REQUIRE(d_x && d_weight && d_out, TSP_ERR_INVALID, "tsp_linear: null pointer");
     TSP_REQUIRE(d_out != d_x, TSP_ERR_INVALID, "tsp_linear: out aliases x");
+    TSP_REQUIRE(n < (int64_t)INT32_MAX, TSP_ERR_INVALID, "tsp_linear: n=%lld out of range",
+                (long long)n);
+    // 16-bit x and weights of one dtype on the matrix cores; everything else on the VALU kernel
+    if (mfma_eligible(x_dtype, weight_dtype, out_dtype, ci, co, d_x, d_weight, d_out))
+        return dispatch_gather(x_dtype, out_dtype, d_x, n, ci, nullptr, 1, d_weight, d_bias, co,
+                               d_out, as_stream(stream));
     return dispatch_narrow(x_dtype, weight_dtype, out_dtype, d_x, n, ci, nullptr, d_weight,
                            d_bias, co, d_out, as_stream(stream));
 }

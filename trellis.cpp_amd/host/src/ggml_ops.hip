@@ -87,6 +87,15 @@ __global__ void k_silu(const float* __restrict__ x, float* __restrict__ y, int64
     }
 }
 
+template <int YDT>
+__global__ void k_silu_to(const float* __restrict__ x, void* __restrict__ y, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = x[i];
+        Io<YDT>::st(y, i, v / (1.0f + expf(-v)));
+    }
+}
+
 template <int XDT>
 __global__ void k_add_inplace(float* __restrict__ y, const void* __restrict__ x, int64_t n) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
@@ -161,6 +170,18 @@ hipError_t launch_binary(int op_mul, const ggml_tensor* a, const ggml_tensor* b,
 hipError_t launch_silu(const float* x, float* y, int64_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(k_silu, dim3(grid_for(n)), dim3(kThreads), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_to(const float* x, void* y, int yd, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const dim3 g(grid_for(n)), blk(kThreads);
+    switch (yd) {
+        case TSP_F16: hipLaunchKernelGGL((k_silu_to<TSP_F16>), g, blk, 0, s, x, y, n); break;
+        case TSP_BF16: hipLaunchKernelGGL((k_silu_to<TSP_BF16>), g, blk, 0, s, x, y, n); break;
+        case TSP_F32: hipLaunchKernelGGL(k_silu, g, blk, 0, s, x, static_cast<float*>(y), n); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

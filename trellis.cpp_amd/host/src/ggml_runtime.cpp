@@ -33,8 +33,12 @@ void hip_check(hipError_t e, const char* what) {
 DeviceBuffer::DeviceBuffer(size_t bytes) : n_(bytes) {
     if (bytes) hip_check(hipMalloc(&p_, bytes), "hipMalloc");
 }
-DeviceBuffer::~DeviceBuffer() {
+DeviceBuffer::~DeviceBuffer() { reset(); }
+
+void DeviceBuffer::reset() {
     if (p_) (void)hipFree(p_);
+    p_ = nullptr;
+    n_ = 0;
 }
 
 int tsp_dtype_of(enum ggml_type t) {

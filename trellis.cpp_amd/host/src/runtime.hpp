@@ -32,6 +32,17 @@ public:
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
     DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr; o.n_ = 0; }
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+        if (this != &o) {
+            reset();
+            p_ = o.p_;
+            n_ = o.n_;
+            o.p_ = nullptr;
+            o.n_ = 0;
+        }
+        return *this;
+    }
+    void reset();
     void* get() const { return p_; }
     template <class T> T* as() const { return static_cast<T*>(p_); }
     size_t size() const { return n_; }
@@ -60,6 +71,8 @@ void context_memo_put(ggml_context* ctx, const ggml_tensor* key, int kind, ggml_
 hipError_t launch_binary(int op_mul, const ggml_tensor* a, const ggml_tensor* b, float* out,
                          hipStream_t s);
 hipError_t launch_silu(const float* x, float* y, int64_t n, hipStream_t s);
+// y[i] = (y_dtype) silu(x[i]) for a 16-bit y
+hipError_t launch_silu_to(const float* x, void* y, int y_dtype, int64_t n, hipStream_t s);
 // y[i] += x[i] (x f32 / f16 / bf16)
 hipError_t launch_add_inplace(float* y, const void* x, int x_dtype, int64_t n, hipStream_t s);
 // y[i] = (dtype) x[i]: f32 -> f16 / bf16 (round to nearest even), and f16 / bf16 -> f32.

@@ -1,0 +1,153 @@
+// The sparse U-Net VAE decoders (reference: src/shape_decoder.cpp:79-138) with every stage
+// resident on the device: features, coordinates, neighbour tables and conv plans never leave
+// HBM between stages; only the subdivision masks (which the texture decoder needs) and the
+// final result are read back.
+//
+// The network is read off the model instead of a fixed table: stage s holds ConvNeXt blocks
+// `blocks.s.j` (those with a `.conv.weight`) followed by one C2S block (the first `blocks.s.j`
+// with a `.conv1.weight`); the channel counts come from the weight shapes. For the TRELLIS.2
+// decoders this is 4 stages of {4, 16, 8, 4} blocks at 1024 -> 512 -> 256 -> 128 -> 64 channels
+// (shape_decoder.cpp:88-90).
+#include "shape_decoder.h"
+
+#include <cstdio>
+#include <string>
+
+#include "ggml.h"
+#include "runtime.hpp"
+#include "sparse_ops.hpp"
+#include "trellis_model.h"
+
+namespace trellis {
+namespace {
+
+using tgr::DeviceBuffer;
+using tgr::fail;
+using tgr::hip_check;
+
+struct Stage {
+    std::vector<std::string> convnext;   // block prefixes
+    std::string c2s;
+    int cin = 0, cout = 0;
+};
+
+std::vector<Stage> stages_of(const Model& m) {
+    std::vector<Stage> st;
+    for (int s = 0;; ++s) {
+        Stage g;
+        for (int j = 0;; ++j) {
+            const std::string p = "blocks." + std::to_string(s) + "." + std::to_string(j);
+            if (m.has(p + ".conv.weight")) {
+                g.convnext.push_back(p);
+            } else if (m.has(p + ".conv1.weight")) {
+                g.c2s = p;
+                const ggml_tensor* w1 = m.get(p + ".conv1.weight");
+                const ggml_tensor* w2 = m.get(p + ".conv2.weight");
+                g.cin = (int)w1->ne[0];
+                g.cout = (int)w2->ne[2];
+                break;
+            } else {
+                break;
+            }
+        }
+        if (g.c2s.empty()) {
+            if (!g.convnext.empty()) fail("decoder: stage " + std::to_string(s) + " has no C2S block");
+            break;
+        }
+        st.push_back(std::move(g));
+    }
+    if (st.empty()) fail("decoder: the model has no blocks.<stage>.<block> weights");
+    return st;
+}
+
+// One decoder pass; coords is updated to the final voxel set.
+std::vector<float> decode(const Model& m, const std::vector<float>& latent, int out_ch,
+                          std::vector<std::array<int, 3>>& coords,
+                          const std::vector<std::vector<uint8_t>>* guide,
+                          std::vector<std::vector<uint8_t>>* subs_out, bool coords_only) {
+    const std::vector<Stage> stages = stages_of(m);
+    if (guide && guide->size() < stages.size()) fail("tex_decode: one subdivision mask per stage is needed");
+    int64_t n = (int64_t)coords.size();
+    const ggml_tensor* wl = m.get("from_latent.weight");
+    const int in_ch = (int)wl->ne[0], c0 = (int)wl->ne[1];
+    if ((int64_t)latent.size() != n * in_ch) fail("decoder: latent must hold " + std::to_string(in_ch) + "*N floats");
+    hip_check(hipSetDevice(tgr::backend_device(m.backend)), "hipSetDevice");
+    hipStream_t s = tgr::backend_stream(m.backend);
+
+    DeviceBuffer dc((size_t)n * 12), dl((size_t)n * in_ch * 4);
+    hip_check(hipMemcpy(dc.get(), coords.data(), (size_t)n * 12, hipMemcpyHostToDevice), "decoder upload");
+    hip_check(hipMemcpy(dl.get(), latent.data(), latent.size() * 4, hipMemcpyHostToDevice), "decoder upload");
+    DeviceBuffer h((size_t)n * c0 * 4);
+    ops::run_linear(m, "from_latent", dl.as<float>(), n, in_ch, c0, false, 0.f, h.as<float>(), s);
+    dl.reset();
+    int c = c0;
+    ops::Table table;
+    ops::build_table(dc.as<int32_t>(), n, table, s);
+    DeviceBuffer scratch, h2;
+    for (size_t si = 0; si < stages.size(); ++si) {
+        const Stage& g = stages[si];
+        for (const std::string& p : g.convnext) {   // ConvNeXt stage, ping-pong buffers
+            ops::ConvNext a = ops::convnext_of(m, p, n);
+            if (a.c != c) fail(p + ": expected " + std::to_string(c) + " channels");
+            if (a.conv.mfma) table.ensure_plan(s);
+            const size_t need = ops::convnext_scratch(a, TSP_F32);
+            if (scratch.size() < need) {
+                hip_check(hipStreamSynchronize(s), "decoder");
+                scratch = DeviceBuffer(need);
+            }
+            if (h2.size() < (size_t)n * c * 4) h2 = DeviceBuffer((size_t)n * c * 4);
+            ops::Carve sc(scratch.get());
+            ops::run_convnext(a, h.get(), TSP_F32, table.nbr.as<int32_t>(), table.plan.get(), h2.as<float>(), sc, s);
+            std::swap(h, h2);
+        }
+        if (g.cin != c) fail(g.c2s + ": expected " + std::to_string(c) + " input channels");
+        const std::vector<uint8_t>* ext = guide ? &(*guide)[si] : nullptr;
+        ops::C2SOut o = ops::run_c2s(m, g.c2s, h.as<float>(), dc.as<int32_t>(), table, g.cin, g.cout, ext, s);
+        if (subs_out) subs_out->push_back(std::move(o.mask));
+        h = std::move(o.feats);
+        dc = std::move(o.coords);
+        table = std::move(o.table);
+        if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s);
+        n = o.m;
+        c = g.cout;
+    }
+    hip_check(hipStreamSynchronize(s), "decoder");
+    coords.resize((size_t)n);
+    if (n) hip_check(hipMemcpy(coords.data(), dc.get(), (size_t)n * 12, hipMemcpyDeviceToHost), "decoder readback");
+    if (coords_only) return {};
+    const ggml_tensor* wo = m.get("output_layer.weight");
+    if (wo->ne[0] != c || wo->ne[1] != out_ch)
+        fail("output_layer.weight: expected ggml shape [" + std::to_string(c) + ", " + std::to_string(out_ch) + "]");
+    DeviceBuffer out((size_t)n * out_ch * 4);
+    if (n) ops::run_linear(m, "output_layer", h.as<float>(), n, c, out_ch, true, 1e-5f, out.as<float>(), s);
+    std::vector<float> r((size_t)n * out_ch);
+    if (n) hip_check(hipMemcpy(r.data(), out.get(), r.size() * 4, hipMemcpyDeviceToHost), "decoder readback");
+    return r;
+}
+
+}  // namespace
+
+ShapeOut shape_decode(const Model& m, const std::vector<float>& latent,
+                      const std::vector<std::array<int, 3>>& coords0, int resolution) {
+    ShapeOut so;
+    so.coords = coords0;
+    so.res = resolution;
+    so.feats7 = decode(m, latent, 7, so.coords, nullptr, &so.subs, false);
+    return so;
+}
+
+std::vector<std::array<int, 3>> shape_upsample(const Model& m, const std::vector<float>& latent,
+                                               const std::vector<std::array<int, 3>>& coords0) {
+    std::vector<std::array<int, 3>> coords = coords0;
+    decode(m, latent, 7, coords, nullptr, nullptr, true);
+    return coords;
+}
+
+std::vector<float> tex_decode(const Model& m, const std::vector<float>& tex_latent,
+                              const std::vector<std::array<int, 3>>& coords0,
+                              const std::vector<std::vector<uint8_t>>& subs) {
+    std::vector<std::array<int, 3>> coords = coords0;
+    return decode(m, tex_latent, 6, coords, &subs, nullptr, false);
+}
+
+}  // namespace trellis

@@ -1,0 +1,291 @@
+// Device-level pieces of the sparse path on libtrellis_sparse (reference: src/sparse.cpp:61-336).
+#include "sparse_ops.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <stdexcept>
+
+#include "sparse.h"
+
+namespace trellis {
+namespace ops {
+
+using tgr::DeviceBuffer;
+using tgr::fail;
+using tgr::hip_check;
+
+void lib(int st, const std::string& what) {
+    if (st != TSP_OK) fail(what + ": " + tsp_last_error());
+}
+
+const ggml_tensor* vec_param(const Model& m, const std::string& name, int64_t n) {
+    const ggml_tensor* t = m.get(name);
+    if (ggml_nelements(t) != n || tgr::tsp_dtype_of(t->type) < 0)
+        fail(name + ": expected " + std::to_string(n) + " floating-point elements");
+    return t;
+}
+
+const ggml_tensor* mat_param(const Model& m, const std::string& name, int64_t k, int64_t rows) {
+    const ggml_tensor* t = m.get(name);
+    if (t->ne[0] != k || t->ne[1] != rows || t->ne[2] != 1 || t->ne[3] != 1 ||
+        tgr::tsp_dtype_of(t->type) < 0)
+        fail(name + ": expected ggml shape [" + std::to_string(k) + ", " + std::to_string(rows) + "]");
+    return t;
+}
+
+const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s) {
+    if (t->type == GGML_TYPE_F32) return static_cast<const float*>(t->data);
+    void* p = sc.take((size_t)ggml_nelements(t) * 4);
+    if (sc.running())
+        hip_check(tgr::launch_convert(t->data, tgr::tsp_dtype_of(t->type), p, TSP_F32, ggml_nelements(t), s),
+                  "parameter conversion");
+    return static_cast<const float*>(p);
+}
+
+// ---- conv --------------------------------------------------------------------------------------
+Conv conv_of(const Model& m, const std::string& prefix) {
+    Conv c;
+    c.w = m.get(prefix + ".weight");
+    c.b = m.get(prefix + ".bias");
+    if (c.w->ne[1] != 27 || c.w->ne[3] != 1) fail(prefix + ".weight: expected ggml shape [Ci, 27, Co]");
+    c.ci = (int)c.w->ne[0];
+    c.co = (int)c.w->ne[2];
+    if (ggml_nelements(c.b) != c.co) fail(prefix + ".bias: expected " + std::to_string(c.co) + " elements");
+    c.wdt = tgr::tsp_dtype_of(c.w->type);
+    if (c.wdt < 0) fail(prefix + ".weight: unsupported tensor type");
+    c.mfma = !g_sparse_cast_f32 && (c.wdt == TSP_F16 || c.wdt == TSP_BF16) && c.ci % 16 == 0 &&
+             c.co % 64 == 0;
+    return c;
+}
+
+// F32 activations are rounded to the weights' 16-bit type for the matrix-core kernel, as ggml's
+// F16 mul_mat rounds its F32 operand (sparse.cpp:74); under g_sparse_cast_f32 or for channel
+// counts the matrix-core tiles do not cover, the fp32 kernel runs on the weights' exact values.
+void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
+              float* out, Carve& sc, hipStream_t s) {
+    const float* bias = f32_param(c.b, sc, s);
+    if (c.mfma) {
+        const void* x16 = x;
+        if (xdt != c.wdt) {
+            void* p = sc.take((size_t)n * c.ci * 2);
+            if (sc.running()) hip_check(tgr::launch_convert(x, xdt, p, c.wdt, n * c.ci, s), "conv input rounding");
+            x16 = p;
+        }
+        void* packed = sc.take((size_t)27 * c.ci * c.co * 2);
+        if (!sc.running()) return;
+        if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
+        lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, packed, s), "weight pack");
+        lib(tsp_subm_conv3x3_planned(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, s),
+            "sparse conv");
+    } else {
+        if (!sc.running()) return;
+        lib(tsp_subm_conv3x3(x, xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
+                             TSP_ALGO_AUTO, s),
+            "sparse conv");
+    }
+}
+
+size_t conv_scratch(const Conv& c, int64_t n, int xdt) {
+    Carve sz;
+    run_conv(c, nullptr, xdt, n, nullptr, nullptr, nullptr, sz, nullptr);
+    return sz.off;
+}
+
+// ---- ConvNeXt block (sparse.cpp:94-137) --------------------------------------------------------
+ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n) {
+    ConvNext a;
+    a.conv = conv_of(m, prefix + ".conv");
+    const int c = a.conv.co;
+    if (a.conv.ci != c) fail(prefix + ".conv: a ConvNeXt conv keeps the channel count");
+    a.nw = vec_param(m, prefix + ".norm.weight", c);
+    a.nb = vec_param(m, prefix + ".norm.bias", c);
+    a.w0 = mat_param(m, prefix + ".mlp.0.weight", c, 4 * (int64_t)c);
+    a.b0 = vec_param(m, prefix + ".mlp.0.bias", 4 * (int64_t)c);
+    a.w2 = mat_param(m, prefix + ".mlp.2.weight", 4 * (int64_t)c, c);
+    a.b2 = vec_param(m, prefix + ".mlp.2.bias", c);
+    a.n = n;
+    a.c = c;
+    // the [chunk, 4C] f32 hidden is bounded to 1 GiB
+    a.chunk = std::max<int64_t>(1, std::min<int64_t>(n, (int64_t(1) << 30) / (16 * (int64_t)c)));
+    a.mlp16 = !g_sparse_cast_f32 && a.w0->type == a.w2->type &&
+              (a.w0->type == GGML_TYPE_F16 || a.w0->type == GGML_TYPE_BF16) && c % 64 == 0;
+    return a;
+}
+
+void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr, const void* plan,
+                  float* out, Carve& sc, hipStream_t s) {
+    const int c = a.c;
+    const int w0dt = tgr::tsp_dtype_of(a.w0->type), w2dt = tgr::tsp_dtype_of(a.w2->type);
+    // the linears' inputs take the weights' 16-bit type so they run on the matrix cores
+    const int adt = a.mlp16 ? w0dt : TSP_F32;
+    const size_t aes = adt == TSP_F32 ? 4 : 2;
+    float* h = static_cast<float*>(sc.take((size_t)a.n * c * 4));
+    void* hn = a.mlp16 ? sc.take((size_t)a.n * c * 2) : h;
+    float* hid = static_cast<float*>(sc.take((size_t)a.chunk * 4 * c * 4));
+    void* hid_in = a.mlp16 ? sc.take((size_t)a.chunk * 4 * c * 2) : hid;
+    const float* gamma = f32_param(a.nw, sc, s);
+    const float* beta = f32_param(a.nb, sc, s);
+    const float* bias0 = f32_param(a.b0, sc, s);
+    const float* bias2 = f32_param(a.b2, sc, s);
+    run_conv(a.conv, x, xdt, a.n, nbr, plan, h, sc, s);
+    if (!sc.running()) return;
+    lib(tsp_layer_norm(h, TSP_F32, a.n, c, gamma, beta, 1e-6f, 0, hn, adt, s), "convnext norm");
+    const size_t xes = xdt == TSP_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < a.n; r0 += a.chunk) {
+        const int64_t nr = std::min(a.chunk, a.n - r0);
+        lib(tsp_linear(static_cast<const char*>(hn) + (size_t)r0 * c * aes, adt, nr, c, a.w0->data, w0dt,
+                       bias0, 4 * c, hid, TSP_F32, s),
+            "convnext mlp.0");
+        hip_check(tgr::launch_silu_to(hid, hid_in, adt, nr * 4 * c, s), "convnext silu");
+        lib(tsp_linear(hid_in, adt, nr, 4 * c, a.w2->data, w2dt, bias2, c, out + r0 * c, TSP_F32, s),
+            "convnext mlp.2");
+        hip_check(tgr::launch_add_inplace(out + r0 * c, static_cast<const char*>(x) + (size_t)r0 * c * xes,
+                                          xdt, nr * c, s),
+                  "convnext residual");
+    }
+}
+
+size_t convnext_scratch(const ConvNext& a, int xdt) {
+    Carve sz;
+    run_convnext(a, nullptr, xdt, nullptr, nullptr, nullptr, sz, nullptr);
+    return sz.off;
+}
+
+// ---- tables --------------------------------------------------------------------------------------
+void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s) {
+    t.n = n;
+    t.plan = DeviceBuffer();
+    t.nbr = DeviceBuffer((size_t)27 * n * 4);
+    if (n == 0) return;
+    DeviceBuffer ws(tsp_rulebook_workspace_bytes(n)), status(4);
+    hip_check(hipMemsetAsync(status.get(), 0, 4, s), "rulebook");
+    lib(tsp_rulebook_build(d_coords, n, t.nbr.as<int32_t>(), ws.get(), ws.size(), status.as<int32_t>(), s),
+        "rulebook");
+    int32_t st = 0;
+    hip_check(hipMemcpyAsync(&st, status.get(), 4, hipMemcpyDeviceToHost, s), "rulebook");
+    hip_check(hipStreamSynchronize(s), "rulebook");   // before `ws` is freed
+    if (st) fail("neighbour table: a coordinate lies outside [0, 2^21-3]");
+}
+
+void Table::ensure_plan(hipStream_t s) {
+    if (plan.get() || n == 0) return;
+    const size_t bytes = tsp_conv_plan_bytes(n);
+    plan = DeviceBuffer(bytes);
+    lib(tsp_conv_plan_build(nbr.as<int32_t>(), n, plan.get(), bytes, s), "conv plan");
+}
+
+// ---- C2S up-block (sparse.cpp:172-336) -----------------------------------------------------------
+C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
+               Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s) {
+    const int64_t n = parent.n;
+    if (cin <= 0 || cin % 8 != 0 || cout <= 0 || cout % (cin / 8) != 0)
+        fail(prefix + ": C2S needs Cin % 8 == 0 and Cout % (Cin/8) == 0");
+    if (ext_mask && (int64_t)ext_mask->size() != 8 * n) fail(prefix + ": ext_subdiv must hold 8*N entries");
+    C2SOut r;
+    r.mask.resize((size_t)8 * n);
+    if (n == 0) return r;
+    const Conv conv1 = conv_of(m, prefix + ".conv1"), conv2 = conv_of(m, prefix + ".conv2");
+    if (conv1.ci != cin || conv1.co != 8 * cout || conv2.ci != cout || conv2.co != cout)
+        fail(prefix + ": conv1 must map Cin -> 8*Cout and conv2 Cout -> Cout");
+    const ggml_tensor* n1w = vec_param(m, prefix + ".norm1.weight", cin);
+    const ggml_tensor* n1b = vec_param(m, prefix + ".norm1.bias", cin);
+
+    // subdivision mask: the caller's, or to_subdiv logits > 0 (sparse.cpp:184-199, 215)
+    DeviceBuffer d_mask((size_t)8 * n);
+    if (ext_mask) {
+        hip_check(hipMemcpyAsync(d_mask.get(), ext_mask->data(), (size_t)8 * n, hipMemcpyHostToDevice, s),
+                  "c2s mask upload");
+    } else {
+        const ggml_tensor* wsub = mat_param(m, prefix + ".to_subdiv.weight", cin, 8);
+        const ggml_tensor* bsub = vec_param(m, prefix + ".to_subdiv.bias", 8);
+        DeviceBuffer d_logits((size_t)8 * n * 4), d_b(256);
+        Carve sc(d_b.get());
+        lib(tsp_linear(d_x, TSP_F32, n, cin, wsub->data, tgr::tsp_dtype_of(wsub->type), f32_param(bsub, sc, s),
+                       8, d_logits.get(), TSP_F32, s),
+            prefix + ".to_subdiv");
+        lib(tsp_mask_positive(d_logits.as<float>(), 8 * n, d_mask.as<uint8_t>(), s), prefix + " mask");
+        hip_check(hipStreamSynchronize(s), "c2s mask");
+    }
+
+    // children, parent-major and octant-ascending (sparse.cpp:205-222)
+    DeviceBuffer d_mstart((size_t)(n + 1) * 4), d_child((size_t)8 * n * 12), d_gidx((size_t)8 * n * 4), d_m(8),
+        d_sws(tsp_subdivide_workspace_bytes(n));
+    lib(tsp_subdivide(d_mask.as<uint8_t>(), d_coords, n, d_mstart.as<int32_t>(), d_child.as<int32_t>(),
+                      d_gidx.as<int32_t>(), d_m.as<int64_t>(), d_sws.get(), d_sws.size(), s),
+        prefix + " subdivide");
+    int64_t mm = 0;
+    hip_check(hipMemcpyAsync(&mm, d_m.get(), 8, hipMemcpyDeviceToHost, s), "c2s");
+    hip_check(hipMemcpyAsync(r.mask.data(), d_mask.get(), (size_t)8 * n, hipMemcpyDeviceToHost, s), "c2s mask");
+    hip_check(hipStreamSynchronize(s), "c2s");
+    r.m = mm;
+    r.coords = DeviceBuffer((size_t)mm * 12);
+    r.feats = DeviceBuffer((size_t)mm * cout * 4);
+    if (mm == 0) return r;
+    hip_check(hipMemcpyAsync(r.coords.get(), d_child.get(), (size_t)mm * 12, hipMemcpyDeviceToDevice, s),
+              "c2s");
+
+    // conv1 on the parents: LN(norm1)+SiLU written straight in the conv's input dtype
+    const int in1 = conv1.mfma ? conv1.wdt : TSP_F32, in2 = conv2.mfma ? conv2.wdt : TSP_F32;
+    const size_t es1 = in1 == TSP_F32 ? 4 : 2, es2 = in2 == TSP_F32 ? 4 : 2;
+    const size_t s1 = conv_scratch(conv1, n, in1), s2 = conv_scratch(conv2, mm, in2);
+    Carve sz;
+    sz.take((size_t)n * cin * es1);
+    sz.take((size_t)n * 8 * cout * 4);
+    sz.take(s1);
+    sz.take((size_t)mm * cout * 4);
+    sz.take((size_t)mm * cout * es2);
+    sz.take(s2);
+    sz.take(2 * (size_t)cin * 4);
+    DeviceBuffer work(sz.off);
+    Carve w(work.get());
+    void* h0 = w.take((size_t)n * cin * es1);
+    float* h1 = static_cast<float*>(w.take((size_t)n * 8 * cout * 4));
+    Carve sc1(w.take(s1));
+    float* g = static_cast<float*>(w.take((size_t)mm * cout * 4));
+    void* h2 = w.take((size_t)mm * cout * es2);
+    Carve sc2(w.take(s2));
+    Carve scp(w.take(2 * (size_t)cin * 4));
+    const float* g1 = f32_param(n1w, scp, s);
+    const float* b1 = f32_param(n1b, scp, s);
+
+    lib(tsp_layer_norm(d_x, TSP_F32, n, cin, g1, b1, 1e-6f, 1, h0, in1, s), prefix + ".norm1");
+    if (conv1.mfma) parent.ensure_plan(s);
+    run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), h1, sc1, s);
+
+    // channel -> spatial gather, norm2 (no affine) + SiLU, conv2 on the children, skip
+    lib(tsp_c2s_gather(h1, TSP_F32, d_gidx.as<int32_t>(), mm, cout, g, s), prefix + " gather");
+    lib(tsp_layer_norm(g, TSP_F32, mm, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s), prefix + " norm2");
+    build_table(r.coords.as<int32_t>(), mm, r.table, s);
+    if (conv2.mfma) r.table.ensure_plan(s);
+    run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s);
+    lib(tsp_c2s_skip_add(d_x, TSP_F32, d_gidx.as<int32_t>(), mm, cin, cout, r.feats.get(), TSP_F32, s),
+        prefix + " skip");
+    hip_check(hipStreamSynchronize(s), "c2s");   // before the temporaries are freed
+    return r;
+}
+
+// ---- per-voxel linear (shape_decoder.cpp:63-77) --------------------------------------------------
+void run_linear(const Model& m, const std::string& prefix, const float* d_x, int64_t n, int ci, int co,
+                bool pre_norm, float eps, float* d_out, hipStream_t s) {
+    const ggml_tensor* w = mat_param(m, prefix + ".weight", ci, co);
+    const ggml_tensor* b = vec_param(m, prefix + ".bias", co);
+    const int wdt = tgr::tsp_dtype_of(w->type);
+    const bool mfma = !g_sparse_cast_f32 && (wdt == TSP_F16 || wdt == TSP_BF16) && ci % 32 == 0 && co % 64 == 0;
+    const int xdt = mfma ? wdt : TSP_F32;
+    DeviceBuffer tmp((pre_norm || mfma) ? (size_t)n * ci * (mfma ? 2 : 4) : 0), pb((size_t)co * 4 + 256);
+    Carve sc(pb.get());
+    const float* bias = f32_param(b, sc, s);
+    const void* x = d_x;
+    if (pre_norm) {
+        lib(tsp_layer_norm(d_x, TSP_F32, n, ci, nullptr, nullptr, eps, 0, tmp.get(), xdt, s), prefix + " norm");
+        x = tmp.get();
+    } else if (mfma) {
+        hip_check(tgr::launch_convert(d_x, TSP_F32, tmp.get(), xdt, n * ci, s), (prefix + " rounding").c_str());
+        x = tmp.get();
+    }
+    lib(tsp_linear(x, xdt, n, ci, w->data, wdt, bias, co, d_out, TSP_F32, s), prefix);
+    hip_check(hipStreamSynchronize(s), prefix.c_str());   // before the temporaries are freed
+}
+
+}  // namespace ops
+}  // namespace trellis

@@ -1,0 +1,97 @@
+// Device-level pieces of the sparse path, shared by the ggml graph nodes of sparse.cpp, the
+// device-resident C2S block and the decoder: everything takes device pointers and a stream, and
+// allocates its own temporaries unless a scratch Carve is passed in.
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "ggml.h"
+#include "runtime.hpp"
+#include "trellis_model.h"
+
+namespace trellis {
+namespace ops {
+
+void lib(int st, const std::string& what);   // throws std::runtime_error with tsp_last_error()
+
+// Scratch carving: the same walk sizes a buffer (a default-constructed Carve: nothing runs) and,
+// over the real buffer, hands out its pieces while the work runs.
+struct Carve {
+    char* base = nullptr;
+    size_t off = 0;
+    bool sizing = true;
+    Carve() = default;
+    explicit Carve(void* b) : base(static_cast<char*>(b)), sizing(false) {}
+    bool running() const { return !sizing; }
+    void* take(size_t bytes) {
+        void* p = sizing ? nullptr : base + off;
+        off += tgr::align_up(bytes);
+        return p;
+    }
+};
+
+const ggml_tensor* vec_param(const Model& m, const std::string& name, int64_t n);
+const ggml_tensor* mat_param(const Model& m, const std::string& name, int64_t k, int64_t rows);
+// f32 view of a 1-D parameter (converted into scratch when stored in 16 bits)
+const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s);
+
+// A submanifold conv's weights (`prefix.weight` ggml [Ci, 27, Co], `prefix.bias` [Co]).
+struct Conv {
+    const ggml_tensor* w = nullptr;
+    const ggml_tensor* b = nullptr;
+    int ci = 0, co = 0, wdt = 0;
+    bool mfma = false;   // matrix-core kernel (16-bit weights, Ci % 16 == 0, Co % 64 == 0)
+};
+Conv conv_of(const Model& m, const std::string& prefix);
+// out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
+void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
+              float* out, Carve& sc, hipStream_t s);
+size_t conv_scratch(const Conv& c, int64_t n, int xdt);
+
+// SparseConvNeXtBlock3d weights and the launch shape of one block over n voxels.
+struct ConvNext {
+    Conv conv;
+    const ggml_tensor *nw = nullptr, *nb = nullptr, *w0 = nullptr, *b0 = nullptr, *w2 = nullptr,
+                      *b2 = nullptr;
+    int64_t n = 0;
+    int c = 0;
+    int64_t chunk = 0;
+    bool mlp16 = false;   // the linears run on 16-bit activations (matrix cores)
+};
+ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n);
+// out [n][c] f32 = block(x [n][c]); out must not alias x.
+void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr, const void* plan,
+                  float* out, Carve& sc, hipStream_t s);
+size_t convnext_scratch(const ConvNext& a, int xdt);
+
+// A voxel set on the device with its neighbour table and (optionally) conv plan.
+struct Table {
+    int64_t n = 0;
+    tgr::DeviceBuffer nbr;    // int32 [27 n]
+    tgr::DeviceBuffer plan;   // empty until ensure_plan
+    void ensure_plan(hipStream_t s);
+};
+// Builds the table of d_coords [n][3]; throws for coordinates outside [0, 2^21-3].
+void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s);
+
+// The C2S up-block on device data: x f32 [n][cin] on coords (table `parent`); ext_mask (host,
+// 8n entries) or, when null, the block's to_subdiv prediction. Returns the children's features
+// f32 [m][cout], coords [m][3], their table (with plan if conv2 uses the matrix cores) and the
+// [8n] mask used (on the host).
+struct C2SOut {
+    int64_t m = 0;
+    tgr::DeviceBuffer feats, coords;
+    Table table;
+    std::vector<uint8_t> mask;
+};
+C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
+               Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s);
+
+// out [n][co] f32 = (optionally LN(eps, no affine) of) x [n][ci] . W^T + b for `prefix.weight`
+// ggml [ci, co]; the input is rounded to the weight's 16-bit type when the matrix cores can run it.
+void run_linear(const Model& m, const std::string& prefix, const float* d_x, int64_t n, int ci, int co,
+                bool pre_norm, float eps, float* d_out, hipStream_t s);
+
+}  // namespace ops
+}  // namespace trellis
