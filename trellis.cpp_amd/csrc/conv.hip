@@ -423,6 +423,9 @@ extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, 
     if (algo == TSP_ALGO_MFMA_GATHER)
         return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, kTaps, d_weight,
                                d_bias, co, d_out, s);
+    if (algo == TSP_ALGO_AUTO && eligible && !halo_fits(n, ci))
+        return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, kTaps, d_weight,
+                               d_bias, co, d_out, s);
     if (algo == TSP_ALGO_MFMA || (algo == TSP_ALGO_AUTO && eligible))
         return halo_conv_launch(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, nullptr, d_weight,
                                 d_bias, co, d_out, s);

@@ -32,6 +32,8 @@ constexpr int HB_M = 512;   // output voxels per workgroup (and per plan tile)
 
 // Bytes of a conv plan for n voxels (see tsp_conv_plan_bytes).
 size_t halo_plan_bytes(int64_t n);
+// whether the LDS-staged kernel can address n rows of ci channels (32-bit byte offsets)
+bool halo_fits(int64_t n, int ci);
 // Builds the plan of neighbour table `nbr` into `plan`.
 int halo_plan_build(const int32_t* nbr, int64_t n, void* plan, hipStream_t s);
 // Packs [co][27][ci] 16-bit weights into the MFMA operand order (ci % 16 == 0, co % 32 == 0).
