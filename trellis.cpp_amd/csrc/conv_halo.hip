@@ -54,9 +54,8 @@ __device__ __forceinline__ int wave_max(int v) {
     return v;
 }
 
-// Plan layout: [n_tiles][4] int32 header {H, direct, 0, 0} | [n_tiles][HB_SLOTS] int32 row of
-// each slot | [n_tiles][27][4][32][4] uint16 slot of each (tap, voxel/128, voxel%32,
-// voxel/32%4).
+// Plan layout: [n_tiles][4] int32 header {H, direct, 0, 0} | [n_tiles][HB_SLOTS] int32 row of each
+// slot | [n_tiles][27][4][32][4] uint16 slot of each (tap, voxel/128, voxel%32, voxel/32%4).
 struct PlanView {
     int32_t* hdr;
     int32_t* rowof;
@@ -306,6 +305,13 @@ template <int BN, int RB, int CB>
 constexpr int hb_waves() { return (HB_M / (32 * RB)) * (BN / (32 * CB)); }
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
+__device__ __forceinline__ void conv_tile(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int n_ctiles, int64_t lin, uint16_t (&sH0)[2][HB_ROWS][8],
+    uint16_t (&sH1)[2][HB_ROWS][8], uint16_t (&sL)[kTaps][4][32][4], int* sRed);
+
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
@@ -315,13 +321,11 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
     constexpr int WAVES = NRG * NCG;
     constexpr int NT = WAVES * 64;
-    constexpr int WN = 32 * CB;              // output channels per wave
-    constexpr int PIECES = 2 * HB_SLOTS / 64 / WAVES;   // slice DMA ops per wave and slice
     static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
     static_assert(RB % 4 == 0 && HB_M % (32 * RB) == 0 && BN % (32 * CB) == 0, "tile split");
     // the two slice buffers [half][slot][8 ch] -- separate objects, so that alias analysis sees
-    // that the DMA into one never feeds the reads of the other and the compiler need not wait
-    // for the DMA before every LDS read -- and the slot table [tap][row block][voxel%32][rb]
+    // that the writes into one never feed the reads of the other and the compiler need not wait
+    // for them before every LDS read -- and the slot table [tap][row block][voxel%32][rb]
     __shared__ __attribute__((aligned(16))) uint16_t sH0[2][HB_ROWS][8];
     __shared__ __attribute__((aligned(16))) uint16_t sH1[2][HB_ROWS][8];
     __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
@@ -329,9 +333,27 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
 
     // XCD-aware order: workgroup ids go round-robin over the 8 XCDs, so each XCD gets one
     // contiguous range of (tile, column-tile) pairs and gathers from rows its L2 already holds.
-    const int64_t b = blockIdx.x;
-    const int64_t lin = (b % 8) * per_xcd + b / 8;
-    if (lin >= n_tiles * n_ctiles) return;
+    const int64_t total = n_tiles * n_ctiles;
+    const int xcd = (int)(blockIdx.x % 8);
+    const int64_t xlo = xcd * per_xcd, xhi = xlo + per_xcd < total ? xlo + per_xcd : total;
+    const int64_t lin = xlo + blockIdx.x / 8;
+    if (lin >= xhi) return;
+    conv_tile<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, lin, sH0, sH1, sL, sRed);
+}
+
+// One (tile, column tile) of the conv: the whole tile pipeline, run by all the workgroup's waves.
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
+__device__ __forceinline__ void conv_tile(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int n_ctiles, int64_t lin, uint16_t (&sH0)[2][HB_ROWS][8],
+    uint16_t (&sH1)[2][HB_ROWS][8], uint16_t (&sL)[kTaps][4][32][4], int* sRed) {
+    constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
+    constexpr int WAVES = NRG * NCG;
+    constexpr int NT = WAVES * 64;
+    constexpr int WN = 32 * CB;              // output channels per wave
+    constexpr int PIECES = 2 * HB_SLOTS / 64 / WAVES;   // slice loads per wave and slice
     const int64_t tile = lin / n_ctiles;
     const int64_t row0 = tile * HB_M;
 
@@ -352,21 +374,28 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     // slice 0: row * ci * 2 + plane * 16; slots past H copy row 0 into an unused slot
     uint32_t poff[PIECES];
     int32_t prow[PIECES];
-    if constexpr (PLANNED) {
-        const int32_t* hdr = plan.hdr + tile * 4;
-        H = hdr[0];
-        direct = hdr[1] != 0;
-        if (!direct) {
-            const char* src = reinterpret_cast<const char*>(plan.slots + tile * HB_SLOT_TABLE);
-            for (int p = wave; p < HB_SLOT_TABLE * 2 / 1024; p += WAVES)   // 27 x 1 KiB
-                __builtin_amdgcn_global_load_lds(
-                    src + p * 1024 + lane * 16,
-                    (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024),
-                    16, 0, 0);
-            // all HB_SLOTS entries of a tile lie inside the plan: load without a branch
-            const int32_t* ro = plan.rowof + tile * HB_SLOTS;
+    // the bias of this lane's output channels, fetched now so the epilogue does not wait for it
+    float bv[CB];
 #pragma unroll
-            for (int j = 0; j < PIECES; ++j) prow[j] = ro[piece_slot(j) + lane];
+    for (int cb = 0; cb < CB; ++cb) bv[cb] = bias[c0 + cb * 32 + r32];
+    if constexpr (PLANNED) {
+        // Header, slot table and piece rows are independent loads (every tile has a full-size
+        // slot table and row list in the plan), issued together so the prologue pays one
+        // memory round trip for them instead of two.
+        const int32_t* hdr = plan.hdr + tile * 4;
+        const int32_t h0 = hdr[0], h1 = hdr[1];
+        const char* src = reinterpret_cast<const char*>(plan.slots + tile * HB_SLOT_TABLE);
+        for (int p = wave; p < HB_SLOT_TABLE * 2 / 1024; p += WAVES)   // 27 x 1 KiB
+            __builtin_amdgcn_global_load_lds(
+                src + p * 1024 + lane * 16,
+                (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024),
+                16, 0, 0);
+        const int32_t* ro = plan.rowof + tile * HB_SLOTS;
+#pragma unroll
+        for (int j = 0; j < PIECES; ++j) prow[j] = ro[piece_slot(j) + lane];
+        H = h0;
+        direct = h1 != 0;
+        if (!direct) {
 #pragma unroll
             for (int j = 0; j < PIECES; ++j)
                 if (piece_slot(j) + lane >= H) prow[j] = 0;
@@ -409,9 +438,7 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
         static_assert((WAVES / 2) * 32 * RS <= (int)sizeof(sH0), "staging must fit a slice buffer");
         char* stage = reinterpret_cast<char*>(wave < WAVES / 2 ? &sH0[0][0][0] : &sH1[0][0][0]) +
                       (wave % (WAVES / 2)) * 32 * RS;
-        float bv[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) bv[cb] = bias[c0 + cb * 32 + r32];
+        const bool full = row0 + HB_M <= n;   // no row of the tile is past n (uniform)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
@@ -421,13 +448,20 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
                     const int r = 8 * (j / 4) + 4 * g + (j % 4);
                     *reinterpret_cast<float*>(stage + r * RS + (cb * 32 + r32) * 4) = acc[rb][cb][j] + bv[cb];
                 }
+            // 32 rows x WN/4 chunks of 4 channels: all LDS reads first (one wait), then the stores
+            f32x4_t vs[WN / 8];
 #pragma unroll
-            for (int q = 0; q < WN / 8; ++q) {           // 32 rows x WN/4 chunks of 4 channels
+            for (int q = 0; q < WN / 8; ++q) {
+                const int c = q * 64 + lane;
+                vs[q] = *reinterpret_cast<const f32x4_t*>(stage + (c / (WN / 4)) * RS + (c % (WN / 4)) * 16);
+            }
+#pragma unroll
+            for (int q = 0; q < WN / 8; ++q) {
                 const int c = q * 64 + lane;
                 const int r = c / (WN / 4), cq = c % (WN / 4);
-                const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stage + r * RS + cq * 16);
+                const f32x4_t v = vs[q];
                 const int64_t i = row0 + 32 * RB * rg + 32 * rb + r;
-                if (i < n) {
+                if (full || i < n) {
                     const int64_t o = i * co + c0 + cq * 4;
                     if constexpr (ODT == TSP_F32) {
                         *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + o) = v;
@@ -510,9 +544,11 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
         static_assert(PIECES * SP <= kTaps, "slice pieces must fit in one slice's taps");
         static_assert((PIECES - 1) * SP + STG < kTaps, "every staged piece is written within its slice");
         // zero slot of both buffers and planes (the barrier below publishes it)
-        if (tid < 4)
-            *reinterpret_cast<u32x4_t*>(tid < 2 ? &sH0[tid & 1][HB_ZERO][0] : &sH1[tid & 1][HB_ZERO][0]) =
-                u32x4_t{0, 0, 0, 0};
+        if (tid < 4) {
+            u32x4_t z{0, 0, 0, 0};
+            asm volatile("" : "+v"(z));   // made here, not held in registers across tiles
+            *reinterpret_cast<u32x4_t*>(tid < 2 ? &sH0[tid & 1][HB_ZERO][0] : &sH1[tid & 1][HB_ZERO][0]) = z;
+        }
 #pragma unroll
         for (int j = 0; j < PIECES; ++j) {
             u32x4_t r;
@@ -606,7 +642,8 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
     // tap, written to LDS 6 taps after its load
     constexpr int RB = 4, CB = BN / 64, PD = 2, SP = 2, STG = 6;
     hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>),
-                       dim3((unsigned)(per_xcd * 8)), dim3(hb_waves<BN, RB, CB>() * 64), 0, s, reinterpret_cast<const uint16_t*>(feats), n, ci,
+                       dim3((unsigned)(per_xcd * 8)), dim3(hb_waves<BN, RB, CB>() * 64), 0, s,
+                       reinterpret_cast<const uint16_t*>(feats), n, ci,
                        nbr, pv, reinterpret_cast<const uint16_t*>(weight), bias, co, out, n_tiles,
                        n_ctiles, per_xcd);
     TSP_CHECK_LAUNCH();
