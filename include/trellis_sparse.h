@@ -65,7 +65,8 @@ int tsp_version(void);
  * coordinates the largest row index (the reference's last insert wins, sparse.cpp:26).
  * ------------------------------------------------------------------------------------- */
 
-/* Device workspace (bytes) tsp_rulebook_build needs for n voxels. */
+/* Device workspace (bytes) tsp_rulebook_build needs for n voxels (64 bytes per bucket of a
+ * 2x2x2-brick hash with 1.5 n + 1024 buckets); the workspace must be 64-byte aligned. */
 size_t tsp_rulebook_workspace_bytes(int64_t n);
 
 /* d_coords int32 [n][3] -> d_nbr int32 [27*n]. d_status, if not NULL, is a device int32 that

@@ -2,15 +2,21 @@
 //
 // Replaces trellis::build_neighbor_table (src/sparse.cpp:21-39). The reference inserts every
 // voxel into a host std::unordered_map (later rows overwrite earlier ones, :26) and probes the
-// 27 offsets of each voxel (:28-37). Here:
-//   * the map is an open-addressing table in HBM: 64-bit keys (21 bits per axis, coordinate+1
-//     so that the -1 probes have a key of their own) and int32 values, linear probing, load
-//     factor <= 1/2;
-//   * inserts claim a slot with a 64-bit CAS and keep the largest row with atomicMax -- the
-//     reference's "last insert wins" for duplicate coordinates, independent of thread order,
-//     so the table is deterministic;
-//   * probes run one thread per (voxel, tap) on a tap-major grid, so every store of the table
-//     is coalesced and consecutive threads probe neighbouring keys.
+// 27 offsets of each voxel (:28-37). Here the map is an open-addressing table in HBM whose
+// entries are bricks, not voxels:
+//   * with X = x + 1 (so that the x - 1 probes stay non-negative), voxel (X, Y, Z) lives in
+//     brick (X>>1, Y>>1, Z>>1) at octant (X&1) | (Y&1)<<1 | (Z&1)<<2. A bucket is one 64-byte
+//     line: the brick's key and the rows of its 8 voxels (row + 1, 0 = absent);
+//   * the 27 neighbours of a voxel lie in the 2x2x2 bricks from ((X-1)>>1, ...), so a voxel
+//     looks up 8 buckets instead of 27 keys, and consecutive voxels of a sorted set look up
+//     mostly the same buckets, which the vector L1 then serves;
+//   * inserts claim a bucket with a 64-bit CAS on its key (linear probing) and keep the largest
+//     row of each voxel with atomicMax -- the reference's "last insert wins" for duplicate
+//     coordinates, independent of thread order, so the table is deterministic;
+//   * one thread per voxel writes its 27 entries, tap-major, so every store of a wave is one
+//     coalesced 256-byte row segment.
+// Capacity: 1.5 N + 1024 buckets, so at most 2/3 full even when every voxel has a brick of its
+// own (scattered sets); surface shells fill about a third of a brick's octants.
 #include <algorithm>
 
 #include "common.hpp"
@@ -18,16 +24,17 @@
 namespace tsp {
 namespace {
 
-constexpr uint64_t kEmptyKey = ~0ull;
 constexpr int32_t kCoordMax = (1 << 21) - 3;   // voxel coords in [0, kCoordMax]
+constexpr int kBucketWords = 16;               // uint32 words of a bucket (64 bytes)
 
-__device__ __forceinline__ uint64_t pack_key(int32_t x, int32_t y, int32_t z) {
-    // x,y,z in [-1, 2^21-2] -> fields of 21 bits; bit 63 is never set, so ~0 is free.
-    return (uint64_t)(uint32_t)(x + 1) | ((uint64_t)(uint32_t)(y + 1) << 21) |
-           ((uint64_t)(uint32_t)(z + 1) << 42);
+// Brick coordinates in [0, 2^20) -> a key that is never 0 (0 marks an empty bucket).
+__device__ __forceinline__ uint64_t brick_key(uint32_t bx, uint32_t by, uint32_t bz) {
+    return 1 + ((uint64_t)bx | ((uint64_t)by << 20) | ((uint64_t)bz << 40));
 }
 
-__device__ __forceinline__ uint64_t slot_hash(uint64_t k) {
+// 64-bit finaliser (a multiply-xorshift mixer) -- the home bucket is its high bits scaled to
+// the capacity, so every key bit reaches the bucket index.
+__device__ __forceinline__ uint64_t mix64(uint64_t k) {
     k ^= k >> 31; k *= 0x7fb5d329728ea185ull;
     k ^= k >> 27; k *= 0x81dadef4bc2dd44dull;
     k ^= k >> 33;
@@ -35,35 +42,26 @@ __device__ __forceinline__ uint64_t slot_hash(uint64_t k) {
 }
 
 struct HashView {
-    uint64_t* keys;
-    int32_t* vals;
-    uint64_t mask;
+    uint32_t* words;   // [cap][16]: key (2 words), rows of octants 0..7 (8 words), unused
+    uint64_t cap;
 };
 
-inline uint64_t table_capacity(int64_t n) {
-    uint64_t cap = 1024;
-    while (cap < (uint64_t)(2 * n)) cap <<= 1;
-    return cap;
+inline uint64_t table_capacity(int64_t n) { return (uint64_t)n + (uint64_t)n / 2 + 1024; }
+
+__device__ __forceinline__ uint64_t home(const HashView& h, uint64_t key) {
+    return __umul64hi(mix64(key), h.cap);
+}
+__device__ __forceinline__ uint64_t next(const HashView& h, uint64_t s) {
+    return s + 1 == h.cap ? 0 : s + 1;
+}
+__device__ __forceinline__ bool coords_ok(int32_t x, int32_t y, int32_t z) {
+    return x >= 0 && y >= 0 && z >= 0 && x <= kCoordMax && y <= kCoordMax && z <= kCoordMax;
 }
 
-inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
-
-inline HashView carve(void* ws, int64_t n) {
-    const uint64_t cap = table_capacity(n);
-    HashView h;
-    h.keys = reinterpret_cast<uint64_t*>(ws);
-    h.vals = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(ws) + align256(cap * 8));
-    h.mask = cap - 1;
-    return h;
-}
-
-__global__ void k_hash_clear(HashView h) {
-    const uint64_t cap = h.mask + 1;
-    for (uint64_t s = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; s < cap;
-         s += (uint64_t)gridDim.x * blockDim.x) {
-        h.keys[s] = kEmptyKey;
-        h.vals[s] = -1;
-    }
+__global__ void k_hash_clear(u32x4_t* __restrict__ words, int64_t n16) {
+    for (int64_t s = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; s < n16;
+         s += (int64_t)gridDim.x * blockDim.x)
+        words[s] = u32x4_t{0, 0, 0, 0};
 }
 
 __global__ void k_hash_insert(const int32_t* __restrict__ coords, int64_t n, HashView h,
@@ -71,52 +69,76 @@ __global__ void k_hash_insert(const int32_t* __restrict__ coords, int64_t n, Has
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
-    if (x < 0 || y < 0 || z < 0 || x > kCoordMax || y > kCoordMax || z > kCoordMax) {
+    if (!coords_ok(x, y, z)) {
         if (status) atomicOr(status, 1);
         return;
     }
-    const uint64_t key = pack_key(x, y, z);
-    uint64_t s = slot_hash(key) & h.mask;
-    // The table holds at least 2n slots, so an empty or matching slot is always reached.
-    for (;;) {
-        unsigned long long prev = atomicCAS(reinterpret_cast<unsigned long long*>(h.keys + s),
-                                            (unsigned long long)kEmptyKey,
-                                            (unsigned long long)key);
-        if (prev == kEmptyKey || prev == key) {
-            atomicMax(h.vals + s, (int32_t)i);
+    const uint32_t X = x + 1, Y = y + 1, Z = z + 1;
+    const uint64_t key = brick_key(X >> 1, Y >> 1, Z >> 1);
+    const int oct = (X & 1) | (Y & 1) << 1 | (Z & 1) << 2;
+    // There are more buckets than voxels, so an empty or matching bucket is always reached.
+    // A plain read first: most bricks were claimed by an earlier voxel, and a bucket whose key
+    // is set never changes, so only buckets that look empty or foreign need the CAS.
+    for (uint64_t s = home(h, key);; s = next(h, s)) {
+        uint32_t* b = h.words + s * kBucketWords;
+        unsigned long long prev = __hip_atomic_load(reinterpret_cast<unsigned long long*>(b),
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == 0)
+            prev = atomicCAS(reinterpret_cast<unsigned long long*>(b), 0ull, (unsigned long long)key);
+        if (prev == 0 || prev == key) {
+            atomicMax(b + 2 + oct, (uint32_t)i + 1);
             return;
         }
-        s = (s + 1) & h.mask;
     }
 }
 
-__device__ __forceinline__ int32_t hash_find(const HashView& h, uint64_t key, int32_t miss) {
-    uint64_t s = slot_hash(key) & h.mask;
-    for (;;) {
-        const uint64_t k = h.keys[s];
-        if (k == key) return h.vals[s];
-        if (k == kEmptyKey) return miss;
-        s = (s + 1) & h.mask;
+// Bucket index of brick (bx, by, bz), or h.cap when it holds no voxel.
+__device__ __forceinline__ uint64_t find(const HashView& h, uint32_t bx, uint32_t by, uint32_t bz) {
+    const uint64_t key = brick_key(bx, by, bz);
+    for (uint64_t s = home(h, key);; s = next(h, s)) {
+        const uint64_t k = *reinterpret_cast<const uint64_t*>(h.words + s * kBucketWords);
+        if (k == key) return s;
+        if (k == 0) return h.cap;
     }
 }
 
-// Grid: x = runs of kProbeRows consecutive voxels, y = tap.
-constexpr int kProbeRows = 256;
+constexpr int kProbeThreads = 256;
 
-__global__ __launch_bounds__(kProbeRows) void k_probe(const int32_t* __restrict__ coords,
-                                                      int64_t n, HashView h,
-                                                      int32_t* __restrict__ nbr) {
-    const int64_t i = blockIdx.x * (int64_t)kProbeRows + threadIdx.x;
-    const int t = blockIdx.y;
+__global__ __launch_bounds__(kProbeThreads) void k_probe(const int32_t* __restrict__ coords,
+                                                         int64_t n, HashView h,
+                                                         int32_t* __restrict__ nbr) {
+    const int64_t i = blockIdx.x * (int64_t)kProbeThreads + threadIdx.x;
     if (i >= n) return;
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
     const int32_t miss = (int32_t)n;
-    int32_t r = miss;
-    if (x >= 0 && y >= 0 && z >= 0 && x <= kCoordMax && y <= kCoordMax && z <= kCoordMax) {
-        const int dx = t / 9 - 1, dy = (t / 3) % 3 - 1, dz = t % 3 - 1;
-        r = hash_find(h, pack_key(x + dx, y + dy, z + dz), miss);
+    if (!coords_ok(x, y, z)) {
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = miss;
+        return;
     }
-    nbr[(int64_t)t * n + i] = r;
+    const uint32_t X = x + 1, Y = y + 1, Z = z + 1;
+    // the 2x2x2 bricks holding the neighbourhood, from (bx, by, bz)
+    const uint32_t bx = (X - 1) >> 1, by = (Y - 1) >> 1, bz = (Z - 1) >> 1;
+    uint64_t bk[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) bk[c] = find(h, bx + (c & 1), by + ((c >> 1) & 1), bz + (c >> 2));
+    // brick of offset -1 / 0 / +1 along an axis: 0 / 1 - (X & 1) / 1
+    const int ex = 1 - (X & 1), ey = 1 - (Y & 1), ez = 1 - (Z & 1);
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) {
+        const int dx = t / 9 - 1, dy = (t / 3) % 3 - 1, dz = t % 3 - 1;
+        const int cx = dx < 0 ? 0 : dx > 0 ? 1 : ex;
+        const int cy = dy < 0 ? 0 : dy > 0 ? 1 : ey;
+        const int cz = dz < 0 ? 0 : dz > 0 ? 1 : ez;
+        const int c = cx | cy << 1 | cz << 2;
+        const int oct = ((X + dx) & 1) | ((Y + dy) & 1) << 1 | ((Z + dz) & 1) << 2;
+        uint64_t s = bk[0];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) s = c == k ? bk[k] : s;
+        uint32_t r = 0;
+        if (s != h.cap) r = h.words[s * kBucketWords + 2 + oct];
+        nbr[(int64_t)t * n + i] = r ? (int32_t)(r - 1) : miss;
+    }
 }
 
 __global__ void k_count_pairs(const int32_t* __restrict__ nbr, int64_t total, int32_t sentinel,
@@ -137,8 +159,7 @@ using namespace tsp;
 
 extern "C" size_t tsp_rulebook_workspace_bytes(int64_t n) {
     if (n < 0) return 0;
-    const uint64_t cap = table_capacity(n);
-    return align256(cap * 8) + align256(cap * 4);
+    return table_capacity(n) * kBucketWords * 4;
 }
 
 extern "C" int tsp_rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d_nbr,
@@ -154,15 +175,18 @@ extern "C" int tsp_rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d
                 "tsp_rulebook_build: workspace %zu < %zu bytes", workspace_bytes,
                 tsp_rulebook_workspace_bytes(n));
     hipStream_t s = as_stream(stream);
-    HashView h = carve(d_workspace, n);
-    const uint64_t cap = h.mask + 1;
-    const int clear_blocks = (int)std::min<uint64_t>(ceil_div((int64_t)cap, 256), 4096);
-    hipLaunchKernelGGL(k_hash_clear, dim3(clear_blocks), dim3(256), 0, s, h);
+    HashView h{reinterpret_cast<uint32_t*>(d_workspace), table_capacity(n)};
+    TSP_REQUIRE((reinterpret_cast<uintptr_t>(d_workspace) & 63) == 0, TSP_ERR_INVALID,
+                "tsp_rulebook_build: workspace must be 64-byte aligned");
+    const int64_t n16 = (int64_t)h.cap * (kBucketWords / 4);
+    const int clear_blocks = (int)std::min<int64_t>(ceil_div(n16, 256), 8192);
+    hipLaunchKernelGGL(k_hash_clear, dim3(clear_blocks), dim3(256), 0, s,
+                       reinterpret_cast<u32x4_t*>(d_workspace), n16);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_hash_insert, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s,
                        d_coords, n, h, d_status);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_probe, dim3((unsigned)ceil_div(n, kProbeRows), kTaps), dim3(kProbeRows),
+    hipLaunchKernelGGL(k_probe, dim3((unsigned)ceil_div(n, kProbeThreads)), dim3(kProbeThreads),
                        0, s, d_coords, n, h, d_nbr);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
