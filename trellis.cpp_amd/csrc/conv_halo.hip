@@ -305,11 +305,12 @@ template <int BN, int RB, int CB>
 constexpr int hb_waves() { return (HB_M / (32 * RB)) * (BN / (32 * CB)); }
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
-__device__ __forceinline__ void conv_tile(
+__device__ __forceinline__ void conv_tiles(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int n_ctiles, int64_t lin, uint16_t (&sH0)[2][HB_ROWS][8],
-    uint16_t (&sH1)[2][HB_ROWS][8], uint16_t (&sL)[kTaps][4][32][4], int* sRed);
+    void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
+    uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed);
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
@@ -333,150 +334,59 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
 
     // XCD-aware order: workgroup ids go round-robin over the 8 XCDs, so each XCD gets one
     // contiguous range of (tile, column-tile) pairs and gathers from rows its L2 already holds.
+    // The workgroups of an XCD walk its range with a stride of their count (a multiple of
+    // n_ctiles, so a workgroup keeps one column tile): with a stored plan the grid is one
+    // workgroup per CU, otherwise one workgroup per pair.
     const int64_t total = n_tiles * n_ctiles;
     const int xcd = (int)(blockIdx.x % 8);
     const int64_t xlo = xcd * per_xcd, xhi = xlo + per_xcd < total ? xlo + per_xcd : total;
-    const int64_t lin = xlo + blockIdx.x / 8;
-    if (lin >= xhi) return;
-    conv_tile<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, lin, sH0, sH1, sL, sRed);
+    conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, xlo + blockIdx.x / 8,
+        gridDim.x / 8, xhi, sH0, sH1, sL, sRed);
 }
 
-// One (tile, column tile) of the conv: the whole tile pipeline, run by all the workgroup's waves.
+// The tiles lin0, lin0 + stride, ... (< xhi) of one workgroup. With a stored plan and an even
+// number of slices, tiles are pipelined: the last slice of a tile streams the next tile's first
+// slice into the idle buffer, the first taps of its weights into the ring and its slot table into
+// registers, so the next tile starts without a memory round trip and its loads are in flight
+// before this tile's output stores.
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
-__device__ __forceinline__ void conv_tile(
+__device__ __forceinline__ void conv_tiles(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int n_ctiles, int64_t lin, uint16_t (&sH0)[2][HB_ROWS][8],
-    uint16_t (&sH1)[2][HB_ROWS][8], uint16_t (&sL)[kTaps][4][32][4], int* sRed) {
+    void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
+    uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed) {
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
     constexpr int WAVES = NRG * NCG;
     constexpr int NT = WAVES * 64;
     constexpr int WN = 32 * CB;              // output channels per wave
     constexpr int PIECES = 2 * HB_SLOTS / 64 / WAVES;   // slice loads per wave and slice
-    const int64_t tile = lin / n_ctiles;
-    const int64_t row0 = tile * HB_M;
+    constexpr int NSTG = (STG + SP - 1) / SP + 1;       // slice pieces in flight
+    constexpr int SLOT_BLOCKS = (HB_SLOT_TABLE * 2 / 1024 + WAVES - 1) / WAVES;   // 1 KiB each
+    constexpr int T_FREE = (PIECES - 1) * SP + STG + 1;   // first tap with the piece ring idle
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int r32 = lane & 31, g = lane >> 5;
-    const int rg = wave % NRG;               // row group: voxels [32 RB rg, +32 RB)
-    const int c0 = (int)(lin % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
+    const int wave = tid >> 6;
+    // lane-dependent values are re-defined (by an empty asm) at every tile, so that the
+    // compiler does not hoist the unrolled loops' per-tap addresses out of the tile loop and
+    // keep them all in registers
+    int lane = tid & 63;
+    int r32 = lane & 31, g = lane >> 5;
+    int rg = wave % NRG;                     // row group: voxels [32 RB rg, +32 RB)
+    const int c0 = (int)(lin0 % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
     const int nkc = ci / HB_KC;
-    // slice DMA: wave w streams plane (w & 1), 64-slot blocks (w >> 1) + (WAVES/2) j
-    const int plane = wave & 1;
+    // slice loads: wave w streams plane (w & 1), 64-slot blocks (w >> 1) + (WAVES/2) j
+    int plane = wave & 1;
     auto piece_slot = [&](int j) { return 64 * ((wave >> 1) + (WAVES / 2) * j); };
+    // cross-tile pipelining needs slices in pairs and the slot table in the idle piece ring
+    const bool pipelined = PLANNED && WAVES == 8 && SLOT_BLOCKS <= NSTG && T_FREE < kTaps &&
+                           nkc % 2 == 0;
 
-    // ---- tile plan: slot table in LDS, rows of this thread's slice pieces in registers
-    int H;
-    bool direct;
-    // byte offset (from feats) of the 8 channels this lane copies for each slice piece at
-    // slice 0: row * ci * 2 + plane * 16; slots past H copy row 0 into an unused slot
-    uint32_t poff[PIECES];
-    int32_t prow[PIECES];
-    // the bias of this lane's output channels, fetched now so the epilogue does not wait for it
+    // the bias of this lane's output channels (one column tile per workgroup)
     float bv[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) bv[cb] = bias[c0 + cb * 32 + r32];
-    if constexpr (PLANNED) {
-        // Header, slot table and piece rows are independent loads (every tile has a full-size
-        // slot table and row list in the plan), issued together so the prologue pays one
-        // memory round trip for them instead of two.
-        const int32_t* hdr = plan.hdr + tile * 4;
-        const int32_t h0 = hdr[0], h1 = hdr[1];
-        const char* src = reinterpret_cast<const char*>(plan.slots + tile * HB_SLOT_TABLE);
-        for (int p = wave; p < HB_SLOT_TABLE * 2 / 1024; p += WAVES)   // 27 x 1 KiB
-            __builtin_amdgcn_global_load_lds(
-                src + p * 1024 + lane * 16,
-                (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024),
-                16, 0, 0);
-        const int32_t* ro = plan.rowof + tile * HB_SLOTS;
-#pragma unroll
-        for (int j = 0; j < PIECES; ++j) prow[j] = ro[piece_slot(j) + lane];
-        H = h0;
-        direct = h1 != 0;
-        if (!direct) {
-#pragma unroll
-            for (int j = 0; j < PIECES; ++j)
-                if (piece_slot(j) + lane >= H) prow[j] = 0;
-#pragma unroll
-            for (int j = 0; j < PIECES; ++j) poff[j] = (uint32_t)prow[j] * (uint32_t)ci * 2u + plane * 16u;
-        }
-    } else {
-        tile_plan<NT>(nbr, n, row0, sL, reinterpret_cast<int32_t*>(&sH0[0][0][0]),
-                         reinterpret_cast<uint32_t*>(&sH1[0][0][0]), sRed, H, direct);
-        if (!direct) {
-            const int32_t* sRowOf = reinterpret_cast<const int32_t*>(&sH0[0][0][0]);
-#pragma unroll
-            for (int j = 0; j < PIECES; ++j) {
-                const int slot = piece_slot(j) + lane;
-                prow[j] = slot < H ? sRowOf[slot] : 0;
-                poff[j] = (uint32_t)prow[j] * (uint32_t)ci * 2u + plane * 16u;
-            }
-            __syncthreads();     // sH0 is overwritten by the first slice below
-        }
-    }
-
-    // Each path below owns its accumulators (zeroed there and passed to the epilogue): one set
-    // live across both paths would be zeroed in the lower registers and spilled.
-    auto zero = [](f32x16_t (&acc)[RB][CB]) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc[rb][cb][j] = 0.f;
-    };
-
-    // ---- epilogue: each wave stages 32-row blocks of its accumulators (fp32, + bias) in its own
-    // 32 RS bytes of the slice buffers, then writes whole row segments, 4 channels per lane. The
-    // row stride WN*4+32 bytes puts the two 32-lane halves of a staging write on disjoint banks.
-    // (The slice buffers are idle: every wave passed the last barrier of the main loop, or
-    // never used them on the direct path.)
-    auto epilogue = [&](f32x16_t (&acc)[RB][CB]) {
-        constexpr int RS = WN * 4 + 32;
-        static_assert((WAVES / 2) * 32 * RS <= (int)sizeof(sH0), "staging must fit a slice buffer");
-        char* stage = reinterpret_cast<char*>(wave < WAVES / 2 ? &sH0[0][0][0] : &sH1[0][0][0]) +
-                      (wave % (WAVES / 2)) * 32 * RS;
-        const bool full = row0 + HB_M <= n;   // no row of the tile is past n (uniform)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int r = 8 * (j / 4) + 4 * g + (j % 4);
-                    *reinterpret_cast<float*>(stage + r * RS + (cb * 32 + r32) * 4) = acc[rb][cb][j] + bv[cb];
-                }
-            // 32 rows x WN/4 chunks of 4 channels: all LDS reads first (one wait), then the stores
-            f32x4_t vs[WN / 8];
-#pragma unroll
-            for (int q = 0; q < WN / 8; ++q) {
-                const int c = q * 64 + lane;
-                vs[q] = *reinterpret_cast<const f32x4_t*>(stage + (c / (WN / 4)) * RS + (c % (WN / 4)) * 16);
-            }
-#pragma unroll
-            for (int q = 0; q < WN / 8; ++q) {
-                const int c = q * 64 + lane;
-                const int r = c / (WN / 4), cq = c % (WN / 4);
-                const f32x4_t v = vs[q];
-                const int64_t i = row0 + 32 * RB * rg + 32 * rb + r;
-                if (full || i < n) {
-                    const int64_t o = i * co + c0 + cq * 4;
-                    if constexpr (ODT == TSP_F32) {
-                        *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + o) = v;
-                    } else {
-                        uint16_t h[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            h[e] = (ODT == TSP_BF16) ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
-                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) =
-                            uint2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
-                    }
-                }
-            }
-        }
-    };
 
     // weights of (tap t, slice kc), column block cb of this wave
     uint32_t boff[CB];
@@ -503,130 +413,349 @@ __device__ __forceinline__ void conv_tile(
         }
     };
 
-    if (!direct) {
-        f32x16_t acc[RB][CB];
-        zero(acc);
-        // Slice pieces go through registers: a 16-byte global load per lane at tap t, its LDS
-        // write at tap t + STG. (A direct-to-LDS DMA would be hidden from the compiler's wait
-        // counting -- it then waits for each DMA right after issuing it, because it cannot tell
-        // the DMA's LDS store from the reads that follow -- while plain loads are counted exactly
-        // and the slice boundary need not wait for the weight loads still in flight.) The zero
-        // slot lies past the loaded slots and is never overwritten.
-        constexpr int NSTG = (STG + SP - 1) / SP + 1;   // pieces in flight
-        u32x4_t stg[NSTG];
-        auto fetch_piece = [&](int kc, int j, u32x4_t& r) {
-            r = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(feats) + poff[j] +
-                                                  (uint32_t)kc * (HB_KC * 2));
-        };
-        auto put_piece = [&](uint16_t (*dst)[HB_ROWS][8], int j, const u32x4_t& r) {
-            *reinterpret_cast<u32x4_t*>(&dst[plane][piece_slot(j) + lane][0]) = r;
-        };
-        // A operands of tap t: per 128 voxels one 8-byte read of four slots, then one 16-byte
-        // read per 32-row block
-        auto load_a = [&](const uint16_t (*cur)[HB_ROWS][8], int t, u32x4_t* a) {
-#pragma unroll
-            for (int q = 0; q < RB / 4; ++q) {
-                const uint2 sl = *reinterpret_cast<const uint2*>(&sL[t][(RB / 4) * rg + q][r32][0]);
-                const int slots[4] = {(int)(sl.x & 0xffffu), (int)(sl.x >> 16),
-                                      (int)(sl.y & 0xffffu), (int)(sl.y >> 16)};
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    a[4 * q + k] = *reinterpret_cast<const u32x4_t*>(&cur[g][slots[k]][0]);
-            }
-        };
-
-        // Vector-memory loads return in issue order, so waiting for a weight load also waits
-        // for every slice DMA issued before it: the weights run PD taps ahead and the slice
-        // pieces go out every SP-th tap, which leaves each piece >= PD+1 taps to land. The
-        // weight ring has PD+1 slots indexed by tap; PD+1 must divide 27 so that the ring
-        // index continues across slices with compile-time register indices.
-        static_assert((2 * kTaps) % (PD + 1) == 0, "weight ring must divide 2 x 27 taps");
-        static_assert(PIECES * SP <= kTaps, "slice pieces must fit in one slice's taps");
-        static_assert((PIECES - 1) * SP + STG < kTaps, "every staged piece is written within its slice");
-        // zero slot of both buffers and planes (the barrier below publishes it)
-        if (tid < 4) {
-            u32x4_t z{0, 0, 0, 0};
-            asm volatile("" : "+v"(z));   // made here, not held in registers across tiles
-            *reinterpret_cast<u32x4_t*>(tid < 2 ? &sH0[tid & 1][HB_ZERO][0] : &sH1[tid & 1][HB_ZERO][0]) = z;
-        }
+    // byte offset (from feats) of the 8 channels this lane copies for each slice piece at
+    // slice 0: row * ci * 2 + plane * 16; slots past H copy row 0 into an unused slot
+    uint32_t poff[PIECES];
+    auto set_poff = [&](int32_t (&prow)[PIECES], int H) {
 #pragma unroll
         for (int j = 0; j < PIECES; ++j) {
-            u32x4_t r;
-            fetch_piece(0, j, r);
-            put_piece(sH0, j, r);
+            const int32_t r = (piece_slot(j) + lane < H && (uint32_t)prow[j] < (uint32_t)n) ? prow[j] : 0;
+            poff[j] = (uint32_t)r * (uint32_t)ci * 2u + plane * 16u;
+            // kept as 32-bit offsets for the scalar-base + vector-offset load form
+            asm volatile("" : "+v"(poff[j]));
         }
-        u32x4_t bR[PD + 1][CB];
+    };
+    auto fetch_piece = [&](int kc, int j, u32x4_t& r) {
+        r = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(feats) + poff[j] +
+                                              (uint32_t)kc * (HB_KC * 2));
+    };
+    auto put_piece = [&](uint16_t (*dst)[HB_ROWS][8], int j, const u32x4_t& r) {
+        *reinterpret_cast<u32x4_t*>(&dst[plane][piece_slot(j) + lane][0]) = r;
+    };
+    // A operands of tap t: per 128 voxels one 8-byte read of four slots, then one 16-byte
+    // read per 32-row block
+    auto load_a = [&](const uint16_t (*cur)[HB_ROWS][8], int t, u32x4_t* a) {
 #pragma unroll
-        for (int q = 0; q < PD; ++q) load_b(q, 0, bR[q]);
-        wait_vmcnt0();
-        __syncthreads();
+        for (int q = 0; q < RB / 4; ++q) {
+            const uint2 sl = *reinterpret_cast<const uint2*>(&sL[t][(RB / 4) * rg + q][r32][0]);
+            const int slots[4] = {(int)(sl.x & 0xffffu), (int)(sl.x >> 16),
+                                  (int)(sl.y & 0xffffu), (int)(sl.y >> 16)};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                a[4 * q + k] = *reinterpret_cast<const u32x4_t*>(&cur[g][slots[k]][0]);
+        }
+    };
+    // zero slot of both planes of a buffer (a barrier before its first read publishes it)
+    auto zero_slot = [&](uint16_t (*buf)[HB_ROWS][8]) {
+        if (tid < 2) {
+            u32x4_t z{0, 0, 0, 0};
+            asm volatile("" : "+v"(z));   // made here, not held in registers across tiles
+            *reinterpret_cast<u32x4_t*>(&buf[tid][HB_ZERO][0]) = z;
+        }
+    };
+    // Each path below owns its accumulators (zeroed there and passed to the epilogue): one set
+    // live across both paths would be zeroed in the lower registers and spilled.
+    auto zero = [](f32x16_t (&acc)[RB][CB]) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[rb][cb][j] = 0.f;
+    };
 
-        // one slice: all 27 taps on `cur` while slice kcn streams into `nxt` (the last slice
-        // re-loads itself into the idle buffer, so there is no branch here either)
-        // R0: the weight ring's slot of this slice's tap 0 (slices go in pairs, so a ring size
-        // that divides 2 x 27 keeps every register index static)
-        auto run_slice = [&](auto ring0, const uint16_t (*cur)[HB_ROWS][8], uint16_t (*nxt)[HB_ROWS][8],
-                             int kc, int kcn) {
-            constexpr int R0 = decltype(ring0)::value;
-            u32x4_t aC[RB], aN[RB];
-            load_a(cur, 0, aC);
-            // all 27 taps unrolled: register rings stay static and every wait is exact
+    // ---- epilogue: each wave stages row blocks of its accumulators (fp32, + bias) in its own part
+    // of the slice buffers (idle: every wave passed the last barrier of the main loop, or never
+    // used them on the direct path), then writes whole row segments, 16 bytes per lane. The row
+    // stride WN*4+32 bytes puts the two 32-lane halves of a staging write on disjoint banks.
+    // NR rows at a time: 32 over both buffers, or 16 in sH1 alone while sH0 holds the next
+    // tile's first slice.
+    auto epilogue = [&](auto nr_c, f32x16_t (&acc)[RB][CB], int64_t row0) {
+        constexpr int NR = decltype(nr_c)::value;
+        constexpr int RS = WN * 4 + 32;
+        static_assert(NR == 32 || NR == 16, "row rounds of 32 or 16");
+        static_assert((NR == 32 ? WAVES / 2 : WAVES) * NR * RS <= (int)sizeof(sH0),
+                      "staging must fit a slice buffer");
+        char* stage = NR == 32 ? reinterpret_cast<char*>(wave < WAVES / 2 ? &sH0[0][0][0] : &sH1[0][0][0]) +
+                                     (wave % (WAVES / 2)) * 32 * RS
+                               : reinterpret_cast<char*>(&sH1[0][0][0]) + wave * 16 * RS;
+        const bool full = row0 + HB_M <= n;   // no row of the tile is past n (uniform)
+        constexpr int CH = ODT == TSP_F32 ? 4 : 8;     // channels per 16-byte store
+        constexpr int NQ = NR * (WN / CH) / 64;        // stores per lane and round
+        static_assert(NR * (WN / CH) % 64 == 0, "whole stores per lane");
 #pragma unroll
-            for (int t = 0; t < kTaps; ++t) {
-                // weights PD taps ahead (the first taps of the next slice at the end)
-                if (t + PD < kTaps) load_b(t + PD, kc, bR[(R0 + t + PD) % (PD + 1)]);
-                else load_b(t + PD - kTaps, kcn, bR[(R0 + t + PD) % (PD + 1)]);
-                if (t % SP == 0 && t / SP < PIECES) fetch_piece(kcn, t / SP, stg[(t / SP) % NSTG]);
-                if (t >= STG && (t - STG) % SP == 0 && (t - STG) / SP < PIECES)
-                    put_piece(nxt, (t - STG) / SP, stg[((t - STG) / SP) % NSTG]);
-                if (t + 1 < kTaps) load_a(cur, t + 1, aN);
+        for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
+            for (int h = 0; h < 32 / NR; ++h) {
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb)
-                        acc[rb][cb] = mfma32x32x16<BF16>(aC[rb], bR[(R0 + t) % (PD + 1)][cb], acc[rb][cb]);
+                for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) aC[rb] = aN[rb];
-                // keep each tap's loads in its tap: unconstrained, the scheduler gathers the
-                // slice DMAs at the end of the slice, where their latency is fully exposed
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            __syncthreads();
-        };
-        for (int kc = 0; kc < nkc; kc += 2) {
-            const int k1 = kc + 1 < nkc ? kc + 1 : kc;
-            run_slice(std::integral_constant<int, 0>{}, sH0, sH1, kc, k1);
-            if (kc + 1 < nkc)
-                run_slice(std::integral_constant<int, kTaps % (PD + 1)>{}, sH1, sH0, kc + 1,
-                          kc + 2 < nkc ? kc + 2 : kc + 1);
-        }
-        epilogue(acc);
-    } else {
-        f32x16_t acc[RB][CB];
-        zero(acc);
-        // ---- direct path: A gathered from global memory
-        for (int kc = 0; kc < nkc; ++kc)
-            for (int t = 0; t < kTaps; ++t) {
-                u32x4_t bq[CB];
-                load_b(t, kc, bq);
-                u32x4_t a[RB];
+                    for (int j = 16 * h * NR / 32; j < 16 * (h + 1) * NR / 32; ++j) {
+                        const int r = 8 * (j / 4) + 4 * g + (j % 4) - NR * h;
+                        *reinterpret_cast<float*>(stage + r * RS + (cb * 32 + r32) * 4) = acc[rb][cb][j] + bv[cb];
+                    }
+                // NR rows x WN/CH chunks: all LDS reads first (one wait), then the stores
+                f32x4_t vs[NQ][CH / 4];
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) {
-                    const int64_t i = row0 + 32 * RB * rg + 32 * rb + r32;
-                    const int32_t v = (i < n) ? nbr[(int64_t)t * n + i] : (int32_t)n;
-                    a[rb] = u32x4_t{0, 0, 0, 0};
-                    if ((uint32_t)v < (uint32_t)n)
-                        a[rb] = *reinterpret_cast<const u32x4_t*>(feats + (int64_t)v * ci +
-                                                                  kc * HB_KC + g * 8);
+                for (int q = 0; q < NQ; ++q) {
+                    const int c = q * 64 + lane;
+                    const char* p = stage + (c / (WN / CH)) * RS + (c % (WN / CH)) * (CH * 4);
+#pragma unroll
+                    for (int e = 0; e < CH / 4; ++e) vs[q][e] = *reinterpret_cast<const f32x4_t*>(p + 16 * e);
                 }
 #pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                    const int c = q * 64 + lane;
+                    const int r = c / (WN / CH), cq = c % (WN / CH);
+                    const int64_t i = row0 + 32 * RB * rg + 32 * rb + NR * h + r;
+                    if (full || i < n) {
+                        const int64_t o = i * co + c0 + cq * CH;
+                        if constexpr (ODT == TSP_F32) {
+                            *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + o) = vs[q][0];
+                        } else {
+                            uint32_t w[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const float lo = vs[q][e / 2][(2 * e) % 4], hi = vs[q][e / 2][(2 * e) % 4 + 1];
+                                const uint32_t a = (ODT == TSP_BF16) ? f32_to_bf16_bits(lo) : f32_to_f16_bits(lo);
+                                const uint32_t b = (ODT == TSP_BF16) ? f32_to_bf16_bits(hi) : f32_to_f16_bits(hi);
+                                w[e] = a | (b << 16);
+                            }
+                            *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + o) =
+                                u32x4_t{w[0], w[1], w[2], w[3]};
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    // Vector-memory loads return in issue order, so waiting for a weight load also waits for
+    // every slice piece issued before it: the weights run PD taps ahead and the slice pieces go
+    // out every SP-th tap, which leaves each piece >= PD+1 taps to land. The weight ring has
+    // PD+1 slots indexed by tap; PD+1 must divide 2 x 27 so that the ring index continues
+    // across slice pairs with compile-time register indices.
+    static_assert((2 * kTaps) % (PD + 1) == 0, "weight ring must divide 2 x 27 taps");
+    static_assert(PIECES * SP <= kTaps, "slice pieces must fit in one slice's taps");
+    static_assert((PIECES - 1) * SP + STG < kTaps, "every staged piece is written within its slice");
+
+    // prologue state: the current tile's plan is in sL, its first slice in sH0 and the weights
+    // of its first PD taps in the ring (set by the previous tile's last slice when pipelined)
+    bool pre = false;
+    int H = 0;
+    bool direct = false;
+    u32x4_t bR[PD + 1][CB];
+
+    for (int64_t lin = lin0; lin < xhi; lin += stride) {
+        asm volatile("" : "+v"(lane), "+v"(r32), "+v"(g), "+v"(rg), "+v"(plane));
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) asm volatile("" : "+v"(boff[cb]));
+        const int64_t tile = lin / n_ctiles;
+        const int64_t row0 = tile * HB_M;
+        if (!pre) {
+            // ---- tile plan: slot table in LDS, rows of this thread's slice pieces in registers
+            int32_t prow[PIECES];
+            if constexpr (PLANNED) {
+                // Header, slot table and piece rows are independent loads (every tile has a
+                // full-size slot table and row list in the plan), issued together so the
+                // prologue pays one memory round trip for them instead of two.
+                const int32_t* hdr = plan.hdr + tile * 4;
+                const int32_t h0 = hdr[0], h1 = hdr[1];
+                const char* src = reinterpret_cast<const char*>(plan.slots + tile * HB_SLOT_TABLE);
+                for (int p = wave; p < HB_SLOT_TABLE * 2 / 1024; p += WAVES)   // 27 x 1 KiB
+                    __builtin_amdgcn_global_load_lds(
+                        src + p * 1024 + lane * 16,
+                        (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024),
+                        16, 0, 0);
+                const int32_t* ro = plan.rowof + tile * HB_SLOTS;
+#pragma unroll
+                for (int j = 0; j < PIECES; ++j) prow[j] = ro[piece_slot(j) + lane];
+                H = h0;
+                direct = h1 != 0;
+            } else {
+                tile_plan<NT>(nbr, n, row0, sL, reinterpret_cast<int32_t*>(&sH0[0][0][0]),
+                              reinterpret_cast<uint32_t*>(&sH1[0][0][0]), sRed, H, direct);
+                const int32_t* sRowOf = reinterpret_cast<const int32_t*>(&sH0[0][0][0]);
+#pragma unroll
+                for (int j = 0; j < PIECES; ++j) prow[j] = direct ? 0 : sRowOf[(piece_slot(j) + lane) % HB_SLOTS];
+                __syncthreads();     // sH0 is overwritten by the first slice below
+            }
+            if (!direct) {
+                set_poff(prow, H);
+                zero_slot(sH0);
+                zero_slot(sH1);
+#pragma unroll
+                for (int j = 0; j < PIECES; ++j) {
+                    u32x4_t r;
+                    fetch_piece(0, j, r);
+                    put_piece(sH0, j, r);
+                }
+#pragma unroll
+                for (int q = 0; q < PD; ++q) load_b(q, 0, bR[q]);
+                wait_vmcnt0();
+                __syncthreads();
+            }
+        }
+        if (!direct) {
+            // Slice pieces go through registers: a 16-byte global load per lane at tap t, its
+            // LDS write at tap t + STG. (A direct-to-LDS DMA would be hidden from the compiler's
+            // wait counting -- it then waits for each DMA right after issuing it, because it
+            // cannot tell the DMA's LDS store from the reads that follow -- while plain loads are
+            // counted exactly and the slice boundary need not wait for the weight loads still in
+            // flight.) The zero slot lies past the loaded slots and is never overwritten.
+            u32x4_t stg[NSTG];
+
+            // one slice: all 27 taps on `cur` while slice kcn streams into `nxt`
+            // R0: the weight ring's slot of this slice's tap 0 (slices go in pairs, so a ring
+            // size that divides 2 x 27 keeps every register index static). With LAST, the piece
+            // ring, once idle, loads the next tile's slot table (this wave's 1 KiB blocks).
+            auto run_slice = [&](f32x16_t (&acc)[RB][CB], auto ring0, auto last_c,
+                                 const uint16_t (*cur)[HB_ROWS][8], uint16_t (*nxt)[HB_ROWS][8], int kc,
+                                 int kcn, const uint16_t* nslots) {
+                constexpr int R0 = decltype(ring0)::value;
+                constexpr bool LAST = decltype(last_c)::value;
+                u32x4_t aC[RB], aN[RB];
+                load_a(cur, 0, aC);
+                // all 27 taps unrolled: register rings stay static and every wait is exact
+#pragma unroll
+                for (int t = 0; t < kTaps; ++t) {
+                    // weights PD taps ahead (the first taps of the next slice at the end)
+                    if (t + PD < kTaps) load_b(t + PD, kc, bR[(R0 + t + PD) % (PD + 1)]);
+                    else load_b(t + PD - kTaps, kcn, bR[(R0 + t + PD) % (PD + 1)]);
+                    if (t % SP == 0 && t / SP < PIECES) fetch_piece(kcn, t / SP, stg[(t / SP) % NSTG]);
+                    if (t >= STG && (t - STG) % SP == 0 && (t - STG) / SP < PIECES)
+                        put_piece(nxt, (t - STG) / SP, stg[((t - STG) / SP) % NSTG]);
+                    if constexpr (LAST) {
+                        if (t == T_FREE) {
+                            // blocks wave + WAVES k of the next tile's slot table (the last
+                            // block again where this wave has fewer)
+#pragma unroll
+                            for (int k = 0; k < SLOT_BLOCKS; ++k) {
+                                const int p = min(wave + WAVES * k, HB_SLOT_TABLE * 2 / 1024 - 1);
+                                stg[k] = *reinterpret_cast<const u32x4_t*>(
+                                    reinterpret_cast<const char*>(nslots) + p * 1024 + lane * 16);
+                            }
+                        }
+                    }
+                    if (t + 1 < kTaps) load_a(cur, t + 1, aN);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb)
+                            acc[rb][cb] = mfma32x32x16<BF16>(aC[rb], bR[(R0 + t) % (PD + 1)][cb], acc[rb][cb]);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) aC[rb] = aN[rb];
+                    // keep each tap's loads in its tap: unconstrained, the scheduler gathers the
+                    // slice loads at the end of the slice, where their latency is fully exposed
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // The accumulators are final here: without this use, the compiler may sink a
+                // slice's MFMA chains past the barrier toward the epilogue that reads them,
+                // keeping every tap's A operands alive (and spilled) until then. (An input
+                // operand only: redefining the registers here would hide from the hazard
+                // recognizer that the epilogue's reads follow MFMA writes.)
+#pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb)
-                        acc[rb][cb] = mfma32x32x16<BF16>(a[rb], bq[cb], acc[rb][cb]);
+                    for (int cb = 0; cb < CB; ++cb) asm volatile("" ::"v"(acc[rb][cb]));
+                __syncthreads();
+            };
+            using I0 = std::integral_constant<int, 0>;
+            using I1 = std::integral_constant<int, kTaps % (PD + 1)>;
+            using NO = std::false_type;
+            if (pipelined) {
+                f32x16_t acc[RB][CB];
+                zero(acc);
+                for (int kc = 0; kc + 2 < nkc; kc += 2) {
+                    run_slice(acc, I0{}, NO{}, sH0, sH1, kc, kc + 1, nullptr);
+                    run_slice(acc, I1{}, NO{}, sH1, sH0, kc + 1, kc + 2, nullptr);
+                }
+                // the next tile of this workgroup (this one again after the last: its loads are
+                // then only unused copies)
+                const int64_t nlin = lin + stride < xhi ? lin + stride : lin;
+                const int64_t ntile = nlin / n_ctiles;
+                const int32_t* nhdr = plan.hdr + ntile * 4;
+                const int32_t nH = nhdr[0], ndirect = nhdr[1];
+                int32_t nrow[PIECES];
+                const int32_t* nro = plan.rowof + ntile * HB_SLOTS;
+#pragma unroll
+                for (int j = 0; j < PIECES; ++j) nrow[j] = nro[piece_slot(j) + lane];
+                run_slice(acc, I0{}, NO{}, sH0, sH1, nkc - 2, nkc - 1, nullptr);
+                // the last slice streams the next tile's slice 0 (rows clamped to 0 where the
+                // plan holds none, e.g. a direct tile) and the first taps of its weights
+                if (ndirect) nrow[0] = 0;
+                set_poff(nrow, ndirect ? 0 : nH);
+                run_slice(acc, I1{}, std::true_type{}, sH1, sH0, nkc - 1, 0, plan.slots + ntile * HB_SLOT_TABLE);
+                // every wave is past its last read of sL and sH1
+#pragma unroll
+                for (int k = 0; k < SLOT_BLOCKS; ++k) {
+                    const int p = wave + WAVES * k;
+                    if (p < HB_SLOT_TABLE * 2 / 1024)
+                        *reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024 + lane * 16) = stg[k];
+                }
+                epilogue(std::integral_constant<int, 16>{}, acc, row0);
+                __syncthreads();       // the next tile's slot table; every wave's staging is done
+                zero_slot(sH1);        // the staging covered it; first read after the next barrier
+                pre = nlin != lin && !ndirect;
+                H = nH;
+                direct = ndirect != 0;
+            } else {
+                f32x16_t acc[RB][CB];
+                zero(acc);
+                // the last slice re-loads itself into the idle buffer, so there is no branch
+                for (int kc = 0; kc < nkc; kc += 2) {
+                    const int k1 = kc + 1 < nkc ? kc + 1 : kc;
+                    run_slice(acc, I0{}, NO{}, sH0, sH1, kc, k1, nullptr);
+                    if (kc + 1 < nkc)
+                        run_slice(acc, I1{}, NO{}, sH1, sH0, kc + 1, kc + 2 < nkc ? kc + 2 : kc + 1, nullptr);
+                }
+                epilogue(std::integral_constant<int, 32>{}, acc, row0);
+                __syncthreads();       // staging reads end before the next tile's loads
+                pre = false;
             }
-        epilogue(acc);
+        } else {
+            f32x16_t acc[RB][CB];
+            zero(acc);
+            // ---- direct path: A gathered from global memory
+            for (int kc = 0; kc < nkc; ++kc)
+                for (int t = 0; t < kTaps; ++t) {
+                    u32x4_t bq[CB];
+                    load_b(t, kc, bq);
+                    u32x4_t a[RB];
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) {
+                        const int64_t i = row0 + 32 * RB * rg + 32 * rb + r32;
+                        const int32_t v = (i < n) ? nbr[(int64_t)t * n + i] : (int32_t)n;
+                        a[rb] = u32x4_t{0, 0, 0, 0};
+                        if ((uint32_t)v < (uint32_t)n)
+                            a[rb] = *reinterpret_cast<const u32x4_t*>(feats + (int64_t)v * ci +
+                                                                      kc * HB_KC + g * 8);
+                    }
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb)
+                            acc[rb][cb] = mfma32x32x16<BF16>(a[rb], bq[cb], acc[rb][cb]);
+                }
+            epilogue(std::integral_constant<int, 32>{}, acc, row0);
+            __syncthreads();           // staging reads end before the next tile's loads
+            pre = false;
+        }
     }
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
 }
 
 template <bool BF16, int BN, int ODT, bool PLANNED>
@@ -641,8 +770,15 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
     // 8 waves of 128 voxels x BN/2 channels; weights 2 taps ahead; a slice piece every other
     // tap, written to LDS 6 taps after its load
     constexpr int RB = 4, CB = BN / 64, PD = 2, SP = 2, STG = 6;
+    // With a plan: one workgroup per CU (the LDS of one fills a CU), a multiple of n_ctiles per
+    // XCD. Without: one per (tile, column tile), each building its own plan.
+    int64_t per_xcd_wg = per_xcd;
+    if (PLANNED) {
+        const int64_t fit = std::max<int64_t>(1, cu_count() / 8 / n_ctiles) * n_ctiles;
+        per_xcd_wg = std::min(per_xcd, fit);
+    }
     hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>),
-                       dim3((unsigned)(per_xcd * 8)), dim3(hb_waves<BN, RB, CB>() * 64), 0, s,
+                       dim3((unsigned)(per_xcd_wg * 8)), dim3(hb_waves<BN, RB, CB>() * 64), 0, s,
                        reinterpret_cast<const uint16_t*>(feats), n, ci,
                        nbr, pv, reinterpret_cast<const uint16_t*>(weight), bias, co, out, n_tiles,
                        n_ctiles, per_xcd);
