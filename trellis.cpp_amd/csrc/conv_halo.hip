@@ -114,9 +114,10 @@ __device__ int scan_popcounts(const uint32_t* words, int nwords, int32_t* pre, i
 
 // Fills sL with the slot of every (tap, voxel) of tile row0 and sRowOf with the row of every
 // slot; returns H (number of distinct rows) and whether the tile must take the direct path.
-// The set of referenced rows is ranked with a two-level bitmap over [lo, hi]: a coarse bit per
-// 32-row block (spans up to 2^21 rows), then one fine word per non-empty block; slot = fine
-// prefix of the block + rank inside the block's word.
+// The set of referenced rows is ranked with a bitmap over [lo, hi]: one fine word per 32 rows
+// when the span is at most 32 * HB_SLOTS rows, otherwise two levels -- a coarse bit per 32-row
+// block (spans up to 2^21 rows), then one fine word per non-empty block. slot = prefix of the
+// fine word + rank inside the word.
 // scratch: HB_PLAN_SCRATCH words; sRed: 2 * NT/64 ints.
 template <int NT>
 __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t row0,
@@ -169,7 +170,16 @@ __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t ro
     for (int w = 0; w < NW; ++w) { lo = min(lo, sRed[w]); hi = max(hi, sRed[NW + w]); }
     __syncthreads();
     bool direct = hi >= 0 && (int64_t)hi - lo + 1 > HB_MAXSPAN;
-    int H = 0, nblocks = 0;
+    // One level when the rows span at most 32 * HB_SLOTS (the usual case for sorted sets: a
+    // tile's neighbours lie in three x-planes): the fine word of row d is d >> 5 directly.
+    const bool one = hi >= 0 && (int64_t)hi - lo + 1 <= 32 * HB_SLOTS;
+    int H = 0, nfine = 0;
+    // fine word of row offset d (two levels: the rank of d's 32-row block among the referenced ones)
+    auto fine_word = [&](int d) -> int {
+        if (one) return d >> 5;
+        const int cw = d >> 10, cb = (d >> 5) & 31;
+        return cpre[cw] + (int)__popc(coarse[cw] & ((1u << cb) - 1u));
+    };
 
     if (!direct && hi >= 0) {
 #pragma unroll
@@ -178,20 +188,38 @@ __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t ro
             fine[tid * WPT + k] = 0u;
         }
         __syncthreads();
-        // level 1: which 32-row blocks are referenced
+        if (one) {
+            nfine = HB_SLOTS;
+        } else {
+            // level 1: which 32-row blocks are referenced
 #pragma unroll
-        for (int t = 0; t < kTaps; ++t)
+            for (int t = 0; t < kTaps; ++t)
 #pragma unroll
-            for (int h = 0; h < VPT; ++h) {
-                const int32_t v = nv[t][h];
-                if (v >= 0) {
-                    const int d = v - lo;
-                    atomicOr(&coarse[d >> 10], 1u << ((d >> 5) & 31));
+                for (int h = 0; h < VPT; ++h) {
+                    const int32_t v = nv[t][h];
+                    if (v >= 0) {
+                        const int d = v - lo;
+                        atomicOr(&coarse[d >> 10], 1u << ((d >> 5) & 31));
+                    }
+                }
+            __syncthreads();
+            nfine = scan_popcounts<NT>(coarse, HB_SLOTS, cpre, sRed);
+            direct = nfine > HB_ZERO;      // every block holds a row: too many rows for LDS
+            if (!direct) {
+                // rank -> block id
+#pragma unroll
+                for (int k = 0; k < WPT; ++k) {
+                    const int w = tid * WPT + k;
+                    uint32_t bits = coarse[w];
+                    int r = cpre[w];
+                    while (bits) {
+                        const int bit = __builtin_ctz(bits);
+                        bits &= bits - 1u;
+                        block_of[r++] = w * 32 + bit;
+                    }
                 }
             }
-        __syncthreads();
-        nblocks = scan_popcounts<NT>(coarse, HB_SLOTS, cpre, sRed);
-        direct = nblocks > HB_ZERO;        // every block holds a row: too many rows for LDS
+        }
         if (!direct) {
             // level 2: rows within each referenced block
 #pragma unroll
@@ -200,25 +228,12 @@ __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t ro
                 for (int h = 0; h < VPT; ++h) {
                     const int32_t v = nv[t][h];
                     if (v >= 0) {
-                        const int d = v - lo, cw = d >> 10, cb = (d >> 5) & 31;
-                        const int blk = cpre[cw] + __popc(coarse[cw] & ((1u << cb) - 1u));
-                        atomicOr(&fine[blk], 1u << (d & 31));
+                        const int d = v - lo;
+                        atomicOr(&fine[fine_word(d)], 1u << (d & 31));
                     }
                 }
-            // rank -> block id
-#pragma unroll
-            for (int k = 0; k < WPT; ++k) {
-                const int w = tid * WPT + k;
-                uint32_t bits = coarse[w];
-                int r = cpre[w];
-                while (bits) {
-                    const int bit = __builtin_ctz(bits);
-                    bits &= bits - 1u;
-                    block_of[r++] = w * 32 + bit;
-                }
-            }
             __syncthreads();
-            H = scan_popcounts<NT>(fine, nblocks, fpre, sRed);
+            H = scan_popcounts<NT>(fine, nfine, fpre, sRed);
             direct = H > HB_ZERO;
         }
     }
@@ -232,9 +247,8 @@ __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t ro
                 const int32_t v = nv[t][h];
                 int slot = HB_ZERO;
                 if (v >= 0) {
-                    const int d = v - lo, cw = d >> 10, cb = (d >> 5) & 31;
-                    const int blk = cpre[cw] + __popc(coarse[cw] & ((1u << cb) - 1u));
-                    slot = fpre[blk] + __popc(fine[blk] & ((1u << (d & 31)) - 1u));
+                    const int d = v - lo, fw = fine_word(d);
+                    slot = fpre[fw] + __popc(fine[fw] & ((1u << (d & 31)) - 1u));
                 }
                 sL[t][rr >> 7][rr & 31][(rr >> 5) & 3] = (uint16_t)slot;
             }
@@ -242,10 +256,10 @@ __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t ro
 #pragma unroll
         for (int k = 0; k < WPT; ++k) {
             const int w = tid * WPT + k;
-            if (w < nblocks) {
+            if (w < nfine) {
                 uint32_t bits = fine[w];
                 int s = fpre[w];
-                const int base = lo + block_of[w] * 32;
+                const int base = lo + (one ? w : block_of[w]) * 32;
                 while (bits) {
                     const int bit = __builtin_ctz(bits);
                     bits &= bits - 1u;
