@@ -11,6 +11,9 @@ the reference's tap-sequential fp32 algorithm) timed on this host's cores over a
 sample of the same workload.
 
     python bench.py [--steps 50] [--warmup 5] [--workload shells256-c128-bf16]
+
+`--workload decoder-shells64-c1024` times the whole texture decoder stack instead (one decode
+per step, through the C++ host library): see trellis_cpp_amd.shells.decoder_workload.
 """
 from __future__ import annotations
 
@@ -92,6 +95,123 @@ def cpu_baseline(w, nbr, budget_s: float):
     }
 
 
+def decoder_bench(args) -> dict:
+    """The texture decoder stack (trellis::tex_decode through the C++ host library) on a
+    synthetic decoder workload: random-init bf16 weights written to a GGUF under the reference's
+    key names, latent and subdivision masks as .npy files; host/bin/decoder_bench times
+    whole decodes (host inputs in, host output back, as the reference's API has it)."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    pkg = load_package()
+    import trellis_cpp_amd.shells as shells
+    from trellis_cpp_amd.gguf_writer import write as write_gguf
+
+    w = shells.decoder_workload(args.workload)
+    exe = os.path.join(ROOT, "trellis.cpp_amd", "host", "bin", "decoder_bench")
+    if not os.path.exists(exe):
+        raise SystemExit(f"{exe} is not built (make -C trellis.cpp_amd/host)")
+    p = shells.decoder_params(w.channels, w.blocks, w.latent.shape[1], w.out_ch, w.std, w.seed)
+    with tempfile.TemporaryDirectory(prefix="decoder_bench_", dir="/tmp") as d:
+        write_gguf(os.path.join(d, "model.gguf"), p,
+                   dtypes={k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()},
+                   arch="trellis2-tex-dec")
+        del p
+        np.save(os.path.join(d, "latent.npy"), w.latent)
+        np.save(os.path.join(d, "coords.npy"), np.ascontiguousarray(w.coords, np.int32))
+        for s, m in enumerate(w.masks):
+            np.save(os.path.join(d, f"subs_{s}.npy"), np.ascontiguousarray(m, np.uint8))
+        r = subprocess.run([exe, os.path.join(d, "model.gguf"), d, "0", str(args.warmup), str(args.steps)],
+                           capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise SystemExit(f"decoder_bench failed ({r.returncode}): {r.stderr[-2000:]}")
+    run = json.loads(r.stdout.strip().splitlines()[-1])
+
+    # algorithmic FLOPs: active pairs of every level from the device neighbour table
+    pairs = []
+    for c in w.level_coords:
+        nbr = pkg.rulebook_build(torch.from_numpy(np.ascontiguousarray(c, np.int32)).cuda())
+        pairs.append(pkg.count_pairs(nbr, len(c)))
+        del nbr
+    ch, nb, cl = w.channels, w.blocks, w.latent.shape[1]
+
+    def total(pp):
+        f = 2.0 * cl * ch[0] * w.counts[0]                          # from_latent
+        for s in range(len(ch) - 1):
+            ci, co, n = ch[s], ch[s + 1], w.counts[s]
+            f += nb * (2.0 * ci * ci * pp[s] + 16.0 * ci * ci * n)  # ConvNeXt: conv + MLP
+            f += 2.0 * ci * 8 * co * pp[s] + 2.0 * co * co * pp[s + 1]   # C2S conv1, conv2
+        return f + 2.0 * ch[-1] * w.out_ch * w.counts[-1]           # output_layer
+    flops = total(pairs)
+    flops_dense = total([27 * n for n in w.counts])
+    ms = run["decode_ms"]
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = decoder_cpu_baseline(w, flops_dense, args.cpu_seconds)
+    return {
+        "metric": "decoder voxels/s & TFLOP/s (texture decoder stack, one decode per step)",
+        "value": run["voxels_out"] / (ms * 1e-3),
+        "unit": "voxels/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": w.name, "voxels_per_level": w.counts, "active_pairs_per_level": pairs,
+                   "channels": list(ch), "convnext_blocks_per_stage": nb, "latent_ch": cl,
+                   "out_ch": w.out_ch, "weights": f"bf16 ~ N(0, {w.std})", "accumulate": "f32",
+                   "model_bytes": run["model_bytes"], "parallelism": "single-gpu"},
+        "tflops": tflops,
+        "tflops_dense27_equivalent": flops_dense / (ms * 1e-3) / 1e12,
+        "min_ms": run["min_ms"], "model_load_ms": run["load_ms"],
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_TFLOPS["bf16"], "traffic": None,
+                     "note": "whole decode, host transfers included; the conv kernels dominate"},
+        "cpu_baseline": cpu,
+    }
+
+
+def decoder_cpu_baseline(w, flops_dense: float, budget_s: float) -> dict:
+    """The CPU oracle's conv (the reference's dense-over-27-taps fp32 algorithm) timed on a row
+    sample of the decoder's widest conv (stage 0: ch[0] -> ch[0] on the latent voxels), its
+    dense-27 FLOP rate then pricing the decoder's dense-27 FLOPs: an extrapolation, since a full
+    CPU decode takes far longer than the time budget."""
+    import statistics
+
+    import numpy as np
+    orc = _load("trellis_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    import trellis_cpp_amd.shells as shells
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    c, n = w.channels[0], len(w.coords)
+    rng = np.random.default_rng(w.seed)
+    x = shells.round_to(shells.standard_normal_rows(rng, n, c), "bf16")
+    wt = shells.round_to(rng.standard_normal((c, 27, c), dtype=np.float32) * np.float32(w.std), "bf16")
+    b = np.zeros(c, np.float32)
+    nbr = orc.neighbor_table(w.coords)
+
+    def timed(r0, r1):
+        t = time.perf_counter()
+        orc.subm_conv_f32_rows(x, nbr, wt, b, r0, r1, threads)
+        return time.perf_counter() - t
+
+    probe = min(n, 256)
+    per_row = timed(0, probe) / probe
+    rows = int(min(n, max(probe, budget_s / 3 / max(per_row, 1e-12))))
+    r0 = (n - rows) // 2
+    runs = [timed(r0, r0 + rows) for _ in range(3)]
+    dt = statistics.median(runs)
+    rate = 2.0 * 27 * c * c * rows / dt
+    est = flops_dense / rate
+    return {"value": w.counts[-1] / est, "unit": "voxels/s", "cores": threads, "kind": "port",
+            "sample": f"extrapolated: the oracle's conv ({c} -> {c} channels, rows [{r0}, {r0 + rows}) of "
+                      f"{n}, median of 3: {dt:.2f} s) runs {rate / 1e9:.1f} dense-27 GFLOP/s; the "
+                      f"decoder's {flops_dense / 1e12:.1f} dense-27 TFLOP at that rate take {est:.0f} s "
+                      f"(LayerNorm, SiLU and gathers not counted)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -109,6 +229,10 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload.startswith("decoder-"):
+        print(json.dumps(decoder_bench(args)))
+        return
 
     import numpy as np
     import torch

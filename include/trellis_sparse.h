@@ -143,11 +143,29 @@ int tsp_subdivide(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
 
 /* out[i] = x[i] . W^T + bias for W [co][ci] (ggml_mul_mat of ne [ci, co] plus ggml_add,
  * sparse.cpp:126-128, 188). Any dtype mix; fp32 accumulation; d_bias may be NULL. f16/bf16 x and
- * weights of one dtype with ci % 32 == 0, co % 64 == 0 and 16-byte aligned buffers run on the
- * matrix cores, the rest on the VALU kernel. */
+ * weights of one dtype with out f32 or that dtype, ci % 8 == 0, co % 8 == 0 and 16-byte aligned
+ * buffers run as a hipBLASLt GEMM; otherwise (or when hipBLASLt has no algorithm for the shape)
+ * f16/bf16 with ci % 32 == 0 and co % 64 == 0 run on this library's matrix-core kernel, the rest
+ * on its VALU kernel. The first hipBLASLt call on a device creates a hipBLASLt handle, kept until
+ * the process ends; the GEMMs use no workspace. */
 int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
                int weight_dtype, const float* d_bias, int co, void* d_out, int out_dtype,
                void* stream);
+
+/* Activations of tsp_linear_ex. */
+enum { TSP_ACT_NONE = 0, TSP_ACT_SILU = 1 };
+
+/* out[i] = act(x[i] . W^T + bias) + residual[i]: the ConvNeXt MLP's mlp.0 -> SiLU and
+ * mlp.2 -> + x (sparse.cpp:126-134: ggml_mul_mat, ggml_add of the bias, ggml_silu; ggml_mul_mat,
+ * ggml_add of the bias, ggml_add of the block input) as one GEMM each, with the bias, the SiLU
+ * (fp32, before the output's rounding) and the residual in the GEMM's epilogue. d_bias and
+ * d_residual (f32 [n][co], 16-byte aligned; needs f32 output) may be NULL. Needs 16-bit x and
+ * weights of one dtype, out f32 or that dtype, ci % 8 == 0, co % 8 == 0, 16-byte aligned buffers;
+ * returns TSP_ERR_UNSUPPORTED otherwise, or when hipBLASLt has no algorithm for the shape, and the
+ * caller then runs tsp_linear and the elementwise steps. */
+int tsp_linear_ex(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
+                  int weight_dtype, const float* d_bias, int co, int act, const float* d_residual,
+                  void* d_out, int out_dtype, void* stream);
 
 /* Row LayerNorm over c channels with biased variance and eps (ggml_norm, sparse.cpp:124,
  * 259, 293), then * gamma + beta when those are not NULL, then x * sigmoid(x) when silu != 0.

@@ -30,6 +30,11 @@ def load_package():
     return mod
 
 
+# the package is importable as trellis_cpp_amd from every test module (the library itself loads
+# lazily, on the first device call)
+load_package()
+
+
 def load_oracle():
     if "trellis_oracle" in sys.modules:
         return sys.modules["trellis_oracle"]

@@ -7,7 +7,7 @@ import os
 
 import numpy as np
 
-from gguf_writer import write as write_gguf
+from trellis_cpp_amd.gguf_writer import write as write_gguf
 
 
 def _f16(a):

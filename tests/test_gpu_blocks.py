@@ -50,6 +50,33 @@ def test_linear(gpu_lib, orc, n, ci, co):
         assert orc.rel_err(out_nb, ref - b.astype(np.float64)) < TOL_32, tdt
 
 
+
+@pytest.mark.parametrize("n,ci,co", [(1000, 64, 256), (777, 128, 512), (3, 32, 64), (4096, 256, 64)])
+def test_linear_ex(gpu_lib, orc, n, ci, co):
+    """The fused MLP pieces: silu(x W^T + b) rounded to x's dtype (mlp.0 -> SiLU, rounded as
+    mlp.2's input) and x W^T + b + residual in f32 (mlp.2 -> + block input), against the oracle
+    on the same 16-bit inputs."""
+    _case(f"linear_ex n={n} ci={ci} co={co}")
+    import torch
+    rng = np.random.default_rng(n * 3 + ci + co)
+    for tdt in (torch.bfloat16, torch.float16):
+        xr = _t(rng.standard_normal((n, ci)).astype(np.float32)).to(tdt)
+        wr = _t((rng.standard_normal((co, ci)) / np.sqrt(ci)).astype(np.float32)).to(tdt)
+        b = rng.standard_normal(co).astype(np.float32)
+        res = rng.standard_normal((n, co)).astype(np.float32)
+        pre = orc.linear(xr.float().cpu().numpy(), wr.float().cpu().numpy(), b)
+        h = gpu_lib.linear_ex(xr, wr, _t(b), act="silu").float().cpu().numpy()
+        ref = orc.silu(pre)
+        # one 16-bit rounding of the output on top of fp32 accumulation
+        assert orc.rel_err(h, ref) < (8e-3 if tdt == torch.bfloat16 else 1e-3), tdt
+        y = gpu_lib.linear_ex(xr, wr, _t(b), residual=_t(res), out_dtype=torch.float32).cpu().numpy()
+        assert orc.rel_err(y, pre + res) < TOL_32, tdt
+        y0 = gpu_lib.linear_ex(xr, wr, out_dtype=torch.float32).cpu().numpy()   # no bias
+        assert orc.rel_err(y0, pre - b.astype(np.float64)) < TOL_32, tdt
+    # f32 inputs are not a library GEMM here: the caller falls back to tsp_linear
+    with pytest.raises(gpu_lib.TspError, match="UNSUPPORTED"):
+        gpu_lib.linear_ex(_t(np.ones((4, 32), np.float32)), _t(np.ones((64, 32), np.float32)))
+
 @pytest.mark.parametrize("c", [7, 64, 1024, 4096])
 def test_layer_norm(gpu_lib, orc, c):
     _case(f"layer_norm c={c}")

@@ -86,7 +86,7 @@ def test_c2s(gpu, orc, shells, tmp_path, cin, cout, ext, f32):
 
 # ---- the device-resident decoders (shape_decode, shape_upsample, tex_decode) ----------------------
 def _decoder_case(tmp_path, orc, shells, out_ch, seed):
-    from gguf_writer import write as write_gguf
+    from trellis_cpp_amd.gguf_writer import write as write_gguf
     from host_cases import decoder_params, stored
     rng = np.random.default_rng(seed)
     coords = shells.random_distinct_voxels(200, 10, seed)
@@ -132,3 +132,29 @@ def test_tex_decode_guided(gpu, orc, shells, tmp_path):
     print(f"tex_decode 16-bit rel={err:.3e} M={len(rcoords)}", flush=True)
     # every conv and linear of 3 stages rounds its input to F16 (measured 1.1e-3)
     assert err < 3e-3
+
+
+def test_tex_decode_bf16_decoder_workload(gpu, orc, shells, tmp_path):
+    """The decoder benchmark's model format on its miniature workload: bf16 weights ~ N(0, 0.02)
+    under the reference's key names, band masks driving the texture route. Against the oracle
+    decoder fed the same bf16-rounded weights; every conv and linear rounds its input to bf16 (a
+    2^-8 relative step, so the bar is looser than the F16 case's)."""
+    from trellis_cpp_amd.gguf_writer import write as write_gguf
+    w = shells.decoder_workload("decoder-shells16-c64")
+    p = shells.decoder_params(w.channels, w.blocks, 32, w.out_ch, w.std, w.seed)
+    write_gguf(str(tmp_path / "model.gguf"), p, dtypes={k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()})
+    np.save(tmp_path / "latent.npy", w.latent)
+    np.save(tmp_path / "coords.npy", np.ascontiguousarray(w.coords, np.int32))
+    for s, m in enumerate(w.masks):
+        np.save(tmp_path / f"subs_{s}.npy", m)
+    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0", "--tex"])
+    q = {k: (shells.round_to(v, "bf16") if v.ndim >= 2 else v) for k, v in p.items()}
+    stages = [([f"blocks.{s}.{j}" for j in range(w.blocks)], (f"blocks.{s}.{w.blocks}", ci, co))
+              for s, (ci, co) in enumerate(zip(w.channels[:-1], w.channels[1:]))]
+    ref, rcoords, _ = orc.decode_unet(w.latent, w.coords, q, stages, w.out_ch, w.masks)
+    assert len(rcoords) == w.counts[-1]
+    out = np.load(tmp_path / "out.npy")
+    assert out.shape == ref.shape
+    err = orc.rel_err(out, ref)
+    print(f"tex_decode bf16 rel={err:.3e} M={len(rcoords)}", flush=True)
+    assert err < 3e-2

@@ -12,7 +12,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from gguf_writer import write as write_gguf
+from trellis_cpp_amd.gguf_writer import write as write_gguf
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HOST = os.path.join(ROOT, "trellis.cpp_amd", "host")

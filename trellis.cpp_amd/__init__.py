@@ -28,7 +28,8 @@ EXPORTS = (
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
     "tsp_subm_conv3x3_planned",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
-    "tsp_linear", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add", "tsp_mask_positive",
+    "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
+    "tsp_mask_positive",
 )
 
 
@@ -80,6 +81,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_linear.restype = c_int
     L.tsp_linear.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_int, c_vp, c_int, c_vp, c_int,
                              c_vp]
+    L.tsp_linear_ex.restype = c_int
+    L.tsp_linear_ex.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_int, c_vp, c_int, c_int, c_vp,
+                                c_vp, c_int, c_vp]
     L.tsp_layer_norm.restype = c_int
     L.tsp_layer_norm.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, ctypes.c_float, c_int,
                                  c_vp, c_int, c_vp]
@@ -265,6 +269,31 @@ def linear(x, weight, bias=None, out_dtype=None, stream=None):
     _check("tsp_linear",
            lib().tsp_linear(_ptr(xc), dtype_code(xc.dtype), n, ci, _ptr(wc), dtype_code(wc.dtype),
                             _ptr(bias), co, _ptr(out), dtype_code(out.dtype), _stream(stream)))
+    return out
+
+
+ACT = {"none": 0, "silu": 1}
+
+
+def linear_ex(x, weight, bias=None, act: str = "none", residual=None, out_dtype=None, stream=None):
+    """act(x [N,Ci] . W^T + bias) + residual for W [Co,Ci] -> [N,Co], one library GEMM with the
+    bias, activation and residual in its epilogue (16-bit x and W of one dtype; raises
+    TspError UNSUPPORTED otherwise)."""
+    torch = _torch()
+    _require_cuda(x, weight, bias, residual)
+    n, ci = x.shape
+    co = weight.shape[0]
+    if weight.shape != (co, ci):
+        raise ValueError("weight must be [Co, Ci]")
+    if residual is not None and (residual.dtype != torch.float32 or residual.shape != (n, co)):
+        raise ValueError("residual must be float32 [N, Co]")
+    out = torch.empty((n, co), dtype=out_dtype or x.dtype, device=x.device)
+    xc, wc = x.contiguous(), weight.contiguous()
+    rc = residual.contiguous() if residual is not None else None
+    _check("tsp_linear_ex",
+           lib().tsp_linear_ex(_ptr(xc), dtype_code(xc.dtype), n, ci, _ptr(wc), dtype_code(wc.dtype),
+                               _ptr(bias), co, ACT[act], _ptr(rc), _ptr(out), dtype_code(out.dtype),
+                               _stream(stream)))
     return out
 
 

@@ -505,7 +505,14 @@ extern "C" int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const
     TSP_REQUIRE(d_out != d_x, TSP_ERR_INVALID, "tsp_linear: out aliases x");
     TSP_REQUIRE(n < (int64_t)INT32_MAX, TSP_ERR_INVALID, "tsp_linear: n=%lld out of range",
                 (long long)n);
-    // 16-bit x and weights of one dtype on the matrix cores; everything else on the VALU kernel
+    // 16-bit x and weights of one dtype as a library GEMM, else on the matrix-core kernel;
+    // everything else on the VALU kernel
+    if (blaslt_eligible(x_dtype, weight_dtype, out_dtype, ci, co, d_x, d_weight, d_out)) {
+        const int st = blaslt_linear(d_x, x_dtype, n, ci, d_weight, d_bias, co, TSP_ACT_NONE, nullptr,
+                                     d_out, out_dtype, as_stream(stream));
+        if (st != TSP_ERR_UNSUPPORTED) return st;
+        clear_error();
+    }
     if (mfma_eligible(x_dtype, weight_dtype, out_dtype, ci, co, d_x, d_weight, d_out))
         return dispatch_gather(x_dtype, out_dtype, d_x, n, ci, nullptr, 1, d_weight, d_bias, co,
                                d_out, as_stream(stream));

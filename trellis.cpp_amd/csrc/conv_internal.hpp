@@ -34,6 +34,14 @@ constexpr int HB_M = 512;   // output voxels per workgroup (and per plan tile)
 size_t halo_plan_bytes(int64_t n);
 // whether the LDS-staged kernel can address n rows of ci channels (32-bit byte offsets)
 bool halo_fits(int64_t n, int ci);
+
+// Dense linear layers on hipBLASLt (linear_blaslt.cpp): 16-bit x and weights of one dtype, out f32
+// or that dtype, ci % 8 == 0, co % 8 == 0, 16-byte aligned. blaslt_linear returns
+// TSP_ERR_UNSUPPORTED when the library has no algorithm for the shape.
+bool blaslt_eligible(int x_dtype, int weight_dtype, int out_dtype, int ci, int co, const void* x,
+                     const void* w, const void* out);
+int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
+                  int co, int act, const float* residual, void* out, int odt, hipStream_t s);
 // Builds the plan of neighbour table `nbr` into `plan`.
 int halo_plan_build(const int32_t* nbr, int64_t n, void* plan, hipStream_t s);
 // Packs [co][27][ci] 16-bit weights into the MFMA operand order (ci % 16 == 0, co % 32 == 0).

@@ -1,4 +1,5 @@
-"""Minimal GGUF v3 writer for the tests: string metadata and F32 / F16 / BF16 / I32 tensors.
+"""Minimal GGUF v3 writer for synthetic models (the tests' fixtures and the decoder benchmark):
+string metadata and F32 / F16 / BF16 / I32 tensors.
 
 The layout is the published GGUF v3 one (magic "GGUF", u32 version, u64 tensor count, u64
 key/value count, the key/value table, the tensor table, padding to general.alignment, data).

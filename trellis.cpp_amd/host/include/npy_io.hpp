@@ -1,5 +1,5 @@
-// Minimal .npy (format 1.0 / 2.0) reader and writer for the host check programs: C-order
-// little-endian float32 ('<f4'), int32 ('<i4') and uint8 ('|u1') arrays.
+// Minimal .npy (format 1.0 / 2.0) reader and writer for the host check programs and the decoder
+// benchmark: C-order little-endian float32 ('<f4'), int32 ('<i4') and uint8 ('|u1') arrays.
 #pragma once
 
 #include <cstdint>

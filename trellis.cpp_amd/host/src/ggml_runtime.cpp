@@ -12,6 +12,7 @@
 #include <cstring>
 #include <deque>
 #include <map>
+#include <mutex>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -39,6 +40,41 @@ void DeviceBuffer::reset() {
     if (p_) (void)hipFree(p_);
     p_ = nullptr;
     n_ = 0;
+}
+
+namespace {
+constexpr size_t kStageChunk = size_t(24) << 20;   // divisible by 4, 12 and 24 (element sizes)
+constexpr int kMaxDevices = 64;
+std::mutex g_stage_mu;
+void* g_stage[2] = {nullptr, nullptr};
+hipEvent_t g_stage_ev[kMaxDevices][2] = {};
+}  // namespace
+
+void download_chunks(const void* src, size_t bytes, hipStream_t s,
+                     const std::function<void(const void*, size_t)>& sink) {
+    if (!bytes) return;
+    std::lock_guard<std::mutex> lock(g_stage_mu);
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) fail("download: device out of range");
+    for (int k = 0; k < 2; ++k) {
+        if (!g_stage[k]) hip_check(hipHostMalloc(&g_stage[k], kStageChunk, hipHostMallocDefault), "hipHostMalloc");
+        if (!g_stage_ev[dev][k])
+            hip_check(hipEventCreateWithFlags(&g_stage_ev[dev][k], hipEventDisableTiming), "hipEventCreate");
+    }
+    const size_t nchunk = (bytes + kStageChunk - 1) / kStageChunk;
+    auto issue = [&](size_t i) {
+        const size_t off = i * kStageChunk, len = std::min(kStageChunk, bytes - off);
+        hip_check(hipMemcpyAsync(g_stage[i % 2], static_cast<const char*>(src) + off, len,
+                                 hipMemcpyDeviceToHost, s), "download");
+        hip_check(hipEventRecord(g_stage_ev[dev][i % 2], s), "hipEventRecord");
+    };
+    issue(0);
+    for (size_t i = 0; i < nchunk; ++i) {
+        if (i + 1 < nchunk) issue(i + 1);   // the other buffer: its chunk i-1 was taken already
+        hip_check(hipEventSynchronize(g_stage_ev[dev][i % 2]), "download");
+        sink(g_stage[i % 2], std::min(kStageChunk, bytes - i * kStageChunk));
+    }
 }
 
 int tsp_dtype_of(enum ggml_type t) {

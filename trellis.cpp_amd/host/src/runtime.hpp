@@ -7,9 +7,11 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "ggml-backend.h"
 #include "ggml.h"
@@ -51,6 +53,24 @@ private:
     void* p_ = nullptr;
     size_t n_ = 0;
 };
+
+// Device -> host copy of `bytes` at src, stream-ordered on s, through two pinned staging
+// buffers (kept until the process ends): while the host takes one chunk (sink(ptr, n), in
+// order), the next one is in flight.
+void download_chunks(const void* src, size_t bytes, hipStream_t s,
+                     const std::function<void(const void*, size_t)>& sink);
+
+// count elements of device memory at src into a new host vector (no zero-fill first).
+template <class T>
+std::vector<T> download(const void* src, size_t count, hipStream_t s) {
+    std::vector<T> v;
+    v.reserve(count);
+    download_chunks(src, count * sizeof(T), s, [&](const void* p, size_t n) {
+        const T* t = static_cast<const T*>(p);
+        v.insert(v.end(), t, t + n / sizeof(T));
+    });
+    return v;
+}
 
 // HIP device and stream of a backend made by ggml_backend_hip_init.
 int backend_device(ggml_backend_t backend);

@@ -64,7 +64,8 @@ std::vector<Stage> stages_of(const Model& m) {
 std::vector<float> decode(const Model& m, const std::vector<float>& latent, int out_ch,
                           std::vector<std::array<int, 3>>& coords,
                           const std::vector<std::vector<uint8_t>>* guide,
-                          std::vector<std::vector<uint8_t>>* subs_out, bool coords_only) {
+                          std::vector<std::vector<uint8_t>>* subs_out, bool coords_only,
+                          bool want_coords = true) {
     const std::vector<Stage> stages = stages_of(m);
     if (guide && guide->size() < stages.size()) fail("tex_decode: one subdivision mask per stage is needed");
     int64_t n = (int64_t)coords.size();
@@ -111,18 +112,14 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         n = o.m;
         c = g.cout;
     }
-    hip_check(hipStreamSynchronize(s), "decoder");
-    coords.resize((size_t)n);
-    if (n) hip_check(hipMemcpy(coords.data(), dc.get(), (size_t)n * 12, hipMemcpyDeviceToHost), "decoder readback");
+    if (want_coords) coords = tgr::download<std::array<int, 3>>(dc.get(), (size_t)n, s);
     if (coords_only) return {};
     const ggml_tensor* wo = m.get("output_layer.weight");
     if (wo->ne[0] != c || wo->ne[1] != out_ch)
         fail("output_layer.weight: expected ggml shape [" + std::to_string(c) + ", " + std::to_string(out_ch) + "]");
     DeviceBuffer out((size_t)n * out_ch * 4);
     if (n) ops::run_linear(m, "output_layer", h.as<float>(), n, c, out_ch, true, 1e-5f, out.as<float>(), s);
-    std::vector<float> r((size_t)n * out_ch);
-    if (n) hip_check(hipMemcpy(r.data(), out.get(), r.size() * 4, hipMemcpyDeviceToHost), "decoder readback");
-    return r;
+    return tgr::download<float>(out.get(), (size_t)n * out_ch, s);
 }
 
 }  // namespace
@@ -147,7 +144,8 @@ std::vector<float> tex_decode(const Model& m, const std::vector<float>& tex_late
                               const std::vector<std::array<int, 3>>& coords0,
                               const std::vector<std::vector<uint8_t>>& subs) {
     std::vector<std::array<int, 3>> coords = coords0;
-    return decode(m, tex_latent, 6, coords, &subs, nullptr, false);
+    // the caller has the final voxel set from shape_decode: only the features come back
+    return decode(m, tex_latent, 6, coords, &subs, nullptr, false, false);
 }
 
 }  // namespace trellis

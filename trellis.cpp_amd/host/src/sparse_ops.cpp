@@ -133,15 +133,31 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
     const size_t xes = xdt == TSP_F32 ? 4 : 2;
     for (int64_t r0 = 0; r0 < a.n; r0 += a.chunk) {
         const int64_t nr = std::min(a.chunk, a.n - r0);
-        lib(tsp_linear(static_cast<const char*>(hn) + (size_t)r0 * c * aes, adt, nr, c, a.w0->data, w0dt,
-                       bias0, 4 * c, hid, TSP_F32, s),
-            "convnext mlp.0");
-        hip_check(tgr::launch_silu_to(hid, hid_in, adt, nr * 4 * c, s), "convnext silu");
-        lib(tsp_linear(hid_in, adt, nr, 4 * c, a.w2->data, w2dt, bias2, c, out + r0 * c, TSP_F32, s),
-            "convnext mlp.2");
-        hip_check(tgr::launch_add_inplace(out + r0 * c, static_cast<const char*>(x) + (size_t)r0 * c * xes,
-                                          xdt, nr * c, s),
-                  "convnext residual");
+        const void* hin = static_cast<const char*>(hn) + (size_t)r0 * c * aes;
+        const void* xr = static_cast<const char*>(x) + (size_t)r0 * c * xes;
+        float* yr = out + r0 * c;
+        // 16-bit MLP: mlp.0 with its bias and SiLU, and mlp.2 with its bias and the f32 block input,
+        // each one library GEMM; the unfused sequence where a shape has no such GEMM
+        int st = TSP_ERR_UNSUPPORTED;
+        if (a.mlp16)
+            st = tsp_linear_ex(hin, adt, nr, c, a.w0->data, w0dt, bias0, 4 * c, TSP_ACT_SILU, nullptr,
+                               hid_in, adt, s);
+        if (st != TSP_ERR_UNSUPPORTED) {
+            lib(st, "convnext mlp.0");
+        } else {
+            lib(tsp_linear(hin, adt, nr, c, a.w0->data, w0dt, bias0, 4 * c, hid, TSP_F32, s), "convnext mlp.0");
+            hip_check(tgr::launch_silu_to(hid, hid_in, adt, nr * 4 * c, s), "convnext silu");
+        }
+        st = TSP_ERR_UNSUPPORTED;
+        if (a.mlp16 && xdt == TSP_F32)
+            st = tsp_linear_ex(hid_in, adt, nr, 4 * c, a.w2->data, w2dt, bias2, c, TSP_ACT_NONE,
+                               static_cast<const float*>(xr), yr, TSP_F32, s);
+        if (st != TSP_ERR_UNSUPPORTED) {
+            lib(st, "convnext mlp.2");
+        } else {
+            lib(tsp_linear(hid_in, adt, nr, 4 * c, a.w2->data, w2dt, bias2, c, yr, TSP_F32, s), "convnext mlp.2");
+            hip_check(tgr::launch_add_inplace(yr, xr, xdt, nr * c, s), "convnext residual");
+        }
     }
 }
 

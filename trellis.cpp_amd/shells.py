@@ -258,3 +258,87 @@ def random_distinct_voxels(n: int, extent: int, seed: int) -> np.ndarray:
             seen.add(p)
             rows.append(p)
     return np.asarray(rows, np.int32).reshape(-1, 3)
+
+
+# ------------------------------------------------------------------------------------------
+# The decoder-stack workload
+# ------------------------------------------------------------------------------------------
+@dataclasses.dataclass
+class DecoderWorkload:
+    name: str
+    coords: np.ndarray        # int32 [N0,3] at the latent resolution
+    latent: np.ndarray        # float32 [N0, latent_ch]
+    masks: list               # uint8 [8 N_s] subdivision mask of each stage
+    counts: list              # voxels at each level (N0 .. N_stages)
+    level_coords: list        # int32 [N_s,3] of each level (N0 .. N_stages)
+    channels: tuple           # stage widths, e.g. (1024, 512, 256, 128, 64)
+    blocks: int               # ConvNeXt blocks per stage
+    out_ch: int
+    std: float                # weight init
+    seed: int
+    description: str
+
+
+def decoder_workload(name: str = "decoder-shells64-c1024") -> DecoderWorkload:
+    """The full decoder stack on a 64^3 latent:
+
+    decoder-shells64-c1024   4 random ellipsoid/box shells at 64^3, semi-axes U[8,20],
+                             thickness 2 (~34K voxels, 32 latent channels ~ N(0,1)); 4 stages
+                             1024 -> 512 -> 256 -> 128 -> 64 channels, each 2 ConvNeXt blocks
+                             and a 2x subdivision pruned to the thickness-2 band of the same
+                             shapes (the mask drives the texture decoder's route), ending at
+                             1024^3; 6 output channels; every weight ~ N(0, 0.02); seed 4
+    decoder-shells16-c64     a 16^3 miniature for tests: 2 shells, semi-axes U[3,6], 2 stages
+                             64 -> 32 -> 16
+    """
+    if name == "decoder-shells64-c1024":
+        grid, count, lo, hi, ch = 64, 4, 8.0, 20.0, (1024, 512, 256, 128, 64)
+    elif name == "decoder-shells16-c64":
+        grid, count, lo, hi, ch = 16, 2, 3.0, 6.0, (64, 32, 16)
+    else:
+        raise KeyError(name)
+    rng = np.random.default_rng(4)
+    shapes = random_shapes(rng, grid, count, lo, hi, boxes=True)
+    coords = band_voxels(shapes, grid, 2.0)
+    latent = standard_normal_rows(rng, len(coords), 32)
+    masks, levels = [], [coords]
+    c = coords
+    for _ in range(len(ch) - 1):
+        m = subdivision_band_mask(c, shapes, 2.0)
+        c = children(m, c)
+        masks.append(m)
+        levels.append(c)
+        shapes = [Shape(sh.kind, sh.center * 2, sh.semi * 2, sh.rot) for sh in shapes]
+    return DecoderWorkload(name, coords, latent, masks, [len(x) for x in levels], levels, ch, 2, 6,
+                           0.02, 4, decoder_workload.__doc__)
+
+
+def decoder_params(channels: tuple, blocks: int, latent_ch: int, out_ch: int, std: float,
+                   seed: int) -> dict:
+    """Random-init weights of the sparse U-Net decoder under the reference's key names
+    (shape_decoder.cpp:79-117, sparse.cpp:104, 125-128, 188, 260, 278, 305): from_latent, per stage
+    `blocks` ConvNeXt blocks `blocks.s.j` then the C2S block `blocks.s.<blocks>`, output_layer.
+    Weights ~ N(0, std); LayerNorm weights 1; biases 0. Conv weights are [Co, 27, Ci]."""
+    rng = np.random.default_rng(seed)
+
+    def w(*shape):
+        return rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+
+    z = lambda n: np.zeros(n, np.float32)
+    one = lambda n: np.ones(n, np.float32)
+    p = {"from_latent.weight": w(channels[0], latent_ch), "from_latent.bias": z(channels[0])}
+    for s, (ci, co) in enumerate(zip(channels[:-1], channels[1:])):
+        for j in range(blocks):
+            q = f"blocks.{s}.{j}"
+            p.update({f"{q}.conv.weight": w(ci, 27, ci), f"{q}.conv.bias": z(ci),
+                      f"{q}.norm.weight": one(ci), f"{q}.norm.bias": z(ci),
+                      f"{q}.mlp.0.weight": w(4 * ci, ci), f"{q}.mlp.0.bias": z(4 * ci),
+                      f"{q}.mlp.2.weight": w(ci, 4 * ci), f"{q}.mlp.2.bias": z(ci)})
+        q = f"blocks.{s}.{blocks}"
+        p.update({f"{q}.to_subdiv.weight": w(8, ci), f"{q}.to_subdiv.bias": z(8),
+                  f"{q}.norm1.weight": one(ci), f"{q}.norm1.bias": z(ci),
+                  f"{q}.conv1.weight": w(8 * co, 27, ci), f"{q}.conv1.bias": z(8 * co),
+                  f"{q}.conv2.weight": w(co, 27, co), f"{q}.conv2.bias": z(co)})
+    p["output_layer.weight"] = w(out_ch, channels[-1])
+    p["output_layer.bias"] = z(out_ch)
+    return p
