@@ -77,7 +77,7 @@ def test_linear_ex(gpu_lib, orc, n, ci, co):
     with pytest.raises(gpu_lib.TspError, match="UNSUPPORTED"):
         gpu_lib.linear_ex(_t(np.ones((4, 32), np.float32)), _t(np.ones((64, 32), np.float32)))
 
-@pytest.mark.parametrize("c", [7, 64, 1024, 4096])
+@pytest.mark.parametrize("c", [7, 64, 128, 256, 512, 1024, 2048, 4096])
 def test_layer_norm(gpu_lib, orc, c):
     _case(f"layer_norm c={c}")
     rng = np.random.default_rng(c)

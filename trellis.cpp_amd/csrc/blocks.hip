@@ -55,6 +55,118 @@ __global__ __launch_bounds__(256) void k_layer_norm(const void* __restrict__ x, 
     }
 }
 
+// 4 consecutive elements (16-byte f32 / 8-byte 16-bit accesses; the index is a multiple of 4).
+template <int DT>
+__device__ __forceinline__ void ld4(const void* p, int64_t i, float (&v)[4]) {
+    if constexpr (DT == TSP_F32) {
+        const f32x4_t t = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(p) + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = t[e];
+    } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+        const uint16_t h[4] = {(uint16_t)(t.x & 0xffffu), (uint16_t)(t.x >> 16), (uint16_t)(t.y & 0xffffu),
+                               (uint16_t)(t.y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = DT == TSP_BF16 ? bf16_bits_to_f32(h[e]) : f16_bits_to_f32(h[e]);
+    }
+}
+template <int DT>
+__device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {
+    if constexpr (DT == TSP_F32) {
+        *reinterpret_cast<f32x4_t*>(static_cast<float*>(p) + i) = f32x4_t{v[0], v[1], v[2], v[3]};
+    } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = DT == TSP_BF16 ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    }
+}
+
+// Rows of c = 4 L V channels held in registers: L lanes per row (64 / L rows per wave), each lane
+// V groups of 4 channels, interleaved so that a row's lanes read consecutive 16 bytes. One read of
+// x, one write of out; every lane takes part in the group reductions, rows past n store nothing.
+template <int XDT, int ODT, int L, int V>
+__global__ __launch_bounds__(256) void k_layer_norm_vec(const void* __restrict__ x, int64_t n, int c,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, float eps,
+                                                        int silu, void* __restrict__ out) {
+    constexpr int R = 64 / L;
+    const int lane = threadIdx.x & 63, sub = lane % L;
+    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R + lane / L;
+    const bool live = row < n;
+    const int64_t base = (live ? row : 0) * c;
+    float v[V][4];
+#pragma unroll
+    for (int j = 0; j < V; ++j) ld4<XDT>(x, base + (j * L + sub) * 4, v[j]);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s += v[j][e];
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    const float mean = s / (float)c;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = v[j][e] - mean;
+            q += d * d;
+        }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+    const float rstd = 1.0f / sqrtf(q / (float)c + eps);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int ch = (j * L + sub) * 4;
+        float g[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {0.f, 0.f, 0.f, 0.f}, y[4];
+        if (gamma) ld4<TSP_F32>(gamma, ch, g);
+        if (beta) ld4<TSP_F32>(beta, ch, b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            y[e] = (v[j][e] - mean) * rstd * g[e] + b[e];
+            if (silu) y[e] = y[e] / (1.0f + expf(-y[e]));
+        }
+        if (live) st4<ODT>(out, base + ch, y);
+    }
+}
+
+// Row copies of 4 elements per thread: out[r][k] = h[gidx[r]][k] (cout % 4 == 0).
+template <int DT>
+__global__ void k_c2s_gather_vec(const void* __restrict__ h, const int32_t* __restrict__ gidx,
+                                 int64_t m, int cout, void* __restrict__ out) {
+    const int q = cout / 4;
+    const int64_t total = m * q;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / q;
+        const int k = (int)(e - r * q) * 4;
+        float v[4];
+        ld4<DT>(h, (int64_t)gidx[r] * cout + k, v);
+        st4<DT>(out, r * cout + k, v);
+    }
+}
+
+// The skip with 4 output channels per thread, all from one source channel (rep % 4 == 0).
+template <int XDT, int ADT>
+__global__ void k_c2s_skip_add_vec(const void* __restrict__ x, const int32_t* __restrict__ gidx,
+                                   int64_t m, int kb, int rep, void* __restrict__ acc) {
+    const int q = kb * rep / 4;
+    const int64_t total = m * q;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / q;
+        const int ch = (int)(e - r * q) * 4;
+        const float xv = ld<XDT>(x, (int64_t)gidx[r] * kb + ch / rep);
+        float a[4];
+        ld4<ADT>(acc, r * kb * rep + ch, a);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t] += xv;
+        st4<ADT>(acc, r * kb * rep + ch, a);
+    }
+}
+
 template <int DT>
 __global__ void k_c2s_gather(const void* __restrict__ h, const int32_t* __restrict__ gidx,
                              int64_t m, int cout, void* __restrict__ out) {
@@ -113,10 +225,32 @@ extern "C" int tsp_layer_norm(const void* d_x, int x_dtype, int64_t n, int c,
     if (n == 0) return TSP_OK;
     TSP_REQUIRE(d_x && d_out, TSP_ERR_INVALID, "tsp_layer_norm: null pointer");
     hipStream_t s = as_stream(stream);
-    const dim3 grid((unsigned)ceil_div(n, 4)), block(256);
-    TSP_DT_SWITCH(x_dtype, XD, TSP_DT_SWITCH(out_dtype, OD,
-        hipLaunchKernelGGL((k_layer_norm<XD, OD>), grid, block, 0, s, d_x, n, c, d_gamma,
-                           d_beta, eps, silu, d_out)));
+    // power-of-two widths 64..2048 with aligned buffers: rows in registers, 16-byte accesses
+    const bool aligned = !(reinterpret_cast<uintptr_t>(d_x) % 16 || reinterpret_cast<uintptr_t>(d_out) % 16 ||
+                           reinterpret_cast<uintptr_t>(d_gamma) % 16 || reinterpret_cast<uintptr_t>(d_beta) % 16);
+    if (aligned && c >= 64 && c <= 2048 && (c & (c - 1)) == 0) {
+        auto go = [&](auto lc, auto vc) {
+            constexpr int L = decltype(lc)::value, V = decltype(vc)::value, R = 64 / L;
+            const dim3 grid((unsigned)ceil_div(n, 4 * R)), block(256);
+            TSP_DT_SWITCH(x_dtype, XD, TSP_DT_SWITCH(out_dtype, OD,
+                hipLaunchKernelGGL((k_layer_norm_vec<XD, OD, L, V>), grid, block, 0, s, d_x, n, c,
+                                   d_gamma, d_beta, eps, silu, d_out)));
+        };
+        using std::integral_constant;
+        switch (c) {
+            case 64: go(integral_constant<int, 16>{}, integral_constant<int, 1>{}); break;
+            case 128: go(integral_constant<int, 32>{}, integral_constant<int, 1>{}); break;
+            case 256: go(integral_constant<int, 64>{}, integral_constant<int, 1>{}); break;
+            case 512: go(integral_constant<int, 64>{}, integral_constant<int, 2>{}); break;
+            case 1024: go(integral_constant<int, 64>{}, integral_constant<int, 4>{}); break;
+            default: go(integral_constant<int, 64>{}, integral_constant<int, 8>{}); break;
+        }
+    } else {
+        const dim3 grid((unsigned)ceil_div(n, 4)), block(256);
+        TSP_DT_SWITCH(x_dtype, XD, TSP_DT_SWITCH(out_dtype, OD,
+            hipLaunchKernelGGL((k_layer_norm<XD, OD>), grid, block, 0, s, d_x, n, c, d_gamma,
+                               d_beta, eps, silu, d_out)));
+    }
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
@@ -131,8 +265,13 @@ extern "C" int tsp_c2s_gather(const void* d_h, int dtype, const int32_t* d_gidx,
     TSP_REQUIRE(d_h && d_gidx && d_out && d_out != d_h, TSP_ERR_INVALID,
                 "tsp_c2s_gather: null or aliased pointer");
     hipStream_t s = as_stream(stream);
-    TSP_DT_SWITCH(dtype, D, hipLaunchKernelGGL((k_c2s_gather<D>), dim3(grid_for(m * cout)),
-                                               dim3(256), 0, s, d_h, d_gidx, m, cout, d_out));
+    if (cout % 4 == 0 && !(reinterpret_cast<uintptr_t>(d_h) % 16 || reinterpret_cast<uintptr_t>(d_out) % 16)) {
+        TSP_DT_SWITCH(dtype, D, hipLaunchKernelGGL((k_c2s_gather_vec<D>), dim3(grid_for(m * cout / 4)),
+                                                   dim3(256), 0, s, d_h, d_gidx, m, cout, d_out));
+    } else {
+        TSP_DT_SWITCH(dtype, D, hipLaunchKernelGGL((k_c2s_gather<D>), dim3(grid_for(m * cout)),
+                                                   dim3(256), 0, s, d_h, d_gidx, m, cout, d_out));
+    }
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
@@ -150,9 +289,15 @@ extern "C" int tsp_c2s_skip_add(const void* d_x, int x_dtype, const int32_t* d_g
                 "tsp_c2s_skip_add: null or aliased pointer");
     hipStream_t s = as_stream(stream);
     const int kb = cin / 8, rep = cout / kb;
-    TSP_DT_SWITCH(x_dtype, XD, TSP_DT_SWITCH(acc_dtype, AD,
-        hipLaunchKernelGGL((k_c2s_skip_add<XD, AD>), dim3(grid_for(m * cout)), dim3(256), 0, s,
-                           d_x, d_gidx, m, kb, rep, d_acc)));
+    if (rep % 4 == 0 && reinterpret_cast<uintptr_t>(d_acc) % 16 == 0) {
+        TSP_DT_SWITCH(x_dtype, XD, TSP_DT_SWITCH(acc_dtype, AD,
+            hipLaunchKernelGGL((k_c2s_skip_add_vec<XD, AD>), dim3(grid_for(m * cout / 4)), dim3(256), 0, s,
+                               d_x, d_gidx, m, kb, rep, d_acc)));
+    } else {
+        TSP_DT_SWITCH(x_dtype, XD, TSP_DT_SWITCH(acc_dtype, AD,
+            hipLaunchKernelGGL((k_c2s_skip_add<XD, AD>), dim3(grid_for(m * cout)), dim3(256), 0, s,
+                               d_x, d_gidx, m, kb, rep, d_acc)));
+    }
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }

@@ -17,6 +17,8 @@
 #include <unordered_set>
 #include <vector>
 
+#include <sys/mman.h>
+
 #include "ggml-alloc.h"
 #include "runtime.hpp"
 
@@ -34,10 +36,53 @@ void hip_check(hipError_t e, const char* what) {
 DeviceBuffer::DeviceBuffer(size_t bytes) : n_(bytes) {
     if (bytes) hip_check(hipMalloc(&p_, bytes), "hipMalloc");
 }
+
+namespace {
+// Per device: 1 = memory pools (their release threshold raised so that freed memory stays in the
+// pool), -1 = no pool support, 0 = not probed yet.
+int g_pool_state[64] = {0};
+std::mutex g_pool_mu;
+
+bool pools_ready() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64) return false;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    if (!g_pool_state[dev]) {
+        int supported = 0;
+        hipMemPool_t pool = nullptr;
+        uint64_t keep = UINT64_MAX;
+        g_pool_state[dev] =
+            hipDeviceGetAttribute(&supported, hipDeviceAttributeMemoryPoolsSupported, dev) == hipSuccess &&
+                    supported && hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess &&
+                    hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) == hipSuccess
+                ? 1 : -1;
+    }
+    return g_pool_state[dev] > 0;
+}
+}  // namespace
+
+DeviceBuffer::DeviceBuffer(size_t bytes, hipStream_t s) : n_(bytes), s_(s) {
+    if (!bytes) return;
+    if (pools_ready()) {
+        mode_ = kPool;
+        hip_check(hipMallocAsync(&p_, bytes, s), "hipMallocAsync");
+    } else {
+        mode_ = kSyncFree;
+        hip_check(hipMalloc(&p_, bytes), "hipMalloc");
+    }
+}
 DeviceBuffer::~DeviceBuffer() { reset(); }
 
 void DeviceBuffer::reset() {
-    if (p_) (void)hipFree(p_);
+    if (p_) {
+        if (mode_ == kPool) {
+            (void)hipFreeAsync(p_, s_);
+        } else {
+            if (mode_ == kSyncFree) (void)hipStreamSynchronize(s_);
+            (void)hipFree(p_);
+        }
+    }
     p_ = nullptr;
     n_ = 0;
 }
@@ -49,6 +94,13 @@ std::mutex g_stage_mu;
 void* g_stage[2] = {nullptr, nullptr};
 hipEvent_t g_stage_ev[kMaxDevices][2] = {};
 }  // namespace
+
+void advise_huge_pages(void* p, size_t bytes) {
+    constexpr uintptr_t kHuge = uintptr_t(2) << 20;
+    const uintptr_t a = (reinterpret_cast<uintptr_t>(p) + kHuge - 1) & ~(kHuge - 1);
+    const uintptr_t e = (reinterpret_cast<uintptr_t>(p) + bytes) & ~(kHuge - 1);
+    if (p && e > a) (void)madvise(reinterpret_cast<void*>(a), e - a, MADV_HUGEPAGE);
+}
 
 void download_chunks(const void* src, size_t bytes, hipStream_t s,
                      const std::function<void(const void*, size_t)>& sink) {

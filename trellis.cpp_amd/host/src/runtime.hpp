@@ -25,20 +25,30 @@ inline size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a
 [[noreturn]] void fail(const std::string& msg);   // throws std::runtime_error
 void hip_check(hipError_t e, const char* what);    // throws on error
 
-// Owning device allocation on the current device.
+// Owning device allocation on the current device. The stream-ordered form allocates from the
+// device's memory pool in the order of stream s and frees in that order too, so a buffer may go
+// out of scope while work queued on s still uses it, without a synchronisation; the pool keeps
+// freed memory for later allocations (no hipMalloc / hipFree, and their implicit device
+// synchronisation, once a decoder has run).
 class DeviceBuffer {
 public:
     DeviceBuffer() = default;
     explicit DeviceBuffer(size_t bytes);
+    DeviceBuffer(size_t bytes, hipStream_t s);
     ~DeviceBuffer();
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr; o.n_ = 0; }
+    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_), s_(o.s_), mode_(o.mode_) {
+        o.p_ = nullptr;
+        o.n_ = 0;
+    }
     DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
         if (this != &o) {
             reset();
             p_ = o.p_;
             n_ = o.n_;
+            s_ = o.s_;
+            mode_ = o.mode_;
             o.p_ = nullptr;
             o.n_ = 0;
         }
@@ -50,8 +60,11 @@ public:
     size_t size() const { return n_; }
 
 private:
+    enum Mode { kPlain, kPool, kSyncFree };   // kSyncFree: no pools -- free after draining s
     void* p_ = nullptr;
     size_t n_ = 0;
+    hipStream_t s_ = nullptr;
+    Mode mode_ = kPlain;
 };
 
 // Device -> host copy of `bytes` at src, stream-ordered on s, through two pinned staging
@@ -60,11 +73,16 @@ private:
 void download_chunks(const void* src, size_t bytes, hipStream_t s,
                      const std::function<void(const void*, size_t)>& sink);
 
+// Asks the kernel to back [p, p + bytes) with huge pages (a hint; first touches of a large fresh
+// buffer otherwise fault one 4 KiB page at a time).
+void advise_huge_pages(void* p, size_t bytes);
+
 // count elements of device memory at src into a new host vector (no zero-fill first).
 template <class T>
 std::vector<T> download(const void* src, size_t count, hipStream_t s) {
     std::vector<T> v;
     v.reserve(count);
+    advise_huge_pages(v.data(), count * sizeof(T));
     download_chunks(src, count * sizeof(T), s, [&](const void* p, size_t n) {
         const T* t = static_cast<const T*>(p);
         v.insert(v.end(), t, t + n / sizeof(T));

@@ -75,15 +75,20 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     hip_check(hipSetDevice(tgr::backend_device(m.backend)), "hipSetDevice");
     hipStream_t s = tgr::backend_stream(m.backend);
 
-    DeviceBuffer dc((size_t)n * 12), dl((size_t)n * in_ch * 4);
-    hip_check(hipMemcpy(dc.get(), coords.data(), (size_t)n * 12, hipMemcpyHostToDevice), "decoder upload");
-    hip_check(hipMemcpy(dl.get(), latent.data(), latent.size() * 4, hipMemcpyHostToDevice), "decoder upload");
-    DeviceBuffer h((size_t)n * c0 * 4);
+    // every device buffer below is stream-ordered on s: nothing waits for the GPU until the end
+    DeviceBuffer dc((size_t)n * 12, s), dl((size_t)n * in_ch * 4, s);
+    hip_check(hipMemcpyAsync(dc.get(), coords.data(), (size_t)n * 12, hipMemcpyHostToDevice, s), "decoder upload");
+    hip_check(hipMemcpyAsync(dl.get(), latent.data(), latent.size() * 4, hipMemcpyHostToDevice, s),
+              "decoder upload");
+    DeviceBuffer h((size_t)n * c0 * 4, s);
     ops::run_linear(m, "from_latent", dl.as<float>(), n, in_ch, c0, false, 0.f, h.as<float>(), s);
     dl.reset();
     int c = c0;
     ops::Table table;
-    ops::build_table(dc.as<int32_t>(), n, table, s);
+    // coordinate range checks of every table of the pass, read once at the end
+    DeviceBuffer status(4, s);
+    hip_check(hipMemsetAsync(status.get(), 0, 4, s), "decoder");
+    ops::build_table(dc.as<int32_t>(), n, table, s, status.as<int32_t>());
     DeviceBuffer scratch, h2;
     for (size_t si = 0; si < stages.size(); ++si) {
         const Stage& g = stages[si];
@@ -92,32 +97,34 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
             if (a.c != c) fail(p + ": expected " + std::to_string(c) + " channels");
             if (a.conv.mfma) table.ensure_plan(s);
             const size_t need = ops::convnext_scratch(a, TSP_F32);
-            if (scratch.size() < need) {
-                hip_check(hipStreamSynchronize(s), "decoder");
-                scratch = DeviceBuffer(need);
-            }
-            if (h2.size() < (size_t)n * c * 4) h2 = DeviceBuffer((size_t)n * c * 4);
+            if (scratch.size() < need) scratch = DeviceBuffer(need, s);
+            if (h2.size() < (size_t)n * c * 4) h2 = DeviceBuffer((size_t)n * c * 4, s);
             ops::Carve sc(scratch.get());
             ops::run_convnext(a, h.get(), TSP_F32, table.nbr.as<int32_t>(), table.plan.get(), h2.as<float>(), sc, s);
             std::swap(h, h2);
         }
         if (g.cin != c) fail(g.c2s + ": expected " + std::to_string(c) + " input channels");
         const std::vector<uint8_t>* ext = guide ? &(*guide)[si] : nullptr;
-        ops::C2SOut o = ops::run_c2s(m, g.c2s, h.as<float>(), dc.as<int32_t>(), table, g.cin, g.cout, ext, s);
+        ops::C2SOut o = ops::run_c2s(m, g.c2s, h.as<float>(), dc.as<int32_t>(), table, g.cin, g.cout, ext, s,
+                                     status.as<int32_t>());
         if (subs_out) subs_out->push_back(std::move(o.mask));
         h = std::move(o.feats);
         dc = std::move(o.coords);
         table = std::move(o.table);
-        if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s);
+        if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s, status.as<int32_t>());
         n = o.m;
         c = g.cout;
     }
+    int32_t st = 0;
+    hip_check(hipMemcpyAsync(&st, status.get(), 4, hipMemcpyDeviceToHost, s), "decoder");
+    hip_check(hipStreamSynchronize(s), "decoder");
+    if (st) fail("decoder: a voxel coordinate lies outside [0, 2^21-3]");
     if (want_coords) coords = tgr::download<std::array<int, 3>>(dc.get(), (size_t)n, s);
     if (coords_only) return {};
     const ggml_tensor* wo = m.get("output_layer.weight");
     if (wo->ne[0] != c || wo->ne[1] != out_ch)
         fail("output_layer.weight: expected ggml shape [" + std::to_string(c) + ", " + std::to_string(out_ch) + "]");
-    DeviceBuffer out((size_t)n * out_ch * 4);
+    DeviceBuffer out((size_t)n * out_ch * 4, s);
     if (n) ops::run_linear(m, "output_layer", h.as<float>(), n, c, out_ch, true, 1e-5f, out.as<float>(), s);
     return tgr::download<float>(out.get(), (size_t)n * out_ch, s);
 }

@@ -168,31 +168,34 @@ size_t convnext_scratch(const ConvNext& a, int xdt) {
 }
 
 // ---- tables --------------------------------------------------------------------------------------
-void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s) {
+void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status) {
     t.n = n;
     t.plan = DeviceBuffer();
-    t.nbr = DeviceBuffer((size_t)27 * n * 4);
+    t.nbr = DeviceBuffer((size_t)27 * n * 4, s);
     if (n == 0) return;
-    DeviceBuffer ws(tsp_rulebook_workspace_bytes(n)), status(4);
-    hip_check(hipMemsetAsync(status.get(), 0, 4, s), "rulebook");
-    lib(tsp_rulebook_build(d_coords, n, t.nbr.as<int32_t>(), ws.get(), ws.size(), status.as<int32_t>(), s),
+    DeviceBuffer ws(tsp_rulebook_workspace_bytes(n), s), status(d_status ? 0 : 4, s);
+    if (!d_status) hip_check(hipMemsetAsync(status.get(), 0, 4, s), "rulebook");
+    lib(tsp_rulebook_build(d_coords, n, t.nbr.as<int32_t>(), ws.get(), ws.size(),
+                           d_status ? d_status : status.as<int32_t>(), s),
         "rulebook");
+    if (d_status) return;
     int32_t st = 0;
     hip_check(hipMemcpyAsync(&st, status.get(), 4, hipMemcpyDeviceToHost, s), "rulebook");
-    hip_check(hipStreamSynchronize(s), "rulebook");   // before `ws` is freed
+    hip_check(hipStreamSynchronize(s), "rulebook");
     if (st) fail("neighbour table: a coordinate lies outside [0, 2^21-3]");
 }
 
 void Table::ensure_plan(hipStream_t s) {
     if (plan.get() || n == 0) return;
     const size_t bytes = tsp_conv_plan_bytes(n);
-    plan = DeviceBuffer(bytes);
+    plan = DeviceBuffer(bytes, s);
     lib(tsp_conv_plan_build(nbr.as<int32_t>(), n, plan.get(), bytes, s), "conv plan");
 }
 
 // ---- C2S up-block (sparse.cpp:172-336) -----------------------------------------------------------
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
-               Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s) {
+               Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
+               int32_t* d_status) {
     const int64_t n = parent.n;
     if (cin <= 0 || cin % 8 != 0 || cout <= 0 || cout % (cin / 8) != 0)
         fail(prefix + ": C2S needs Cin % 8 == 0 and Cout % (Cin/8) == 0");
@@ -207,35 +210,41 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     const ggml_tensor* n1b = vec_param(m, prefix + ".norm1.bias", cin);
 
     // subdivision mask: the caller's, or to_subdiv logits > 0 (sparse.cpp:184-199, 215)
-    DeviceBuffer d_mask((size_t)8 * n);
+    // temporaries are stream-ordered on s: freed in queue order, no wait at the end
+    DeviceBuffer d_mask((size_t)8 * n, s);
     if (ext_mask) {
         hip_check(hipMemcpyAsync(d_mask.get(), ext_mask->data(), (size_t)8 * n, hipMemcpyHostToDevice, s),
                   "c2s mask upload");
     } else {
         const ggml_tensor* wsub = mat_param(m, prefix + ".to_subdiv.weight", cin, 8);
         const ggml_tensor* bsub = vec_param(m, prefix + ".to_subdiv.bias", 8);
-        DeviceBuffer d_logits((size_t)8 * n * 4), d_b(256);
+        DeviceBuffer d_logits((size_t)8 * n * 4, s), d_b(256, s);
         Carve sc(d_b.get());
         lib(tsp_linear(d_x, TSP_F32, n, cin, wsub->data, tgr::tsp_dtype_of(wsub->type), f32_param(bsub, sc, s),
                        8, d_logits.get(), TSP_F32, s),
             prefix + ".to_subdiv");
         lib(tsp_mask_positive(d_logits.as<float>(), 8 * n, d_mask.as<uint8_t>(), s), prefix + " mask");
-        hip_check(hipStreamSynchronize(s), "c2s mask");
     }
 
     // children, parent-major and octant-ascending (sparse.cpp:205-222)
-    DeviceBuffer d_mstart((size_t)(n + 1) * 4), d_child((size_t)8 * n * 12), d_gidx((size_t)8 * n * 4), d_m(8),
-        d_sws(tsp_subdivide_workspace_bytes(n));
+    DeviceBuffer d_mstart((size_t)(n + 1) * 4, s), d_child((size_t)8 * n * 12, s), d_gidx((size_t)8 * n * 4, s),
+        d_m(8, s), d_sws(tsp_subdivide_workspace_bytes(n), s);
     lib(tsp_subdivide(d_mask.as<uint8_t>(), d_coords, n, d_mstart.as<int32_t>(), d_child.as<int32_t>(),
                       d_gidx.as<int32_t>(), d_m.as<int64_t>(), d_sws.get(), d_sws.size(), s),
         prefix + " subdivide");
     int64_t mm = 0;
-    hip_check(hipMemcpyAsync(&mm, d_m.get(), 8, hipMemcpyDeviceToHost, s), "c2s");
-    hip_check(hipMemcpyAsync(r.mask.data(), d_mask.get(), (size_t)8 * n, hipMemcpyDeviceToHost, s), "c2s mask");
-    hip_check(hipStreamSynchronize(s), "c2s");
+    if (ext_mask) {
+        // the child count is the caller's mask's: no need to wait for the device
+        for (uint8_t b : *ext_mask) mm += b != 0;
+        std::copy(ext_mask->begin(), ext_mask->end(), r.mask.begin());
+    } else {
+        hip_check(hipMemcpyAsync(&mm, d_m.get(), 8, hipMemcpyDeviceToHost, s), "c2s");
+        hip_check(hipMemcpyAsync(r.mask.data(), d_mask.get(), (size_t)8 * n, hipMemcpyDeviceToHost, s), "c2s mask");
+        hip_check(hipStreamSynchronize(s), "c2s");
+    }
     r.m = mm;
-    r.coords = DeviceBuffer((size_t)mm * 12);
-    r.feats = DeviceBuffer((size_t)mm * cout * 4);
+    r.coords = DeviceBuffer((size_t)mm * 12, s);
+    r.feats = DeviceBuffer((size_t)mm * cout * 4, s);
     if (mm == 0) return r;
     hip_check(hipMemcpyAsync(r.coords.get(), d_child.get(), (size_t)mm * 12, hipMemcpyDeviceToDevice, s),
               "c2s");
@@ -252,7 +261,7 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     sz.take((size_t)mm * cout * es2);
     sz.take(s2);
     sz.take(2 * (size_t)cin * 4);
-    DeviceBuffer work(sz.off);
+    DeviceBuffer work(sz.off, s);
     Carve w(work.get());
     void* h0 = w.take((size_t)n * cin * es1);
     float* h1 = static_cast<float*>(w.take((size_t)n * 8 * cout * 4));
@@ -271,12 +280,11 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     // channel -> spatial gather, norm2 (no affine) + SiLU, conv2 on the children, skip
     lib(tsp_c2s_gather(h1, TSP_F32, d_gidx.as<int32_t>(), mm, cout, g, s), prefix + " gather");
     lib(tsp_layer_norm(g, TSP_F32, mm, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s), prefix + " norm2");
-    build_table(r.coords.as<int32_t>(), mm, r.table, s);
+    build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status);
     if (conv2.mfma) r.table.ensure_plan(s);
     run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s);
     lib(tsp_c2s_skip_add(d_x, TSP_F32, d_gidx.as<int32_t>(), mm, cin, cout, r.feats.get(), TSP_F32, s),
         prefix + " skip");
-    hip_check(hipStreamSynchronize(s), "c2s");   // before the temporaries are freed
     return r;
 }
 
@@ -288,7 +296,7 @@ void run_linear(const Model& m, const std::string& prefix, const float* d_x, int
     const int wdt = tgr::tsp_dtype_of(w->type);
     const bool mfma = !g_sparse_cast_f32 && (wdt == TSP_F16 || wdt == TSP_BF16) && ci % 32 == 0 && co % 64 == 0;
     const int xdt = mfma ? wdt : TSP_F32;
-    DeviceBuffer tmp((pre_norm || mfma) ? (size_t)n * ci * (mfma ? 2 : 4) : 0), pb((size_t)co * 4 + 256);
+    DeviceBuffer tmp((pre_norm || mfma) ? (size_t)n * ci * (mfma ? 2 : 4) : 0, s), pb((size_t)co * 4 + 256, s);
     Carve sc(pb.get());
     const float* bias = f32_param(b, sc, s);
     const void* x = d_x;
@@ -300,7 +308,6 @@ void run_linear(const Model& m, const std::string& prefix, const float* d_x, int
         x = tmp.get();
     }
     lib(tsp_linear(x, xdt, n, ci, w->data, wdt, bias, co, d_out, TSP_F32, s), prefix);
-    hip_check(hipStreamSynchronize(s), prefix.c_str());   // before the temporaries are freed
 }
 
 }  // namespace ops

@@ -72,8 +72,10 @@ struct Table {
     tgr::DeviceBuffer plan;   // empty until ensure_plan
     void ensure_plan(hipStream_t s);
 };
-// Builds the table of d_coords [n][3]; throws for coordinates outside [0, 2^21-3].
-void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s);
+// Builds the table of d_coords [n][3] (its buffers stream-ordered on s). Without d_status it
+// waits for the build and throws for coordinates outside [0, 2^21-3]; with d_status (a device
+// int32 the caller zeroed) it ORs the range check into it and returns without waiting.
+void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status = nullptr);
 
 // The C2S up-block on device data: x f32 [n][cin] on coords (table `parent`); ext_mask (host,
 // 8n entries) or, when null, the block's to_subdiv prediction. Returns the children's features
@@ -86,7 +88,8 @@ struct C2SOut {
     std::vector<uint8_t> mask;
 };
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
-               Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s);
+               Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
+               int32_t* d_status = nullptr);
 
 // out [n][co] f32 = (optionally LN(eps, no affine) of) x [n][ci] . W^T + b for `prefix.weight`
 // ggml [ci, co]; the input is rounded to the weight's 16-bit type when the matrix cores can run it.
