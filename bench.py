@@ -114,16 +114,23 @@ def decoder_bench(args) -> dict:
     exe = os.path.join(ROOT, "trellis.cpp_amd", "host", "bin", "decoder_bench")
     if not os.path.exists(exe):
         raise SystemExit(f"{exe} is not built (make -C trellis.cpp_amd/host)")
-    p = shells.decoder_params(w.channels, w.blocks, w.latent.shape[1], w.out_ch, w.std, w.seed)
-    with tempfile.TemporaryDirectory(prefix="decoder_bench_", dir="/tmp") as d:
+    def prepare(d):
+        p = shells.decoder_params(w.channels, w.blocks, w.latent.shape[1], w.out_ch, w.std, w.seed)
         write_gguf(os.path.join(d, "model.gguf"), p,
                    dtypes={k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()},
                    arch="trellis2-tex-dec")
-        del p
         np.save(os.path.join(d, "latent.npy"), w.latent)
         np.save(os.path.join(d, "coords.npy"), np.ascontiguousarray(w.coords, np.int32))
         for s, m in enumerate(w.masks):
             np.save(os.path.join(d, f"subs_{s}.npy"), np.ascontiguousarray(m, np.uint8))
+
+    if args.prepare_only:
+        os.makedirs(args.prepare_only, exist_ok=True)
+        prepare(args.prepare_only)
+        return {"prepared": args.prepare_only, "voxels_per_level": w.counts,
+                "run": f"{exe} {args.prepare_only}/model.gguf {args.prepare_only} 0 <warmup> <steps>"}
+    with tempfile.TemporaryDirectory(prefix="decoder_bench_", dir="/tmp") as d:
+        prepare(d)
         r = subprocess.run([exe, os.path.join(d, "model.gguf"), d, "0", str(args.warmup), str(args.steps)],
                            capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
@@ -221,6 +228,9 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prepare-only", default="", metavar="DIR",
+                    help="decoder workloads: only write the model and inputs into DIR (for running "
+                         "trellis.cpp_amd/host/bin/decoder_bench on them, e.g. under a profiler)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (the known-size kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
