@@ -121,3 +121,25 @@ def test_python_binding_rejects_host_tensors(pkg):
     import torch
     with pytest.raises(ValueError):
         pkg.rulebook_build(torch.zeros((4, 3), dtype=torch.int32))
+
+
+def test_linear_ex_validation(pkg):
+    """tsp_linear_ex: argument checks, and TSP_ERR_UNSUPPORTED (4) -- the caller's cue to fall
+    back to tsp_linear -- for f32 inputs, mixed dtypes, widths not a multiple of 8, misalignment
+    and a residual with 16-bit output, all before any device work."""
+    L = pkg.lib()
+    X, W, O, R = (ctypes.c_void_p(a) for a in (0x1000, 0x2000, 0x3000, 0x4000))
+    f = lambda **kw: L.tsp_linear_ex(
+        kw.get("x", X), kw.get("xdt", 2), kw.get("n", 100), kw.get("ci", 64), kw.get("w", W),
+        kw.get("wdt", 2), NULL, kw.get("co", 256), kw.get("act", 0), kw.get("res", NULL),
+        kw.get("out", O), kw.get("odt", 2), NULL)
+    assert f(n=-1) == 1 and f(act=7) == 1 and f(xdt=9) == 1
+    assert f(n=0) == 0                                   # empty: no-op
+    assert f(x=NULL) == 1 and f(out=X) == 1              # null / aliased
+    assert f(xdt=0, wdt=0, odt=0) == 4                   # f32: not a library GEMM here
+    assert f(wdt=1) == 4                                 # mixed 16-bit dtypes
+    assert f(ci=36) == 4 and f(co=250) == 4              # widths not multiples of 8
+    assert f(x=ctypes.c_void_p(0x1008)) == 4             # misaligned
+    assert f(res=R) == 4                                 # residual needs f32 output
+    assert f(res=ctypes.c_void_p(0x4004), odt=0) == 1    # misaligned residual
+    assert "residual" in _err(pkg)
