@@ -6,10 +6,11 @@
 // sorted surface sets those 512 voxels reference only ~1700 distinct input rows (against
 // ~9600 (voxel, tap) pairs), so instead of gathering every pair from L2 the tile gathers each
 // distinct row once:
-//   * tile plan: mark every referenced row in a two-level bitmap over [lo, hi] (the range of
-//     the tile's table entries), exclusive-scan the popcounts, and give each (tap, voxel) its
-//     rank in the set -- its slot. Slots are sorted by row, so consecutive voxels at one tap
-//     mostly get consecutive slots. Absent taps get the zero slot. The plan depends only on
+//   * tile plan: mark every referenced row in a bitmap over [lo, hi] (the range of the tile's
+//     table entries; one level for spans up to 64K rows, two beyond), exclusive-scan the
+//     popcounts, and give each (tap, voxel) its rank in the set -- its slot. Slots are sorted
+//     by row, so consecutive voxels at one tap mostly get consecutive slots. Absent taps get
+//     the zero slot. The plan depends only on
 //     the neighbour table, so it is built once and reused by every conv on that table (the
 //     reference shares one table across a decoder stage, shape_decoder.cpp:93-103); without a
 //     stored plan the kernel builds it in LDS itself.
@@ -23,7 +24,10 @@
 //     taps ahead. Packed weights ([co/32][ci/16][27][64 lanes][8]) make every weight load one
 //     contiguous 1 KiB per wave. All 27 taps are unrolled and slices go in pairs, so every
 //     register ring index is static and the compiler's load waits are exact.
-//   * the epilogue stages 32-row blocks of the accumulators in LDS and writes whole rows.
+//   * the epilogue stages row blocks of the accumulators in LDS and writes whole rows.
+//   * with a stored plan the grid is persistent (one workgroup per CU, each XCD's workgroups
+//     walking its range of tiles) and tiles are pipelined: a tile's last slice loads the next
+//     tile's first slice, first weight taps and slot table, so a tile starts with no round trip.
 // A tile whose row range or distinct-row count does not fit (scattered or unsorted inputs)
 // takes the direct path: the same MFMA loop with A gathered straight from global memory.
 #include <algorithm>
@@ -697,7 +701,6 @@ __device__ __forceinline__ void conv_tiles(
                 run_slice(acc, I0{}, NO{}, sH0, sH1, nkc - 2, nkc - 1, nullptr);
                 // the last slice streams the next tile's slice 0 (rows clamped to 0 where the
                 // plan holds none, e.g. a direct tile) and the first taps of its weights
-                if (ndirect) nrow[0] = 0;
                 set_poff(nrow, ndirect ? 0 : nH);
                 run_slice(acc, I1{}, std::true_type{}, sH1, sH0, nkc - 1, 0, plan.slots + ntile * HB_SLOT_TABLE);
                 // every wave is past its last read of sL and sH1
