@@ -16,10 +16,11 @@
 //     stored plan the kernel builds it in LDS itself.
 //   * the distinct rows stream through LDS 16 channels at a time (two buffers, each a separate
 //     LDS object), the next slice loading while the current one runs all 27 taps: each lane
-//     loads its 16-byte pieces into registers and writes them to LDS a few taps later. Each
-//     buffer holds the two 8-channel halves of a row in separate planes, so the 32 lanes that
-//     feed one MFMA operand read 32 consecutive 16-byte words when the slots are consecutive;
-//     absent taps read a zero slot kept past the loaded ones.
+//     loads its 16-byte pieces (a lane pair per row, so a load touches 32 rows) into registers
+//     and writes them to LDS a few taps later. Each buffer holds the two 8-channel halves of a
+//     row in separate planes, so the 32 lanes that feed one MFMA operand read 32 consecutive
+//     16-byte words when the slots are consecutive; absent taps read a zero slot kept past the
+//     loaded ones.
 //   * per tap, A operands are read from LDS by slot and B operands (weights) come from L2 two
 //     taps ahead. Packed weights ([co/32][ci/16][27][64 lanes][8]) make every weight load one
 //     contiguous 1 KiB per wave. All 27 taps are unrolled and slices go in pairs, so every
@@ -394,9 +395,10 @@ __device__ __forceinline__ void conv_tiles(
     int rg = wave % NRG;                     // row group: voxels [32 RB rg, +32 RB)
     const int c0 = (int)(lin0 % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
     const int nkc = ci / HB_KC;
-    // slice loads: wave w streams plane (w & 1), 64-slot blocks (w >> 1) + (WAVES/2) j
-    int plane = wave & 1;
-    auto piece_slot = [&](int j) { return 64 * ((wave >> 1) + (WAVES / 2) * j); };
+    // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
+    // planes of one row (32 contiguous bytes; a load touches 32 rows, not 64)
+    int plane = lane & 1;
+    auto piece_slot = [&](int j) { return 32 * (wave + WAVES * j); };
     // cross-tile pipelining needs slices in pairs and the slot table in the idle piece ring
     const bool pipelined = PLANNED && WAVES == 8 && SLOT_BLOCKS <= NSTG && T_FREE < kTaps &&
                            nkc % 2 == 0;
@@ -437,7 +439,7 @@ __device__ __forceinline__ void conv_tiles(
     auto set_poff = [&](int32_t (&prow)[PIECES], int H) {
 #pragma unroll
         for (int j = 0; j < PIECES; ++j) {
-            const int32_t r = (piece_slot(j) + lane < H && (uint32_t)prow[j] < (uint32_t)n) ? prow[j] : 0;
+            const int32_t r = (piece_slot(j) + (lane >> 1) < H && (uint32_t)prow[j] < (uint32_t)n) ? prow[j] : 0;
             poff[j] = (uint32_t)r * (uint32_t)ci * 2u + plane * 16u;
             // kept as 32-bit offsets for the scalar-base + vector-offset load form
             asm volatile("" : "+v"(poff[j]));
@@ -448,7 +450,7 @@ __device__ __forceinline__ void conv_tiles(
                                               (uint32_t)kc * (HB_KC * 2));
     };
     auto put_piece = [&](uint16_t (*dst)[HB_ROWS][8], int j, const u32x4_t& r) {
-        *reinterpret_cast<u32x4_t*>(&dst[plane][piece_slot(j) + lane][0]) = r;
+        *reinterpret_cast<u32x4_t*>(&dst[plane][piece_slot(j) + (lane >> 1)][0]) = r;
     };
     // A operands of tap t: per 128 voxels one 8-byte read of four slots, then one 16-byte
     // read per 32-row block
@@ -587,7 +589,7 @@ __device__ __forceinline__ void conv_tiles(
                         16, 0, 0);
                 const int32_t* ro = plan.rowof + tile * HB_SLOTS;
 #pragma unroll
-                for (int j = 0; j < PIECES; ++j) prow[j] = ro[piece_slot(j) + lane];
+                for (int j = 0; j < PIECES; ++j) prow[j] = ro[piece_slot(j) + (lane >> 1)];
                 H = h0;
                 direct = h1 != 0;
             } else {
@@ -595,7 +597,7 @@ __device__ __forceinline__ void conv_tiles(
                               reinterpret_cast<uint32_t*>(&sH1[0][0][0]), sRed, H, direct);
                 const int32_t* sRowOf = reinterpret_cast<const int32_t*>(&sH0[0][0][0]);
 #pragma unroll
-                for (int j = 0; j < PIECES; ++j) prow[j] = direct ? 0 : sRowOf[(piece_slot(j) + lane) % HB_SLOTS];
+                for (int j = 0; j < PIECES; ++j) prow[j] = direct ? 0 : sRowOf[(piece_slot(j) + (lane >> 1)) % HB_SLOTS];
                 __syncthreads();     // sH0 is overwritten by the first slice below
             }
             if (!direct) {
@@ -697,7 +699,7 @@ __device__ __forceinline__ void conv_tiles(
                 int32_t nrow[PIECES];
                 const int32_t* nro = plan.rowof + ntile * HB_SLOTS;
 #pragma unroll
-                for (int j = 0; j < PIECES; ++j) nrow[j] = nro[piece_slot(j) + lane];
+                for (int j = 0; j < PIECES; ++j) nrow[j] = nro[piece_slot(j) + (lane >> 1)];
                 run_slice(acc, I0{}, NO{}, sH0, sH1, nkc - 2, nkc - 1, nullptr);
                 // the last slice streams the next tile's slice 0 (rows clamped to 0 where the
                 // plan holds none, e.g. a direct tile) and the first taps of its weights
