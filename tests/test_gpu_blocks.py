@@ -115,6 +115,37 @@ def test_c2s_gather_and_skip(gpu_lib, golden):
     assert np.array_equal(acc.cpu().numpy(), acc0 + skip)
 
 
+@pytest.mark.parametrize("rep", [1, 4])
+def test_bf16_store_rounding(gpu_lib, rep):
+    """fp32 -> bf16 stores round to nearest even, bit for bit: the C2S skip into a zeroed bf16
+    accumulator stores bf16(x + 0) for every element of x (rep 4 takes the vectorized kernel,
+    rep 1 the scalar one). The expected bits come from torch's CPU conversion. Inputs: random
+    finite bit patterns, exact ties (low half 0x8000) on even and odd bf16 values, the patterns
+    next to them, subnormals, values that round up to the next binade or to infinity, and
+    +-infinity."""
+    _case(f"bf16 rounding rep={rep}")
+    import torch
+    rng = np.random.default_rng(11 + rep)
+    hi = rng.integers(0, 1 << 16, 1 << 16, dtype=np.uint32)
+    parts = [rng.integers(0, 1 << 32, 1 << 18, dtype=np.uint64).astype(np.uint32)]
+    parts += [(hi << 16) | low for low in (0x8000, 0x7FFF, 0x8001, 0xFFFF, 0x0000)]
+    parts.append(rng.integers(1, 1 << 23, 1 << 14, dtype=np.uint32) | (rng.integers(0, 2, 1 << 14, dtype=np.uint32) << 31))
+    parts.append(np.arange(0x7F7F7F00, 0x7F800000, dtype=np.uint32))
+    parts.append(np.array([0x7F800000, 0xFF800000, 0x3F7FFFFF, 0x3F7F8000, 0x00008000], np.uint32))
+    bits = np.concatenate(parts)
+    bits = bits[(bits & 0x7FFFFFFF) <= 0x7F800000]      # NaN excluded: x + 0 may requiet it
+    k = 16
+    bits = np.concatenate([bits, np.zeros((-len(bits)) % (8 * k), np.uint32)])
+    x = bits.view(np.float32).reshape(-1, 8 * k)
+    m = x.shape[0] * 8
+    gidx = np.arange(m, dtype=np.int32)
+    acc = torch.zeros((m, k * rep), dtype=torch.bfloat16, device="cuda")
+    gpu_lib.c2s_skip_add(_t(x), _t(gidx), acc)
+    want = torch.from_numpy(np.repeat(x.reshape(m, k) + np.float32(0), rep, axis=1)).to(torch.bfloat16)
+    got = acc.cpu()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 def test_mask_positive(gpu_lib):
     _case("mask")
     x = np.array([[-1.0, 0.0, 2.0, -0.0, 1e-30, -1e-30, np.inf, -np.inf]], np.float32)

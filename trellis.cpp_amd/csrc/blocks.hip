@@ -75,10 +75,12 @@ __device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {
     if constexpr (DT == TSP_F32) {
         *reinterpret_cast<f32x4_t*>(static_cast<float*>(p) + i) = f32x4_t{v[0], v[1], v[2], v[3]};
     } else {
-        uint32_t h[4];
+        uint32_t w[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = DT == TSP_BF16 ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        for (int e = 0; e < 2; ++e)
+            w[e] = DT == TSP_BF16 ? f32x2_to_bf16x2_bits(v[2 * e], v[2 * e + 1])
+                                  : f32_to_f16_bits(v[2 * e]) | ((uint32_t)f32_to_f16_bits(v[2 * e + 1]) << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = uint2{w[0], w[1]};
     }
 }
 

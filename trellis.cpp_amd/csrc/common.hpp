@@ -48,12 +48,17 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
-// Round to nearest even; NaN stays NaN (quiet bit forced).
+// Round to nearest even; NaN stays NaN with its sign and upper payload bits and the quiet bit
+// forced. On gfx950 the conversion is v_cvt_pk_bf16_f32, two values per instruction; it gives
+// exactly these bits for every one of the 2^32 float patterns (checked against the integer form
+// u += 0x7fff + ((u >> 16) & 1), NaN -> (u >> 16) | 0x40).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return static_cast<uint16_t>(f32x2_to_bf16x2_bits(f, 0.f));
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return __half2float(__ushort_as_half(b));

@@ -537,9 +537,8 @@ __device__ __forceinline__ void conv_tiles(
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const float lo = vs[q][e / 2][(2 * e) % 4], hi = vs[q][e / 2][(2 * e) % 4 + 1];
-                                const uint32_t a = (ODT == TSP_BF16) ? f32_to_bf16_bits(lo) : f32_to_f16_bits(lo);
-                                const uint32_t b = (ODT == TSP_BF16) ? f32_to_bf16_bits(hi) : f32_to_f16_bits(hi);
-                                w[e] = a | (b << 16);
+                                w[e] = (ODT == TSP_BF16) ? f32x2_to_bf16x2_bits(lo, hi)
+                                                         : f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
                             }
                             *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + o) =
                                 u32x4_t{w[0], w[1], w[2], w[3]};
