@@ -38,53 +38,76 @@ DeviceBuffer::DeviceBuffer(size_t bytes) : n_(bytes) {
 }
 
 namespace {
-// Per device: 1 = memory pools (their release threshold raised so that freed memory stays in the
-// pool), -1 = no pool support, 0 = not probed yet.
-int g_pool_state[64] = {0};
-std::mutex g_pool_mu;
-
-bool pools_ready() {
-    int dev = 0;
-    hip_check(hipGetDevice(&dev), "hipGetDevice");
-    if (dev < 0 || dev >= 64) return false;
-    std::lock_guard<std::mutex> lock(g_pool_mu);
-    if (!g_pool_state[dev]) {
-        int supported = 0;
-        hipMemPool_t pool = nullptr;
-        uint64_t keep = UINT64_MAX;
-        g_pool_state[dev] =
-            hipDeviceGetAttribute(&supported, hipDeviceAttributeMemoryPoolsSupported, dev) == hipSuccess &&
-                    supported && hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess &&
-                    hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) == hipSuccess
-                ? 1 : -1;
+// Idle blocks per (device, stream), by size. Allocated once and never destroyed, so that buffers
+// released during static destruction still find it.
+struct BlockCache {
+    std::mutex mu;
+    std::map<std::pair<int, hipStream_t>, std::multimap<size_t, void*>> idle;
+};
+BlockCache& block_cache() {
+    static BlockCache* c = new BlockCache;
+    return *c;
+}
+// Block sizes: 4 KiB steps up to 1 MiB, 2 MiB steps above, so that a repeated request pattern
+// (the same decoder again) is served from the cache block for block.
+size_t block_bytes(size_t bytes) {
+    constexpr size_t kSmall = size_t(1) << 20, kPage = size_t(4) << 10, kLarge = size_t(2) << 20;
+    return bytes <= kSmall ? (bytes + kPage - 1) / kPage * kPage : (bytes + kLarge - 1) / kLarge * kLarge;
+}
+// Frees every idle block of device dev once the device has finished all queued work.
+void free_idle_blocks(int dev) {
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    BlockCache& c = block_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    for (auto& [key, blocks] : c.idle) {
+        if (key.first != dev) continue;
+        for (auto& [bytes, p] : blocks) (void)hipFree(p);
+        blocks.clear();
     }
-    return g_pool_state[dev] > 0;
 }
 }  // namespace
 
-DeviceBuffer::DeviceBuffer(size_t bytes, hipStream_t s) : n_(bytes), s_(s) {
+DeviceBuffer::DeviceBuffer(size_t bytes, hipStream_t s) : n_(bytes), s_(s), mode_(kCached) {
     if (!bytes) return;
-    if (pools_ready()) {
-        mode_ = kPool;
-        hip_check(hipMallocAsync(&p_, bytes, s), "hipMallocAsync");
-    } else {
-        mode_ = kSyncFree;
-        hip_check(hipMalloc(&p_, bytes), "hipMalloc");
+    hip_check(hipGetDevice(&dev_), "hipGetDevice");
+    const size_t want = block_bytes(bytes);
+    {
+        BlockCache& c = block_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        auto& idle = c.idle[{dev_, s}];
+        // the smallest idle block that fits, unless it is more than twice the size needed
+        auto it = idle.lower_bound(want);
+        if (it != idle.end() && it->first <= 2 * want) {
+            cap_ = it->first;
+            p_ = it->second;
+            idle.erase(it);
+            return;
+        }
     }
+    hipError_t e = hipMalloc(&p_, want);
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        p_ = nullptr;
+        free_idle_blocks(dev_);
+        e = hipMalloc(&p_, want);
+    }
+    hip_check(e, "hipMalloc");
+    cap_ = want;
 }
 DeviceBuffer::~DeviceBuffer() { reset(); }
 
 void DeviceBuffer::reset() {
     if (p_) {
-        if (mode_ == kPool) {
-            (void)hipFreeAsync(p_, s_);
+        if (mode_ == kCached) {
+            BlockCache& c = block_cache();
+            std::lock_guard<std::mutex> lock(c.mu);
+            c.idle[{dev_, s_}].emplace(cap_, p_);
         } else {
-            if (mode_ == kSyncFree) (void)hipStreamSynchronize(s_);
             (void)hipFree(p_);
         }
     }
     p_ = nullptr;
-    n_ = 0;
+    n_ = cap_ = 0;
 }
 
 namespace {

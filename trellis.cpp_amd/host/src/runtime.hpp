@@ -25,11 +25,14 @@ inline size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a
 [[noreturn]] void fail(const std::string& msg);   // throws std::runtime_error
 void hip_check(hipError_t e, const char* what);    // throws on error
 
-// Owning device allocation on the current device. The stream-ordered form allocates from the
-// device's memory pool in the order of stream s and frees in that order too, so a buffer may go
-// out of scope while work queued on s still uses it, without a synchronisation; the pool keeps
-// freed memory for later allocations (no hipMalloc / hipFree, and their implicit device
-// synchronisation, once a decoder has run).
+// Owning device allocation on the current device. The stream-ordered form takes a block from a
+// cache kept per (device, stream) and gives it back there when it goes out of scope, without a
+// synchronisation: the block is only handed out again to a later allocation on the same stream,
+// whose work runs after everything queued before the release. Blocks come from hipMalloc and stay
+// cached until the process ends; an allocation that finds the device full first synchronises the
+// device and frees the cached blocks. (HIP's stream-ordered pool, hipMallocAsync / hipFreeAsync,
+// is not used: under the decoders' allocation pattern its calls blocked the host for 0.1-5 s at
+// times.)
 class DeviceBuffer {
 public:
     DeviceBuffer() = default;
@@ -38,19 +41,22 @@ public:
     ~DeviceBuffer();
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_), s_(o.s_), mode_(o.mode_) {
+    DeviceBuffer(DeviceBuffer&& o) noexcept
+        : p_(o.p_), n_(o.n_), cap_(o.cap_), s_(o.s_), dev_(o.dev_), mode_(o.mode_) {
         o.p_ = nullptr;
-        o.n_ = 0;
+        o.n_ = o.cap_ = 0;
     }
     DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
         if (this != &o) {
             reset();
             p_ = o.p_;
             n_ = o.n_;
+            cap_ = o.cap_;
             s_ = o.s_;
+            dev_ = o.dev_;
             mode_ = o.mode_;
             o.p_ = nullptr;
-            o.n_ = 0;
+            o.n_ = o.cap_ = 0;
         }
         return *this;
     }
@@ -60,10 +66,12 @@ public:
     size_t size() const { return n_; }
 
 private:
-    enum Mode { kPlain, kPool, kSyncFree };   // kSyncFree: no pools -- free after draining s
+    enum Mode { kPlain, kCached };
     void* p_ = nullptr;
-    size_t n_ = 0;
+    size_t n_ = 0;     // bytes asked for
+    size_t cap_ = 0;   // bytes of the cached block
     hipStream_t s_ = nullptr;
+    int dev_ = 0;
     Mode mode_ = kPlain;
 };
 
