@@ -1,9 +1,10 @@
 // Runs the device-resident decoders of this build on a GGUF model and writes their results:
-//   decoder_check <model.gguf> <dir> [gpu] [--f32] [--tex | --upsample]
+//   decoder_check <model.gguf> <dir> [gpu] [--f32] [--tex | --upsample] [--repeat K]
 // dir holds latent.npy [N, Cl] f32 and coords.npy [N, 3] int32; with --tex also subs_<s>.npy
 // (u8 [8 N_s]) per stage, which drive tex_decode. shape_decode writes out.npy [M, 7] f32,
 // coords_out.npy [M, 3] and subs_out_<s>.npy; tex_decode writes out.npy [M, 6]; shape_upsample
-// writes coords_out.npy. Prints "M=<m> ...".
+// writes coords_out.npy. Prints "M=<m> ...". With --repeat K, tex_decode runs K times (the later
+// runs reuse the device blocks the earlier ones released) and every run must give the same bits.
 #include <array>
 #include <cstdio>
 #include <cstdlib>
@@ -24,8 +25,10 @@ int main(int argc, char** argv) {
     const std::string dir = argv[2];
     int gpu = 0;
     bool tex = false, upsample = false;
+    int repeat = 1;
     for (int i = 3; i < argc; ++i) {
         if (!strcmp(argv[i], "--f32")) trellis::g_sparse_cast_f32 = true;
+        else if (!strcmp(argv[i], "--repeat") && i + 1 < argc) repeat = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--tex")) tex = true;
         else if (!strcmp(argv[i], "--upsample")) upsample = true;
         else gpu = atoi(argv[i]);
@@ -52,6 +55,13 @@ int main(int argc, char** argv) {
                 subs.emplace_back(a.bytes.begin(), a.bytes.end());
             }
             out = trellis::tex_decode(m, latent, coords, subs);
+            for (int r = 1; r < repeat; ++r) {
+                const std::vector<float> again = trellis::tex_decode(m, latent, coords, subs);
+                if (again.size() != out.size() || memcmp(again.data(), out.data(), out.size() * 4)) {
+                    fprintf(stderr, "error: tex_decode run %d differs from run 0\n", r);
+                    return 4;
+                }
+            }
             out_ch = 6;
         } else if (upsample) {
             oc = trellis::shape_upsample(m, latent, coords);

@@ -147,7 +147,9 @@ def test_tex_decode_bf16_decoder_workload(gpu, orc, shells, tmp_path):
     np.save(tmp_path / "coords.npy", np.ascontiguousarray(w.coords, np.int32))
     for s, m in enumerate(w.masks):
         np.save(tmp_path / f"subs_{s}.npy", m)
-    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0", "--tex"])
+    # three decodes in one process: the later ones run on device blocks the first released
+    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0", "--tex",
+          "--repeat", "3"])
     q = {k: (shells.round_to(v, "bf16") if v.ndim >= 2 else v) for k, v in p.items()}
     stages = [([f"blocks.{s}.{j}" for j in range(w.blocks)], (f"blocks.{s}.{w.blocks}", ci, co))
               for s, (ci, co) in enumerate(zip(w.channels[:-1], w.channels[1:]))]
