@@ -15,6 +15,7 @@
 #include <mutex>
 #include <unordered_map>
 #include <unordered_set>
+#include <thread>
 #include <vector>
 
 #include <sys/mman.h>
@@ -150,6 +151,25 @@ void download_chunks(const void* src, size_t bytes, hipStream_t s,
         hip_check(hipEventSynchronize(g_stage_ev[dev][i % 2]), "download");
         sink(g_stage[i % 2], std::min(kStageChunk, bytes - i * kStageChunk));
     }
+}
+
+void download_into(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const size_t nthr = std::max<size_t>(1, std::min<size_t>(8, hw ? hw : 1));
+    char* out = static_cast<char*>(dst);
+    size_t done = 0;
+    download_chunks(src, bytes, s, [&](const void* p, size_t n) {
+        // n is a multiple of 64 except for the last chunk; each thread copies a 64-byte-aligned part
+        const size_t part = (n / nthr + 63) / 64 * 64;
+        std::vector<std::thread> th;
+        for (size_t k = 1; k < nthr && k * part < n; ++k)
+            th.emplace_back([=] {
+                memcpy(out + done + k * part, static_cast<const char*>(p) + k * part, std::min(part, n - k * part));
+            });
+        memcpy(out + done, p, std::min(part, n));
+        for (auto& t : th) t.join();
+        done += n;
+    });
 }
 
 int tsp_dtype_of(enum ggml_type t) {

@@ -7,10 +7,12 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <exception>
 #include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "ggml-backend.h"
@@ -84,6 +86,49 @@ void download_chunks(const void* src, size_t bytes, hipStream_t s,
 // Asks the kernel to back [p, p + bytes) with huge pages (a hint; first touches of a large fresh
 // buffer otherwise fault one 4 KiB page at a time).
 void advise_huge_pages(void* p, size_t bytes);
+
+// Device -> host copy of `bytes` at src into host memory at dst, stream-ordered on s: each staged
+// chunk is copied out by several host threads. dst should be touched memory (see HostVector).
+void download_into(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+// A host vector of `count` value-initialised elements, made on a thread of its own: the first
+// touches of a large fresh buffer (page faults, the kernel zeroing the pages) then overlap with
+// device work queued before the result is needed. take() waits for the thread and hands the
+// vector over (rethrowing what the thread threw).
+template <class T>
+class HostVector {
+public:
+    HostVector() = default;
+    explicit HostVector(size_t count) { start(count); }
+    HostVector(const HostVector&) = delete;
+    HostVector& operator=(const HostVector&) = delete;
+    ~HostVector() {
+        if (th_.joinable()) th_.join();
+    }
+    void start(size_t count) {
+        if (th_.joinable()) th_.join();
+        th_ = std::thread([this, count] {
+            try {
+                v_.clear();
+                v_.reserve(count);
+                advise_huge_pages(v_.data(), count * sizeof(T));
+                v_.resize(count);
+            } catch (...) {
+                err_ = std::current_exception();
+            }
+        });
+    }
+    std::vector<T> take() {
+        if (th_.joinable()) th_.join();
+        if (err_) std::rethrow_exception(err_);
+        return std::move(v_);
+    }
+
+private:
+    std::vector<T> v_;
+    std::thread th_;
+    std::exception_ptr err_;
+};
 
 // count elements of device memory at src into a new host vector (no zero-fill first).
 template <class T>

@@ -90,6 +90,21 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     hip_check(hipMemsetAsync(status.get(), 0, 4, s), "decoder");
     ops::build_table(dc.as<int32_t>(), n, table, s, status.as<int32_t>());
     DeviceBuffer scratch, h2;
+    // The result's host memory is touched on threads of their own while the device works: from
+    // the start when the masks fix the final voxel count, else once the last subdivision is known.
+    tgr::HostVector<float> result;
+    tgr::HostVector<std::array<int, 3>> result_coords;
+    bool result_started = false;
+    auto start_result = [&](int64_t m_final) {
+        if (!coords_only) result.start((size_t)m_final * out_ch);
+        if (want_coords) result_coords.start((size_t)m_final);
+        result_started = true;
+    };
+    if (guide && !stages.empty()) {
+        int64_t m_final = 0;
+        for (uint8_t b : (*guide)[stages.size() - 1]) m_final += b != 0;
+        start_result(m_final);
+    }
     for (size_t si = 0; si < stages.size(); ++si) {
         const Stage& g = stages[si];
         for (const std::string& p : g.convnext) {   // ConvNeXt stage, ping-pong buffers
@@ -114,19 +129,28 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s, status.as<int32_t>());
         n = o.m;
         c = g.cout;
+        if (!result_started && si + 1 == stages.size()) start_result(n);
     }
+    if (!result_started) start_result(n);
     int32_t st = 0;
     hip_check(hipMemcpyAsync(&st, status.get(), 4, hipMemcpyDeviceToHost, s), "decoder");
     hip_check(hipStreamSynchronize(s), "decoder");
     if (st) fail("decoder: a voxel coordinate lies outside [0, 2^21-3]");
-    if (want_coords) coords = tgr::download<std::array<int, 3>>(dc.get(), (size_t)n, s);
+    if (want_coords) {
+        coords = result_coords.take();
+        if (coords.size() != (size_t)n) fail("decoder: the masks' final voxel count is not the decoded one");
+        tgr::download_into(coords.data(), dc.get(), (size_t)n * 12, s);
+    }
     if (coords_only) return {};
     const ggml_tensor* wo = m.get("output_layer.weight");
     if (wo->ne[0] != c || wo->ne[1] != out_ch)
         fail("output_layer.weight: expected ggml shape [" + std::to_string(c) + ", " + std::to_string(out_ch) + "]");
     DeviceBuffer out((size_t)n * out_ch * 4, s);
     if (n) ops::run_linear(m, "output_layer", h.as<float>(), n, c, out_ch, true, 1e-5f, out.as<float>(), s);
-    return tgr::download<float>(out.get(), (size_t)n * out_ch, s);
+    std::vector<float> feats = result.take();
+    if (feats.size() != (size_t)n * out_ch) fail("decoder: the masks' final voxel count is not the decoded one");
+    tgr::download_into(feats.data(), out.get(), feats.size() * 4, s);
+    return feats;
 }
 
 }  // namespace
