@@ -11,6 +11,7 @@
 #include "shape_decoder.h"
 
 #include <cstdio>
+#include <future>
 #include <string>
 
 #include "ggml.h"
@@ -100,11 +101,16 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         if (want_coords) result_coords.start((size_t)m_final);
         result_started = true;
     };
-    if (guide && !stages.empty()) {
-        int64_t m_final = 0;
-        for (uint8_t b : (*guide)[stages.size() - 1]) m_final += b != 0;
-        start_result(m_final);
-    }
+    // with masks, every stage's child count is counted on a thread of its own, off the path that
+    // keeps the device fed
+    std::future<std::vector<int64_t>> guide_counts;
+    std::vector<int64_t> counts;
+    if (guide)
+        guide_counts = std::async(std::launch::async, [guide, ns = stages.size()] {
+            std::vector<int64_t> c(ns);
+            for (size_t i = 0; i < ns; ++i) c[i] = ops::count_nonzero((*guide)[i].data(), (*guide)[i].size());
+            return c;
+        });
     for (size_t si = 0; si < stages.size(); ++si) {
         const Stage& g = stages[si];
         for (const std::string& p : g.convnext) {   // ConvNeXt stage, ping-pong buffers
@@ -120,8 +126,12 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         }
         if (g.cin != c) fail(g.c2s + ": expected " + std::to_string(c) + " input channels");
         const std::vector<uint8_t>* ext = guide ? &(*guide)[si] : nullptr;
+        if (guide && counts.empty()) {
+            counts = guide_counts.get();
+            start_result(counts.back());
+        }
         ops::C2SOut o = ops::run_c2s(m, g.c2s, h.as<float>(), dc.as<int32_t>(), table, g.cin, g.cout, ext, s,
-                                     status.as<int32_t>());
+                                     status.as<int32_t>(), subs_out != nullptr, guide ? counts[si] : -1);
         if (subs_out) subs_out->push_back(std::move(o.mask));
         h = std::move(o.feats);
         dc = std::move(o.coords);

@@ -193,15 +193,30 @@ void Table::ensure_plan(hipStream_t s) {
 }
 
 // ---- C2S up-block (sparse.cpp:172-336) -----------------------------------------------------------
+int64_t count_nonzero(const uint8_t* p, size_t n) {
+    // eight bytes at a time: a byte's high bit is set in z exactly when the byte is zero
+    constexpr uint64_t kLow7 = 0x7f7f7f7f7f7f7f7full;
+    int64_t zeros = 0;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        uint64_t w;
+        memcpy(&w, p + i, 8);
+        const uint64_t z = ~(((w & kLow7) + kLow7) | w | kLow7);
+        zeros += __builtin_popcountll(z);
+    }
+    for (; i < n; ++i) zeros += p[i] == 0;
+    return (int64_t)n - zeros;
+}
+
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
                Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
-               int32_t* d_status) {
+               int32_t* d_status, bool want_mask, int64_t ext_count) {
     const int64_t n = parent.n;
     if (cin <= 0 || cin % 8 != 0 || cout <= 0 || cout % (cin / 8) != 0)
         fail(prefix + ": C2S needs Cin % 8 == 0 and Cout % (Cin/8) == 0");
     if (ext_mask && (int64_t)ext_mask->size() != 8 * n) fail(prefix + ": ext_subdiv must hold 8*N entries");
     C2SOut r;
-    r.mask.resize((size_t)8 * n);
+    if (want_mask) r.mask.resize((size_t)8 * n);
     if (n == 0) return r;
     const Conv conv1 = conv_of(m, prefix + ".conv1"), conv2 = conv_of(m, prefix + ".conv2");
     if (conv1.ci != cin || conv1.co != 8 * cout || conv2.ci != cout || conv2.co != cout)
@@ -235,11 +250,13 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     int64_t mm = 0;
     if (ext_mask) {
         // the child count is the caller's mask's: no need to wait for the device
-        for (uint8_t b : *ext_mask) mm += b != 0;
-        std::copy(ext_mask->begin(), ext_mask->end(), r.mask.begin());
+        mm = ext_count >= 0 ? ext_count : count_nonzero(ext_mask->data(), ext_mask->size());
+        if (want_mask) std::copy(ext_mask->begin(), ext_mask->end(), r.mask.begin());
     } else {
         hip_check(hipMemcpyAsync(&mm, d_m.get(), 8, hipMemcpyDeviceToHost, s), "c2s");
-        hip_check(hipMemcpyAsync(r.mask.data(), d_mask.get(), (size_t)8 * n, hipMemcpyDeviceToHost, s), "c2s mask");
+        if (want_mask)
+            hip_check(hipMemcpyAsync(r.mask.data(), d_mask.get(), (size_t)8 * n, hipMemcpyDeviceToHost, s),
+                      "c2s mask");
         hip_check(hipStreamSynchronize(s), "c2s");
     }
     r.m = mm;

@@ -77,10 +77,14 @@ struct Table {
 // int32 the caller zeroed) it ORs the range check into it and returns without waiting.
 void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status = nullptr);
 
+// Nonzero bytes of p[0, n) (the children a subdivision mask asks for).
+int64_t count_nonzero(const uint8_t* p, size_t n);
+
 // The C2S up-block on device data: x f32 [n][cin] on coords (table `parent`); ext_mask (host,
 // 8n entries) or, when null, the block's to_subdiv prediction. Returns the children's features
-// f32 [m][cout], coords [m][3], their table (with plan if conv2 uses the matrix cores) and the
-// [8n] mask used (on the host).
+// f32 [m][cout], coords [m][3], their table (with plan if conv2 uses the matrix cores) and, with
+// want_mask, the [8n] mask used (on the host). ext_count, when >= 0, is count_nonzero of ext_mask,
+// counted by the caller beforehand.
 struct C2SOut {
     int64_t m = 0;
     tgr::DeviceBuffer feats, coords;
@@ -89,7 +93,7 @@ struct C2SOut {
 };
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
                Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
-               int32_t* d_status = nullptr);
+               int32_t* d_status = nullptr, bool want_mask = true, int64_t ext_count = -1);
 
 // out [n][co] f32 = (optionally LN(eps, no affine) of) x [n][ci] . W^T + b for `prefix.weight`
 // ggml [ci, co]; the input is rounded to the weight's 16-bit type when the matrix cores can run it.
