@@ -159,7 +159,95 @@ hipError_t binary_typed(const ggml_tensor* a, const ggml_tensor* b, float* out, 
     return hipErrorInvalidValue;
 }
 
+// The decoders' head (shape_decoder.cpp:63-77, 116): out[r][o] = bias[o] + sum_i LN(x[r])[i] W[o][i]
+// with LN the row LayerNorm of eps without affine, for co <= 8 outputs. L lanes hold a row, each V
+// groups of 4 channels (ci = 4 L V); the row is normalised in registers and every output is a
+// reduction over the row's lanes, so x is read once and nothing else is written.
+constexpr int kHeadMaxCo = 8;
+template <int WDT, int L, int V>
+__global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x, int64_t n, float eps,
+                                                     const void* __restrict__ w, const float* __restrict__ bias,
+                                                     int co, float* __restrict__ out) {
+    constexpr int R = 64 / L, C = 4 * L * V;
+    const int lane = threadIdx.x & 63, sub = lane % L;
+    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R + lane / L;
+    const bool live = row < n;
+    const float* xr = x + (live ? row : 0) * C;
+    float v[V][4];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const float4 t = *reinterpret_cast<const float4*>(xr + (j * L + sub) * 4);
+        v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += v[j][e];
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float mean = sum / (float)C;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[j][e] -= mean;
+            q += v[j][e] * v[j][e];
+        }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+    const float rstd = 1.0f / sqrtf(q / (float)C + eps);
+    float acc[kHeadMaxCo];
+#pragma unroll
+    for (int o = 0; o < kHeadMaxCo; ++o) {
+        acc[o] = 0.f;
+        if (o < co) {
+#pragma unroll
+            for (int j = 0; j < V; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[o] += v[j][e] * rstd * Io<WDT>::ld(w, (int64_t)o * C + (j * L + sub) * 4 + e);
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < kHeadMaxCo; ++o) {
+#pragma unroll
+        for (int off = L / 2; off > 0; off >>= 1) acc[o] += __shfl_xor(acc[o], off, 64);
+    }
+    if (live && sub == 0) {
+#pragma unroll
+        for (int o = 0; o < kHeadMaxCo; ++o)
+            if (o < co) out[row * co + o] = acc[o] + bias[o];
+    }
+}
+
 }  // namespace
+
+hipError_t launch_norm_linear(const float* x, int64_t n, int ci, float eps, const void* w, int w_dtype,
+                              const float* bias, int co, float* out, hipStream_t s) {
+    if (co < 1 || co > kHeadMaxCo) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(x) % 16) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+#define TGR_HEAD(WD, L, V)                                                                        \
+    if (w_dtype == WD && ci == 4 * L * V) {                                                         \
+        const int64_t rows_per_block = 4 * (64 / L);                                                \
+        const dim3 g((unsigned)((n + rows_per_block - 1) / rows_per_block)), blk(256);              \
+        hipLaunchKernelGGL((k_norm_linear<WD, L, V>), g, blk, 0, s, x, n, eps, w, bias, co, out);   \
+        return hipGetLastError();                                                                    \
+    }
+#define TGR_HEAD_W(L, V) TGR_HEAD(TSP_F32, L, V) TGR_HEAD(TSP_F16, L, V) TGR_HEAD(TSP_BF16, L, V)
+    TGR_HEAD_W(4, 1)
+    TGR_HEAD_W(8, 1)
+    TGR_HEAD_W(16, 1)
+    TGR_HEAD_W(32, 1)
+    TGR_HEAD_W(64, 1)
+    TGR_HEAD_W(64, 2)
+    TGR_HEAD_W(64, 4)
+#undef TGR_HEAD_W
+#undef TGR_HEAD
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_binary(int op_mul, const ggml_tensor* a, const ggml_tensor* b, float* out,
                          hipStream_t s) {

@@ -169,6 +169,11 @@ hipError_t launch_add_inplace(float* y, const void* x, int x_dtype, int64_t n, h
 // y[i] = (dtype) x[i]: f32 -> f16 / bf16 (round to nearest even), and f16 / bf16 -> f32.
 hipError_t launch_convert(const void* x, int x_dtype, void* y, int y_dtype, int64_t n,
                           hipStream_t s);
+// The decoders' head: out [n][co] f32 = LN(eps, no affine)(x [n][ci] f32) . W^T + bias, W [co][ci]
+// of w_dtype, bias f32 [co]; co <= 8, ci in {16, 32, 64, 128, 256, 512, 1024}, x 16-byte aligned
+// (hipErrorInvalidValue otherwise: the caller takes the two-pass route).
+hipError_t launch_norm_linear(const float* x, int64_t n, int ci, float eps, const void* w, int w_dtype,
+                              const float* bias, int co, float* out, hipStream_t s);
 // out[r][k] = a[idx[r]][k] for a [rows][k] (f32/f16/i32 -> f32, i32 -> i32).
 hipError_t launch_get_rows(const ggml_tensor* a, const int32_t* idx, int64_t n_idx, void* out,
                            hipStream_t s);

@@ -313,9 +313,18 @@ void run_linear(const Model& m, const std::string& prefix, const float* d_x, int
     const int wdt = tgr::tsp_dtype_of(w->type);
     const bool mfma = !g_sparse_cast_f32 && (wdt == TSP_F16 || wdt == TSP_BF16) && ci % 32 == 0 && co % 64 == 0;
     const int xdt = mfma ? wdt : TSP_F32;
-    DeviceBuffer tmp((pre_norm || mfma) ? (size_t)n * ci * (mfma ? 2 : 4) : 0, s), pb((size_t)co * 4 + 256, s);
+    DeviceBuffer pb((size_t)co * 4 + 256, s);
     Carve sc(pb.get());
     const float* bias = f32_param(b, sc, s);
+    // a narrow head after a LayerNorm runs as one pass over x (shapes it does not take fall back)
+    if (pre_norm && !mfma && co <= 8) {
+        const hipError_t e = tgr::launch_norm_linear(d_x, n, ci, eps, w->data, wdt, bias, co, d_out, s);
+        if (e != hipErrorInvalidValue) {
+            hip_check(e, (prefix + " head").c_str());
+            return;
+        }
+    }
+    DeviceBuffer tmp((pre_norm || mfma) ? (size_t)n * ci * (mfma ? 2 : 4) : 0, s);
     const void* x = d_x;
     if (pre_norm) {
         lib(tsp_layer_norm(d_x, TSP_F32, n, ci, nullptr, nullptr, eps, 0, tmp.get(), xdt, s), prefix + " norm");
