@@ -162,7 +162,8 @@ hipError_t binary_typed(const ggml_tensor* a, const ggml_tensor* b, float* out, 
 // The decoders' head (shape_decoder.cpp:63-77, 116): out[r][o] = bias[o] + sum_i LN(x[r])[i] W[o][i]
 // with LN the row LayerNorm of eps without affine, for co <= 8 outputs. L lanes hold a row, each V
 // groups of 4 channels (ci = 4 L V); the row is normalised in registers and every output is a
-// reduction over the row's lanes, so x is read once and nothing else is written.
+// reduction over the row's lanes, so x is read once and nothing else is written. Waves walk the
+// rows with a grid stride, keeping their weights in registers.
 constexpr int kHeadMaxCo = 8;
 template <int WDT, int L, int V>
 __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x, int64_t n, float eps,
@@ -170,55 +171,69 @@ __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x
                                                      int co, float* __restrict__ out) {
     constexpr int R = 64 / L, C = 4 * L * V;
     const int lane = threadIdx.x & 63, sub = lane % L;
-    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R + lane / L;
-    const bool live = row < n;
-    const float* xr = x + (live ? row : 0) * C;
-    float v[V][4];
+    float wv[kHeadMaxCo][V][4];
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-        const float4 t = *reinterpret_cast<const float4*>(xr + (j * L + sub) * 4);
-        v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
-    }
-    float sum = 0.f;
+    for (int o = 0; o < kHeadMaxCo; ++o)
 #pragma unroll
-    for (int j = 0; j < V; ++j)
+        for (int j = 0; j < V; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum += v[j][e];
+            for (int e = 0; e < 4; ++e)
+                wv[o][j][e] = o < co ? Io<WDT>::ld(w, (int64_t)o * C + (j * L + sub) * 4 + e) : 0.f;
+    constexpr int NO = (kHeadMaxCo + L - 1) / L;   // outputs per lane: o = k L + sub
+    float bo[NO];
 #pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    const float mean = sum / (float)C;
-    float q = 0.f;
+    for (int k = 0; k < NO; ++k) bo[k] = k * L + sub < co ? bias[k * L + sub] : 0.f;
+    const int64_t waves = (int64_t)gridDim.x * 4;
+    for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g * R < n; g += waves) {
+        const int64_t row = g * R + lane / L;
+        const bool live = row < n;
+        const float* xr = x + (live ? row : 0) * C;
+        float v[V][4];
 #pragma unroll
-    for (int j = 0; j < V; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[j][e] -= mean;
-            q += v[j][e] * v[j][e];
+        for (int j = 0; j < V; ++j) {
+            const float4 t = *reinterpret_cast<const float4*>(xr + (j * L + sub) * 4);
+            v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
         }
+        float sum = 0.f;
 #pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
-    const float rstd = 1.0f / sqrtf(q / (float)C + eps);
-    float acc[kHeadMaxCo];
+        for (int j = 0; j < V; ++j)
 #pragma unroll
-    for (int o = 0; o < kHeadMaxCo; ++o) {
-        acc[o] = 0.f;
-        if (o < co) {
+            for (int e = 0; e < 4; ++e) sum += v[j][e];
+#pragma unroll
+        for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        const float mean = sum / (float)C;
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[j][e] -= mean;
+                q += v[j][e] * v[j][e];
+            }
+#pragma unroll
+        for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+        const float rstd = 1.0f / sqrtf(q / (float)C + eps);
+        float acc[kHeadMaxCo];
+#pragma unroll
+        for (int o = 0; o < kHeadMaxCo; ++o) {
+            acc[o] = 0.f;
 #pragma unroll
             for (int j = 0; j < V; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc[o] += v[j][e] * rstd * Io<WDT>::ld(w, (int64_t)o * C + (j * L + sub) * 4 + e);
+                for (int e = 0; e < 4; ++e) acc[o] += v[j][e] * rstd * wv[o][j][e];
+#pragma unroll
+            for (int off = L / 2; off > 0; off >>= 1) acc[o] += __shfl_xor(acc[o], off, 64);
         }
-    }
+        // every lane of the row holds every sum: lane sub of the row writes outputs k L + sub
 #pragma unroll
-    for (int o = 0; o < kHeadMaxCo; ++o) {
+        for (int k = 0; k < NO; ++k) {
+            const int o = k * L + sub;
+            float r = 0.f;
 #pragma unroll
-        for (int off = L / 2; off > 0; off >>= 1) acc[o] += __shfl_xor(acc[o], off, 64);
-    }
-    if (live && sub == 0) {
-#pragma unroll
-        for (int o = 0; o < kHeadMaxCo; ++o)
-            if (o < co) out[row * co + o] = acc[o] + bias[o];
+            for (int i = 0; i < kHeadMaxCo; ++i)
+                if (o == i) r = acc[i];
+            if (live && o < co) out[row * co + o] = r + bo[k];
+        }
     }
 }
 
@@ -232,7 +247,8 @@ hipError_t launch_norm_linear(const float* x, int64_t n, int ci, float eps, cons
 #define TGR_HEAD(WD, L, V)                                                                        \
     if (w_dtype == WD && ci == 4 * L * V) {                                                         \
         const int64_t rows_per_block = 4 * (64 / L);                                                \
-        const dim3 g((unsigned)((n + rows_per_block - 1) / rows_per_block)), blk(256);              \
+        const dim3 g((unsigned)std::min<int64_t>((n + rows_per_block - 1) / rows_per_block, 4096)),   \
+            blk(256);                                                                                \
         hipLaunchKernelGGL((k_norm_linear<WD, L, V>), g, blk, 0, s, x, n, eps, w, bias, co, out);   \
         return hipGetLastError();                                                                    \
     }
