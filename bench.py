@@ -174,6 +174,7 @@ def decoder_bench(args) -> dict:
         "tflops": tflops,
         "tflops_dense27_equivalent": flops_dense / (ms * 1e-3) / 1e12,
         "min_ms": run["min_ms"], "model_load_ms": run["load_ms"],
+        "device_gb_in_use": run.get("device_bytes_in_use", 0) / 1e9,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
                      "frac": tflops / PEAK_TFLOPS["bf16"], "traffic": None,
                      "note": "whole decode, host transfers included; the conv kernels dominate"},

@@ -3,7 +3,8 @@
 //   decoder_bench <model.gguf> <dir> <gpu> <warmup> <steps>
 // dir holds latent.npy [N, Cl] f32, coords.npy [N, 3] int32 and subs_<s>.npy (u8 [8 N_s]) per
 // stage. Each decode is one call: host inputs in, host output [6 M] back (the reference's API),
-// so the time includes those transfers. Prints one JSON line.
+// so the time includes those transfers. Prints one JSON line, with the device memory in use
+// after the decodes (the model and the host library's cached blocks).
 #include <algorithm>
 #include <array>
 #include <chrono>
@@ -12,6 +13,8 @@
 #include <cstring>
 #include <string>
 #include <vector>
+
+#include <hip/hip_runtime.h>
 
 #include "npy_io.hpp"
 #include "shape_decoder.h"
@@ -57,10 +60,13 @@ int main(int argc, char** argv) {
         for (double d : ms) { sum += d; mn = std::min(mn, d); }
         double checksum = 0;
         for (size_t i = 0; i < out.size(); i += 97) checksum += out[i];
+        size_t free_b = 0, total_b = 0;
+        if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) free_b = total_b = 0;
         printf("{\"decode_ms\": %.4f, \"min_ms\": %.4f, \"steps\": %d, \"load_ms\": %.1f, \"voxels_in\": %d, "
-               "\"voxels_out\": %zu, \"stages\": %zu, \"model_bytes\": %zu, \"checksum\": %.6e}\n",
+               "\"voxels_out\": %zu, \"stages\": %zu, \"model_bytes\": %zu, \"device_bytes_in_use\": %zu, "
+               "\"checksum\": %.6e}\n",
                sum / std::max<size_t>(1, ms.size()), mn, steps, load_ms, n, out.size() / 6, subs.size(),
-               m.total_bytes(), checksum);
+               m.total_bytes(), total_b - free_b, checksum);
         m.free();
     } catch (const std::exception& e) {
         fprintf(stderr, "error: %s\n", e.what());
