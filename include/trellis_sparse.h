@@ -122,6 +122,20 @@ int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t n, int ci,
                              const void* d_packed_weight, const float* d_bias, int co,
                              void* d_out, int out_dtype, void* stream);
 
+/* The C2S block's conv1 with its octant gather fused into the stores (sparse.cpp:263-291: conv1
+ * maps Cin -> 8*Cout, then child m takes channels [(gidx[m]%8)*Cout, +Cout) of parent
+ * gidx[m]/8; the stores here put them there directly, and the [N][8*Cout] intermediate is never
+ * written). The conv of tsp_subm_conv3x3_planned with co = 8*cout; channel o*cout + k of parent
+ * row i goes to row mstart[i] + #{o' < o : mask[8i+o'] != 0} of d_out [M][cout] (f32) when
+ * mask[8i+o] != 0, and nowhere otherwise: every child row is written once. d_mask [8N] and
+ * d_mstart [N+1] are tsp_subdivide's input mask and output (M = d_mstart[N]). cout % 64 == 0;
+ * d_mask 8-byte aligned. */
+int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, int64_t n, int ci,
+                                     const int32_t* d_nbr, const void* d_plan,
+                                     const void* d_packed_weight, const float* d_bias, int cout,
+                                     const uint8_t* d_mask, const int32_t* d_mstart, float* d_out,
+                                     void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * 2x subdivision (channel-to-spatial) index math.
  * Replaces the host loop of trellis::sparse_c2s (src/sparse.cpp:205-222): parent i keeps

@@ -143,3 +143,24 @@ def test_linear_ex_validation(pkg):
     assert f(res=R) == 4                                 # residual needs f32 output
     assert f(res=ctypes.c_void_p(0x4004), odt=0) == 1    # misaligned residual
     assert "residual" in _err(pkg)
+
+
+def test_planned_octants_validation(pkg):
+    """tsp_subm_conv3x3_planned_octants: argument checks before any device work -- range and dtype
+    (1 / 4), cout not a multiple of 64 and ci not a multiple of 16 (4), the empty case (0), null,
+    aliased and misaligned pointers (1)."""
+    L = pkg.lib()
+    F, NB, P, W, B, M, S, O = (ctypes.c_void_p(a) for a in
+                               (0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000, 0x7000, 0x8000))
+    f = lambda **kw: L.tsp_subm_conv3x3_planned_octants(
+        kw.get("f", F), kw.get("dt", 2), kw.get("n", 100), kw.get("ci", 64), kw.get("nbr", NB),
+        kw.get("plan", P), kw.get("w", W), kw.get("b", B), kw.get("cout", 64), kw.get("mask", M),
+        kw.get("mstart", S), kw.get("out", O), NULL)
+    assert f(n=-1) == 1 and f(ci=0) == 1 and f(cout=0) == 1
+    assert f(dt=0) == 4                                    # f32 features: not the MFMA kernel
+    assert f(cout=96) == 4 and f(ci=40) == 4               # cout % 64, ci % 16
+    assert f(n=0) == 0                                     # empty: no-op
+    assert f(mask=NULL) == 1 and f(mstart=NULL) == 1 and f(plan=NULL) == 1
+    assert f(out=F) == 1                                   # out aliases feats
+    assert f(mask=ctypes.c_void_p(0x6004)) == 1            # mask not 8-byte aligned
+    assert "aligned" in _err(pkg)

@@ -115,6 +115,46 @@ def test_planned_vs_oracle(gpu_lib, orc, shells, ci, co, n, dtype_name):
     assert orc.rel_err(out16, ref) < TOL_16_OUT
 
 
+
+@pytest.mark.parametrize("ci,cout,n,keep", [(32, 64, 0, 0.5), (64, 128, 1500, 0.3), (16, 64, 513, 1.0),
+                                           (48, 64, 700, 0.0)])
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_planned_octants(gpu_lib, orc, shells, ci, cout, n, keep, dtype_name):
+    """The C2S conv1 with the octant gather in its stores (sparse.cpp:263-291) against the planned
+    conv to 8*cout channels followed by the gather: bit for bit. And against the oracle's conv
+    plus the reference's gather (out[m] = h[gidx/8][(gidx%8)*cout, +cout)) within TOL_16. Masks
+    keep a random fraction of octants, with some parents dropped whole and some kept whole, and
+    mark kept octants with bytes other than 1; keep 0 drops every child."""
+    _case(f"planned octants ci={ci} cout={cout} n={n} keep={keep} {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(ci * 31 + cout + n)
+    coords, feats, weight, bias = _rand_case(shells, rng, n, ci, 8 * cout, key)
+    nv = len(coords)
+    mask = np.where(rng.random((nv, 8)) < keep, rng.integers(1, 256, (nv, 8)), 0).astype(np.uint8)
+    if 0 < keep < 1:
+        mask[::7] = 0
+        mask[3::11] = 0x80
+    c = torch.from_numpy(np.ascontiguousarray(coords, np.int32)).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, nv)
+    pw = gpu_lib.conv_weight_pack(_dev(weight, dt))
+    f, b = _dev(feats, dt), _dev(bias, torch.float32)
+    mask_t = torch.from_numpy(mask.reshape(-1)).cuda()
+    _, gidx, mstart = gpu_lib.subdivide(mask_t, c)
+    m = len(gidx)
+    assert m == int(np.count_nonzero(mask))
+    if m == 0:
+        return
+    fused = gpu_lib.subm_conv3x3_planned_octants(f, nbr, plan, pw, b, cout, mask_t, mstart, m)
+    full = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, 8 * cout, out_dtype=torch.float32)
+    assert torch.equal(fused, gpu_lib.c2s_gather(full, gidx, cout))
+    h = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    ref = h.reshape(nv * 8, cout)[gidx.cpu().numpy()]
+    assert orc.rel_err(fused.cpu().numpy(), ref) < TOL_16
+
+
 def test_weight_pack_layout(gpu_lib):
     """packed[((c32*nkc + kc)*27 + t)*64 + lane][e] = W[32*c32 + lane%32][t][16*kc + 8*(lane//32) + e]"""
     _case("weight pack layout")

@@ -26,7 +26,7 @@ EXPORTS = (
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
     "tsp_subm_conv3x3",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
-    "tsp_subm_conv3x3_planned",
+    "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_octants",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
     "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
@@ -78,6 +78,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_subm_conv3x3_planned.restype = c_int
     L.tsp_subm_conv3x3_planned.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
                                            c_int, c_vp, c_int, c_vp]
+    L.tsp_subm_conv3x3_planned_octants.restype = c_int
+    L.tsp_subm_conv3x3_planned_octants.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp,
+                                                   c_vp, c_int, c_vp, c_vp, c_vp, c_vp]
     L.tsp_linear.restype = c_int
     L.tsp_linear.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_int, c_vp, c_int, c_vp, c_int,
                              c_vp]
@@ -230,6 +233,34 @@ def subm_conv3x3_planned(feats, nbr, plan, packed_weight, bias, co: int, out_dty
            lib().tsp_subm_conv3x3_planned(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr),
                                           _ptr(plan), _ptr(packed_weight), _ptr(bias), co,
                                           _ptr(out), dtype_code(out.dtype), _stream(stream)))
+    return out
+
+
+def subm_conv3x3_planned_octants(feats, nbr, plan, packed_weight, bias, cout: int, mask, mstart,
+                                 m: int, stream=None):
+    """The C2S conv1 with its octant gather in the stores: the planned conv to 8*cout channels,
+    parent i's channels [o*cout, +cout) written to its child of octant o (mask and mstart as
+    given to / returned by subdivide) -> float32 [M, cout]."""
+    torch = _torch()
+    _require_cuda(feats, nbr, plan, packed_weight, bias, mask, mstart)
+    n, ci = feats.shape
+    co = 8 * cout
+    if packed_weight.numel() != co * 27 * ci:
+        raise ValueError("packed weight size does not match [8*cout,27,Ci]")
+    if bias.dtype != torch.float32 or bias.numel() != co:
+        raise ValueError("bias must be float32 [8*cout]")
+    m8 = mask.reshape(-1).contiguous()
+    if m8.dtype != torch.uint8 or m8.numel() != 8 * n:
+        raise ValueError("mask must be uint8 with 8*N entries")
+    if mstart.dtype != torch.int32 or mstart.numel() != n + 1:
+        raise ValueError("mstart must be int32 [N+1]")
+    out = torch.empty((m, cout), dtype=torch.float32, device=feats.device)
+    f = feats.contiguous()
+    _check("tsp_subm_conv3x3_planned_octants",
+           lib().tsp_subm_conv3x3_planned_octants(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr),
+                                                  _ptr(plan), _ptr(packed_weight), _ptr(bias), cout,
+                                                  _ptr(m8), _ptr(mstart), _ptr(out),
+                                                  _stream(stream)))
     return out
 
 

@@ -492,6 +492,43 @@ extern "C" int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t 
                             d_bias, co, d_out, as_stream(stream));
 }
 
+extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, int64_t n, int ci,
+                                                const int32_t* d_nbr, const void* d_plan,
+                                                const void* d_packed_weight, const float* d_bias,
+                                                int cout, const uint8_t* d_mask,
+                                                const int32_t* d_mstart, float* d_out,
+                                                void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && ci > 0 && cout > 0, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_octants: n=%lld ci=%d cout=%d", (long long)n, ci, cout);
+    TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_octants: features are f16 or bf16, not dtype %d", dtype);
+    TSP_REQUIRE(ci % 16 == 0 && cout % 64 == 0 && cout <= INT32_MAX / 8, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_octants: needs ci %% 16 == 0 and cout %% 64 == 0 "
+                "(ci=%d cout=%d)", ci, cout);
+    const int co = 8 * cout;
+    TSP_REQUIRE((int64_t)kTaps * ci * co * 2 < ((int64_t)1 << 32), TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_octants: weight of 4 GiB or more");
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_feats && d_nbr && d_plan && d_packed_weight && d_bias && d_mask && d_mstart && d_out,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_octants: null pointer");
+    TSP_REQUIRE(static_cast<const void*>(d_out) != d_feats, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_octants: out aliases feats");
+    TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_feats) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_packed_weight) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_out) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_mask) % 8 == 0,
+                TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_octants: feats, weights and out must be 16-byte aligned, "
+                "mask 8-byte aligned");
+    OctantScatter osc;
+    osc.mask = d_mask;
+    osc.mstart = d_mstart;
+    osc.cout = cout;
+    return halo_conv_launch(dtype, TSP_F32, d_feats, n, ci, d_nbr, d_plan, d_packed_weight, d_bias,
+                            co, d_out, as_stream(stream), osc);
+}
+
 extern "C" int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
                           int weight_dtype, const float* d_bias, int co, void* d_out,
                           int out_dtype, void* stream) {

@@ -323,19 +323,19 @@ __global__ void k_weight_pack(const uint16_t* __restrict__ w, int ci, int co,
 template <int BN, int RB, int CB>
 constexpr int hb_waves() { return (HB_M / (32 * RB)) * (BN / (32 * CB)); }
 
-template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, bool OCT>
 __device__ __forceinline__ void conv_tiles(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed);
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc);
 
-template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
-__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, bool OCT>
+__device__ __forceinline__ void conv_grid(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc) {
     // wave w owns voxels [32 RB rg, +32 RB) x channels [32 CB cg, +32 CB) of the tile, with
     // rg = w % NRG and cg = w / NRG
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
@@ -359,9 +359,28 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     const int64_t total = n_tiles * n_ctiles;
     const int xcd = (int)(blockIdx.x % 8);
     const int64_t xlo = xcd * per_xcd, xhi = xlo + per_xcd < total ? xlo + per_xcd : total;
-    conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>(
+    conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, OCT>(
         feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, xlo + blockIdx.x / 8,
-        gridDim.x / 8, xhi, sH0, sH1, sL, sRed);
+        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc);
+}
+
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
+__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd) {
+    conv_grid<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, false>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{});
+}
+
+// The same conv with f32 output rows scattered to the children of a 2x subdivision (stored plan).
+template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
+__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_octants(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc) {
+    conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, true>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc);
 }
 
 // The tiles lin0, lin0 + stride, ... (< xhi) of one workgroup. With a stored plan and an even
@@ -369,13 +388,13 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
 // slice into the idle buffer, the first taps of its weights into the ring and its slot table into
 // registers, so the next tile starts without a memory round trip and its loads are in flight
 // before this tile's output stores.
-template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, bool OCT>
 __device__ __forceinline__ void conv_tiles(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed) {
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc) {
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
     constexpr int WAVES = NRG * NCG;
     constexpr int NT = WAVES * 64;
@@ -394,6 +413,9 @@ __device__ __forceinline__ void conv_tiles(
     int r32 = lane & 31, g = lane >> 5;
     int rg = wave % NRG;                     // row group: voxels [32 RB rg, +32 RB)
     const int c0 = (int)(lin0 % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
+    // with an octant scatter, the wave's channels lie in octant oct, from column ocol of a child
+    const int oct = OCT ? c0 / osc.cout : 0;
+    const int ocol = OCT ? c0 - oct * osc.cout : 0;
     const int nkc = ci / HB_KC;
     // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
     // planes of one row (32 contiguous bytes; a load touches 32 rows, not 64)
@@ -503,6 +525,24 @@ __device__ __forceinline__ void conv_tiles(
         constexpr int CH = ODT == TSP_F32 ? 4 : 8;     // channels per 16-byte store
         constexpr int NQ = NR * (WN / CH) / 64;        // stores per lane and round
         static_assert(NR * (WN / CH) % 64 == 0, "whole stores per lane");
+        // Octant stores: the child row of octant oct of each of the wave's 32 RB rows, or -1,
+        // looked up once per tile (lane l holds rows 2l and 2l + 1) and shuffled to the lanes
+        // that store them.
+        int child2[2] = {-1, -1};
+        if constexpr (OCT) {
+            static_assert(RB == 4, "two rows per lane");
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int64_t i = row0 + 32 * RB * rg + 2 * lane + k;
+                if (i < n) {
+                    constexpr uint64_t kLow7 = 0x7f7f7f7f7f7f7f7full;
+                    const uint64_t mw = *reinterpret_cast<const uint64_t*>(osc.mask + 8 * i);
+                    const uint64_t kept = (((mw & kLow7) + kLow7) | mw) & ~kLow7;   // bit 8b+7: byte b != 0
+                    const int rank = __popcll(kept & ((1ull << (8 * oct)) - 1));
+                    child2[k] = ((kept >> (8 * oct + 7)) & 1) ? osc.mstart[i] + rank : -1;
+                }
+            }
+        }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
@@ -528,8 +568,17 @@ __device__ __forceinline__ void conv_tiles(
                     const int c = q * 64 + lane;
                     const int r = c / (WN / CH), cq = c % (WN / CH);
                     const int64_t i = row0 + 32 * RB * rg + 32 * rb + NR * h + r;
-                    if (full || i < n) {
-                        const int64_t o = i * co + c0 + cq * CH;
+                    int64_t o = i * co + c0 + cq * CH;
+                    bool keep = full || i < n;
+                    if constexpr (OCT) {
+                        // parent row lr of the wave: its child of octant oct (or -1)
+                        const int lr = 32 * rb + NR * h + r;
+                        const int a = __shfl(child2[0], lr >> 1, 64), b = __shfl(child2[1], lr >> 1, 64);
+                        const int child = (lr & 1) ? b : a;
+                        keep = keep && child >= 0;
+                        o = (int64_t)child * osc.cout + ocol + cq * CH;
+                    }
+                    if (keep) {
                         if constexpr (ODT == TSP_F32) {
                             *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + o) = vs[q][0];
                         } else {
@@ -783,7 +832,7 @@ int cu_count() {
 
 template <bool BF16, int BN, int ODT, bool PLANNED>
 int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* plan,
-           const void* weight, const float* bias, int co, void* out, hipStream_t s) {
+           const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     const int n_ctiles = co / BN;
     const int64_t total = n_tiles * n_ctiles;
@@ -800,11 +849,23 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
         const int64_t fit = std::max<int64_t>(1, cu_count() / 8 / n_ctiles) * n_ctiles;
         per_xcd_wg = std::min(per_xcd, fit);
     }
-    hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>),
-                       dim3((unsigned)(per_xcd_wg * 8)), dim3(hb_waves<BN, RB, CB>() * 64), 0, s,
-                       reinterpret_cast<const uint16_t*>(feats), n, ci,
-                       nbr, pv, reinterpret_cast<const uint16_t*>(weight), bias, co, out, n_tiles,
-                       n_ctiles, per_xcd);
+    const dim3 grid((unsigned)(per_xcd_wg * 8)), block(hb_waves<BN, RB, CB>() * 64);
+    const uint16_t* f16 = reinterpret_cast<const uint16_t*>(feats);
+    const uint16_t* w16 = reinterpret_cast<const uint16_t*>(weight);
+    if constexpr (PLANNED && ODT == TSP_F32) {
+        if (osc.cout) {
+            hipLaunchKernelGGL((k_conv_halo_octants<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
+                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, osc);
+            TSP_CHECK_LAUNCH();
+            return TSP_OK;
+        }
+    }
+    if (osc.cout) {
+        set_error("MFMA conv: an octant scatter writes f32 from a stored plan");
+        return TSP_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>), grid, block, 0, s,
+                       f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
@@ -812,21 +873,21 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
 template <bool BF16, int BN, int ODT>
 int launch_planned(bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                    const void* plan, const void* weight, const float* bias, int co, void* out,
-                   hipStream_t s) {
-    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s);
-    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s);
+                   hipStream_t s, OctantScatter osc) {
+    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
+    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc);
 }
 
 template <bool BF16, int BN>
 int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                const void* plan, const void* weight, const float* bias, int co, void* out,
-               hipStream_t s) {
+               hipStream_t s, OctantScatter osc) {
     if (odt == TSP_F32)
-        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s);
+        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
     if (BF16 && odt == TSP_BF16)
-        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s);
+        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
     if (!BF16 && odt == TSP_F16)
-        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s);
+        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
     set_error("MFMA conv writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
@@ -862,9 +923,14 @@ int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s)
 
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s) {
+                     hipStream_t s, OctantScatter osc) {
     const bool planned = plan != nullptr;
     const bool bn128 = co % 128 == 0;
+    if (osc.cout && (!planned || osc.cout % (bn128 ? 64 : 32) != 0 || (int64_t)osc.cout * 8 != co)) {
+        set_error("MFMA conv: an octant scatter needs a plan, co = 8 * cout and cout %% %d == 0 "
+                  "(co=%d cout=%d)", bn128 ? 64 : 32, co, osc.cout);
+        return TSP_ERR_UNSUPPORTED;
+    }
     // the slice DMA addresses feature rows with 32-bit byte offsets
     if (!halo_fits(n, ci)) {
         set_error("MFMA conv: n * ci * 2 = %lld bytes of features exceed the 4 GiB the LDS-staged "
@@ -872,10 +938,10 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
         return TSP_ERR_UNSUPPORTED;
     }
     if (fdt == TSP_BF16)
-        return bn128 ? launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s)
-                     : launch_out<true, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s);
-    return bn128 ? launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s)
-                 : launch_out<false, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s);
+        return bn128 ? launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc)
+                     : launch_out<true, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
+    return bn128 ? launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc)
+                 : launch_out<false, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
 }
 
 }  // namespace tsp

@@ -46,10 +46,22 @@ int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, cons
 int halo_plan_build(const int32_t* nbr, int64_t n, void* plan, hipStream_t s);
 // Packs [co][27][ci] 16-bit weights into the MFMA operand order (ci % 16 == 0, co % 32 == 0).
 int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s);
+// Output rows scattered to the children of a 2x subdivision: with cout > 0, the conv's output
+// channel c = o * cout + k of row i goes to row mstart[i] + (octants of parent i kept before o)
+// of an [M][cout] output when mask[8 i + o] != 0, and nowhere otherwise (the octant gather of
+// sparse.cpp:263-291 done by the conv's stores). mask must be 8-byte aligned.
+struct OctantScatter {
+    const uint8_t* mask = nullptr;
+    const int32_t* mstart = nullptr;
+    int cout = 0;
+};
+
 // The conv. With plan == nullptr the tile plan is built inside the kernel and `weight` is in
-// the [co][27][ci] layout; with a plan, `weight` must be packed by halo_weight_pack.
+// the [co][27][ci] layout; with a plan, `weight` must be packed by halo_weight_pack. An
+// OctantScatter needs a plan and cout a multiple of the channels one wave owns (64 when
+// co % 128 == 0, else 32).
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s);
+                     hipStream_t s, OctantScatter osc = {});
 
 }  // namespace tsp

@@ -62,7 +62,8 @@ Conv conv_of(const Model& m, const std::string& prefix) {
 // F16 mul_mat rounds its F32 operand (sparse.cpp:74); under g_sparse_cast_f32 or for channel
 // counts the matrix-core tiles do not cover, the fp32 kernel runs on the weights' exact values.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
-              float* out, Carve& sc, hipStream_t s) {
+              float* out, Carve& sc, hipStream_t s, const uint8_t* omask, const int32_t* omstart,
+              int ocout) {
     const float* bias = f32_param(c.b, sc, s);
     if (c.mfma) {
         const void* x16 = x;
@@ -75,9 +76,15 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
         lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, packed, s), "weight pack");
-        lib(tsp_subm_conv3x3_planned(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, s),
-            "sparse conv");
+        if (ocout)
+            lib(tsp_subm_conv3x3_planned_octants(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, ocout, omask,
+                                                 omstart, out, s),
+                "sparse conv (octant stores)");
+        else
+            lib(tsp_subm_conv3x3_planned(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, s),
+                "sparse conv");
     } else {
+        if (ocout) fail("sparse conv: octant stores need the matrix-core path");
         if (!sc.running()) return;
         lib(tsp_subm_conv3x3(x, xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
                              TSP_ALGO_AUTO, s),
@@ -266,13 +273,16 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     hip_check(hipMemcpyAsync(r.coords.get(), d_child.get(), (size_t)mm * 12, hipMemcpyDeviceToDevice, s),
               "c2s");
 
-    // conv1 on the parents: LN(norm1)+SiLU written straight in the conv's input dtype
+    // conv1 on the parents: LN(norm1)+SiLU written straight in the conv's input dtype. On the
+    // matrix cores (cout % 64 == 0) its stores do the octant gather, and the [n][8 cout]
+    // intermediate is never written.
     const int in1 = conv1.mfma ? conv1.wdt : TSP_F32, in2 = conv2.mfma ? conv2.wdt : TSP_F32;
     const size_t es1 = in1 == TSP_F32 ? 4 : 2, es2 = in2 == TSP_F32 ? 4 : 2;
     const size_t s1 = conv_scratch(conv1, n, in1), s2 = conv_scratch(conv2, mm, in2);
+    const bool octant_stores = conv1.mfma && cout % 64 == 0;
     Carve sz;
     sz.take((size_t)n * cin * es1);
-    sz.take((size_t)n * 8 * cout * 4);
+    sz.take(octant_stores ? 0 : (size_t)n * 8 * cout * 4);
     sz.take(s1);
     sz.take((size_t)mm * cout * 4);
     sz.take((size_t)mm * cout * es2);
@@ -281,7 +291,7 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     DeviceBuffer work(sz.off, s);
     Carve w(work.get());
     void* h0 = w.take((size_t)n * cin * es1);
-    float* h1 = static_cast<float*>(w.take((size_t)n * 8 * cout * 4));
+    float* h1 = static_cast<float*>(w.take(octant_stores ? 0 : (size_t)n * 8 * cout * 4));
     Carve sc1(w.take(s1));
     float* g = static_cast<float*>(w.take((size_t)mm * cout * 4));
     void* h2 = w.take((size_t)mm * cout * es2);
@@ -292,10 +302,16 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
 
     lib(tsp_layer_norm(d_x, TSP_F32, n, cin, g1, b1, 1e-6f, 1, h0, in1, s), prefix + ".norm1");
     if (conv1.mfma) parent.ensure_plan(s);
-    run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), h1, sc1, s);
+    if (octant_stores) {
+        run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), g, sc1, s,
+                 d_mask.as<uint8_t>(), d_mstart.as<int32_t>(), cout);
+    } else {
+        run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), h1, sc1, s);
+        // channel -> spatial gather
+        lib(tsp_c2s_gather(h1, TSP_F32, d_gidx.as<int32_t>(), mm, cout, g, s), prefix + " gather");
+    }
 
-    // channel -> spatial gather, norm2 (no affine) + SiLU, conv2 on the children, skip
-    lib(tsp_c2s_gather(h1, TSP_F32, d_gidx.as<int32_t>(), mm, cout, g, s), prefix + " gather");
+    // norm2 (no affine) + SiLU, conv2 on the children, skip
     lib(tsp_layer_norm(g, TSP_F32, mm, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s), prefix + " norm2");
     build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status);
     if (conv2.mfma) r.table.ensure_plan(s);

@@ -44,9 +44,12 @@ struct Conv {
     bool mfma = false;   // matrix-core kernel (16-bit weights, Ci % 16 == 0, Co % 64 == 0)
 };
 Conv conv_of(const Model& m, const std::string& prefix);
-// out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
+// out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma. With ocout > 0
+// (c.mfma, co = 8 * ocout, ocout % 64 == 0) the rows go to the children instead: out [M][ocout]
+// as tsp_subm_conv3x3_planned_octants writes it, from the subdivision's mask and mstart.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
-              float* out, Carve& sc, hipStream_t s);
+              float* out, Carve& sc, hipStream_t s, const uint8_t* omask = nullptr,
+              const int32_t* omstart = nullptr, int ocout = 0);
 size_t conv_scratch(const Conv& c, int64_t n, int xdt);
 
 // SparseConvNeXtBlock3d weights and the launch shape of one block over n voxels.
