@@ -839,9 +839,10 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
     const int64_t per_xcd = ceil_div(total, 8);
     PlanView pv{};
     if (plan) pv = carve_plan(const_cast<void*>(plan), n_tiles);
-    // 8 waves of 128 voxels x BN/2 channels; weights 2 taps ahead; a slice piece every other
-    // tap, written to LDS 6 taps after its load
-    constexpr int RB = 4, CB = BN / 64, PD = 2, SP = 2, STG = 6;
+    // 8 waves of 128 voxels x BN/2 channels; weights 2 taps ahead (5 at BN = 64, whose waves
+    // have the registers for it: 3 % faster there, while at BN = 128 the deeper ring spills);
+    // a slice piece every other tap, written to LDS 6 taps after its load
+    constexpr int RB = 4, CB = BN / 64, PD = BN == 128 ? 2 : 5, SP = 2, STG = 6;
     // With a plan: one workgroup per CU (the LDS of one fills a CU), a multiple of n_ctiles per
     // XCD. Without: one per (tile, column tile), each building its own plan.
     int64_t per_xcd_wg = per_xcd;
