@@ -136,6 +136,18 @@ int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, int64_t n, 
                                      const uint8_t* d_mask, const int32_t* d_mstart, float* d_out,
                                      void* stream);
 
+/* The C2S block's conv2 with its skip connection added by the stores (sparse.cpp:302-323: the
+ * block input x, octant block K = cin/8 repeated R = co/K times, added to conv2's output): the
+ * conv of tsp_subm_conv3x3_planned with f32 output over the M children, plus
+ * x[gidx[m]/8][(gidx[m]%8)*K + c/R] in output channel c of row m -- the result of
+ * tsp_subm_conv3x3_planned followed by tsp_c2s_skip_add, without the second pass over the
+ * output. x f32 [N][cin]; gidx [M] from tsp_subdivide; cin % 8 == 0 and R % 4 == 0. */
+int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int ci,
+                                  const int32_t* d_nbr, const void* d_plan,
+                                  const void* d_packed_weight, const float* d_bias, int co,
+                                  const float* d_x, int cin, const int32_t* d_gidx, float* d_out,
+                                  void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * 2x subdivision (channel-to-spatial) index math.
  * Replaces the host loop of trellis::sparse_c2s (src/sparse.cpp:205-222): parent i keeps

@@ -164,3 +164,24 @@ def test_planned_octants_validation(pkg):
     assert f(out=F) == 1                                   # out aliases feats
     assert f(mask=ctypes.c_void_p(0x6004)) == 1            # mask not 8-byte aligned
     assert "aligned" in _err(pkg)
+
+
+def test_planned_skip_validation(pkg):
+    """tsp_subm_conv3x3_planned_skip: argument checks before any device work -- range (1), dtype
+    and shape limits (4: f32 features, co % 64, cin % 8, a repeat co / (cin / 8) not a multiple
+    of 4), the empty case (0), null and aliased pointers (1)."""
+    L = pkg.lib()
+    F, NB, P, W, B, X, G, O = (ctypes.c_void_p(a) for a in
+                               (0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000, 0x7000, 0x8000))
+    f = lambda **kw: L.tsp_subm_conv3x3_planned_skip(
+        kw.get("f", F), kw.get("dt", 2), kw.get("n", 100), kw.get("ci", 64), kw.get("nbr", NB),
+        kw.get("plan", P), kw.get("w", W), kw.get("b", B), kw.get("co", 64), kw.get("x", X),
+        kw.get("cin", 128), kw.get("gidx", G), kw.get("out", O), NULL)
+    assert f(n=-1) == 1 and f(cin=0) == 1 and f(co=0) == 1
+    assert f(dt=0) == 4 and f(co=96) == 4                  # f32 features; co % 64
+    assert f(cin=12) == 4                                  # cin % 8
+    assert f(cin=256) == 4                                 # R = 64 / 32 = 2: not a multiple of 4
+    assert f(n=0) == 0                                     # empty: no-op
+    assert f(x=NULL) == 1 and f(gidx=NULL) == 1
+    assert f(out=X) == 1                                   # out aliases x
+    assert "alias" in _err(pkg)

@@ -155,6 +155,47 @@ def test_planned_octants(gpu_lib, orc, shells, ci, cout, n, keep, dtype_name):
     assert orc.rel_err(fused.cpu().numpy(), ref) < TOL_16
 
 
+
+@pytest.mark.parametrize("cin,ci,co,n", [(128, 64, 64, 0), (256, 128, 128, 1500), (64, 32, 64, 513)])
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_planned_skip(gpu_lib, orc, shells, cin, ci, co, n, dtype_name):
+    """The C2S conv2 with the skip added by its stores (sparse.cpp:302-323) against the planned
+    conv followed by the skip pass: bit for bit. And against the oracle's conv plus the
+    reference's repeat-interleaved octant block of x within TOL_16. The children come from a
+    random subdivision of random parents, so gidx reaches every octant."""
+    _case(f"planned skip cin={cin} ci={ci} co={co} n={n} {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(cin + ci * 3 + co + n)
+    pcoords = shells.sphere_shell(24, 12.0, 7.0, 9.0)
+    pcoords = pcoords[:max(1, (n or 4000) // 4)]
+    npar = len(pcoords)
+    mask = (rng.random(npar * 8) < 0.5).astype(np.uint8)
+    _, gidx, _ = gpu_lib.subdivide(torch.from_numpy(mask).cuda(),
+                                   torch.from_numpy(np.ascontiguousarray(pcoords, np.int32)).cuda())
+    child = np.ascontiguousarray(orc.subdivide(mask, pcoords)[0], np.int32)
+    m = len(child)
+    feats = shells.round_to(rng.standard_normal((m, ci)).astype(np.float32), key)
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32), key)
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    x = rng.standard_normal((npar, cin)).astype(np.float32)
+    c = torch.from_numpy(child).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, m)
+    pw = gpu_lib.conv_weight_pack(_dev(weight, dt))
+    f, b, xt = _dev(feats, dt), _dev(bias, torch.float32), _dev(x, torch.float32)
+    fused = gpu_lib.subm_conv3x3_planned_skip(f, nbr, plan, pw, b, co, xt, gidx)
+    two_pass = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, co, out_dtype=torch.float32)
+    gpu_lib.c2s_skip_add(xt, gidx, two_pass)
+    assert torch.equal(fused, two_pass)
+    k = cin // 8
+    g = gidx.cpu().numpy()
+    skip = np.repeat(x.reshape(npar * 8, k)[g], co // k, axis=1)
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(child), weight, bias) + skip
+    assert orc.rel_err(fused.cpu().numpy(), ref) < TOL_16
+
+
 def test_weight_pack_layout(gpu_lib):
     """packed[((c32*nkc + kc)*27 + t)*64 + lane][e] = W[32*c32 + lane%32][t][16*kc + 8*(lane//32) + e]"""
     _case("weight pack layout")

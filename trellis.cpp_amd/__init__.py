@@ -27,6 +27,7 @@ EXPORTS = (
     "tsp_subm_conv3x3",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
     "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_octants",
+    "tsp_subm_conv3x3_planned_skip",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
     "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
@@ -81,6 +82,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_subm_conv3x3_planned_octants.restype = c_int
     L.tsp_subm_conv3x3_planned_octants.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp,
                                                    c_vp, c_int, c_vp, c_vp, c_vp, c_vp]
+    L.tsp_subm_conv3x3_planned_skip.restype = c_int
+    L.tsp_subm_conv3x3_planned_skip.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
+                                                c_int, c_vp, c_int, c_vp, c_vp, c_vp]
     L.tsp_linear.restype = c_int
     L.tsp_linear.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_int, c_vp, c_int, c_vp, c_int,
                              c_vp]
@@ -261,6 +265,32 @@ def subm_conv3x3_planned_octants(feats, nbr, plan, packed_weight, bias, cout: in
                                                   _ptr(plan), _ptr(packed_weight), _ptr(bias), cout,
                                                   _ptr(m8), _ptr(mstart), _ptr(out),
                                                   _stream(stream)))
+    return out
+
+
+def subm_conv3x3_planned_skip(feats, nbr, plan, packed_weight, bias, co: int, x, gidx, stream=None):
+    """The C2S conv2 with the block's skip added by its stores: the planned conv (f32 out) over
+    the M children plus repeat_interleave of x's octant blocks (x float32 [N, cin], gidx from
+    subdivide) -> float32 [M, co]."""
+    torch = _torch()
+    _require_cuda(feats, nbr, plan, packed_weight, bias, x, gidx)
+    m, ci = feats.shape
+    if packed_weight.numel() != co * 27 * ci:
+        raise ValueError("packed weight size does not match [Co,27,Ci]")
+    if bias.dtype != torch.float32 or bias.numel() != co:
+        raise ValueError("bias must be float32 [Co]")
+    xc = x.contiguous()
+    if xc.dtype != torch.float32 or xc.dim() != 2:
+        raise ValueError("x must be float32 [N, cin]")
+    if gidx.dtype != torch.int32 or gidx.numel() != m:
+        raise ValueError("gidx must be int32 [M]")
+    out = torch.empty((m, co), dtype=torch.float32, device=feats.device)
+    f = feats.contiguous()
+    _check("tsp_subm_conv3x3_planned_skip",
+           lib().tsp_subm_conv3x3_planned_skip(_ptr(f), dtype_code(f.dtype), m, ci, _ptr(nbr),
+                                               _ptr(plan), _ptr(packed_weight), _ptr(bias), co,
+                                               _ptr(xc), xc.shape[1], _ptr(gidx), _ptr(out),
+                                               _stream(stream)))
     return out
 
 

@@ -529,6 +529,41 @@ extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, 
                             co, d_out, as_stream(stream), osc);
 }
 
+extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int ci,
+                                             const int32_t* d_nbr, const void* d_plan,
+                                             const void* d_packed_weight, const float* d_bias, int co,
+                                             const float* d_x, int cin, const int32_t* d_gidx,
+                                             float* d_out, void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && ci > 0 && co > 0 && cin > 0, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_skip: n=%lld ci=%d co=%d cin=%d", (long long)n, ci, co, cin);
+    TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_skip: features are f16 or bf16, not dtype %d", dtype);
+    TSP_REQUIRE(ci % 16 == 0 && co % 64 == 0, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_skip: needs ci %% 16 == 0 and co %% 64 == 0 (ci=%d co=%d)",
+                ci, co);
+    TSP_REQUIRE(cin % 8 == 0 && co % (cin / 8) == 0 && (co / (cin / 8)) % 4 == 0, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_skip: needs cin %% 8 == 0 and co / (cin / 8) a multiple of 4 "
+                "(cin=%d co=%d)", cin, co);
+    TSP_REQUIRE((int64_t)kTaps * ci * co * 2 < ((int64_t)1 << 32), TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_skip: weight of 4 GiB or more");
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_feats && d_nbr && d_plan && d_packed_weight && d_bias && d_x && d_gidx && d_out,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_skip: null pointer");
+    TSP_REQUIRE(static_cast<const void*>(d_out) != d_feats && d_out != d_x, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_skip: out aliases feats or x");
+    TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_feats) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_packed_weight) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_out) % 16 == 0,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_skip: buffers must be 16-byte aligned");
+    SkipAdd skip;
+    skip.x = d_x;
+    skip.gidx = d_gidx;
+    skip.cin = cin;
+    return halo_conv_launch(dtype, TSP_F32, d_feats, n, ci, d_nbr, d_plan, d_packed_weight, d_bias, co,
+                            d_out, as_stream(stream), OctantScatter{}, skip);
+}
+
 extern "C" int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
                           int weight_dtype, const float* d_bias, int co, void* d_out,
                           int out_dtype, void* stream) {

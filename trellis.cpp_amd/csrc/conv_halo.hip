@@ -323,19 +323,20 @@ __global__ void k_weight_pack(const uint16_t* __restrict__ w, int ci, int co,
 template <int BN, int RB, int CB>
 constexpr int hb_waves() { return (HB_M / (32 * RB)) * (BN / (32 * CB)); }
 
-template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, bool OCT>
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, int EPI>
 __device__ __forceinline__ void conv_tiles(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc);
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip);
 
-template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, bool OCT>
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, int EPI>
 __device__ __forceinline__ void conv_grid(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
+    SkipAdd skip) {
     // wave w owns voxels [32 RB rg, +32 RB) x channels [32 CB cg, +32 CB) of the tile, with
     // rg = w % NRG and cg = w / NRG
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
@@ -359,9 +360,9 @@ __device__ __forceinline__ void conv_grid(
     const int64_t total = n_tiles * n_ctiles;
     const int xcd = (int)(blockIdx.x % 8);
     const int64_t xlo = xcd * per_xcd, xhi = xlo + per_xcd < total ? xlo + per_xcd : total;
-    conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, OCT>(
+    conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, EPI>(
         feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, xlo + blockIdx.x / 8,
-        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc);
+        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc, skip);
 }
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
@@ -369,8 +370,9 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd) {
-    conv_grid<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, false>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{});
+    conv_grid<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, 0>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{},
+        SkipAdd{});
 }
 
 // The same conv with f32 output rows scattered to the children of a 2x subdivision (stored plan).
@@ -379,8 +381,18 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc) {
-    conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, true>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc);
+    conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, 1>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{});
+}
+
+// The same conv with f32 output and the C2S skip added by its stores (stored plan).
+template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
+__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_skip(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, SkipAdd skip) {
+    conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, 2>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{}, skip);
 }
 
 // The tiles lin0, lin0 + stride, ... (< xhi) of one workgroup. With a stored plan and an even
@@ -388,13 +400,13 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_
 // slice into the idle buffer, the first taps of its weights into the ring and its slot table into
 // registers, so the next tile starts without a memory round trip and its loads are in flight
 // before this tile's output stores.
-template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, bool OCT>
+template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, int EPI>
 __device__ __forceinline__ void conv_tiles(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc) {
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip) {
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
     constexpr int WAVES = NRG * NCG;
     constexpr int NT = WAVES * 64;
@@ -414,8 +426,8 @@ __device__ __forceinline__ void conv_tiles(
     int rg = wave % NRG;                     // row group: voxels [32 RB rg, +32 RB)
     const int c0 = (int)(lin0 % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
     // with an octant scatter, the wave's channels lie in octant oct, from column ocol of a child
-    const int oct = OCT ? c0 / osc.cout : 0;
-    const int ocol = OCT ? c0 - oct * osc.cout : 0;
+    const int oct = EPI == 1 ? c0 / osc.cout : 0;
+    const int ocol = EPI == 1 ? c0 - oct * osc.cout : 0;
     const int nkc = ci / HB_KC;
     // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
     // planes of one row (32 contiguous bytes; a load touches 32 rows, not 64)
@@ -529,7 +541,7 @@ __device__ __forceinline__ void conv_tiles(
         // looked up once per tile (lane l holds rows 2l and 2l + 1) and shuffled to the lanes
         // that store them.
         int child2[2] = {-1, -1};
-        if constexpr (OCT) {
+        if constexpr (EPI == 1) {
             static_assert(RB == 4, "two rows per lane");
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
@@ -543,6 +555,34 @@ __device__ __forceinline__ void conv_tiles(
                 }
             }
         }
+        // Skip add: the gidx of each of the wave's rows, looked up and shuffled the same way.
+        int gidx2[2] = {0, 0};
+        if constexpr (EPI == 2) {
+            static_assert(RB == 4, "two rows per lane");
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int64_t i = row0 + 32 * RB * rg + 2 * lane + k;
+                if (i < n) gidx2[k] = skip.gidx[i];
+            }
+        }
+        // the skip elements of round (rb, h), one per store (its 4 channels share one); loaded a
+        // round ahead of their use, so the loads' latency overlaps a round of staging and stores
+        auto skip_vals = [&](int rb, int h, float (&sv)[NQ]) {
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const int c = q * 64 + lane;
+                const int r = c / (WN / CH), cq = c % (WN / CH);
+                const int lr = 32 * rb + NR * h + r;
+                const int a = __shfl(gidx2[0], lr >> 1, 64), b = __shfl(gidx2[1], lr >> 1, 64);
+                const int gi = (lr & 1) ? b : a;
+                const int kk = skip.cin / 8, rep_r = co / kk;
+                const int64_t i = row0 + 32 * RB * rg + lr;
+                sv[q] = i < n ? skip.x[(int64_t)(gi >> 3) * skip.cin + (gi & 7) * kk + (c0 + cq * CH) / rep_r]
+                              : 0.f;
+            }
+        };
+        float sv_cur[NQ] = {}, sv_nxt[NQ] = {};
+        if constexpr (EPI == 2) skip_vals(0, 0, sv_cur);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
@@ -563,6 +603,11 @@ __device__ __forceinline__ void conv_tiles(
 #pragma unroll
                     for (int e = 0; e < CH / 4; ++e) vs[q][e] = *reinterpret_cast<const f32x4_t*>(p + 16 * e);
                 }
+                if constexpr (EPI == 2) {
+                    constexpr int NH = 32 / NR;
+                    if (h + 1 < NH) skip_vals(rb, h + 1, sv_nxt);
+                    else if (rb + 1 < RB) skip_vals(rb + 1, 0, sv_nxt);
+                }
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
                     const int c = q * 64 + lane;
@@ -570,13 +615,18 @@ __device__ __forceinline__ void conv_tiles(
                     const int64_t i = row0 + 32 * RB * rg + 32 * rb + NR * h + r;
                     int64_t o = i * co + c0 + cq * CH;
                     bool keep = full || i < n;
-                    if constexpr (OCT) {
+                    if constexpr (EPI == 1) {
                         // parent row lr of the wave: its child of octant oct (or -1)
                         const int lr = 32 * rb + NR * h + r;
                         const int a = __shfl(child2[0], lr >> 1, 64), b = __shfl(child2[1], lr >> 1, 64);
                         const int child = (lr & 1) ? b : a;
                         keep = keep && child >= 0;
                         o = (int64_t)child * osc.cout + ocol + cq * CH;
+                    }
+                    if constexpr (EPI == 2) {
+                        // child row: + x[gidx / 8][(gidx % 8) K + c / R]
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) vs[q][0][e] += sv_cur[q];
                     }
                     if (keep) {
                         if constexpr (ODT == TSP_F32) {
@@ -593,6 +643,10 @@ __device__ __forceinline__ void conv_tiles(
                                 u32x4_t{w[0], w[1], w[2], w[3]};
                         }
                     }
+                }
+                if constexpr (EPI == 2) {
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) sv_cur[q] = sv_nxt[q];
                 }
             }
         }
@@ -832,7 +886,8 @@ int cu_count() {
 
 template <bool BF16, int BN, int ODT, bool PLANNED>
 int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* plan,
-           const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc) {
+           const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc,
+           SkipAdd skip) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     const int n_ctiles = co / BN;
     const int64_t total = n_tiles * n_ctiles;
@@ -860,9 +915,15 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
             TSP_CHECK_LAUNCH();
             return TSP_OK;
         }
+        if (skip.cin) {
+            hipLaunchKernelGGL((k_conv_halo_skip<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
+                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, skip);
+            TSP_CHECK_LAUNCH();
+            return TSP_OK;
+        }
     }
-    if (osc.cout) {
-        set_error("MFMA conv: an octant scatter writes f32 from a stored plan");
+    if (osc.cout || skip.cin) {
+        set_error("MFMA conv: octant stores and the skip add write f32 from a stored plan");
         return TSP_ERR_UNSUPPORTED;
     }
     hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>), grid, block, 0, s,
@@ -874,21 +935,21 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
 template <bool BF16, int BN, int ODT>
 int launch_planned(bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                    const void* plan, const void* weight, const float* bias, int co, void* out,
-                   hipStream_t s, OctantScatter osc) {
-    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
-    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc);
+                   hipStream_t s, OctantScatter osc, SkipAdd skip) {
+    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
+    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip);
 }
 
 template <bool BF16, int BN>
 int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                const void* plan, const void* weight, const float* bias, int co, void* out,
-               hipStream_t s, OctantScatter osc) {
+               hipStream_t s, OctantScatter osc, SkipAdd skip) {
     if (odt == TSP_F32)
-        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
+        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
     if (BF16 && odt == TSP_BF16)
-        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
+        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
     if (!BF16 && odt == TSP_F16)
-        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
+        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
     set_error("MFMA conv writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
@@ -924,12 +985,17 @@ int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s)
 
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc) {
+                     hipStream_t s, OctantScatter osc, SkipAdd skip) {
     const bool planned = plan != nullptr;
     const bool bn128 = co % 128 == 0;
     if (osc.cout && (!planned || osc.cout % (bn128 ? 64 : 32) != 0 || (int64_t)osc.cout * 8 != co)) {
         set_error("MFMA conv: an octant scatter needs a plan, co = 8 * cout and cout %% %d == 0 "
                   "(co=%d cout=%d)", bn128 ? 64 : 32, co, osc.cout);
+        return TSP_ERR_UNSUPPORTED;
+    }
+    if (skip.cin && (!planned || skip.cin % 8 != 0 || co % (skip.cin / 8) != 0 || (co / (skip.cin / 8)) % 4 != 0)) {
+        set_error("MFMA conv: a skip add needs a plan, cin %% 8 == 0 and co / (cin / 8) a multiple of 4 "
+                  "(cin=%d co=%d)", skip.cin, co);
         return TSP_ERR_UNSUPPORTED;
     }
     // the slice DMA addresses feature rows with 32-bit byte offsets
@@ -939,10 +1005,10 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
         return TSP_ERR_UNSUPPORTED;
     }
     if (fdt == TSP_BF16)
-        return bn128 ? launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc)
-                     : launch_out<true, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
-    return bn128 ? launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc)
-                 : launch_out<false, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc);
+        return bn128 ? launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip)
+                     : launch_out<true, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
+    return bn128 ? launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip)
+                 : launch_out<false, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
 }
 
 }  // namespace tsp

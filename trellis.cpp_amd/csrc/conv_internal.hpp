@@ -56,12 +56,21 @@ struct OctantScatter {
     int cout = 0;
 };
 
+// The C2S skip added by the conv's stores (sparse.cpp:302-323): with cin > 0, output row m
+// channel c gets x[gidx[m] / 8][(gidx[m] % 8) * K + c / R] added, K = cin / 8, R = co / K
+// (R % 4 == 0), x f32 [N][cin].
+struct SkipAdd {
+    const float* x = nullptr;
+    const int32_t* gidx = nullptr;
+    int cin = 0;
+};
+
 // The conv. With plan == nullptr the tile plan is built inside the kernel and `weight` is in
 // the [co][27][ci] layout; with a plan, `weight` must be packed by halo_weight_pack. An
-// OctantScatter needs a plan and cout a multiple of the channels one wave owns (64 when
-// co % 128 == 0, else 32).
+// OctantScatter or a SkipAdd needs a plan and f32 output; an OctantScatter needs cout a multiple
+// of the channels one wave owns (64 when co % 128 == 0, else 32).
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc = {});
+                     hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {});
 
 }  // namespace tsp

@@ -62,8 +62,7 @@ Conv conv_of(const Model& m, const std::string& prefix) {
 // F16 mul_mat rounds its F32 operand (sparse.cpp:74); under g_sparse_cast_f32 or for channel
 // counts the matrix-core tiles do not cover, the fp32 kernel runs on the weights' exact values.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
-              float* out, Carve& sc, hipStream_t s, const uint8_t* omask, const int32_t* omstart,
-              int ocout) {
+              float* out, Carve& sc, hipStream_t s, const ConvStores& st) {
     const float* bias = f32_param(c.b, sc, s);
     if (c.mfma) {
         const void* x16 = x;
@@ -76,15 +75,19 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
         lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, packed, s), "weight pack");
-        if (ocout)
-            lib(tsp_subm_conv3x3_planned_octants(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, ocout, omask,
-                                                 omstart, out, s),
+        if (st.ocout)
+            lib(tsp_subm_conv3x3_planned_octants(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, st.ocout,
+                                                 st.omask, st.omstart, out, s),
                 "sparse conv (octant stores)");
+        else if (st.skip_cin)
+            lib(tsp_subm_conv3x3_planned_skip(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, st.skip_x,
+                                              st.skip_cin, st.skip_gidx, out, s),
+                "sparse conv (skip stores)");
         else
             lib(tsp_subm_conv3x3_planned(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, s),
                 "sparse conv");
     } else {
-        if (ocout) fail("sparse conv: octant stores need the matrix-core path");
+        if (st.ocout || st.skip_cin) fail("sparse conv: fused stores need the matrix-core path");
         if (!sc.running()) return;
         lib(tsp_subm_conv3x3(x, xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
                              TSP_ALGO_AUTO, s),
@@ -303,8 +306,11 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     lib(tsp_layer_norm(d_x, TSP_F32, n, cin, g1, b1, 1e-6f, 1, h0, in1, s), prefix + ".norm1");
     if (conv1.mfma) parent.ensure_plan(s);
     if (octant_stores) {
-        run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), g, sc1, s,
-                 d_mask.as<uint8_t>(), d_mstart.as<int32_t>(), cout);
+        ConvStores st;
+        st.omask = d_mask.as<uint8_t>();
+        st.omstart = d_mstart.as<int32_t>();
+        st.ocout = cout;
+        run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), g, sc1, s, st);
     } else {
         run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), h1, sc1, s);
         // channel -> spatial gather
@@ -315,9 +321,19 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     lib(tsp_layer_norm(g, TSP_F32, mm, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s), prefix + " norm2");
     build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status);
     if (conv2.mfma) r.table.ensure_plan(s);
-    run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s);
-    lib(tsp_c2s_skip_add(d_x, TSP_F32, d_gidx.as<int32_t>(), mm, cin, cout, r.feats.get(), TSP_F32, s),
-        prefix + " skip");
+    // the skip: added by conv2's stores on the matrix cores (repeat R % 4 == 0), else its own pass
+    if (conv2.mfma && (cout / (cin / 8)) % 4 == 0) {
+        ConvStores st;
+        st.skip_x = d_x;
+        st.skip_gidx = d_gidx.as<int32_t>();
+        st.skip_cin = cin;
+        run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s,
+                 st);
+    } else {
+        run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s);
+        lib(tsp_c2s_skip_add(d_x, TSP_F32, d_gidx.as<int32_t>(), mm, cin, cout, r.feats.get(), TSP_F32, s),
+            prefix + " skip");
+    }
     return r;
 }
 

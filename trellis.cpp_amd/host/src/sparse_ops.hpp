@@ -44,12 +44,21 @@ struct Conv {
     bool mfma = false;   // matrix-core kernel (16-bit weights, Ci % 16 == 0, Co % 64 == 0)
 };
 Conv conv_of(const Model& m, const std::string& prefix);
-// out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma. With ocout > 0
-// (c.mfma, co = 8 * ocout, ocout % 64 == 0) the rows go to the children instead: out [M][ocout]
-// as tsp_subm_conv3x3_planned_octants writes it, from the subdivision's mask and mstart.
+// What a matrix-core conv's stores do besides writing its rows (the C2S block's fusions).
+struct ConvStores {
+    // ocout > 0: rows go to the children, out [M][ocout] as tsp_subm_conv3x3_planned_octants
+    // writes it (co = 8 * ocout, ocout % 64 == 0), from the subdivision's mask and mstart
+    const uint8_t* omask = nullptr;
+    const int32_t* omstart = nullptr;
+    int ocout = 0;
+    // skip_cin > 0: the skip of tsp_subm_conv3x3_planned_skip is added (x f32 [N][skip_cin])
+    const float* skip_x = nullptr;
+    const int32_t* skip_gidx = nullptr;
+    int skip_cin = 0;
+};
+// out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
-              float* out, Carve& sc, hipStream_t s, const uint8_t* omask = nullptr,
-              const int32_t* omstart = nullptr, int ocout = 0);
+              float* out, Carve& sc, hipStream_t s, const ConvStores& st = {});
 size_t conv_scratch(const Conv& c, int64_t n, int xdt);
 
 // SparseConvNeXtBlock3d weights and the launch shape of one block over n voxels.
