@@ -110,6 +110,27 @@ __global__ void k_convert(const void* __restrict__ x, void* __restrict__ y, int6
         Io<YDT>::st(y, i, Io<XDT>::ld(x, i));
 }
 
+// f32 -> f16 / bf16, four elements per thread (16-byte loads, 8-byte stores). bf16 through the
+// packed hardware conversion, which rounds to nearest even exactly as Io<TSP_BF16>::st does.
+template <int YDT>
+__global__ void k_convert_f32_x4(const float4* __restrict__ x, uint2* __restrict__ y, int64_t n4) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float4 v = x[i];
+        uint32_t lo, hi;
+        if constexpr (YDT == TSP_BF16) {
+            lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v.x, v.y}, bf16x2));
+            hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v.z, v.w}, bf16x2));
+        } else {
+            lo = (uint32_t)__half_as_ushort(__float2half_rn(v.x)) | ((uint32_t)__half_as_ushort(__float2half_rn(v.y)) << 16);
+            hi = (uint32_t)__half_as_ushort(__float2half_rn(v.z)) | ((uint32_t)__half_as_ushort(__float2half_rn(v.w)) << 16);
+        }
+        y[i] = uint2{lo, hi};
+    }
+}
+
 template <int DT>
 __global__ void k_get_rows(const void* __restrict__ a, int64_t rows, const int32_t* __restrict__ idx,
                            int64_t n_idx, int64_t k, float* __restrict__ out) {
@@ -304,6 +325,17 @@ hipError_t launch_add_inplace(float* y, const void* x, int xd, int64_t n, hipStr
 hipError_t launch_convert(const void* x, int xd, void* y, int yd, int64_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     const dim3 g(grid_for(n)), blk(kThreads);
+    if (xd == TSP_F32 && (yd == TSP_BF16 || yd == TSP_F16) && n % 4 == 0 &&
+        reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0) {
+        const dim3 g4(grid_for(n / 4));
+        if (yd == TSP_BF16)
+            hipLaunchKernelGGL(k_convert_f32_x4<TSP_BF16>, g4, blk, 0, s, static_cast<const float4*>(x),
+                               static_cast<uint2*>(y), n / 4);
+        else
+            hipLaunchKernelGGL(k_convert_f32_x4<TSP_F16>, g4, blk, 0, s, static_cast<const float4*>(x),
+                               static_cast<uint2*>(y), n / 4);
+        return hipGetLastError();
+    }
 #define TGR_CVT(XD, YD)                                                                   \
     if (xd == XD && yd == YD) {                                                           \
         hipLaunchKernelGGL((k_convert<XD, YD>), g, blk, 0, s, x, y, n);                   \
