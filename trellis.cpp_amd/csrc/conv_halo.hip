@@ -31,6 +31,10 @@
 //     tile's first slice, first weight taps and slot table, so a tile starts with no round trip.
 // A tile whose row range or distinct-row count does not fit (scattered or unsorted inputs)
 // takes the direct path: the same MFMA loop with A gathered straight from global memory.
+// Two more kernels instantiate the same loop for the C2S block with f32 output: its conv1 with
+// octant stores (each parent's octant channels go straight to the child rows, so the
+// [N][8 Cout] intermediate and the gather pass are never needed) and its conv2 with skip stores
+// (the block's repeat-interleaved skip added as the rows are stored).
 #include <algorithm>
 #include <type_traits>
 
