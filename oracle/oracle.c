@@ -4,6 +4,7 @@
  */
 #include "oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -137,8 +138,12 @@ void orc_subm_conv_f32_rows(const float* feats, int64_t n, int ci, const int32_t
                             const float* weight, const float* bias, int co, float* out,
                             int64_t r0, int64_t r1, int threads) {
     set_threads(threads);
+    /* the sentinel row N = 0 * feats[0] (submconv_pad, sparse.cpp:81-85): +-0 for finite
+       values, NaN where feats[0] holds an Inf or a NaN */
     const float* zero_row = NULL;
-    float* zbuf = (float*)calloc((size_t)ci, sizeof(float));   /* the sentinel row N */
+    float* zbuf = (float*)calloc((size_t)ci, sizeof(float));
+    if (n > 0)
+        for (int k = 0; k < ci; ++k) zbuf[k] = 0.0f * feats[k];
     zero_row = zbuf;
 #pragma omp parallel
     {
@@ -170,10 +175,20 @@ void orc_subm_conv_f32(const float* feats, int64_t n, int ci, const int32_t* nbr
     orc_subm_conv_f32_rows(feats, n, ci, nbr, weight, bias, co, out, 0, n, threads);
 }
 
+/* Whether the sentinel row 0 * feats[0] holds a NaN (feats[0] has an Inf or a NaN): then every
+   absent tap makes the whole output row NaN, as in the reference. */
+static int sentinel_nan(const float* feats, int64_t n, int ci) {
+    if (n <= 0) return 0;
+    for (int k = 0; k < ci; ++k)
+        if (!isfinite(feats[k])) return 1;
+    return 0;
+}
+
 void orc_subm_conv_f64_rows(const float* feats, int64_t n, int ci, const int32_t* nbr,
                             const float* weight, const float* bias, int co, double* out,
                             const int64_t* rows, int64_t nrows, int threads) {
     set_threads(threads);
+    const int snan = sentinel_nan(feats, n, ci);
 #pragma omp parallel for schedule(static)
     for (int64_t j = 0; j < nrows; ++j) {
         const int64_t i = rows[j];
@@ -181,7 +196,11 @@ void orc_subm_conv_f64_rows(const float* feats, int64_t n, int ci, const int32_t
         for (int o = 0; o < co; ++o) dst[o] = (double)bias[o];
         for (int t = 0; t < 27; ++t) {
             const int32_t r = nbr[(int64_t)t * n + i];
-            if (r == (int32_t)n) continue;
+            if (r == (int32_t)n) {   /* 0 * feats[0]: contributes +-0, or NaN */
+                if (snan)
+                    for (int o = 0; o < co; ++o) dst[o] = NAN;
+                continue;
+            }
             const float* g = feats + (int64_t)r * ci;
             for (int o = 0; o < co; ++o) {
                 const float* w = weight + ((int64_t)o * 27 + t) * ci;
@@ -197,13 +216,18 @@ void orc_subm_conv_f64(const float* feats, int64_t n, int ci, const int32_t* nbr
                        const float* weight, const float* bias, int co, double* out,
                        int threads) {
     set_threads(threads);
+    const int snan = sentinel_nan(feats, n, ci);
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
         double* dst = out + i * co;
         for (int o = 0; o < co; ++o) dst[o] = (double)bias[o];
         for (int t = 0; t < 27; ++t) {
             const int32_t r = nbr[(int64_t)t * n + i];
-            if (r == (int32_t)n) continue;
+            if (r == (int32_t)n) {   /* 0 * feats[0]: contributes +-0, or NaN */
+                if (snan)
+                    for (int o = 0; o < co; ++o) dst[o] = NAN;
+                continue;
+            }
             const float* g = feats + (int64_t)r * ci;
             for (int o = 0; o < co; ++o) {
                 const float* w = weight + ((int64_t)o * 27 + t) * ci;

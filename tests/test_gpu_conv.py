@@ -196,6 +196,50 @@ def test_planned_skip(gpu_lib, orc, shells, cin, ci, co, n, dtype_name):
     assert orc.rel_err(fused.cpu().numpy(), ref) < TOL_16
 
 
+
+@pytest.mark.parametrize("bad", ["inf", "nan"])
+@pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "unsorted"])
+def test_nonfinite_row0(gpu_lib, orc, shells, path, bad):
+    """Absent taps read the padding row 0 * feats[0] (sparse.cpp:81-85). With an Inf or a NaN in
+    row 0 every output row that has an absent tap is NaN in every channel, on every kernel path
+    (the LDS-staged kernel with and without a stored plan, its direct path on unsorted rows, the
+    gather kernel, the VALU kernel in 16 and 32 bits); rows whose 27 taps are all present keep
+    their finite values (checked against the oracle away from row 0's own neighbours)."""
+    _case(f"non-finite row 0 {path} {bad}")
+    import torch
+    rng = np.random.default_rng(23)
+    coords = np.concatenate([shells.sphere_shell(24, 12.0, 7.0, 9.0),
+                             np.stack(np.meshgrid(*[np.arange(40, 45)] * 3, indexing="ij"), -1).reshape(-1, 3)])
+    if path == "unsorted":
+        coords = np.concatenate([coords[:1], rng.permutation(coords[1:])])
+    coords = np.ascontiguousarray(coords, np.int32)
+    n, ci, co = len(coords), 32, 64
+    key = "f32" if path == "f32" else "bf16"
+    feats = rng.standard_normal((n, ci)).astype(np.float32)
+    feats[0, 7] = np.inf if bad == "inf" else np.nan
+    weight = (rng.standard_normal((co, 27, ci)) / 30).astype(np.float32)
+    if key == "bf16":
+        feats, weight = shells.round_to(feats, "bf16"), shells.round_to(weight, "bf16")
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    ref = orc.subm_conv_f64(feats, nbr, weight, bias)
+    dt = torch.float32 if key == "f32" else torch.bfloat16
+    if path == "planned":
+        out = _run_planned(gpu_lib, coords, feats, weight, bias, dt)
+    else:
+        algo = {"auto": "auto", "unsorted": "mfma", "mfma_gather": "mfma_gather", "narrow": "narrow",
+                "f32": "auto"}[path]
+        out, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo=algo)
+    t = nbr.reshape(27, n)
+    absent = (t == n).any(axis=0)
+    near0 = (t == 0).any(axis=0)
+    assert absent.any() and (~absent & ~near0).any()
+    assert np.isnan(out[absent]).all()
+    keep = ~absent & ~near0
+    assert np.isfinite(out[keep]).all()
+    assert orc.rel_err(out[keep], ref[keep]) < (TOL_32 if key == "f32" else TOL_16)
+
+
 def test_weight_pack_layout(gpu_lib):
     """packed[((c32*nkc + kc)*27 + t)*64 + lane][e] = W[32*c32 + lane%32][t][16*kc + 8*(lane//32) + e]"""
     _case("weight pack layout")

@@ -165,6 +165,38 @@ def test_conv_invariants(orc, shells):
     assert np.allclose(orc.subm_conv_f64(f1, nbr, w, bias), y1 + bias, atol=1e-12)
 
 
+
+def test_conv_sentinel_row(orc, shells):
+    """The padding row absent taps read is 0 * feats[0] (submconv_pad, sparse.cpp:81-85), not a
+    zero row: with finite features it contributes nothing, so changing row 0 moves only the
+    outputs of row 0's neighbours; with an Inf or a NaN in row 0 every output row that has an
+    absent tap is NaN in every channel (0 * Inf = NaN, and NaN * w = NaN), and the rows whose 27
+    taps are all present stay finite. A zero sentinel row would leave them all finite."""
+    rng = np.random.default_rng(17)
+    coords = np.concatenate([shells.sphere_shell(20, 10.0, 5.0, 7.0),
+                             np.stack(np.meshgrid(*[np.arange(30, 34)] * 3, indexing="ij"), -1).reshape(-1, 3)])
+    coords = np.ascontiguousarray(coords, np.int32)
+    n = len(coords)
+    f = rng.standard_normal((n, 16)).astype(np.float32)
+    w = rng.standard_normal((8, 27, 16)).astype(np.float32)
+    b = rng.standard_normal(8).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    absent = (nbr.reshape(27, n) == n).any(axis=0)
+    assert absent.any() and (~absent).any()             # the 4^3 block's interior has all 27
+    near0 = (nbr.reshape(27, n) == 0).any(axis=0)
+    f2 = f.copy()
+    f2[0] = rng.standard_normal(16).astype(np.float32) * 100
+    for conv in (orc.subm_conv_f64, orc.subm_conv_f32):
+        y, y2 = conv(f, nbr, w, b), conv(f2, nbr, w, b)
+        assert np.array_equal(y[~near0], y2[~near0])    # finite row 0: the padding adds +-0
+        for bad in (np.inf, -np.inf, np.nan):
+            f3 = f.copy()
+            f3[0, 5] = bad
+            y3 = conv(f3, nbr, w, b)
+            assert np.isnan(y3[absent]).all()
+            assert np.isfinite(y3[~absent & ~near0]).all()
+
+
 def test_conv_rows_variants(orc, golden):
     g = golden("conv_rand800_c32.npz")
     nbr = orc.neighbor_table(g["coords"])

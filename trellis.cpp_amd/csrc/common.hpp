@@ -91,6 +91,23 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// The padding row that absent taps read, 0 * x (submconv_pad, sparse.cpp:81-85: row N of the
+// padded input is feats[0] scaled by 0), for eight 16-bit values of x: a zero with x's sign, or
+// a quiet NaN where x is an Inf or a NaN.
+template <bool BF16>
+__device__ __forceinline__ u32x4_t zero_times16(u32x4_t x) {
+    constexpr uint32_t kExp = BF16 ? 0x7F80u : 0x7C00u, kNan = BF16 ? 0x7FC0u : 0x7E00u;
+    u32x4_t r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = x[e] & 0xffffu, hi = x[e] >> 16;
+        const uint32_t zlo = (lo & kExp) == kExp ? kNan : (lo & 0x8000u);
+        const uint32_t zhi = (hi & kExp) == kExp ? kNan : (hi & 0x8000u);
+        r[e] = zlo | (zhi << 16);
+    }
+    return r;
+}
+
 constexpr int kWave = 64;
 constexpr int kTaps = 27;
 

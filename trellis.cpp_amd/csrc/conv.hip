@@ -47,6 +47,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
     const int64_t row0 = (int64_t)blockIdx.x * NB_M;
     const int co0 = blockIdx.y * NB_N;
     const int32_t sentinel = (int32_t)n;
+    // whether the padding row 0 * feats[0] (sparse.cpp:81-85) holds a NaN: then no tap is skipped
+    bool row0_bad = false;
+    if (nbr)
+        for (int k = tid; k < ci; k += NB_THREADS) row0_bad |= !__builtin_isfinite(Elem<FDT>::load(feats, k));
+    row0_bad = __syncthreads_or(row0_bad);
 
     float acc[4][4];
 #pragma unroll
@@ -62,7 +67,8 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
             sRow[tid] = r;
             valid = r != sentinel;
         }
-        if (!__syncthreads_or(valid)) continue;   // no voxel of the tile has this neighbour
+        // no voxel of the tile has this neighbour: skipped, unless the padding row is not zero
+        if (!__syncthreads_or(valid) && !row0_bad) continue;
 
         for (int kc = 0; kc < ci; kc += NB_K) {
             {   // gathered input rows -> sA[k][row]
@@ -72,9 +78,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
                 for (int j = 0; j < 8; ++j) {
                     const int k = kc + kk + j;
                     float v = 0.f;
-                    // unsigned compare: the sentinel N (and any value outside [0,N)) reads zero
-                    if ((uint32_t)src < (uint32_t)n && k < ci)
-                        v = Elem<FDT>::load(feats, (int64_t)src * ci + k);
+                    // unsigned compare: the sentinel N (and any value outside [0,N)) reads the
+                    // padding row 0 * feats[0] (sparse.cpp:81-85)
+                    if (k < ci)
+                        v = (uint32_t)src < (uint32_t)n ? Elem<FDT>::load(feats, (int64_t)src * ci + k)
+                                                        : 0.f * Elem<FDT>::load(feats, k);
                     sA[kk + j][r] = v;
                 }
             }
@@ -156,14 +164,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
     const int64_t wrow0 = tile * BM + (int64_t)wave * 64;   // this wave's first voxel
     const int32_t sentinel = (int32_t)n;
 
-    // Taps that some voxel of the workgroup has (wave ballots, OR in LDS).
+    // Taps that some voxel of the workgroup has (wave ballots, OR in LDS). Absent taps read the
+    // padding row 0 * feats[0] (sparse.cpp:81-85): zeros, unless row 0 holds an Inf or a NaN --
+    // then every tap counts, as the padding row makes the sums of absent taps NaN.
     if (tid == 0) sMask = 0;
-    __syncthreads();
+    bool row0_bad = false;
+    for (int k = tid * 8; k < ci; k += NT * 8) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(feats + k);
+        const u32x4_t z = zero_times16<BF16>(v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) row0_bad |= (z[e] & 0x7fff7fffu) != 0;
+    }
+    row0_bad = __syncthreads_or(row0_bad);
     {
         uint32_t wm = 0;
         const int64_t i = wrow0 + lane;
         for (int t = 0; t < taps; ++t) {
-            const bool v = (i < n) && (!nbr || nbr[(int64_t)t * n + i] != sentinel);
+            const bool v = (i < n) && (row0_bad || !nbr || nbr[(int64_t)t * n + i] != sentinel);
             if (__ballot(v)) wm |= 1u << t;
         }
         if (lane == 0 && wm) atomicOr(&sMask, wm);
@@ -208,11 +225,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    if ((uint32_t)r[rb] < (uint32_t)n) {   // sentinel N -> zero operand
+                    if ((uint32_t)r[rb] < (uint32_t)n) {   // sentinel N -> the padding row
                         a[rb][s] = *reinterpret_cast<const u32x4_t*>(
                             feats + (int64_t)r[rb] * ci + kc + s * 16 + g * 8);
                     } else {
-                        a[rb][s] = u32x4_t{0u, 0u, 0u, 0u};
+                        a[rb][s] = zero_times16<BF16>(
+                            *reinterpret_cast<const u32x4_t*>(feats + kc + s * 16 + g * 8));
                     }
                 }
         };

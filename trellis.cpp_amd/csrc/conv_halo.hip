@@ -433,6 +433,19 @@ __device__ __forceinline__ void conv_tiles(
     const int oct = EPI == 1 ? c0 / osc.cout : 0;
     const int ocol = EPI == 1 ? c0 - oct * osc.cout : 0;
     const int nkc = ci / HB_KC;
+    // The reference's absent taps read the padding row 0 * feats[0] (submconv_pad,
+    // sparse.cpp:81-85), zeros here. Where row 0 holds an Inf or a NaN that row is NaN in those
+    // channels, so every output row with an absent tap is NaN in every channel: the epilogue then
+    // writes NaN for those rows (found in the table), as the reference's sum would.
+    bool row0_bad = false;
+    for (int k = tid * 8; k < ci; k += NT * 8) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(feats + k);
+        constexpr uint32_t kExp = BF16 ? 0x7F807F80u : 0x7C007C00u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            row0_bad |= ((v[e] & kExp & 0xffffu) == (kExp & 0xffffu)) || ((v[e] & kExp & 0xffff0000u) == (kExp & 0xffff0000u));
+    }
+    row0_bad = __syncthreads_or(row0_bad);
     // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
     // planes of one row (32 contiguous bytes; a load touches 32 rows, not 64)
     int plane = lane & 1;
@@ -619,6 +632,14 @@ __device__ __forceinline__ void conv_tiles(
                     const int64_t i = row0 + 32 * RB * rg + 32 * rb + NR * h + r;
                     int64_t o = i * co + c0 + cq * CH;
                     bool keep = full || i < n;
+                    if (row0_bad && keep) {
+                        bool absent = false;
+                        for (int t = 0; t < kTaps; ++t) absent |= nbr[(int64_t)t * n + i] == (int32_t)n;
+                        if (absent) {
+#pragma unroll
+                            for (int e = 0; e < CH / 4; ++e) vs[q][e] = f32x4_t{NAN, NAN, NAN, NAN};
+                        }
+                    }
                     if constexpr (EPI == 1) {
                         // parent row lr of the wave: its child of octant oct (or -1)
                         const int lr = 32 * rb + NR * h + r;
