@@ -43,7 +43,7 @@
 namespace tsp {
 namespace {
 
-constexpr int HB_PLAN_NT = 256;            // threads of a plan-build workgroup
+constexpr int HB_PLAN_NT = 512;            // threads of a plan-build workgroup
 constexpr int HB_KC = 16;                  // channels per LDS slice
 constexpr int HB_SLOTS = 2048;             // slots per slice buffer
 constexpr int HB_ZERO = HB_SLOTS;          // slot that always holds zeros (absent taps)
