@@ -80,9 +80,10 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
                     float v = 0.f;
                     // unsigned compare: the sentinel N (and any value outside [0,N)) reads the
                     // padding row 0 * feats[0] (sparse.cpp:81-85)
-                    if (k < ci)
-                        v = (uint32_t)src < (uint32_t)n ? Elem<FDT>::load(feats, (int64_t)src * ci + k)
-                                                        : 0.f * Elem<FDT>::load(feats, k);
+                    if (k < ci) {
+                        if ((uint32_t)src < (uint32_t)n) v = Elem<FDT>::load(feats, (int64_t)src * ci + k);
+                        else if (row0_bad) v = 0.f * Elem<FDT>::load(feats, k);
+                    }
                     sA[kk + j][r] = v;
                 }
             }
