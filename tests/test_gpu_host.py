@@ -9,6 +9,8 @@ for that conv against the oracle fed the same F16-rounded features; <= 1e-5 on t
 (--f32, the reference's g_sparse_cast_f32)."""
 from __future__ import annotations
 
+import dataclasses
+
 import os
 import re
 import subprocess
@@ -134,13 +136,19 @@ def test_tex_decode_guided(gpu, orc, shells, tmp_path):
     assert err < 3e-3
 
 
-def test_tex_decode_bf16_decoder_workload(gpu, orc, shells, tmp_path):
+@pytest.mark.parametrize("channels", [None, (128, 64)])
+def test_tex_decode_bf16_decoder_workload(gpu, orc, shells, tmp_path, channels):
     """The decoder benchmark's model format on its miniature workload: bf16 weights ~ N(0, 0.02)
     under the reference's key names, band masks driving the texture route. Against the oracle
     decoder fed the same bf16-rounded weights; every conv and linear rounds its input to bf16 (a
-    2^-8 relative step, so the bar is looser than the F16 case's)."""
+    2^-8 relative step, so the bar is looser than the F16 case's). channels (128, 64): one stage
+    whose C2S conv1 stores its octants into the children and whose conv2 adds the skip as it
+    stores, and the fused LayerNorm + output head over 64 channels."""
     from trellis_cpp_amd.gguf_writer import write as write_gguf
     w = shells.decoder_workload("decoder-shells16-c64")
+    if channels is not None:
+        w = dataclasses.replace(w, channels=channels, masks=w.masks[:len(channels) - 1],
+                                counts=w.counts[:len(channels)])
     p = shells.decoder_params(w.channels, w.blocks, 32, w.out_ch, w.std, w.seed)
     write_gguf(str(tmp_path / "model.gguf"), p, dtypes={k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()})
     np.save(tmp_path / "latent.npy", w.latent)
