@@ -92,13 +92,19 @@ __global__ void k_hash_insert(const int32_t* __restrict__ coords, int64_t n, Has
     }
 }
 
-// Bucket index of brick (bx, by, bz), or h.cap when it holds no voxel.
-__device__ __forceinline__ uint64_t find(const HashView& h, uint32_t bx, uint32_t by, uint32_t bz) {
-    const uint64_t key = brick_key(bx, by, bz);
-    for (uint64_t s = home(h, key);; s = next(h, s)) {
-        const uint64_t k = *reinterpret_cast<const uint64_t*>(h.words + s * kBucketWords);
+__device__ __forceinline__ uint64_t bucket_key(const HashView& h, uint64_t s) {
+    return *reinterpret_cast<const uint64_t*>(h.words + s * kBucketWords);
+}
+
+// Bucket index of `key`, or h.cap when no bucket holds it, given the key k already read from
+// bucket s (the probe sequence continues from s).
+__device__ __forceinline__ uint64_t find_from(const HashView& h, uint64_t key, uint64_t s,
+                                              uint64_t k) {
+    for (;;) {
         if (k == key) return s;
         if (k == 0) return h.cap;
+        s = next(h, s);
+        k = bucket_key(h, s);
     }
 }
 
@@ -119,11 +125,22 @@ __global__ __launch_bounds__(kProbeThreads) void k_probe(const int32_t* __restri
     const uint32_t X = x + 1, Y = y + 1, Z = z + 1;
     // the 2x2x2 bricks holding the neighbourhood, from (bx, by, bz)
     const uint32_t bx = (X - 1) >> 1, by = (Y - 1) >> 1, bz = (Z - 1) >> 1;
-    uint64_t bk[8];
+    // The home buckets' keys are read together, so the usual case (the brick is in its home
+    // bucket, or the home bucket is empty) costs one memory round trip instead of eight.
+    uint64_t bk[8], key[8], got[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) bk[c] = find(h, bx + (c & 1), by + ((c >> 1) & 1), bz + (c >> 2));
+    for (int c = 0; c < 8; ++c) {
+        key[c] = brick_key(bx + (c & 1), by + ((c >> 1) & 1), bz + (c >> 2));
+        bk[c] = home(h, key[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) got[c] = bucket_key(h, bk[c]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) bk[c] = find_from(h, key[c], bk[c], got[c]);
     // brick of offset -1 / 0 / +1 along an axis: 0 / 1 - (X & 1) / 1
     const int ex = 1 - (X & 1), ey = 1 - (Y & 1), ez = 1 - (Z & 1);
+    // All 27 reads come before the first store, so they go out together.
+    uint32_t r[kTaps];
 #pragma unroll
     for (int t = 0; t < kTaps; ++t) {
         const int dx = t / 9 - 1, dy = (t / 3) % 3 - 1, dz = t % 3 - 1;
@@ -135,10 +152,14 @@ __global__ __launch_bounds__(kProbeThreads) void k_probe(const int32_t* __restri
         uint64_t s = bk[0];
 #pragma unroll
         for (int k = 1; k < 8; ++k) s = c == k ? bk[k] : s;
-        uint32_t r = 0;
-        if (s != h.cap) r = h.words[s * kBucketWords + 2 + oct];
-        nbr[(int64_t)t * n + i] = r ? (int32_t)(r - 1) : miss;
+        // Read unconditionally (bucket 0 stands in for an absent brick) and discard afterwards,
+        // so no read sits behind a branch.
+        const bool have = s != h.cap;
+        const uint32_t w = h.words[(have ? s : 0) * kBucketWords + 2 + oct];
+        r[t] = have ? w : 0;
     }
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = r[t] ? (int32_t)(r[t] - 1) : miss;
 }
 
 __global__ void k_count_pairs(const int32_t* __restrict__ nbr, int64_t total, int32_t sentinel,
