@@ -74,3 +74,18 @@ def test_workload_bit_exact(gpu_lib, orc, shells, name):
     assert np.array_equal(got, ref)
     assert torch.equal(nbr, again)                                   # deterministic
     assert gpu_lib.count_pairs(nbr, w.n) == orc.count_pairs(ref, w.n)
+
+
+def test_one_voxel_per_brick_bit_exact(gpu_lib, orc):
+    """Every voxel in a 2x2x2 brick of its own: the table holds N bricks in 1.5 N + 1024 buckets,
+    the fullest it gets, so probe sequences run longest. 10^6 voxels on a 100^3 brick grid, each
+    at a random octant, so neighbouring bricks still give neighbours."""
+    _case("one-voxel-per-brick 100^3")
+    rng = np.random.default_rng(5)
+    a = np.stack(np.meshgrid(*(np.arange(100, dtype=np.int32),) * 3, indexing="ij"), -1)
+    # voxel x lies in brick (x + 1) >> 1: x = 2a + 1 + e with e in {0, 1} gives brick a + 1
+    c = (2 * a.reshape(-1, 3) + rng.integers(0, 2, size=(a.size // 3, 3)) + 1).astype(np.int32)
+    c = c[rng.permutation(len(c))]
+    ref = orc.neighbor_table(c)
+    assert np.array_equal(_gpu_table(gpu_lib, c), ref)
+    assert (ref[13 * len(c):14 * len(c)] == np.arange(len(c))).all()   # centre tap: itself
