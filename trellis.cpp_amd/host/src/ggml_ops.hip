@@ -186,6 +186,21 @@ hipError_t binary_typed(const ggml_tensor* a, const ggml_tensor* b, float* out, 
 // reduction over the row's lanes, so x is read once and nothing else is written. Waves walk the
 // rows with a grid stride, keeping their weights in registers.
 constexpr int kHeadMaxCo = 8;
+
+// DPP lane moves within a row of 16 lanes: lane ^ 1, lane ^ 2, 7 - lane within each 8, 15 - lane.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the 16 lanes of a DPP row; every lane ends with the same value.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    return v;
+}
 template <int WDT, int L, int V>
 __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x, int64_t n, float eps,
                                                      const void* __restrict__ w, const float* __restrict__ bias,
@@ -204,24 +219,40 @@ __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x
     float bo[NO];
 #pragma unroll
     for (int k = 0; k < NO; ++k) bo[k] = k * L + sub < co ? bias[k * L + sub] : 0.f;
+    const int o16 = (sub & 8 ? 4 : 0) + (sub & 4 ? 2 : 0) + (sub & 2 ? 1 : 0);   // L == 16 path
+    const float bo16 = o16 < co ? bias[o16] : 0.f;
     const int64_t waves = (int64_t)gridDim.x * 4;
-    for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g * R < n; g += waves) {
+    // The next row group's x is loaded before this group's reductions, so a load is always in
+    // flight while the lanes shuffle.
+    auto load = [&](int64_t g, float4 (&t)[V]) {
+        const int64_t row = g * R + lane / L;
+        const float* xr = x + (row < n ? row : 0) * C;
+#pragma unroll
+        for (int j = 0; j < V; ++j) t[j] = *reinterpret_cast<const float4*>(xr + (j * L + sub) * 4);
+    };
+    int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    float4 nxt[V];
+    load(g, nxt);
+    for (; g * R < n; g += waves) {
         const int64_t row = g * R + lane / L;
         const bool live = row < n;
-        const float* xr = x + (live ? row : 0) * C;
         float v[V][4];
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-            const float4 t = *reinterpret_cast<const float4*>(xr + (j * L + sub) * 4);
-            v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
+            v[j][0] = nxt[j].x; v[j][1] = nxt[j].y; v[j][2] = nxt[j].z; v[j][3] = nxt[j].w;
         }
+        load(g + waves, nxt);
         float sum = 0.f;
 #pragma unroll
         for (int j = 0; j < V; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) sum += v[j][e];
+        if constexpr (L == 16) {
+            sum = row16_sum(sum);
+        } else {
 #pragma unroll
-        for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+            for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        }
         const float mean = sum / (float)C;
         float q = 0.f;
 #pragma unroll
@@ -231,8 +262,12 @@ __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x
                 v[j][e] -= mean;
                 q += v[j][e] * v[j][e];
             }
+        if constexpr (L == 16) {
+            q = row16_sum(q);
+        } else {
 #pragma unroll
-        for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+            for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+        }
         const float rstd = 1.0f / sqrtf(q / (float)C + eps);
         float acc[kHeadMaxCo];
 #pragma unroll
@@ -242,6 +277,28 @@ __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x
             for (int j = 0; j < V; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[o] += v[j][e] * rstd * wv[o][j][e];
+        }
+        if constexpr (L == 16) {
+            // Reduce-scatter of the 8 sums over the row's 16 lanes in 8 DPP moves: each step
+            // pairs lanes that differ in one of bits 3, 2, 1 of sub, and the lane keeps the half
+            // of its sums that bit selects. Lanes sub and sub ^ 1 end with the total of output
+            // o = 4 b3 + 2 b2 + b1; the even one stores it.
+            const bool h3 = sub & 8, h2 = sub & 4, h1 = sub & 2;
+            float a4[4], a2[2];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                a4[k] = (h3 ? acc[4 + k] : acc[k]) + dpp<kDppMirror>(h3 ? acc[k] : acc[4 + k]);
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                a2[k] = (h2 ? a4[2 + k] : a4[k]) + dpp<kDppHalfMirror>(h2 ? a4[k] : a4[2 + k]);
+            float r = (h1 ? a2[1] : a2[0]) + dpp<kDppXor2>(h1 ? a2[0] : a2[1]);
+            r += dpp<kDppXor1>(r);
+            const int o = (h3 ? 4 : 0) + (h2 ? 2 : 0) + (h1 ? 1 : 0);
+            if (live && !(sub & 1) && o < co) out[row * co + o] = r + bo16;
+            continue;
+        }
+#pragma unroll
+        for (int o = 0; o < kHeadMaxCo; ++o) {
 #pragma unroll
             for (int off = L / 2; off > 0; off >>= 1) acc[o] += __shfl_xor(acc[o], off, 64);
         }
