@@ -84,6 +84,25 @@ __device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {
     }
 }
 
+// Sum over aligned groups of L lanes (16 <= L <= 64); every lane of a group ends with the same
+// value. Within a 16-lane DPP row the moves are lane ^ 1, lane ^ 2, 7 - lane within each 8 and
+// 15 - lane, each pairing lanes whose partial sums cover disjoint lanes; across rows, shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(L == 16 || L == 32 || L == 64, "group of 16, 32 or 64 lanes");
+    v += dpp_move<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    v += dpp_move<0x141>(v);   // row_half_mirror
+    v += dpp_move<0x140>(v);   // row_mirror
+    if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // Rows of c = 4 L V channels held in registers: L lanes per row (64 / L rows per wave), each lane
 // V groups of 4 channels, interleaved so that a row's lanes read consecutive 16 bytes. One read of
 // x, one write of out; every lane takes part in the group reductions, rows past n store nothing.
@@ -105,8 +124,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_vec(const void* __restrict__
     for (int j = 0; j < V; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) s += v[j][e];
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    s = group_sum<L>(s);
     const float mean = s / (float)c;
     float q = 0.f;
 #pragma unroll
@@ -116,8 +134,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_vec(const void* __restrict__
             const float d = v[j][e] - mean;
             q += d * d;
         }
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+    q = group_sum<L>(q);
     const float rstd = 1.0f / sqrtf(q / (float)c + eps);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
