@@ -6,7 +6,7 @@
 // entries are bricks, not voxels:
 //   * with X = x + 1 (so that the x - 1 probes stay non-negative), voxel (X, Y, Z) lives in
 //     brick (X>>1, Y>>1, Z>>1) at octant (X&1) | (Y&1)<<1 | (Z&1)<<2. A bucket is one 64-byte
-//     line: the brick's key and the rows of its 8 voxels (row + 1, 0 = absent);
+//     line: the rows of its 8 voxels (row + 1, 0 = absent) in words 0-7, then the brick's key;
 //   * the 27 neighbours of a voxel lie in the 2x2x2 bricks from ((X-1)>>1, ...), so a voxel
 //     looks up 8 buckets instead of 27 keys, and consecutive voxels of a sorted set look up
 //     mostly the same buckets, which the vector L1 then serves;
@@ -26,6 +26,7 @@ namespace {
 
 constexpr int32_t kCoordMax = (1 << 21) - 3;   // voxel coords in [0, kCoordMax]
 constexpr int kBucketWords = 16;               // uint32 words of a bucket (64 bytes)
+constexpr int kKeyWord = 8;                    // the key's first word; rows are words 0-7
 
 // Brick coordinates in [0, 2^20) -> a key that is never 0 (0 marks an empty bucket).
 __device__ __forceinline__ uint64_t brick_key(uint32_t bx, uint32_t by, uint32_t bz) {
@@ -42,7 +43,7 @@ __device__ __forceinline__ uint64_t mix64(uint64_t k) {
 }
 
 struct HashView {
-    uint32_t* words;   // [cap][16]: key (2 words), rows of octants 0..7 (8 words), unused
+    uint32_t* words;   // [cap][16]: rows of octants 0..7 (8 words), key (2 words), unused
     uint64_t cap;
 };
 
@@ -81,19 +82,18 @@ __global__ void k_hash_insert(const int32_t* __restrict__ coords, int64_t n, Has
     // is set never changes, so only buckets that look empty or foreign need the CAS.
     for (uint64_t s = home(h, key);; s = next(h, s)) {
         uint32_t* b = h.words + s * kBucketWords;
-        unsigned long long prev = __hip_atomic_load(reinterpret_cast<unsigned long long*>(b),
-                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (prev == 0)
-            prev = atomicCAS(reinterpret_cast<unsigned long long*>(b), 0ull, (unsigned long long)key);
+        unsigned long long* kp = reinterpret_cast<unsigned long long*>(b + kKeyWord);
+        unsigned long long prev = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == 0) prev = atomicCAS(kp, 0ull, (unsigned long long)key);
         if (prev == 0 || prev == key) {
-            atomicMax(b + 2 + oct, (uint32_t)i + 1);
+            atomicMax(b + oct, (uint32_t)i + 1);
             return;
         }
     }
 }
 
 __device__ __forceinline__ uint64_t bucket_key(const HashView& h, uint64_t s) {
-    return *reinterpret_cast<const uint64_t*>(h.words + s * kBucketWords);
+    return *reinterpret_cast<const uint64_t*>(h.words + s * kBucketWords + kKeyWord);
 }
 
 // Bucket index of `key`, or h.cap when no bucket holds it, given the key k already read from
@@ -137,27 +137,45 @@ __global__ __launch_bounds__(kProbeThreads) void k_probe(const int32_t* __restri
     for (int c = 0; c < 8; ++c) got[c] = bucket_key(h, bk[c]);
 #pragma unroll
     for (int c = 0; c < 8; ++c) bk[c] = find_from(h, key[c], bk[c], got[c]);
-    // brick of offset -1 / 0 / +1 along an axis: 0 / 1 - (X & 1) / 1
-    const int ex = 1 - (X & 1), ey = 1 - (Y & 1), ez = 1 - (Z & 1);
-    // All 27 reads come before the first store, so they go out together.
-    uint32_t r[kTaps];
+    // The 8 bricks cover a 4x4x4 block of voxels, a[px][py][pz] with p = 2 (brick bit) +
+    // (octant bit) per axis; rows are read as two 16-byte loads per brick (bucket 0 stands in for
+    // an absent brick and is discarded), all before the first store.
+    uint32_t a[4][4][4];
 #pragma unroll
-    for (int t = 0; t < kTaps; ++t) {
-        const int dx = t / 9 - 1, dy = (t / 3) % 3 - 1, dz = t % 3 - 1;
-        const int cx = dx < 0 ? 0 : dx > 0 ? 1 : ex;
-        const int cy = dy < 0 ? 0 : dy > 0 ? 1 : ey;
-        const int cz = dz < 0 ? 0 : dz > 0 ? 1 : ez;
-        const int c = cx | cy << 1 | cz << 2;
-        const int oct = ((X + dx) & 1) | ((Y + dy) & 1) << 1 | ((Z + dz) & 1) << 2;
-        uint64_t s = bk[0];
+    for (int c = 0; c < 8; ++c) {
+        const bool have = bk[c] != h.cap;
+        const u32x4_t* b = reinterpret_cast<const u32x4_t*>(h.words + (have ? bk[c] : 0) * kBucketWords);
+        const u32x4_t lo = b[0], hi = b[1];
 #pragma unroll
-        for (int k = 1; k < 8; ++k) s = c == k ? bk[k] : s;
-        // Read unconditionally (bucket 0 stands in for an absent brick) and discard afterwards,
-        // so no read sits behind a branch.
-        const bool have = s != h.cap;
-        const uint32_t w = h.words[(have ? s : 0) * kBucketWords + 2 + oct];
-        r[t] = have ? w : 0;
+        for (int o = 0; o < 8; ++o) {
+            const uint32_t w = o < 4 ? lo[o] : hi[o - 4];
+            a[2 * (c & 1) + (o & 1)][2 * ((c >> 1) & 1) + ((o >> 1) & 1)][2 * (c >> 2) + (o >> 2)] =
+                have ? w : 0u;
+        }
     }
+    // The neighbourhood is the 3x3x3 window at e = 1 - (X & 1) per axis: offset d in {-1, 0, 1}
+    // sits at p = d + 1 + e. Selected one axis at a time.
+    const bool ex = !(X & 1), ey = !(Y & 1), ez = !(Z & 1);
+    uint32_t bx3[3][4][4], by3[3][3][4], r[kTaps];
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+        for (int py = 0; py < 4; ++py)
+#pragma unroll
+            for (int pz = 0; pz < 4; ++pz) bx3[q][py][pz] = ex ? a[q + 1][py][pz] : a[q][py][pz];
+#pragma unroll
+    for (int qx = 0; qx < 3; ++qx)
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+#pragma unroll
+            for (int pz = 0; pz < 4; ++pz) by3[qx][q][pz] = ey ? bx3[qx][q + 1][pz] : bx3[qx][q][pz];
+#pragma unroll
+    for (int qx = 0; qx < 3; ++qx)
+#pragma unroll
+        for (int qy = 0; qy < 3; ++qy)
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+                r[qx * 9 + qy * 3 + q] = ez ? by3[qx][qy][q + 1] : by3[qx][qy][q];
 #pragma unroll
     for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = r[t] ? (int32_t)(r[t] - 1) : miss;
 }
