@@ -41,10 +41,19 @@ def test_edge_cases(gpu_lib, orc, shells):
         "shell-257": shells.sphere_shell(40, 20.0, 10.0, 11.0)[:257],
         "unsorted": rng.permutation(shells.sphere_shell(40, 20.0, 12.0, 14.0)),
     }
+    import torch
     for name, c in cases.items():
         _case(name)
         ref = orc.neighbor_table_sorted(c)
         assert np.array_equal(_gpu_table(gpu_lib, c), ref), name
+        # pair count, also of a copy of the table that starts 1-3 elements past a 16-byte boundary
+        n, want = len(c), int((ref != len(c)).sum())
+        for off in range(4):
+            buf = torch.zeros(27 * n + off, dtype=torch.int32, device="cuda")
+            buf[off:] = torch.from_numpy(ref).cuda()
+            view = buf[off:]
+            assert view.data_ptr() % 16 == 4 * off
+            assert gpu_lib.count_pairs(view, n) == want, (name, off)
 
 
 def test_empty(gpu_lib):
