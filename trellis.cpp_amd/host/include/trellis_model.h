@@ -1,5 +1,6 @@
-// trellis_model.h -- the GGUF model container of trellis.cpp (include/trellis_model.h), same
-// members and functions, with the weights uploaded to a HIP device of this build's runtime.
+// trellis_model.h -- the GGUF model container that trellis.cpp's sparse-path callers use
+// (include/trellis_model.h): the declarations are the reference's, so callers compile unchanged;
+// the weights live on a HIP device of this build's runtime.
 #pragma once
 
 #include <cstdint>
@@ -30,7 +31,7 @@ struct Model {
     // gpu = HIP device index. This build has no CPU backend: gpu < 0 throws.
     static Model load(const std::string& path, int gpu = 0);
 
-    ggml_tensor* get(const std::string& name) const;       // throws "missing tensor: <name>"
+    ggml_tensor* get(const std::string& name) const;       // throws std::runtime_error if missing
     ggml_tensor* try_get(const std::string& name) const;   // nullptr if missing
     bool has(const std::string& name) const;
 
@@ -38,7 +39,7 @@ struct Model {
     void free();
 };
 
-// A tensor's contents on the host as float32 (F32 and F16; throws for other types).
+// A tensor's contents on the host as float32 (F32, F16 and BF16; throws for other types).
 std::vector<float> tensor_to_f32(ggml_tensor* t);
 
 }  // namespace trellis
