@@ -95,6 +95,19 @@ int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
                      const float* d_bias, int co, void* d_out, int out_dtype, int algo,
                      void* stream);
 
+/* Flags of the *_ex convs. TSP_CONV_ZERO_PAD: absent taps read an exact zero row instead of
+ * the reference's padding row 0 * feats[0] (whose NaN channels, where feats[0] holds an Inf or
+ * a NaN, make every output row with an absent tap NaN). The C2S block's conv2 reads such a row:
+ * its padding column is silu(norm(0)) = 0 (sparse.cpp:289-306). */
+enum { TSP_CONV_ZERO_PAD = 1 };
+
+/* tsp_subm_conv3x3 with flags (same replaced function, sparse.cpp:61-92; flags 0 = the same
+ * call). */
+int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
+                        const int32_t* d_nbr, const void* d_weight, int weight_dtype,
+                        const float* d_bias, int co, void* d_out, int out_dtype, int algo,
+                        int flags, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Reusable conv plan and packed weights (no counterpart call in the reference: they split
  * the work sparse_submconv repeats on every call, sparse.cpp:61-92, into what depends only on
@@ -122,6 +135,17 @@ int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t n, int ci,
                              const void* d_packed_weight, const float* d_bias, int co,
                              void* d_out, int out_dtype, void* stream);
 
+/* tsp_subm_conv3x3_planned with flags (TSP_CONV_ZERO_PAD) and, optionally, d_row0: the f32
+ * row 0 (ci floats) that a caller rounded d_feats from (ggml's F16 mul_mat rounds F32
+ * activations, sparse.cpp:74, while the padding row 0 * feats[0] is formed before that, in F32,
+ * sparse.cpp:81-85). Where d_row0 is given, the padding row's NaN channels are those of
+ * 0 * d_row0; NULL tests feats row 0 itself. flags 0 and d_row0 NULL = the same call. */
+int tsp_subm_conv3x3_planned_ex(const void* d_feats, int dtype, int64_t n, int ci,
+                                const int32_t* d_nbr, const void* d_plan,
+                                const void* d_packed_weight, const float* d_bias, int co,
+                                void* d_out, int out_dtype, int flags, const float* d_row0,
+                                void* stream);
+
 /* The C2S block's conv1 with its octant gather fused into the stores (sparse.cpp:263-291: conv1
  * maps Cin -> 8*Cout, then child m takes channels [(gidx[m]%8)*Cout, +Cout) of parent
  * gidx[m]/8; the stores here put them there directly, and the [N][8*Cout] intermediate is never
@@ -141,7 +165,8 @@ int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, int64_t n, 
  * conv of tsp_subm_conv3x3_planned with f32 output over the M children, plus
  * x[gidx[m]/8][(gidx[m]%8)*K + c/R] in output channel c of row m -- the result of
  * tsp_subm_conv3x3_planned followed by tsp_c2s_skip_add, without the second pass over the
- * output. x f32 [N][cin]; gidx [M] from tsp_subdivide; cin % 8 == 0 and R % 4 == 0. */
+ * output. x f32 [N][cin]; gidx [M] from tsp_subdivide; cin % 8 == 0 and R % 4 == 0. Absent
+ * taps read an exact zero row (TSP_CONV_ZERO_PAD), as the reference's conv2 does. */
 int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int ci,
                                   const int32_t* d_nbr, const void* d_plan,
                                   const void* d_packed_weight, const float* d_bias, int co,

@@ -186,9 +186,11 @@ static int sentinel_nan(const float* feats, int64_t n, int ci) {
 
 void orc_subm_conv_f64_rows(const float* feats, int64_t n, int ci, const int32_t* nbr,
                             const float* weight, const float* bias, int co, double* out,
-                            const int64_t* rows, int64_t nrows, int threads) {
+                            const int64_t* rows, int64_t nrows, int threads, int zero_pad) {
     set_threads(threads);
-    const int snan = sentinel_nan(feats, n, ci);
+    /* zero_pad: the padding row is an exact zero column (the C2S conv2 reads hn, whose column M
+       is silu(norm(0)) = 0, sparse.cpp:289-306) instead of 0 * feats[0] */
+    const int snan = zero_pad ? 0 : sentinel_nan(feats, n, ci);
 #pragma omp parallel for schedule(static)
     for (int64_t j = 0; j < nrows; ++j) {
         const int64_t i = rows[j];
@@ -214,9 +216,9 @@ void orc_subm_conv_f64_rows(const float* feats, int64_t n, int ci, const int32_t
 
 void orc_subm_conv_f64(const float* feats, int64_t n, int ci, const int32_t* nbr,
                        const float* weight, const float* bias, int co, double* out,
-                       int threads) {
+                       int threads, int zero_pad) {
     set_threads(threads);
-    const int snan = sentinel_nan(feats, n, ci);
+    const int snan = zero_pad ? 0 : sentinel_nan(feats, n, ci);   /* as in the _rows form */
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
         double* dst = out + i * co;

@@ -49,12 +49,13 @@ void orc_subm_conv_f32(const float* feats, int64_t n, int ci, const int32_t* nbr
 /* The same sum evaluated in fp64 over only the active taps: the judge for tolerances. */
 void orc_subm_conv_f64(const float* feats, int64_t n, int ci, const int32_t* nbr,
                        const float* weight, const float* bias, int co, double* out,
-                       int threads);
+                       int threads, int zero_pad);
 
-/* orc_subm_conv_f64 for the output rows listed in rows[0..nrows) only; out is [nrows][Co]. */
+/* orc_subm_conv_f64 for the output rows listed in rows[0..nrows) only; out is [nrows][Co].
+ * zero_pad (both forms): absent taps read an exact zero row, not 0 * feats[0]. */
 void orc_subm_conv_f64_rows(const float* feats, int64_t n, int ci, const int32_t* nbr,
                             const float* weight, const float* bias, int co, double* out,
-                            const int64_t* rows, int64_t nrows, int threads);
+                            const int64_t* rows, int64_t nrows, int threads, int zero_pad);
 
 /* Timed CPU baseline: orc_subm_conv_f32 over output rows [r0, r1) only. */
 void orc_subm_conv_f32_rows(const float* feats, int64_t n, int ci, const int32_t* nbr,

@@ -56,13 +56,13 @@ def lib():
                                              ctypes.c_int64, ctypes.c_int]
         L.orc_subm_conv_f32_rows.restype = None
         L.orc_subm_conv_f64.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _i32p, _f32p, _f32p,
-                                        ctypes.c_int, _f64p, ctypes.c_int]
+                                        ctypes.c_int, _f64p, ctypes.c_int, ctypes.c_int]
         L.orc_subm_conv_f64.restype = None
         L.orc_subm_conv_f64_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _i32p, _f32p,
                                              _f32p, ctypes.c_int, _f64p,
                                              np.ctypeslib.ndpointer(dtype=np.int64,
                                                                     flags="C_CONTIGUOUS"),
-                                             ctypes.c_int64, ctypes.c_int]
+                                             ctypes.c_int64, ctypes.c_int, ctypes.c_int]
         L.orc_subm_conv_f64_rows.restype = None
         L.orc_subdivide.argtypes = [_u8p, _i32p, ctypes.c_int64, _i32p, _i32p, _i32p]
         L.orc_subdivide.restype = ctypes.c_int64
@@ -158,8 +158,10 @@ def subm_conv_f32_rows(feats, nbr, weight, bias, r0: int, r1: int, threads: int 
     return out
 
 
-def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0) -> np.ndarray:
-    """The same sum in fp64 over active taps only: the tolerance judge."""
+def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0, zero_pad: bool = False) -> np.ndarray:
+    """The same sum in fp64 over active taps only: the tolerance judge. Absent taps read the
+    padding row 0 * feats[0] (NaN rows where feats[0] is not finite), or with zero_pad an exact
+    zero row (the C2S conv2, sparse.cpp:289-306)."""
     f = np.ascontiguousarray(feats, dtype=np.float32)
     n, ci = f.shape
     w = np.ascontiguousarray(weight, dtype=np.float32)
@@ -167,11 +169,12 @@ def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0) -> np.ndarray:
     b = np.ascontiguousarray(bias, dtype=np.float32).reshape(co)
     nb = np.ascontiguousarray(nbr, dtype=np.int32).reshape(27 * n)
     out = np.empty((n, co), np.float64)
-    lib().orc_subm_conv_f64(f, n, ci, nb, w, b, co, out, threads)
+    lib().orc_subm_conv_f64(f, n, ci, nb, w, b, co, out, threads, 1 if zero_pad else 0)
     return out
 
 
-def subm_conv_f64_rows(feats, nbr, weight, bias, rows, threads: int = 0) -> np.ndarray:
+def subm_conv_f64_rows(feats, nbr, weight, bias, rows, threads: int = 0,
+                      zero_pad: bool = False) -> np.ndarray:
     """fp64 conv for the listed output rows only -> [len(rows), Co]."""
     f = np.ascontiguousarray(feats, dtype=np.float32)
     n, ci = f.shape
@@ -181,7 +184,7 @@ def subm_conv_f64_rows(feats, nbr, weight, bias, rows, threads: int = 0) -> np.n
     nb = np.ascontiguousarray(nbr, dtype=np.int32).reshape(27 * n)
     r = np.ascontiguousarray(rows, dtype=np.int64)
     out = np.empty((len(r), co), np.float64)
-    lib().orc_subm_conv_f64_rows(f, n, ci, nb, w, b, co, out, r, len(r), threads)
+    lib().orc_subm_conv_f64_rows(f, n, ci, nb, w, b, co, out, r, len(r), threads, 1 if zero_pad else 0)
     return out
 
 
@@ -284,7 +287,9 @@ def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None):
     h = h.reshape(n * 8, cout)[gidx]                              # octant gather, :288
     h = silu(layer_norm(h, None, None, 1e-6))                     # norm2 without affine, :293
     nbr2 = neighbor_table(child)
-    h = subm_conv_f64(h.astype(np.float32), nbr2, p[prefix + ".conv2.weight"], p[prefix + ".conv2.bias"])
+    # conv2 reads hn padded with its zero column M (silu(norm(0)) = 0, :289-306), not 0 * hn[0]
+    h = subm_conv_f64(h.astype(np.float32), nbr2, p[prefix + ".conv2.weight"], p[prefix + ".conv2.bias"],
+                      zero_pad=True)
     xs = x.reshape(n * 8, k)[gidx].astype(np.float64)             # skip gather, :307
     skip = np.repeat(xs, r, axis=1)                               # repeat_interleave, :322
     return h + skip, child, mask

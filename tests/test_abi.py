@@ -185,3 +185,58 @@ def test_planned_skip_validation(pkg):
     assert f(x=NULL) == 1 and f(gidx=NULL) == 1
     assert f(out=X) == 1                                   # out aliases x
     assert "alias" in _err(pkg)
+
+
+def test_conv_ex_flags_validation(pkg):
+    """The *_ex convs: unknown flag bits are rejected (1) before any device work; flags 0 takes
+    the same checks as the plain calls."""
+    L = pkg.lib()
+    O = ctypes.c_void_p(0x2000)
+    f = lambda flags, **kw: L.tsp_subm_conv3x3_ex(
+        FAKE, 2, kw.get("n", 100), 64, FAKE, FAKE, 2, FAKE, 64, kw.get("out", O), 0, 0, flags, NULL)
+    assert f(2) == 1 and "flags" in _err(pkg)
+    assert f(1, n=0) == 0 and f(0, n=0) == 0
+    assert f(1, out=FAKE) == 1 and "alias" in _err(pkg)
+    p = lambda flags, **kw: L.tsp_subm_conv3x3_planned_ex(
+        FAKE, kw.get("dt", 2), kw.get("n", 100), 64, FAKE, FAKE, FAKE, FAKE, 64, O, 0, flags,
+        kw.get("row0", NULL), NULL)
+    assert p(4) == 1 and "flags" in _err(pkg)
+    assert p(1, dt=0) == 4
+    assert p(1, n=0) == 0 and p(0, n=0, row0=FAKE) == 0
+
+
+def test_python_conv_argument_checks(pkg):
+    """The binding checks every buffer the kernels index before any launch: a caller's out (shape,
+    dtype, contiguity), the table's size and dtype, the plan's size against tsp_conv_plan_bytes,
+    the packed weight's dtype and size. Host tensors reach each check (they run before the device
+    check), so the ValueError names the problem."""
+    import torch
+    n, ci, co = 100, 64, 64
+    f = torch.zeros((n, ci), dtype=torch.bfloat16)
+    nbr = torch.zeros(27 * n, dtype=torch.int32)
+    w = torch.zeros((co, 27, ci), dtype=torch.bfloat16)
+    b = torch.zeros(co, dtype=torch.float32)
+    with pytest.raises(ValueError, match="shape"):
+        pkg.subm_conv3x3(f, nbr, w, b, out=torch.zeros((n - 1, co)))
+    with pytest.raises(ValueError, match="must be torch.float32"):
+        pkg.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, out=torch.zeros((n, co), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="contiguous"):
+        pkg.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, out=torch.zeros((co, n)).t())
+    with pytest.raises(ValueError, match="27\\*N"):
+        pkg.subm_conv3x3(f, nbr[:-1], w, b)
+    with pytest.raises(ValueError, match="27\\*N"):
+        pkg.subm_conv3x3(f, nbr.to(torch.int64), w, b)
+    plan_ok = torch.zeros(pkg.lib().tsp_conv_plan_bytes(n), dtype=torch.uint8)
+    packed = torch.zeros(co * 27 * ci, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="plan holds"):
+        pkg.subm_conv3x3_planned(f, nbr, plan_ok[:-1], packed, b, co)
+    with pytest.raises(ValueError, match="packed weight is"):
+        pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed.to(torch.float16), b, co)
+    with pytest.raises(ValueError, match="packed weight size"):
+        pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed[:-8], b, co)
+    with pytest.raises(ValueError, match="shape"):
+        pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed, b, co, out=torch.zeros((n, co + 1)))
+    with pytest.raises(ValueError, match="row0"):
+        pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed, b, co, row0=torch.zeros(ci - 1))
+    with pytest.raises(ValueError, match="GPU"):   # every check passed: only the device is wrong
+        pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed, b, co)

@@ -374,3 +374,100 @@ def test_full_size_sampled_rows(gpu_lib, orc, shells, name):
     got = out.cpu().numpy()
     assert orc.rel_err(got[rows], ref) < TOL_16
     assert orc.rel_err(got, outn.cpu().numpy()) < TOL_16
+
+
+def _nan_aware(out, ref, tol):
+    """Non-finite entries at the same places (NaN vs Inf not distinguished); the finite rest
+    within tol of max|ref| over the finite reference entries."""
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(out), fin)
+    err = np.abs(out[fin] - ref[fin]).max() / max(np.abs(ref[fin]).max(), 1e-30)
+    assert err < tol, err
+
+
+@pytest.mark.parametrize("bad", ["inf", "nan"])
+@pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "unsorted", "skip"])
+def test_zero_padding_row(gpu_lib, orc, shells, path, bad):
+    """TSP_CONV_ZERO_PAD: absent taps read an exact zero row, as the C2S conv2 reads hn's zero
+    padding column (sparse.cpp:289-306). With an Inf or a NaN in feature row 0, only the rows
+    that reference row 0 become non-finite; every other row keeps its finite value, against the
+    oracle's zero-padded conv. "skip" is the fused C2S conv2 (always zero padded)."""
+    _case(f"zero padding row {path} {bad}")
+    import torch
+    rng = np.random.default_rng(29)
+    coords = np.concatenate([shells.sphere_shell(24, 12.0, 7.0, 9.0),
+                             np.stack(np.meshgrid(*[np.arange(40, 45)] * 3, indexing="ij"), -1).reshape(-1, 3)])
+    if path == "unsorted":
+        coords = np.concatenate([coords[:1], rng.permutation(coords[1:])])
+    coords = np.ascontiguousarray(coords, np.int32)
+    n, ci, co = len(coords), 32, 64
+    key = "f32" if path == "f32" else "bf16"
+    feats = rng.standard_normal((n, ci)).astype(np.float32)
+    feats[0, 5] = np.inf if bad == "inf" else np.nan
+    weight = (rng.standard_normal((co, 27, ci)) / 30).astype(np.float32)
+    if key == "bf16":
+        feats, weight = shells.round_to(feats, "bf16"), shells.round_to(weight, "bf16")
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    ref = orc.subm_conv_f64(feats, nbr, weight, bias, zero_pad=True)
+    dt = torch.float32 if key == "f32" else torch.bfloat16
+    c = torch.from_numpy(coords).cuda()
+    nbr_d = gpu_lib.rulebook_build(c)
+    f, w, b = _dev(feats, dt), _dev(weight, dt), _dev(bias, torch.float32)
+    if path in ("planned", "skip"):
+        plan = gpu_lib.conv_plan_build(nbr_d, n)
+        pw = gpu_lib.conv_weight_pack(w)
+        if path == "planned":
+            out = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32,
+                                               zero_pad=True)
+        else:
+            # children of n // 8 parents: every child m has gidx = m, so x row m // 8 feeds it
+            cin = 128
+            x = rng.standard_normal((n // 8 + 1, cin)).astype(np.float32)
+            gidx = torch.arange(n, dtype=torch.int32, device="cuda")
+            out = gpu_lib.subm_conv3x3_planned_skip(f, nbr_d, plan, pw, b, co, _dev(x, torch.float32), gidx)
+            k = cin // 8
+            ref = ref + np.repeat(x.reshape(-1, k)[np.arange(n)], co // k, axis=1)
+    else:
+        algo = {"auto": "auto", "unsorted": "mfma", "mfma_gather": "mfma_gather", "narrow": "narrow",
+                "f32": "auto"}[path]
+        out = gpu_lib.subm_conv3x3(f, nbr_d, w, b, out_dtype=torch.float32, algo=algo, zero_pad=True)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    t = nbr.reshape(27, n)
+    refs0 = (t == 0).any(axis=0)
+    absent = (t == n).any(axis=0)
+    assert (absent & ~refs0).any()
+    assert np.isfinite(out[~refs0]).all()
+    _nan_aware(out, ref, TOL_32 if key == "f32" else TOL_16)
+
+
+def test_padding_row_from_f32_source(gpu_lib, orc, shells):
+    """A finite f32 row 0 beyond the f16 range rounds to Inf. The reference forms its padding row
+    0 * feats[0] in F32 before ggml's F16 mul_mat rounds the activations (sparse.cpp:74, 81-85), so
+    the padding row is zero: given the f32 row 0 (row0=), only rows that reference row 0 turn
+    non-finite. Without it the rounded Inf row makes every row with an absent tap NaN."""
+    _case("padding row from the f32 source row")
+    import torch
+    rng = np.random.default_rng(37)
+    coords = np.ascontiguousarray(shells.sphere_shell(24, 12.0, 7.0, 9.0), np.int32)
+    n, ci, co = len(coords), 32, 64
+    feats32 = rng.standard_normal((n, ci)).astype(np.float32)
+    feats32[0, 3] = 1.0e5                                   # finite, > 65504
+    feats16 = shells.round_to(feats32, "f16")
+    assert np.isinf(feats16[0, 3])
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / 30).astype(np.float32), "f16")
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    c = torch.from_numpy(coords).cuda()
+    nbr_d = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr_d, n)
+    pw = gpu_lib.conv_weight_pack(_dev(weight, torch.float16))
+    f, b = _dev(feats16, torch.float16), _dev(bias, torch.float32)
+    with_src = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32,
+                                            row0=_dev(feats32[0], torch.float32))
+    without = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _nan_aware(with_src.cpu().numpy(), orc.subm_conv_f64(feats16, nbr, weight, bias, zero_pad=True), TOL_16)
+    absent = (nbr.reshape(27, n) == n).any(axis=0)
+    assert np.isnan(without.cpu().numpy()[absent]).all()

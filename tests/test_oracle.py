@@ -116,6 +116,38 @@ def test_conv_dense_box_equals_conv3d(orc):
     assert orc.rel_err(orc.subm_conv_f32(feats, nbr, weight, bias), ref) < 1e-6
 
 
+def test_conv_zero_pad_dense_box(orc):
+    """zero_pad: absent taps read an exact zero row. On a dense box the only absent taps point
+    out of the box, where conv3d's zero padding reads zeros too, so with an Inf at one voxel the
+    zero-padded sparse conv equals conv3d, NaN and Inf positions included: only that voxel's
+    neighbours are non-finite. The reference padding 0 * feats[0] instead makes every boundary
+    voxel NaN when the Inf sits in row 0, so it must differ from conv3d there."""
+    rng = np.random.default_rng(8)
+    dims = (4, 5, 4)
+    coords, feats = _dense_box(rng, dims, 6)
+    weight = rng.standard_normal((5, 27, 6)).astype(np.float32)
+    bias = rng.standard_normal(5).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    for row in (0, 37):
+        f = feats.copy()
+        f[row, 2] = np.inf
+        with np.errstate(invalid="ignore"):
+            ref = _conv3d_reference(coords, f, weight, bias, dims)
+        got = orc.subm_conv_f64(f, nbr, weight, bias, zero_pad=True)
+        assert np.array_equal(np.isfinite(got), np.isfinite(ref))
+        fin = np.isfinite(ref)
+        assert np.allclose(got[fin], ref[fin], rtol=1e-12, atol=1e-10)
+        assert (~np.isfinite(got)).any(axis=1).sum() == (nbr.reshape(27, -1) == row).any(axis=0).sum()
+        rows = np.arange(0, len(coords), 3)
+        assert np.array_equal(np.isfinite(orc.subm_conv_f64_rows(f, nbr, weight, bias, rows, zero_pad=True)),
+                              np.isfinite(got[rows]))
+    f0 = feats.copy()
+    f0[0, 2] = np.inf
+    default = orc.subm_conv_f64(f0, nbr, weight, bias)
+    boundary = (nbr.reshape(27, -1) == len(coords)).any(axis=0)
+    assert np.isnan(default[boundary]).all()
+
+
 def test_conv_dense_box_planted(orc):
     """Weights with the tap axis mirrored (a transposed kernel) must fail the conv3d check."""
     rng = np.random.default_rng(6)
@@ -316,6 +348,12 @@ def test_c2s_block_vs_loops(orc, shells):
     kids = np.array(kids, np.int32)
     assert np.array_equal(kids, child)
     hn = F.silu(F.layer_norm(T(np.array(rows)), (cout,), None, None, 1e-6)).numpy()
-    nbr2 = orc.neighbor_table(kids)
-    h2 = orc.subm_conv_f64(hn.astype(np.float32), nbr2, p["c2s.conv2.weight"], p["c2s.conv2.bias"])
+    nbr2 = orc.neighbor_table(kids).reshape(27, -1)
+    # conv2 as the reference states it: hn with its zero padding column M appended
+    # (silu(norm(0)) = 0, sparse.cpp:289-306), gathered per tap and multiplied
+    m = len(kids)
+    hn_pad = np.concatenate([hn.astype(np.float32).astype(np.float64), np.zeros((1, cout))])
+    w2 = p["c2s.conv2.weight"].astype(np.float64)
+    h2 = p["c2s.conv2.bias"].astype(np.float64) + sum(hn_pad[nbr2[t]] @ w2[:, t, :].T for t in range(27))
+    assert nbr2.shape[1] == m
     assert np.allclose(out, h2 + np.array(skips), atol=1e-9)

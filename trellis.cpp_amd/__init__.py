@@ -24,9 +24,9 @@ STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "RANGE", 4: "UNSUPPORTED", 5: "WOR
 EXPORTS = (
     "tsp_last_error", "tsp_version",
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
-    "tsp_subm_conv3x3",
+    "tsp_subm_conv3x3", "tsp_subm_conv3x3_ex",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
-    "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_octants",
+    "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_ex", "tsp_subm_conv3x3_planned_octants",
     "tsp_subm_conv3x3_planned_skip",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
     "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
@@ -70,6 +70,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_subm_conv3x3.restype = c_int
     L.tsp_subm_conv3x3.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int,
                                    c_vp, c_int, c_int, c_vp]
+    L.tsp_subm_conv3x3_ex.restype = c_int
+    L.tsp_subm_conv3x3_ex.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int,
+                                      c_vp, c_int, c_int, c_int, c_vp]
     L.tsp_conv_plan_bytes.restype = c_sz
     L.tsp_conv_plan_bytes.argtypes = [c_i64]
     L.tsp_conv_plan_build.restype = c_int
@@ -79,6 +82,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_subm_conv3x3_planned.restype = c_int
     L.tsp_subm_conv3x3_planned.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
                                            c_int, c_vp, c_int, c_vp]
+    L.tsp_subm_conv3x3_planned_ex.restype = c_int
+    L.tsp_subm_conv3x3_planned_ex.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
+                                              c_int, c_vp, c_int, c_int, c_vp, c_vp]
     L.tsp_subm_conv3x3_planned_octants.restype = c_int
     L.tsp_subm_conv3x3_planned_octants.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp,
                                                    c_vp, c_int, c_vp, c_vp, c_vp, c_vp]
@@ -171,27 +177,53 @@ def count_pairs(nbr, n: int, stream=None) -> int:
     return int(cnt.item())
 
 
-def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", out=None,
-                 stream=None):
-    """feats [N,Ci], nbr int32 [27*N], weight [Co,27,Ci], bias f32 [Co] -> out [N,Co]."""
+def _check_out(out, n: int, co: int, dtype, device):
+    """A caller's out= must be a contiguous [n, co] tensor of the output dtype on the device the
+    inputs are on: the kernels write n * co elements through its raw pointer."""
+    if tuple(out.shape) != (n, co):
+        raise ValueError(f"out must have shape ({n}, {co}), got {tuple(out.shape)}")
+    if out.dtype != dtype:
+        raise ValueError(f"out must be {dtype}, got {out.dtype}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+    if out.device != device:
+        raise ValueError(f"out must live on {device}, got {out.device}")
+
+
+def _check_nbr(nbr, n: int, device):
     torch = _torch()
-    _require_cuda(feats, nbr, weight, bias)
+    if nbr.dtype != torch.int32 or nbr.numel() != 27 * n or not nbr.is_contiguous():
+        raise ValueError(f"nbr must be a contiguous int32 table of 27*N = {27 * n} entries")
+    if nbr.device != device:
+        raise ValueError("nbr must live on the features' device")
+
+
+def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", out=None,
+                 zero_pad: bool = False, stream=None):
+    """feats [N,Ci], nbr int32 [27*N], weight [Co,27,Ci], bias f32 [Co] -> out [N,Co].
+    zero_pad: absent taps read an exact zero row instead of 0 * feats[0]."""
+    torch = _torch()
+    if feats.dim() != 2:
+        raise ValueError("feats must be [N, Ci]")
     n, ci = feats.shape
     co = weight.shape[0]
     if weight.shape != (co, 27, ci):
         raise ValueError(f"weight must be [Co,27,Ci]=[{co},27,{ci}], got {tuple(weight.shape)}")
-    if nbr.numel() != 27 * n or nbr.dtype != torch.int32:
-        raise ValueError("nbr must be int32 [27*N]")
+    _check_nbr(nbr, n, feats.device)
     if bias.dtype != torch.float32 or bias.numel() != co:
         raise ValueError("bias must be float32 [Co]")
     odt = out_dtype or feats.dtype
     if out is None:
         out = torch.empty((n, co), dtype=odt, device=feats.device)
+    else:
+        _check_out(out, n, co, odt, feats.device)
+    _require_cuda(feats, nbr, weight, bias, out)
     f, w, b = feats.contiguous(), weight.contiguous(), bias.contiguous()
-    _check("tsp_subm_conv3x3",
-           lib().tsp_subm_conv3x3(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr), _ptr(w),
-                                  dtype_code(w.dtype), _ptr(b), co, _ptr(out),
-                                  dtype_code(out.dtype), ALGO[algo], _stream(stream)))
+    _check("tsp_subm_conv3x3_ex",
+           lib().tsp_subm_conv3x3_ex(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr), _ptr(w),
+                                     dtype_code(w.dtype), _ptr(b), co, _ptr(out),
+                                     dtype_code(out.dtype), ALGO[algo], 1 if zero_pad else 0,
+                                     _stream(stream)))
     return out
 
 
@@ -199,6 +231,7 @@ def conv_plan_build(nbr, n: int, stream=None):
     """Plan of neighbour table nbr (int32 [27*N]) for tsp_subm_conv3x3_planned -> uint8 buffer."""
     torch = _torch()
     _require_cuda(nbr)
+    _check_nbr(nbr, n, nbr.device)
     nb = lib().tsp_conv_plan_bytes(n)
     plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=nbr.device)
     _check("tsp_conv_plan_build",
@@ -219,24 +252,48 @@ def conv_weight_pack(weight, stream=None):
     return packed
 
 
-def subm_conv3x3_planned(feats, nbr, plan, packed_weight, bias, co: int, out_dtype=None, out=None,
-                         stream=None):
-    """The MFMA conv with a plan (conv_plan_build) and packed weights (conv_weight_pack)."""
-    torch = _torch()
-    _require_cuda(feats, nbr, plan, packed_weight, bias)
-    n, ci = feats.shape
+def _check_planned(feats, nbr, plan, packed_weight, ci: int, co: int):
+    n = feats.shape[0]
+    _check_nbr(nbr, n, feats.device)
+    need = lib().tsp_conv_plan_bytes(n)
+    if plan.numel() * plan.element_size() < need:
+        raise ValueError(f"plan holds {plan.numel() * plan.element_size()} bytes; a table of {n} "
+                         f"voxels needs {need}")
+    if packed_weight.dtype != feats.dtype:
+        raise ValueError(f"packed weight is {packed_weight.dtype}, features are {feats.dtype}")
     if packed_weight.numel() != co * 27 * ci:
         raise ValueError("packed weight size does not match [Co,27,Ci]")
+    if not packed_weight.is_contiguous():
+        raise ValueError("packed weight must be contiguous")
+
+
+def subm_conv3x3_planned(feats, nbr, plan, packed_weight, bias, co: int, out_dtype=None, out=None,
+                         zero_pad: bool = False, row0=None, stream=None):
+    """The MFMA conv with a plan (conv_plan_build) and packed weights (conv_weight_pack).
+    zero_pad: absent taps read an exact zero row; row0 (float32 [Ci]): the unrounded row 0 the
+    features were rounded from, whose 0 * row0 is the padding row."""
+    torch = _torch()
+    if feats.dim() != 2:
+        raise ValueError("feats must be [N, Ci]")
+    n, ci = feats.shape
+    _check_planned(feats, nbr, plan, packed_weight, ci, co)
     if bias.dtype != torch.float32 or bias.numel() != co:
         raise ValueError("bias must be float32 [Co]")
+    if row0 is not None and (row0.dtype != torch.float32 or row0.numel() != ci):
+        raise ValueError("row0 must be float32 [Ci]")
     odt = out_dtype or feats.dtype
     if out is None:
         out = torch.empty((n, co), dtype=odt, device=feats.device)
+    else:
+        _check_out(out, n, co, odt, feats.device)
+    _require_cuda(feats, nbr, plan, packed_weight, bias, out, row0)
     f = feats.contiguous()
-    _check("tsp_subm_conv3x3_planned",
-           lib().tsp_subm_conv3x3_planned(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr),
-                                          _ptr(plan), _ptr(packed_weight), _ptr(bias), co,
-                                          _ptr(out), dtype_code(out.dtype), _stream(stream)))
+    r0 = row0.contiguous() if row0 is not None else None
+    _check("tsp_subm_conv3x3_planned_ex",
+           lib().tsp_subm_conv3x3_planned_ex(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr),
+                                             _ptr(plan), _ptr(packed_weight), _ptr(bias), co,
+                                             _ptr(out), dtype_code(out.dtype),
+                                             1 if zero_pad else 0, _ptr(r0), _stream(stream)))
     return out
 
 
@@ -246,11 +303,9 @@ def subm_conv3x3_planned_octants(feats, nbr, plan, packed_weight, bias, cout: in
     parent i's channels [o*cout, +cout) written to its child of octant o (mask and mstart as
     given to / returned by subdivide) -> float32 [M, cout]."""
     torch = _torch()
-    _require_cuda(feats, nbr, plan, packed_weight, bias, mask, mstart)
     n, ci = feats.shape
     co = 8 * cout
-    if packed_weight.numel() != co * 27 * ci:
-        raise ValueError("packed weight size does not match [8*cout,27,Ci]")
+    _check_planned(feats, nbr, plan, packed_weight, ci, co)
     if bias.dtype != torch.float32 or bias.numel() != co:
         raise ValueError("bias must be float32 [8*cout]")
     m8 = mask.reshape(-1).contiguous()
@@ -258,6 +313,10 @@ def subm_conv3x3_planned_octants(feats, nbr, plan, packed_weight, bias, cout: in
         raise ValueError("mask must be uint8 with 8*N entries")
     if mstart.dtype != torch.int32 or mstart.numel() != n + 1:
         raise ValueError("mstart must be int32 [N+1]")
+    _require_cuda(feats, nbr, plan, packed_weight, bias, mask, mstart)
+    # the kernel writes rows up to mstart[N] - 1: the output must hold exactly that many
+    if n and int(mstart[-1].item()) != m:
+        raise ValueError(f"m={m} but the subdivision has mstart[N]={int(mstart[-1].item())} children")
     out = torch.empty((m, cout), dtype=torch.float32, device=feats.device)
     f = feats.contiguous()
     _check("tsp_subm_conv3x3_planned_octants",
@@ -273,10 +332,8 @@ def subm_conv3x3_planned_skip(feats, nbr, plan, packed_weight, bias, co: int, x,
     the M children plus repeat_interleave of x's octant blocks (x float32 [N, cin], gidx from
     subdivide) -> float32 [M, co]."""
     torch = _torch()
-    _require_cuda(feats, nbr, plan, packed_weight, bias, x, gidx)
     m, ci = feats.shape
-    if packed_weight.numel() != co * 27 * ci:
-        raise ValueError("packed weight size does not match [Co,27,Ci]")
+    _check_planned(feats, nbr, plan, packed_weight, ci, co)
     if bias.dtype != torch.float32 or bias.numel() != co:
         raise ValueError("bias must be float32 [Co]")
     xc = x.contiguous()
@@ -284,6 +341,10 @@ def subm_conv3x3_planned_skip(feats, nbr, plan, packed_weight, bias, co: int, x,
         raise ValueError("x must be float32 [N, cin]")
     if gidx.dtype != torch.int32 or gidx.numel() != m:
         raise ValueError("gidx must be int32 [M]")
+    _require_cuda(feats, nbr, plan, packed_weight, bias, x, gidx)
+    # the stores read x[gidx // 8]: every gidx must name an octant of a row of x
+    if m and not (0 <= int(gidx.min().item()) and int(gidx.max().item()) < 8 * xc.shape[0]):
+        raise ValueError("gidx holds an octant outside x's rows")
     out = torch.empty((m, co), dtype=torch.float32, device=feats.device)
     f = feats.contiguous()
     _check("tsp_subm_conv3x3_planned_skip",

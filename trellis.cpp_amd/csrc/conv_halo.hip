@@ -333,14 +333,14 @@ __device__ __forceinline__ void conv_tiles(
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip);
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip, PadRow pad);
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, int EPI>
 __device__ __forceinline__ void conv_grid(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
-    SkipAdd skip) {
+    SkipAdd skip, PadRow pad) {
     // wave w owns voxels [32 RB rg, +32 RB) x channels [32 CB cg, +32 CB) of the tile, with
     // rg = w % NRG and cg = w / NRG
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
@@ -366,17 +366,17 @@ __device__ __forceinline__ void conv_grid(
     const int64_t xlo = xcd * per_xcd, xhi = xlo + per_xcd < total ? xlo + per_xcd : total;
     conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, EPI>(
         feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, xlo + blockIdx.x / 8,
-        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc, skip);
+        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc, skip, pad);
 }
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, PadRow pad) {
     conv_grid<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, 0>(
         feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{},
-        SkipAdd{});
+        SkipAdd{}, pad);
 }
 
 // The same conv with f32 output rows scattered to the children of a 2x subdivision (stored plan).
@@ -384,9 +384,10 @@ template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_octants(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
+    PadRow pad) {
     conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, 1>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{});
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{}, pad);
 }
 
 // The same conv with f32 output and the C2S skip added by its stores (stored plan).
@@ -394,9 +395,11 @@ template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_skip(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, SkipAdd skip) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, SkipAdd skip,
+    PadRow pad) {
     conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, 2>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{}, skip);
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{}, skip,
+        pad);
 }
 
 // The tiles lin0, lin0 + stride, ... (< xhi) of one workgroup. With a stored plan and an even
@@ -410,7 +413,7 @@ __device__ __forceinline__ void conv_tiles(
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip) {
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip, PadRow pad) {
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
     constexpr int WAVES = NRG * NCG;
     constexpr int NT = WAVES * 64;
@@ -436,14 +439,22 @@ __device__ __forceinline__ void conv_tiles(
     // The reference's absent taps read the padding row 0 * feats[0] (submconv_pad,
     // sparse.cpp:81-85), zeros here. Where row 0 holds an Inf or a NaN that row is NaN in those
     // channels, so every output row with an absent tap is NaN in every channel: the epilogue then
-    // writes NaN for those rows (found in the table), as the reference's sum would.
+    // writes NaN for those rows (found in the table), as the reference's sum would. With a zero
+    // padding row (the C2S conv2) nothing is tested; with an f32 source row, that row is tested.
     bool row0_bad = false;
-    for (int k = tid * 8; k < ci; k += NT * 8) {
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(feats + k);
-        constexpr uint32_t kExp = BF16 ? 0x7F807F80u : 0x7C007C00u;
+    if (!pad.zero) {
+        if (pad.row0) {
+            for (int k = tid; k < ci; k += NT) row0_bad |= !__builtin_isfinite(pad.row0[k]);
+        } else {
+            for (int k = tid * 8; k < ci; k += NT * 8) {
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(feats + k);
+                constexpr uint32_t kExp = BF16 ? 0x7F807F80u : 0x7C007C00u;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            row0_bad |= ((v[e] & kExp & 0xffffu) == (kExp & 0xffffu)) || ((v[e] & kExp & 0xffff0000u) == (kExp & 0xffff0000u));
+                for (int e = 0; e < 4; ++e)
+                    row0_bad |= ((v[e] & kExp & 0xffffu) == (kExp & 0xffffu)) ||
+                                ((v[e] & kExp & 0xffff0000u) == (kExp & 0xffff0000u));
+            }
+        }
     }
     row0_bad = __syncthreads_or(row0_bad);
     // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
@@ -912,7 +923,7 @@ int cu_count() {
 template <bool BF16, int BN, int ODT, bool PLANNED>
 int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* plan,
            const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc,
-           SkipAdd skip) {
+           SkipAdd skip, PadRow pad) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     const int n_ctiles = co / BN;
     const int64_t total = n_tiles * n_ctiles;
@@ -936,13 +947,13 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
     if constexpr (PLANNED && ODT == TSP_F32) {
         if (osc.cout) {
             hipLaunchKernelGGL((k_conv_halo_octants<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
-                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, osc);
+                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, pad);
             TSP_CHECK_LAUNCH();
             return TSP_OK;
         }
         if (skip.cin) {
             hipLaunchKernelGGL((k_conv_halo_skip<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
-                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, skip);
+                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, skip, pad);
             TSP_CHECK_LAUNCH();
             return TSP_OK;
         }
@@ -952,7 +963,7 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
         return TSP_ERR_UNSUPPORTED;
     }
     hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>), grid, block, 0, s,
-                       f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd);
+                       f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, pad);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
@@ -960,21 +971,21 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
 template <bool BF16, int BN, int ODT>
 int launch_planned(bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                    const void* plan, const void* weight, const float* bias, int co, void* out,
-                   hipStream_t s, OctantScatter osc, SkipAdd skip) {
-    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
-    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip);
+                   hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad) {
+    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
+    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip, pad);
 }
 
 template <bool BF16, int BN>
 int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                const void* plan, const void* weight, const float* bias, int co, void* out,
-               hipStream_t s, OctantScatter osc, SkipAdd skip) {
+               hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad) {
     if (odt == TSP_F32)
-        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
+        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
     if (BF16 && odt == TSP_BF16)
-        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
+        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
     if (!BF16 && odt == TSP_F16)
-        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
+        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
     set_error("MFMA conv writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
@@ -1010,7 +1021,7 @@ int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s)
 
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc, SkipAdd skip) {
+                     hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad) {
     const bool planned = plan != nullptr;
     const bool bn128 = co % 128 == 0;
     if (osc.cout && (!planned || osc.cout % (bn128 ? 64 : 32) != 0 || (int64_t)osc.cout * 8 != co)) {
@@ -1030,10 +1041,10 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
         return TSP_ERR_UNSUPPORTED;
     }
     if (fdt == TSP_BF16)
-        return bn128 ? launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip)
-                     : launch_out<true, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
-    return bn128 ? launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip)
-                 : launch_out<false, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip);
+        return bn128 ? launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad)
+                     : launch_out<true, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
+    return bn128 ? launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad)
+                 : launch_out<false, 64>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
 }
 
 }  // namespace tsp

@@ -65,12 +65,22 @@ struct SkipAdd {
     int cin = 0;
 };
 
+// The padding row that absent taps read. The reference's is 0 * feats[0] (submconv_pad,
+// sparse.cpp:81-85): zeros, or NaN in the channels where row 0 holds an Inf or a NaN. With
+// `zero` set it is an exact zero row instead (the C2S block's conv2, whose padding column is
+// silu(norm(0)) = 0, sparse.cpp:289-306). `row0`, when not null, is the f32 row 0 that the
+// 16-bit features were rounded from; the NaN test then reads it instead of the rounded row.
+struct PadRow {
+    const float* row0 = nullptr;
+    bool zero = false;
+};
+
 // The conv. With plan == nullptr the tile plan is built inside the kernel and `weight` is in
 // the [co][27][ci] layout; with a plan, `weight` must be packed by halo_weight_pack. An
 // OctantScatter or a SkipAdd needs a plan and f32 output; an OctantScatter needs cout a multiple
 // of the channels one wave owns (64 when co % 128 == 0, else 32).
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {});
+                     hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {});
 
 }  // namespace tsp

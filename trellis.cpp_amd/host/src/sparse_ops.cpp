@@ -61,11 +61,14 @@ Conv conv_of(const Model& m, const std::string& prefix) {
 // F32 activations are rounded to the weights' 16-bit type for the matrix-core kernel, as ggml's
 // F16 mul_mat rounds its F32 operand (sparse.cpp:74); under g_sparse_cast_f32 or for channel
 // counts the matrix-core tiles do not cover, the fp32 kernel runs on the weights' exact values.
+// The padding row is formed from the unrounded row 0 (sparse.cpp:81-85 pads the F32 input).
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
               float* out, Carve& sc, hipStream_t s, const ConvStores& st) {
     const float* bias = f32_param(c.b, sc, s);
+    const int flags = st.zero_pad ? TSP_CONV_ZERO_PAD : 0;
     if (c.mfma) {
         const void* x16 = x;
+        const float* row0 = xdt == TSP_F32 ? static_cast<const float*>(x) : nullptr;
         if (xdt != c.wdt) {
             void* p = sc.take((size_t)n * c.ci * 2);
             if (sc.running()) hip_check(tgr::launch_convert(x, xdt, p, c.wdt, n * c.ci, s), "conv input rounding");
@@ -79,18 +82,19 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
             lib(tsp_subm_conv3x3_planned_octants(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, st.ocout,
                                                  st.omask, st.omstart, out, s),
                 "sparse conv (octant stores)");
-        else if (st.skip_cin)
+        else if (st.skip_cin)   // always an exact zero padding row: the C2S conv2
             lib(tsp_subm_conv3x3_planned_skip(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, st.skip_x,
                                               st.skip_cin, st.skip_gidx, out, s),
                 "sparse conv (skip stores)");
         else
-            lib(tsp_subm_conv3x3_planned(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, s),
+            lib(tsp_subm_conv3x3_planned_ex(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32,
+                                            flags, row0, s),
                 "sparse conv");
     } else {
         if (st.ocout || st.skip_cin) fail("sparse conv: fused stores need the matrix-core path");
         if (!sc.running()) return;
-        lib(tsp_subm_conv3x3(x, xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
-                             TSP_ALGO_AUTO, s),
+        lib(tsp_subm_conv3x3_ex(x, xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
+                                TSP_ALGO_AUTO, flags, s),
             "sparse conv");
     }
 }
@@ -322,15 +326,20 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status);
     if (conv2.mfma) r.table.ensure_plan(s);
     // the skip: added by conv2's stores on the matrix cores (repeat R % 4 == 0), else its own pass
+    // conv2's absent taps read hn's zero padding column (sparse.cpp:289-306)
     if (conv2.mfma && (cout / (cin / 8)) % 4 == 0) {
         ConvStores st;
         st.skip_x = d_x;
         st.skip_gidx = d_gidx.as<int32_t>();
         st.skip_cin = cin;
+        st.zero_pad = true;
         run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s,
                  st);
     } else {
-        run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s);
+        ConvStores st;
+        st.zero_pad = true;
+        run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s,
+                 st);
         lib(tsp_c2s_skip_add(d_x, TSP_F32, d_gidx.as<int32_t>(), mm, cin, cout, r.feats.get(), TSP_F32, s),
             prefix + " skip");
     }

@@ -55,6 +55,8 @@ struct ConvStores {
     const float* skip_x = nullptr;
     const int32_t* skip_gidx = nullptr;
     int skip_cin = 0;
+    // absent taps read an exact zero row (the C2S conv2, sparse.cpp:289-306), not 0 * x[0]
+    bool zero_pad = false;
 };
 // out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
