@@ -211,7 +211,7 @@ def test_c2s_block_composed(gpu_lib, orc, shells, ext):
                              P["c2s.conv1.bias"])
     h = gpu_lib.layer_norm(gpu_lib.c2s_gather(h, gidx, cout), None, None, 1e-6, silu=True)
     out = gpu_lib.subm_conv3x3(h, gpu_lib.rulebook_build(child), P["c2s.conv2.weight"],
-                               P["c2s.conv2.bias"])
+                               P["c2s.conv2.bias"], zero_pad=True)
     gpu_lib.c2s_skip_add(xc, gidx, out)
     ref, rchild, rmask = orc.c2s_block(x, coords, p, "c2s", cout, ext_mask)
     assert np.array_equal(mask.cpu().numpy().reshape(-1), rmask)

@@ -196,7 +196,9 @@ def standard_normal_rows(rng, rows: int, cols: int) -> np.ndarray:
     return out
 
 
-def _inputs(rng, n, ci, co, std, dtype, bias_std):
+def conv_inputs(rng, n, ci, co, std, dtype, bias_std):
+    """Seeded conv inputs: feats [n, ci] ~ N(0,1), W [co, 27, ci] ~ N(0, std), bias ~ N(0, bias_std)
+    (zeros when bias_std is 0), feats and W rounded to dtype."""
     feats = round_to(standard_normal_rows(rng, n, ci), dtype)
     weight = round_to(rng.standard_normal((co, 27, ci), dtype=np.float32) * np.float32(std), dtype)
     bias = (rng.standard_normal(co, dtype=np.float32) * np.float32(bias_std)
@@ -219,27 +221,36 @@ def workload(name: str) -> ConvWorkload:
     if name == "shell64-c64-f32":
         rng = np.random.default_rng(0)
         coords = sphere_shell(64, 32.0, 23.0, 25.0)
-        f, w, b = _inputs(rng, len(coords), 64, 64, 1 / np.sqrt(27 * 64), "f32", 0.0)
+        f, w, b = conv_inputs(rng, len(coords), 64, 64, 1 / np.sqrt(27 * 64), "f32", 0.0)
         return ConvWorkload(name, coords, f, w, b, "f32", 64, workload.__doc__)
     if name == "ellipsoids128-c256-bf16":
         rng = np.random.default_rng(1)
         coords = band_voxels(random_shapes(rng, 128, 4, 20, 50, boxes=False), 128, 2.0)
-        f, w, b = _inputs(rng, len(coords), 256, 256, 1 / np.sqrt(27 * 256), "bf16", 0.1)
+        f, w, b = conv_inputs(rng, len(coords), 256, 256, 1 / np.sqrt(27 * 256), "bf16", 0.1)
         return ConvWorkload(name, coords, f, w, b, "bf16", 128, workload.__doc__)
     if name == "shells256-c128-bf16":
         rng = np.random.default_rng(2)
         coords = band_voxels(random_shapes(rng, 256, 8, 40, 110, boxes=True), 256, 2.0)
-        f, w, b = _inputs(rng, len(coords), 128, 128, np.sqrt(2 / (27 * 128)), "bf16", 0.1)
+        f, w, b = conv_inputs(rng, len(coords), 128, 128, np.sqrt(2 / (27 * 128)), "bf16", 0.1)
         return ConvWorkload(name, coords, f, w, b, "bf16", 256, workload.__doc__)
     if name == "band512-c64-bf16":
-        rng = np.random.default_rng(3)
-        shapes = random_shapes(rng, 256, 8, 40, 110, boxes=True)
-        parents = band_voxels(shapes, 256, 2.0)
-        mask = subdivision_band_mask(parents, shapes, 2.0)
+        rng, parents, mask = band512_parents()
         coords = children(mask, parents)
-        f, w, b = _inputs(rng, len(coords), 64, 64, 1 / np.sqrt(27 * 64), "bf16", 0.1)
+        f, w, b = conv_inputs(rng, len(coords), 64, 64, 1 / np.sqrt(27 * 64), "bf16", 0.1)
         return ConvWorkload(name, coords, f, w, b, "bf16", 512, workload.__doc__)
     raise KeyError(name)
+
+
+def band512_parents():
+    """The band512 workload's parents and subdivision: 8 random ellipsoid/box shells (semi-axes
+    U[40,110], thickness 2, seed 3) voxelised at 256^3, and the mask [8N] that keeps each child
+    whose centre lies in the thickness-2 band at 512^3. Returns (rng after the draws, parents,
+    mask); the children are children(mask, parents)."""
+    rng = np.random.default_rng(3)
+    shapes = random_shapes(rng, 256, 8, 40, 110, boxes=True)
+    parents = band_voxels(shapes, 256, 2.0)
+    mask = subdivision_band_mask(parents, shapes, 2.0)
+    return rng, parents, mask
 
 
 WORKLOADS = ("shell64-c64-f32", "ellipsoids128-c256-bf16", "shells256-c128-bf16",
