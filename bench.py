@@ -229,6 +229,8 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--plan-order", default="morton", choices=["morton", "rows"],
+                    help="conv plan tiles: Morton order of 8^3 cells, or consecutive rows")
     ap.add_argument("--prepare-only", default="", metavar="DIR",
                     help="decoder workloads: only write the model and inputs into DIR (for running "
                          "trellis.cpp_amd/host/bin/decoder_bench on them, e.g. under a profiler)")
@@ -291,12 +293,15 @@ def main():
                and w.ci % 16 == 0 and w.co % 64 == 0)
     plan_ms = None
     if planned:
-        plan = pkg.conv_plan_build(nbr, w.n)
+        # tiles in the Morton order of the voxels' 8^3 cells (or, with --plan-order rows, runs of
+        # consecutive rows)
+        pcoords = coords if args.plan_order == "morton" else None
+        plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
         packed = pkg.conv_weight_pack(weight)
         torch.cuda.synchronize()
         rb_ev[0].record(stream)
         for _ in range(5):
-            plan = pkg.conv_plan_build(nbr, w.n)
+            plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
         rb_ev[1].record(stream)
         torch.cuda.synchronize()
         plan_ms = rb_ev[0].elapsed_time(rb_ev[1]) / 5
@@ -368,6 +373,7 @@ def main():
             "pairs_per_voxel": pairs / max(w.n, 1), "c_in": w.ci, "c_out": w.co,
             "accumulate": "f32", "out_dtype": w.dtype,
             "algo": "mfma-planned" if planned else args.algo,
+            "plan_order": args.plan_order if planned else None,
             "parallelism": "single-gpu",
         },
         "tflops": tflops,

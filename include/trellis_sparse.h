@@ -114,14 +114,23 @@ int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
  * the neighbour table -- shared by every conv of a decoder stage, shape_decoder.cpp:93-103 --
  * and what depends only on the weights, loaded once per model, trellis_model.cpp:96-142).
  *
- * A plan holds, for every tile of 512 consecutive voxels, the sorted set of input rows the
- * tile's table entries reference and each entry's rank in that set; the planned conv stages
- * those rows in LDS once per tile. Packed weights hold W [Co][27][Ci] in the order the
- * matrix-core operands are read. Both are plain device buffers owned by the caller.
+ * A plan splits the voxels into tiles of 512 and holds, for each tile, its voxels' rows (in
+ * increasing order inside the tile), the sorted set of input rows their table entries reference
+ * and each entry's rank in that set (the planned conv stages those rows in LDS once per tile).
+ * Packed weights hold W [Co][27][Ci] in the order the matrix-core operands are read. Both are
+ * plain device buffers owned by the caller; every tap of every voxel is computed, so the results
+ * of a planned conv do not depend on how the plan grouped the voxels.
  * ------------------------------------------------------------------------------------- */
 size_t tsp_conv_plan_bytes(int64_t n);
+/* Tiles of 512 consecutive rows. d_plan 16-byte aligned, plan_bytes >= tsp_conv_plan_bytes(n). */
 int tsp_conv_plan_build(const int32_t* d_nbr, int64_t n, void* d_plan, size_t plan_bytes,
                         void* stream);
+/* Tiles of 512 voxels in the Morton order of their 8^3 cells (d_coords int32 [n][3], the
+ * coordinates d_nbr was built from): compact patches of a surface, whose 27-neighbourhoods
+ * overlap, so a tile stages about half the rows of one made of consecutive rows. The plan's
+ * buffer also serves the ordering's sort. */
+int tsp_conv_plan_build_ordered(const int32_t* d_nbr, const int32_t* d_coords, int64_t n,
+                                void* d_plan, size_t plan_bytes, void* stream);
 
 /* W [co][27][ci] (f16 or bf16; ci % 16 == 0, co % 32 == 0) -> d_packed, same byte size. */
 int tsp_conv_weight_pack(const void* d_weight, int dtype, int ci, int co, void* d_packed,

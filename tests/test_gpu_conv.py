@@ -359,7 +359,7 @@ def test_full_size_sampled_rows(gpu_lib, orc, shells, name):
     out2 = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma")
     outg = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="mfma_gather")
     outn = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="narrow")
-    plan = gpu_lib.conv_plan_build(nbr, w.n)
+    plan = gpu_lib.conv_plan_build(nbr, w.n, coords=c)
     outp = gpu_lib.subm_conv3x3_planned(f, nbr, plan, gpu_lib.conv_weight_pack(wt), b, w.co,
                                         out_dtype=torch.float32)
     torch.cuda.synchronize()
@@ -471,3 +471,161 @@ def test_padding_row_from_f32_source(gpu_lib, orc, shells):
     _nan_aware(with_src.cpu().numpy(), orc.subm_conv_f64(feats16, nbr, weight, bias, zero_pad=True), TOL_16)
     absent = (nbr.reshape(27, n) == n).any(axis=0)
     assert np.isnan(without.cpu().numpy()[absent]).all()
+
+
+def _plan_parts(plan, n):
+    """Views of a plan buffer's tile records (layout of tile_plan.hpp's carve_plan)."""
+    al = lambda b: (b + 255) // 256 * 256
+    t = (n + 511) // 512
+    raw = plan.cpu().numpy()
+    off, parts = 0, {}
+    for name, nbytes, dt, shape in (("hdr", t * 16, np.int32, (t, 4)), ("rowof", t * 2048 * 4, np.int32, (t, 2048)),
+                                    ("slots", t * 27 * 512 * 2, np.uint16, (t, 27, 4, 32, 4)),
+                                    ("vox", t * 512 * 4, np.int32, (t, 512))):
+        parts[name] = raw[off:off + nbytes].view(dt).reshape(shape)
+        off += al(nbytes)
+    return parts
+
+
+def _check_plan(p, table, n, order):
+    """What a plan promises the conv: the tiles' positions hold every voxel once, in row order
+    inside a tile (consecutive rows for a plan without coordinates); each (tap, position) slot
+    names the row the table gives, through the tile's sorted row list, or the zero slot."""
+    vox = p["vox"].reshape(-1)
+    assert np.array_equal(np.sort(vox[vox >= 0]), np.arange(n))
+    assert (vox < 0).sum() == p["vox"].size - n
+    H = p["hdr"][:, 0]
+    for t in range(p["vox"].shape[0]):
+        v = p["vox"][t]
+        k = int((v >= 0).sum())
+        assert (v[:k] >= 0).all() and np.all(np.diff(v[:k]) > 0)
+        if order == "rows":
+            assert np.array_equal(v[:k], np.arange(512 * t, 512 * t + k))
+        if p["hdr"][t, 1]:
+            continue
+        rows = p["rowof"][t, :H[t]]
+        assert np.all(np.diff(rows) > 0)
+        for tap in (0, 4, 13, 22, 26):
+            sl = p["slots"][t, tap].transpose(0, 2, 1).reshape(512)   # [group][block][row] = position order
+            got = np.where(sl == 2048, n, rows[np.minimum(sl, max(H[t] - 1, 0))])
+            want = np.where(v >= 0, table[tap][np.maximum(v, 0)], n)
+            assert np.array_equal(got, want), (t, tap)
+    return H
+
+
+@pytest.mark.parametrize("order", ["rows", "morton"])
+def test_plan_records(gpu_lib, orc, shells, order):
+    """The plan's records checked on the host (see _check_plan); Morton tiles reference fewer
+    distinct rows than row tiles on a thin shell, and every tile fits the LDS stage."""
+    _case(f"plan records {order}")
+    import torch
+    coords = np.ascontiguousarray(shells.sphere_shell(64, 32.0, 20.0, 22.0), np.int32)
+    n = len(coords)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c if order == "morton" else None)
+    torch.cuda.synchronize()
+    p = _plan_parts(plan, n)
+    H = _check_plan(p, nbr.cpu().numpy().reshape(27, n), n, order)
+    assert (p["hdr"][:, 1] == 0).all()
+    print(f"{order}: distinct rows per voxel {H.sum() / n:.2f}", flush=True)
+    if order == "morton":
+        rplan = gpu_lib.conv_plan_build(nbr, n)
+        assert H.sum() < 0.8 * _plan_parts(rplan, n)["hdr"][:, 0].sum()
+
+
+def test_plan_wide_row_span(gpu_lib, orc, shells):
+    """A tile whose voxels lie at both ends of a 2.2M-row range (half a compact cube in the first
+    rows, the other half in the last, a dense box in between): its rows span more than the
+    two-level bitmap's 2^21, so the planner cuts the empty stretch out and the tile still stages
+    its rows in LDS. Records checked as in test_plan_records; the conv equals the unplanned one bit
+    for bit and the oracle on the cube's rows."""
+    _case("plan: wide row span")
+    import torch
+    cube = np.stack(np.meshgrid(*[np.arange(8)] * 3, indexing="ij"), -1).reshape(-1, 3).astype(np.int32)
+    box = (np.stack(np.meshgrid(*[np.arange(131)] * 3, indexing="ij"), -1).reshape(-1, 3) + 100).astype(np.int32)
+    coords = np.ascontiguousarray(np.concatenate([cube[:256], box, cube[256:]]))
+    n = len(coords)
+    assert n - 256 > (1 << 21)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    torch.cuda.synchronize()
+    p = _plan_parts(plan, n)
+    table = nbr.cpu().numpy().reshape(27, n)
+    first = np.nonzero((p["vox"] == 0).any(axis=1))[0][0]          # the tile holding row 0
+    assert (p["vox"][first] == n - 1).any()                         # ... and the last row
+    assert (p["hdr"][:, 1] == 0).all()
+    H = p["hdr"][first, 0]
+    rows = p["rowof"][first, :H]
+    assert rows[0] == 0 and rows[-1] == n - 1 and np.all(np.diff(rows) > 0)
+    v = p["vox"][first]
+    for tap in range(27):
+        sl = p["slots"][first, tap].transpose(0, 2, 1).reshape(512)
+        got = np.where(sl == 2048, n, rows[np.minimum(sl, H - 1)])
+        assert np.array_equal(got, np.where(v >= 0, table[tap][np.maximum(v, 0)], n)), tap
+    rng = np.random.default_rng(9)
+    feats = shells.round_to(rng.standard_normal((n, 32)).astype(np.float32), "bf16")
+    weight = shells.round_to((rng.standard_normal((64, 27, 32)) / 30).astype(np.float32), "bf16")
+    bias = (rng.standard_normal(64) * 0.1).astype(np.float32)
+    f, w, b = _dev(feats, torch.bfloat16), _dev(weight, torch.bfloat16), _dev(bias, torch.float32)
+    out = gpu_lib.subm_conv3x3_planned(f, nbr, plan, gpu_lib.conv_weight_pack(w), b, 64, out_dtype=torch.float32)
+    ref_d = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_d)
+    rows_chk = np.concatenate([np.arange(256), np.arange(n - 256, n)])
+    ref = orc.subm_conv_f64_rows(feats, nbr.cpu().numpy(), weight, bias, rows_chk)
+    assert orc.rel_err(out.cpu().numpy()[rows_chk], ref) < TOL_16
+
+
+@pytest.mark.parametrize("ci,co", [(128, 128), (64, 64), (256, 64)])
+def test_ordered_plan_results(gpu_lib, orc, shells, ci, co):
+    """The planned conv on Morton tiles, on row tiles and without a plan: the same bits, and the
+    fp64 oracle within TOL_16. Ordering and skipping dead taps change nothing in any row's sum."""
+    _case(f"ordered plan ci={ci} co={co}")
+    import torch
+    rng = np.random.default_rng(ci + 3 * co)
+    coords = np.ascontiguousarray(rng.permutation(shells.sphere_shell(64, 32.0, 18.0, 20.5)), np.int32)
+    n = len(coords)
+    feats = shells.round_to(rng.standard_normal((n, ci)).astype(np.float32), "bf16")
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32), "bf16")
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    f, w, b = _dev(feats, torch.bfloat16), _dev(weight, torch.bfloat16), _dev(bias, torch.float32)
+    pw = gpu_lib.conv_weight_pack(w)
+    outs = {}
+    for name, pc in (("morton", c), ("rows", None)):
+        plan = gpu_lib.conv_plan_build(nbr, n, coords=pc)
+        outs[name] = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, co, out_dtype=torch.float32)
+    outs["none"] = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(outs["morton"], outs["none"]) and torch.equal(outs["rows"], outs["none"])
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    assert orc.rel_err(outs["morton"].cpu().numpy(), ref) < TOL_16
+
+
+@pytest.mark.parametrize("bad", ["inf", "nan"])
+def test_nonfinite_weight_runs_every_tap(gpu_lib, shells, bad):
+    """Absent taps multiply the zero slot by W: zero for finite weights, NaN where W holds an Inf
+    or a NaN (as the reference's padding row times W gives). The planned conv on Morton tiles
+    matches the unplanned kernel NaN for NaN and value for value."""
+    _case(f"non-finite weight {bad}")
+    import torch
+    rng = np.random.default_rng(71)
+    coords = np.ascontiguousarray(shells.sphere_shell(40, 20.0, 12.0, 14.0), np.int32)
+    n, ci, co = len(coords), 64, 128
+    feats = shells.round_to(rng.standard_normal((n, ci)).astype(np.float32), "bf16")
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / 30).astype(np.float32), "bf16")
+    weight[5, 0, 3] = np.inf if bad == "inf" else np.nan      # tap 0: absent for most voxels
+    bias = np.zeros(co, np.float32)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    f, w, b = _dev(feats, torch.bfloat16), _dev(weight, torch.bfloat16), _dev(bias, torch.float32)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    got = gpu_lib.subm_conv3x3_planned(f, nbr, plan, gpu_lib.conv_weight_pack(w), b, co,
+                                       out_dtype=torch.float32).cpu().numpy()
+    want = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma").cpu().numpy()
+    assert np.isnan(want[:, 5]).any()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(want)], want[~np.isnan(want)])

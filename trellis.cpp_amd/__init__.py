@@ -25,7 +25,8 @@ EXPORTS = (
     "tsp_last_error", "tsp_version",
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
     "tsp_subm_conv3x3", "tsp_subm_conv3x3_ex",
-    "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_weight_pack",
+    "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_plan_build_ordered",
+    "tsp_conv_weight_pack",
     "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_ex", "tsp_subm_conv3x3_planned_octants",
     "tsp_subm_conv3x3_planned_skip",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide",
@@ -77,6 +78,8 @@ def lib() -> ctypes.CDLL:
     L.tsp_conv_plan_bytes.argtypes = [c_i64]
     L.tsp_conv_plan_build.restype = c_int
     L.tsp_conv_plan_build.argtypes = [c_vp, c_i64, c_vp, c_sz, c_vp]
+    L.tsp_conv_plan_build_ordered.restype = c_int
+    L.tsp_conv_plan_build_ordered.argtypes = [c_vp, c_vp, c_i64, c_vp, c_sz, c_vp]
     L.tsp_conv_weight_pack.restype = c_int
     L.tsp_conv_weight_pack.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
     L.tsp_subm_conv3x3_planned.restype = c_int
@@ -227,15 +230,24 @@ def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", o
     return out
 
 
-def conv_plan_build(nbr, n: int, stream=None):
-    """Plan of neighbour table nbr (int32 [27*N]) for tsp_subm_conv3x3_planned -> uint8 buffer."""
+def conv_plan_build(nbr, n: int, coords=None, stream=None):
+    """Plan of neighbour table nbr (int32 [27*N]) for the planned convs -> uint8 buffer. With
+    coords (int32 [N, 3], the coordinates the table was built from) tiles follow the Morton order
+    of the voxels' 8^3 cells; without, tiles are consecutive rows."""
     torch = _torch()
-    _require_cuda(nbr)
+    _require_cuda(nbr, coords)
     _check_nbr(nbr, n, nbr.device)
     nb = lib().tsp_conv_plan_bytes(n)
     plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=nbr.device)
-    _check("tsp_conv_plan_build",
-           lib().tsp_conv_plan_build(_ptr(nbr), n, _ptr(plan), nb, _stream(stream)))
+    if coords is None:
+        _check("tsp_conv_plan_build",
+               lib().tsp_conv_plan_build(_ptr(nbr), n, _ptr(plan), nb, _stream(stream)))
+    else:
+        c = coords.contiguous()
+        if c.dtype != torch.int32 or tuple(c.shape) != (n, 3):
+            raise ValueError("coords must be int32 [N, 3]")
+        _check("tsp_conv_plan_build_ordered",
+               lib().tsp_conv_plan_build_ordered(_ptr(nbr), _ptr(c), n, _ptr(plan), nb, _stream(stream)))
     return plan
 
 

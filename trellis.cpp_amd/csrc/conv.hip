@@ -471,17 +471,33 @@ extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, 
 
 extern "C" size_t tsp_conv_plan_bytes(int64_t n) { return n < 0 ? 0 : halo_plan_bytes(n); }
 
+static int plan_build_checked(const char* fn, const int32_t* d_nbr, const int32_t* d_coords, int64_t n,
+                              void* d_plan, size_t plan_bytes, void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX, TSP_ERR_INVALID, "%s: n=%lld out of range", fn,
+                (long long)n);
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_nbr && d_plan, TSP_ERR_INVALID, "%s: null pointer", fn);
+    TSP_REQUIRE(plan_bytes >= halo_plan_bytes(n), TSP_ERR_WORKSPACE, "%s: plan buffer %zu < %zu bytes", fn,
+                plan_bytes, halo_plan_bytes(n));
+    TSP_REQUIRE((reinterpret_cast<uintptr_t>(d_plan) & 15) == 0, TSP_ERR_INVALID,
+                "%s: the plan buffer must be 16-byte aligned", fn);
+    return halo_plan_build(d_nbr, d_coords, n, d_plan, as_stream(stream));
+}
+
 extern "C" int tsp_conv_plan_build(const int32_t* d_nbr, int64_t n, void* d_plan,
                                    size_t plan_bytes, void* stream) {
-    clear_error();
-    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX, TSP_ERR_INVALID,
-                "tsp_conv_plan_build: n=%lld out of range", (long long)n);
-    if (n == 0) return TSP_OK;
-    TSP_REQUIRE(d_nbr && d_plan, TSP_ERR_INVALID, "tsp_conv_plan_build: null pointer");
-    TSP_REQUIRE(plan_bytes >= halo_plan_bytes(n), TSP_ERR_WORKSPACE,
-                "tsp_conv_plan_build: plan buffer %zu < %zu bytes", plan_bytes,
-                halo_plan_bytes(n));
-    return halo_plan_build(d_nbr, n, d_plan, as_stream(stream));
+    return plan_build_checked("tsp_conv_plan_build", d_nbr, nullptr, n, d_plan, plan_bytes, stream);
+}
+
+extern "C" int tsp_conv_plan_build_ordered(const int32_t* d_nbr, const int32_t* d_coords, int64_t n,
+                                           void* d_plan, size_t plan_bytes, void* stream) {
+    if (!d_coords && n > 0) {
+        clear_error();
+        set_error("tsp_conv_plan_build_ordered: null coordinates");
+        return TSP_ERR_INVALID;
+    }
+    return plan_build_checked("tsp_conv_plan_build_ordered", d_nbr, d_coords, n, d_plan, plan_bytes, stream);
 }
 
 extern "C" int tsp_conv_weight_pack(const void* d_weight, int dtype, int ci, int co,

@@ -38,272 +38,31 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "conv_internal.hpp"
+#include "tile_plan.hpp"
 
 namespace tsp {
 namespace {
 
-constexpr int HB_PLAN_NT = 512;            // threads of a plan-build workgroup
-constexpr int HB_KC = 16;                  // channels per LDS slice
-constexpr int HB_SLOTS = 2048;             // slots per slice buffer
-constexpr int HB_ZERO = HB_SLOTS;          // slot that always holds zeros (absent taps)
-constexpr int HB_ROWS = HB_SLOTS + 1;      // rows of a slice buffer plane: the slots + zero
-constexpr int HB_SLOT_TABLE = kTaps * HB_M;                    // uint16 slots per tile
-constexpr int HB_PLAN_SCRATCH = 5 * HB_SLOTS;                  // tile_plan scratch words
-constexpr int64_t HB_MAXSPAN = (int64_t)HB_SLOTS * 32 * 32;    // 2^21 rows
-
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00); }
 
-__device__ __forceinline__ int wave_min(int v) {
-    for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, 64));
-    return v;
-}
-__device__ __forceinline__ int wave_max(int v) {
-    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// Plan layout: [n_tiles][4] int32 header {H, direct, 0, 0} | [n_tiles][HB_SLOTS] int32 row of each
-// slot | [n_tiles][27][4][32][4] uint16 slot of each (tap, voxel/128, voxel%32, voxel/32%4).
-struct PlanView {
-    int32_t* hdr;
-    int32_t* rowof;
-    uint16_t* slots;
-};
-inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
-__host__ __device__ inline PlanView carve_plan(void* p, int64_t n_tiles) {
-    char* c = reinterpret_cast<char*>(p);
-    PlanView v;
-    v.hdr = reinterpret_cast<int32_t*>(c);
-    c += align256((size_t)n_tiles * 16);
-    v.rowof = reinterpret_cast<int32_t*>(c);
-    c += align256((size_t)n_tiles * HB_SLOTS * 4);
-    v.slots = reinterpret_cast<uint16_t*>(c);
-    return v;
-}
-
-// ---- tile plan (all NT threads of the block) -----------------------------------------------
-// Exclusive scan of the popcounts of words[0..nwords) (nwords <= HB_SLOTS) into pre[];
-// returns the total. sRed: NT/64 ints of scratch.
-template <int NT>
-__device__ int scan_popcounts(const uint32_t* words, int nwords, int32_t* pre, int* sRed) {
-    constexpr int WPT = HB_SLOTS / NT;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    int cnt[WPT];
-    int mine = 0;
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) {
-        const int w = tid * WPT + k;
-        cnt[k] = (w < nwords) ? __popc(words[w]) : 0;
-        mine += cnt[k];
-    }
-    int x = mine;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
-    if (lane == 63) sRed[wave] = x;
-    __syncthreads();
-    int base = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < NT / 64; ++w) {
-        if (w < wave) base += sRed[w];
-        total += sRed[w];
-    }
-    base += x - mine;
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) {
-        pre[tid * WPT + k] = base;
-        base += cnt[k];
-    }
-    __syncthreads();
-    return total;
-}
-
-// Fills sL with the slot of every (tap, voxel) of tile row0 and sRowOf with the row of every
-// slot; returns H (number of distinct rows) and whether the tile must take the direct path.
-// The set of referenced rows is ranked with a bitmap over [lo, hi]: one fine word per 32 rows
-// when the span is at most 32 * HB_SLOTS rows, otherwise two levels -- a coarse bit per 32-row
-// block (spans up to 2^21 rows), then one fine word per non-empty block. slot = prefix of the
-// fine word + rank inside the word.
-// scratch: HB_PLAN_SCRATCH words; sRed: 2 * NT/64 ints.
+// The plan of tile row0 (HB_M consecutive rows) built in LDS by the conv itself when no stored
+// plan is given: tile positions are the rows in order.
 template <int NT>
 __device__ void tile_plan(const int32_t* __restrict__ nbr, int64_t n, int64_t row0,
                           uint16_t (*sL)[4][32][4], int32_t* sRowOf, uint32_t* scratch,
                           int* sRed, int& H_out, bool& direct_out) {
     constexpr int VPT = HB_M / NT;         // voxels per thread
-    constexpr int WPT = HB_SLOTS / NT;     // bitmap words per thread
-    constexpr int NW = NT / 64;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    uint32_t* coarse = scratch;                                       // bit per 32-row block
-    int32_t* cpre = reinterpret_cast<int32_t*>(scratch + HB_SLOTS);   // block rank of a word
-    uint32_t* fine = scratch + 2 * HB_SLOTS;                          // rows of each block
-    int32_t* fpre = reinterpret_cast<int32_t*>(scratch + 3 * HB_SLOTS);
-    int32_t* block_of = reinterpret_cast<int32_t*>(scratch + 4 * HB_SLOTS);   // rank -> block
-    // this thread's table entries (voxels tid + NT h, all taps), loaded once and without
-    // branches so all loads are in flight together; absent taps / voxels past n -> -1
-    int32_t nv[kTaps][VPT];
-    {
-        int64_t ic[VPT];
-        bool in[VPT];
-#pragma unroll
-        for (int h = 0; h < VPT; ++h) {
-            const int64_t i = row0 + tid + NT * h;
-            in[h] = i < n;
-            ic[h] = in[h] ? i : n - 1;
-        }
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t)
-#pragma unroll
-            for (int h = 0; h < VPT; ++h) nv[t][h] = nbr[(int64_t)t * n + ic[h]];
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t)
-#pragma unroll
-            for (int h = 0; h < VPT; ++h)
-                nv[t][h] = (in[h] && (uint32_t)nv[t][h] < (uint32_t)n) ? nv[t][h] : -1;
-    }
-    int lo = INT32_MAX, hi = -1;
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t)
-#pragma unroll
-        for (int h = 0; h < VPT; ++h)
-            if (nv[t][h] >= 0) { lo = min(lo, nv[t][h]); hi = max(hi, nv[t][h]); }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
-    if (lane == 0) { sRed[wave] = lo; sRed[NW + wave] = hi; }
-    __syncthreads();
-    lo = INT32_MAX;
-    hi = -1;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) { lo = min(lo, sRed[w]); hi = max(hi, sRed[NW + w]); }
-    __syncthreads();
-    bool direct = hi >= 0 && (int64_t)hi - lo + 1 > HB_MAXSPAN;
-    // One level when the rows span at most 32 * HB_SLOTS (the usual case for sorted sets: a
-    // tile's neighbours lie in three x-planes): the fine word of row d is d >> 5 directly.
-    const bool one = hi >= 0 && (int64_t)hi - lo + 1 <= 32 * HB_SLOTS;
-    int H = 0, nfine = 0;
-    // fine word of row offset d (two levels: the rank of d's 32-row block among the referenced ones)
-    auto fine_word = [&](int d) -> int {
-        if (one) return d >> 5;
-        const int cw = d >> 10, cb = (d >> 5) & 31;
-        return cpre[cw] + (int)__popc(coarse[cw] & ((1u << cb) - 1u));
-    };
-
-    if (!direct && hi >= 0) {
-#pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            coarse[tid * WPT + k] = 0u;
-            fine[tid * WPT + k] = 0u;
-        }
-        __syncthreads();
-        if (one) {
-            nfine = HB_SLOTS;
-        } else {
-            // level 1: which 32-row blocks are referenced
-#pragma unroll
-            for (int t = 0; t < kTaps; ++t)
-#pragma unroll
-                for (int h = 0; h < VPT; ++h) {
-                    const int32_t v = nv[t][h];
-                    if (v >= 0) {
-                        const int d = v - lo;
-                        atomicOr(&coarse[d >> 10], 1u << ((d >> 5) & 31));
-                    }
-                }
-            __syncthreads();
-            nfine = scan_popcounts<NT>(coarse, HB_SLOTS, cpre, sRed);
-            direct = nfine > HB_ZERO;      // every block holds a row: too many rows for LDS
-            if (!direct) {
-                // rank -> block id
-#pragma unroll
-                for (int k = 0; k < WPT; ++k) {
-                    const int w = tid * WPT + k;
-                    uint32_t bits = coarse[w];
-                    int r = cpre[w];
-                    while (bits) {
-                        const int bit = __builtin_ctz(bits);
-                        bits &= bits - 1u;
-                        block_of[r++] = w * 32 + bit;
-                    }
-                }
-            }
-        }
-        if (!direct) {
-            // level 2: rows within each referenced block
-#pragma unroll
-            for (int t = 0; t < kTaps; ++t)
-#pragma unroll
-                for (int h = 0; h < VPT; ++h) {
-                    const int32_t v = nv[t][h];
-                    if (v >= 0) {
-                        const int d = v - lo;
-                        atomicOr(&fine[fine_word(d)], 1u << (d & 31));
-                    }
-                }
-            __syncthreads();
-            H = scan_popcounts<NT>(fine, nfine, fpre, sRed);
-            direct = H > HB_ZERO;
-        }
-    }
-    if (!direct) {
-        // slot of every (tap, voxel)
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t)
-#pragma unroll
-            for (int h = 0; h < VPT; ++h) {
-                const int rr = tid + NT * h;                   // voxel within the tile
-                const int32_t v = nv[t][h];
-                int slot = HB_ZERO;
-                if (v >= 0) {
-                    const int d = v - lo, fw = fine_word(d);
-                    slot = fpre[fw] + __popc(fine[fw] & ((1u << (d & 31)) - 1u));
-                }
-                sL[t][rr >> 7][rr & 31][(rr >> 5) & 3] = (uint16_t)slot;
-            }
-        // row of every slot
-#pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            const int w = tid * WPT + k;
-            if (w < nfine) {
-                uint32_t bits = fine[w];
-                int s = fpre[w];
-                const int base = lo + (one ? w : block_of[w]) * 32;
-                while (bits) {
-                    const int bit = __builtin_ctz(bits);
-                    bits &= bits - 1u;
-                    sRowOf[s++] = base + bit;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    H_out = H;
-    direct_out = direct;
-}
-
-__global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __restrict__ nbr,
-                                                           int64_t n, int64_t n_tiles,
-                                                           PlanView plan) {
-    __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
-    __shared__ int32_t sRowOf[HB_SLOTS];
-    __shared__ uint32_t sScratch[HB_PLAN_SCRATCH];
-    __shared__ int sRed[2 * HB_PLAN_NT / 64];
-    const int64_t tile = blockIdx.x;
-    int H;
-    bool direct;
-    tile_plan<HB_PLAN_NT>(nbr, n, tile * HB_M, sL, sRowOf, sScratch, sRed, H, direct);
     const int tid = threadIdx.x;
-    if (tid == 0) {
-        int32_t* h = plan.hdr + tile * 4;
-        h[0] = H; h[1] = direct ? 1 : 0; h[2] = 0; h[3] = 0;
+    int64_t i[VPT];
+    int pos[VPT];
+#pragma unroll
+    for (int h = 0; h < VPT; ++h) {
+        pos[h] = tid + NT * h;
+        i[h] = row0 + pos[h] < n ? row0 + pos[h] : -1;
     }
-    if (direct) return;
-    int32_t* ro = plan.rowof + tile * HB_SLOTS;
-    for (int s = tid; s < H; s += HB_PLAN_NT) ro[s] = sRowOf[s];
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(&sL[0][0][0][0]);
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(plan.slots + tile * HB_SLOT_TABLE);
-    for (int p = tid; p < HB_SLOT_TABLE / 8; p += HB_PLAN_NT) dst[p] = src[p];
+    int32_t nv[kTaps][VPT];
+    load_entries<VPT>(nbr, n, i, nv);
+    tile_plan_core<NT, VPT>(nv, pos, sL, sRowOf, scratch, sRed, H_out, direct_out);
 }
 
 // packed[((c32 * nkc + kc) * 27 + t) * 64 + lane][0..7] = W[32 c32 + lane%32][t][16 kc + 8 (lane/32) ..]
@@ -457,6 +216,7 @@ __device__ __forceinline__ void conv_tiles(
         }
     }
     row0_bad = __syncthreads_or(row0_bad);
+
     // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
     // planes of one row (32 contiguous bytes; a load touches 32 rows, not 64)
     int plane = lane & 1;
@@ -552,7 +312,7 @@ __device__ __forceinline__ void conv_tiles(
     // stride WN*4+32 bytes puts the two 32-lane halves of a staging write on disjoint banks.
     // NR rows at a time: 32 over both buffers, or 16 in sH1 alone while sH0 holds the next
     // tile's first slice.
-    auto epilogue = [&](auto nr_c, f32x16_t (&acc)[RB][CB], int64_t row0) {
+    auto epilogue = [&](auto nr_c, f32x16_t (&acc)[RB][CB], int64_t tile) {
         constexpr int NR = decltype(nr_c)::value;
         constexpr int RS = WN * 4 + 32;
         static_assert(NR == 32 || NR == 16, "row rounds of 32 or 16");
@@ -561,20 +321,32 @@ __device__ __forceinline__ void conv_tiles(
         char* stage = NR == 32 ? reinterpret_cast<char*>(wave < WAVES / 2 ? &sH0[0][0][0] : &sH1[0][0][0]) +
                                      (wave % (WAVES / 2)) * 32 * RS
                                : reinterpret_cast<char*>(&sH1[0][0][0]) + wave * 16 * RS;
-        const bool full = row0 + HB_M <= n;   // no row of the tile is past n (uniform)
         constexpr int CH = ODT == TSP_F32 ? 4 : 8;     // channels per 16-byte store
         constexpr int NQ = NR * (WN / CH) / 64;        // stores per lane and round
         static_assert(NR * (WN / CH) % 64 == 0, "whole stores per lane");
-        // Octant stores: the child row of octant oct of each of the wave's 32 RB rows, or -1,
-        // looked up once per tile (lane l holds rows 2l and 2l + 1) and shuffled to the lanes
-        // that store them.
+        // The output row of each of the wave's 32 RB tile positions (the plan's order, or the
+        // tile's rows in order without one), -1 where there is none: lane l holds positions 2l and
+        // 2l + 1, and row_at(lr) shuffles position lr's row to the lane that stores it.
+        static_assert(RB == 4, "two positions per lane");
+        int vrow[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = 32 * RB * rg + 2 * lane + k;
+            if constexpr (PLANNED) vrow[k] = plan.vox[tile * HB_M + p];
+            else vrow[k] = tile * HB_M + p < n ? (int)(tile * HB_M + p) : -1;
+        }
+        auto row_at = [&](int lr) {
+            const int a = __shfl(vrow[0], lr >> 1, 64), b = __shfl(vrow[1], lr >> 1, 64);
+            return (lr & 1) ? b : a;
+        };
+        // Octant stores: the child row of octant oct of each of the wave's rows, or -1, looked up
+        // once per tile for the lane's two positions and shuffled the same way.
         int child2[2] = {-1, -1};
         if constexpr (EPI == 1) {
-            static_assert(RB == 4, "two rows per lane");
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                const int64_t i = row0 + 32 * RB * rg + 2 * lane + k;
-                if (i < n) {
+                const int64_t i = vrow[k];
+                if (i >= 0) {
                     constexpr uint64_t kLow7 = 0x7f7f7f7f7f7f7f7full;
                     const uint64_t mw = *reinterpret_cast<const uint64_t*>(osc.mask + 8 * i);
                     const uint64_t kept = (((mw & kLow7) + kLow7) | mw) & ~kLow7;   // bit 8b+7: byte b != 0
@@ -583,15 +355,13 @@ __device__ __forceinline__ void conv_tiles(
                 }
             }
         }
-        // Skip add: the gidx of each of the wave's rows, looked up and shuffled the same way.
-        int gidx2[2] = {0, 0};
+        // Skip add: the gidx of each of the wave's rows (-1 for none), looked up and shuffled
+        // the same way.
+        int gidx2[2] = {-1, -1};
         if constexpr (EPI == 2) {
-            static_assert(RB == 4, "two rows per lane");
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int64_t i = row0 + 32 * RB * rg + 2 * lane + k;
-                if (i < n) gidx2[k] = skip.gidx[i];
-            }
+            for (int k = 0; k < 2; ++k)
+                if (vrow[k] >= 0) gidx2[k] = skip.gidx[vrow[k]];
         }
         // the skip elements of round (rb, h), one per store (its 4 channels share one); loaded a
         // round ahead of their use, so the loads' latency overlaps a round of staging and stores
@@ -604,9 +374,8 @@ __device__ __forceinline__ void conv_tiles(
                 const int a = __shfl(gidx2[0], lr >> 1, 64), b = __shfl(gidx2[1], lr >> 1, 64);
                 const int gi = (lr & 1) ? b : a;
                 const int kk = skip.cin / 8, rep_r = co / kk;
-                const int64_t i = row0 + 32 * RB * rg + lr;
-                sv[q] = i < n ? skip.x[(int64_t)(gi >> 3) * skip.cin + (gi & 7) * kk + (c0 + cq * CH) / rep_r]
-                              : 0.f;
+                sv[q] = gi >= 0 ? skip.x[(int64_t)(gi >> 3) * skip.cin + (gi & 7) * kk + (c0 + cq * CH) / rep_r]
+                                : 0.f;
             }
         };
         float sv_cur[NQ] = {}, sv_nxt[NQ] = {};
@@ -640,9 +409,9 @@ __device__ __forceinline__ void conv_tiles(
                 for (int q = 0; q < NQ; ++q) {
                     const int c = q * 64 + lane;
                     const int r = c / (WN / CH), cq = c % (WN / CH);
-                    const int64_t i = row0 + 32 * RB * rg + 32 * rb + NR * h + r;
+                    const int64_t i = row_at(32 * rb + NR * h + r);
                     int64_t o = i * co + c0 + cq * CH;
-                    bool keep = full || i < n;
+                    bool keep = i >= 0;
                     if (row0_bad && keep) {
                         bool absent = false;
                         for (int t = 0; t < kTaps; ++t) absent |= nbr[(int64_t)t * n + i] == (int32_t)n;
@@ -703,6 +472,7 @@ __device__ __forceinline__ void conv_tiles(
     int H = 0;
     bool direct = false;
     u32x4_t bR[PD + 1][CB];
+
 
     for (int64_t lin = lin0; lin < xhi; lin += stride) {
         asm volatile("" : "+v"(lane), "+v"(r32), "+v"(g), "+v"(rg), "+v"(plane));
@@ -777,10 +547,11 @@ __device__ __forceinline__ void conv_tiles(
                 // all 27 taps unrolled: register rings stay static and every wait is exact
 #pragma unroll
                 for (int t = 0; t < kTaps; ++t) {
-                    // Even and odd waves (neighbouring SIMDs) take turns at the higher issue
-                    // priority, tap by tap. Against equal priorities this measured 3.5 % faster
-                    // at 128 output channels and the same at 64.
-                    if ((t + wave) & 1) __builtin_amdgcn_s_setprio(1);
+                    // The higher issue priority on odd taps, the lower on even ones (every wave
+                    // alike), so that waves at different taps of the slice are not served
+                    // alike. Against equal priorities this measured 3.5 % faster at 128 output
+                    // channels and the same at 64; priority on the even taps instead, 0.5 % slower.
+                    if (t & 1) __builtin_amdgcn_s_setprio(1);
                     else __builtin_amdgcn_s_setprio(0);
                     // weights PD taps ahead (the first taps of the next slice at the end)
                     if (t + PD < kTaps) load_b(t + PD, kc, bR[(R0 + t + PD) % (PD + 1)]);
@@ -855,7 +626,7 @@ __device__ __forceinline__ void conv_tiles(
                     if (p < HB_SLOT_TABLE * 2 / 1024)
                         *reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024 + lane * 16) = stg[k];
                 }
-                epilogue(std::integral_constant<int, 16>{}, acc, row0);
+                epilogue(std::integral_constant<int, 16>{}, acc, tile);
                 __syncthreads();       // the next tile's slot table; every wave's staging is done
                 zero_slot(sH1);        // the staging covered it; first read after the next barrier
                 pre = nlin != lin && !ndirect;
@@ -871,7 +642,7 @@ __device__ __forceinline__ void conv_tiles(
                     if (kc + 1 < nkc)
                         run_slice(acc, I1{}, NO{}, sH1, sH0, kc + 1, kc + 2 < nkc ? kc + 2 : kc + 1, nullptr);
                 }
-                epilogue(std::integral_constant<int, 32>{}, acc, row0);
+                epilogue(std::integral_constant<int, 32>{}, acc, tile);
                 __syncthreads();       // staging reads end before the next tile's loads
                 pre = false;
             }
@@ -886,8 +657,10 @@ __device__ __forceinline__ void conv_tiles(
                     u32x4_t a[RB];
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) {
-                        const int64_t i = row0 + 32 * RB * rg + 32 * rb + r32;
-                        const int32_t v = (i < n) ? nbr[(int64_t)t * n + i] : (int32_t)n;
+                        const int p = 32 * RB * rg + 32 * rb + r32;   // tile position
+                        int64_t i = row0 + p;
+                        if constexpr (PLANNED) i = plan.vox[tile * HB_M + p];
+                        const int32_t v = (i >= 0 && i < n) ? nbr[(int64_t)t * n + i] : (int32_t)n;
                         a[rb] = u32x4_t{0, 0, 0, 0};
                         if ((uint32_t)v < (uint32_t)n)
                             a[rb] = *reinterpret_cast<const u32x4_t*>(feats + (int64_t)v * ci +
@@ -899,7 +672,7 @@ __device__ __forceinline__ void conv_tiles(
                         for (int cb = 0; cb < CB; ++cb)
                             acc[rb][cb] = mfma32x32x16<BF16>(a[rb], bq[cb], acc[rb][cb]);
                 }
-            epilogue(std::integral_constant<int, 32>{}, acc, row0);
+            epilogue(std::integral_constant<int, 32>{}, acc, tile);
             __syncthreads();           // staging reads end before the next tile's loads
             pre = false;
         }
@@ -993,21 +766,6 @@ int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, cons
 }  // namespace
 
 bool halo_fits(int64_t n, int ci) { return n * (int64_t)ci * 2 < ((int64_t)1 << 32); }
-
-size_t halo_plan_bytes(int64_t n) {
-    const int64_t n_tiles = std::max<int64_t>(1, ceil_div(n, HB_M));
-    return align256((size_t)n_tiles * 16) + align256((size_t)n_tiles * HB_SLOTS * 4) +
-           align256((size_t)n_tiles * HB_SLOT_TABLE * 2);
-}
-
-int halo_plan_build(const int32_t* nbr, int64_t n, void* plan, hipStream_t s) {
-    const int64_t n_tiles = ceil_div(n, HB_M);
-    if (n_tiles == 0) return TSP_OK;
-    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n,
-                       n_tiles, carve_plan(plan, n_tiles));
-    TSP_CHECK_LAUNCH();
-    return TSP_OK;
-}
 
 int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s) {
     const int64_t blocks = (int64_t)(co / 32) * (ci / HB_KC) * kTaps;

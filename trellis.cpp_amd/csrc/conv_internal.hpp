@@ -30,7 +30,7 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 // ---- LDS-staged ("halo") MFMA conv, conv_halo.hip --------------------------------------------
 constexpr int HB_M = 512;   // output voxels per workgroup (and per plan tile)
 
-// Bytes of a conv plan for n voxels (see tsp_conv_plan_bytes).
+// Bytes of a conv plan for n voxels (see tsp_conv_plan_bytes), with the scratch its build sorts in.
 size_t halo_plan_bytes(int64_t n);
 // whether the LDS-staged kernel can address n rows of ci channels (32-bit byte offsets)
 bool halo_fits(int64_t n, int ci);
@@ -42,8 +42,9 @@ bool blaslt_eligible(int x_dtype, int weight_dtype, int out_dtype, int ci, int c
                      const void* w, const void* out);
 int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
                   int co, int act, const float* residual, void* out, int odt, hipStream_t s);
-// Builds the plan of neighbour table `nbr` into `plan`.
-int halo_plan_build(const int32_t* nbr, int64_t n, void* plan, hipStream_t s);
+// Builds the plan of neighbour table `nbr` into `plan`: tiles in the Morton order of the voxels'
+// 8^3 cells when `coords` is given, else tiles of consecutive rows.
+int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s);
 // Packs [co][27][ci] 16-bit weights into the MFMA operand order (ci % 16 == 0, co % 32 == 0).
 int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s);
 // Output rows scattered to the children of a 2x subdivision: with cout > 0, the conv's output

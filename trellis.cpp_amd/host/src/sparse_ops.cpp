@@ -184,6 +184,7 @@ size_t convnext_scratch(const ConvNext& a, int xdt) {
 // ---- tables --------------------------------------------------------------------------------------
 void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status) {
     t.n = n;
+    t.coords = nullptr;
     t.plan = DeviceBuffer();
     t.nbr = DeviceBuffer((size_t)27 * n * 4, s);
     if (n == 0) return;
@@ -203,7 +204,10 @@ void Table::ensure_plan(hipStream_t s) {
     if (plan.get() || n == 0) return;
     const size_t bytes = tsp_conv_plan_bytes(n);
     plan = DeviceBuffer(bytes, s);
-    lib(tsp_conv_plan_build(nbr.as<int32_t>(), n, plan.get(), bytes, s), "conv plan");
+    if (coords)
+        lib(tsp_conv_plan_build_ordered(nbr.as<int32_t>(), coords, n, plan.get(), bytes, s), "conv plan");
+    else
+        lib(tsp_conv_plan_build(nbr.as<int32_t>(), n, plan.get(), bytes, s), "conv plan");
 }
 
 // ---- C2S up-block (sparse.cpp:172-336) -----------------------------------------------------------
