@@ -195,6 +195,16 @@ size_t tsp_subdivide_workspace_bytes(int64_t n);
 int tsp_subdivide(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
                   int32_t* d_mstart, int32_t* d_child_coords, int32_t* d_gidx, int64_t* d_m,
                   void* d_workspace, size_t workspace_bytes, void* stream);
+/* tsp_subdivide without a workspace argument and without allocating: no counterpart in the
+ * reference; for callers that cannot allocate device memory (HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Its block counts live in a 1 MiB array that the library
+ * holds on each device it runs on until the process ends, which covers every n tsp_subdivide
+ * accepts (8n < 2^31); larger n is rejected with TSP_ERR_INVALID. Calls on one device share
+ * that array, so calls that overlap on one device (different streams, other threads) race;
+ * calls in stream order do not. Results are identical to tsp_subdivide's. */
+int tsp_subdivide_noalloc(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
+                          int32_t* d_mstart, int32_t* d_child_coords, int32_t* d_gidx,
+                          int64_t* d_m, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Per-voxel pieces of the ConvNeXt and C2S blocks (sparse_convnext, sparse.cpp:94-137;

@@ -115,6 +115,12 @@ def test_subdivide_validation(pkg):
     assert L.tsp_subdivide(FAKE, FAKE, 1 << 29, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, NULL) == 1
     ws = L.tsp_subdivide_workspace_bytes(5000)
     assert L.tsp_subdivide(FAKE, FAKE, 5000, FAKE, FAKE, FAKE, FAKE, FAKE, ws - 1, NULL) == 5
+    # the allocation-free variant: the same argument checks, no workspace
+    assert L.tsp_subdivide_noalloc(FAKE, FAKE, -1, FAKE, FAKE, FAKE, FAKE, NULL) == 1
+    assert L.tsp_subdivide_noalloc(FAKE, FAKE, 1 << 28, FAKE, FAKE, FAKE, FAKE, NULL) == 1
+    assert "out of range" in _err(pkg)
+    assert L.tsp_subdivide_noalloc(NULL, NULL, 10, FAKE, FAKE, FAKE, FAKE, NULL) == 1
+    assert L.tsp_subdivide_noalloc(FAKE, FAKE, 10, FAKE, FAKE, FAKE, NULL, NULL) == 1
 
 
 def test_python_binding_rejects_host_tensors(pkg):

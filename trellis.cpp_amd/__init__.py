@@ -29,7 +29,7 @@ EXPORTS = (
     "tsp_conv_weight_pack",
     "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_ex", "tsp_subm_conv3x3_planned_octants",
     "tsp_subm_conv3x3_planned_skip",
-    "tsp_subdivide_workspace_bytes", "tsp_subdivide",
+    "tsp_subdivide_workspace_bytes", "tsp_subdivide", "tsp_subdivide_noalloc",
     "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
 )
@@ -113,6 +113,8 @@ def lib() -> ctypes.CDLL:
     L.tsp_subdivide_workspace_bytes.argtypes = [c_i64]
     L.tsp_subdivide.restype = c_int
     L.tsp_subdivide.argtypes = [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]
+    L.tsp_subdivide_noalloc.restype = c_int
+    L.tsp_subdivide_noalloc.argtypes = [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]
     _lib = L
     return L
 

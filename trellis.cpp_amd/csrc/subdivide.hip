@@ -8,6 +8,7 @@
 // Three launches: per-block child counts -> one-workgroup scan of the block counts (which also
 // writes M) -> per-block rescan that writes mstart, the child coordinates and gidx.
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -112,6 +113,46 @@ __global__ __launch_bounds__(SD_THREADS) void k_emit_children(
     }
 }
 
+// The per-block child counts of tsp_subdivide_noalloc: one int32 per SD_ITEMS parents, enough
+// for the largest n the subdivision accepts (8n < 2^31 -> at most 2^18 blocks), 1 MiB on each
+// device. Host code reaches it only through the address hipGetSymbolAddress gives per device.
+constexpr int64_t SD_SCRATCH_WORDS = int64_t(1) << 18;
+static __device__ __align__(256) int32_t scratch[SD_SCRATCH_WORDS];
+
+constexpr int SD_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[SD_MAX_DEVICES] = {};
+
+// The three launches over `sums` (nb = ceil(n / SD_ITEMS) int32; every entry is written by
+// k_block_counts before it is read, so nothing needs clearing).
+int subdivide_launch(const uint8_t* mask, const int32_t* coords, int64_t n, int32_t* mstart,
+                     int32_t* child, int32_t* gidx, int64_t* m_out, int32_t* sums, hipStream_t s) {
+    const int64_t nb = ceil_div(n, SD_ITEMS);
+    if (nb > 0) {
+        hipLaunchKernelGGL(k_block_counts, dim3((unsigned)nb), dim3(SD_THREADS), 0, s, mask, n, sums);
+        TSP_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(SD_THREADS), 0, s, sums, nb, n, mstart, m_out);
+    TSP_CHECK_LAUNCH();
+    if (nb > 0) {
+        hipLaunchKernelGGL(k_emit_children, dim3((unsigned)nb), dim3(SD_THREADS), 0, s, mask, coords,
+                           n, sums, mstart, child, gidx);
+        TSP_CHECK_LAUNCH();
+    }
+    return TSP_OK;
+}
+
+int check_subdivide_args(const char* fn, const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
+                         const int32_t* d_mstart, const int32_t* d_child, const int32_t* d_gidx,
+                         const int64_t* d_m) {
+    TSP_REQUIRE(n >= 0 && 8 * n < (int64_t)INT32_MAX, TSP_ERR_INVALID,
+                "%s: n=%lld out of range (8n must fit int32)", fn, (long long)n);
+    TSP_REQUIRE(d_mstart && d_m, TSP_ERR_INVALID, "%s: null pointer", fn);
+    TSP_REQUIRE(n == 0 || (d_mask && d_coords && d_child && d_gidx), TSP_ERR_INVALID,
+                "%s: null pointer", fn);
+    return TSP_OK;
+}
+
 }  // namespace
 }  // namespace tsp
 
@@ -128,29 +169,45 @@ extern "C" int tsp_subdivide(const uint8_t* d_mask, const int32_t* d_coords, int
                              int64_t* d_m, void* d_workspace, size_t workspace_bytes,
                              void* stream) {
     clear_error();
-    TSP_REQUIRE(n >= 0 && 8 * n < (int64_t)INT32_MAX, TSP_ERR_INVALID,
-                "tsp_subdivide: n=%lld out of range (8n must fit int32)", (long long)n);
-    TSP_REQUIRE(d_mstart && d_m && d_workspace, TSP_ERR_INVALID, "tsp_subdivide: null pointer");
-    TSP_REQUIRE(n == 0 || (d_mask && d_coords && d_child_coords && d_gidx), TSP_ERR_INVALID,
-                "tsp_subdivide: null pointer");
+    if (int st = check_subdivide_args("tsp_subdivide", d_mask, d_coords, n, d_mstart,
+                                      d_child_coords, d_gidx, d_m))
+        return st;
+    TSP_REQUIRE(d_workspace, TSP_ERR_INVALID, "tsp_subdivide: null pointer");
     TSP_REQUIRE(workspace_bytes >= tsp_subdivide_workspace_bytes(n), TSP_ERR_WORKSPACE,
                 "tsp_subdivide: workspace %zu < %zu bytes", workspace_bytes,
                 tsp_subdivide_workspace_bytes(n));
-    hipStream_t s = as_stream(stream);
-    int32_t* sums = reinterpret_cast<int32_t*>(d_workspace);
+    return subdivide_launch(d_mask, d_coords, n, d_mstart, d_child_coords, d_gidx, d_m,
+                            reinterpret_cast<int32_t*>(d_workspace), as_stream(stream));
+}
+
+extern "C" int tsp_subdivide_noalloc(const uint8_t* d_mask, const int32_t* d_coords, int64_t n,
+                                     int32_t* d_mstart, int32_t* d_child_coords, int32_t* d_gidx,
+                                     int64_t* d_m, void* stream) {
+    clear_error();
+    if (int st = check_subdivide_args("tsp_subdivide_noalloc", d_mask, d_coords, n, d_mstart,
+                                      d_child_coords, d_gidx, d_m))
+        return st;
     const int64_t nb = ceil_div(n, SD_ITEMS);
-    if (nb > 0) {
-        hipLaunchKernelGGL(k_block_counts, dim3((unsigned)nb), dim3(SD_THREADS), 0, s, d_mask, n,
-                           sums);
-        TSP_CHECK_LAUNCH();
+    TSP_REQUIRE(nb <= SD_SCRATCH_WORDS, TSP_ERR_INVALID,
+                "tsp_subdivide_noalloc: n=%lld exceeds the scratch's %lld parents", (long long)n,
+                (long long)(SD_SCRATCH_WORDS * SD_ITEMS));
+    int dev = 0;
+    TSP_CHECK_HIP(hipGetDevice(&dev));
+    TSP_REQUIRE(dev >= 0 && dev < SD_MAX_DEVICES, TSP_ERR_INVALID,
+                "tsp_subdivide_noalloc: device %d beyond the %d this library tracks", dev,
+                SD_MAX_DEVICES);
+    int32_t* sums = nullptr;
+    {
+        // first call on this device (it is current): look up its copy of the scratch array
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            void* p = nullptr;
+            TSP_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+            TSP_REQUIRE(p, TSP_ERR_HIP, "tsp_subdivide_noalloc: no device address for the scratch");
+            g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+        }
+        sums = g_scratch_ptr[dev];
     }
-    hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(SD_THREADS), 0, s, sums, nb, n, d_mstart,
-                       d_m);
-    TSP_CHECK_LAUNCH();
-    if (nb > 0) {
-        hipLaunchKernelGGL(k_emit_children, dim3((unsigned)nb), dim3(SD_THREADS), 0, s, d_mask,
-                           d_coords, n, sums, d_mstart, d_child_coords, d_gidx);
-        TSP_CHECK_LAUNCH();
-    }
-    return TSP_OK;
+    return subdivide_launch(d_mask, d_coords, n, d_mstart, d_child_coords, d_gidx, d_m, sums,
+                            as_stream(stream));
 }
