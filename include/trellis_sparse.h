@@ -101,12 +101,15 @@ int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
  * its padding column is silu(norm(0)) = 0 (sparse.cpp:289-306). */
 enum { TSP_CONV_ZERO_PAD = 1 };
 
-/* tsp_subm_conv3x3 with flags (same replaced function, sparse.cpp:61-92; flags 0 = the same
- * call). */
+/* tsp_subm_conv3x3 with flags and, optionally, d_row0: the f32 row 0 (ci floats) that a caller
+ * rounded 16-bit d_feats from (ggml's F16/BF16 mul_mat rounds F32 activations, sparse.cpp:74,
+ * while the padding row 0 * feats[0] is formed before that, in F32, sparse.cpp:81-85). Where
+ * d_row0 is given, the padding row's NaN channels are those of 0 * d_row0; NULL tests feats row 0
+ * itself. Same replaced function, sparse.cpp:61-92; flags 0 and d_row0 NULL = the same call. */
 int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
                         const int32_t* d_nbr, const void* d_weight, int weight_dtype,
                         const float* d_bias, int co, void* d_out, int out_dtype, int algo,
-                        int flags, void* stream);
+                        int flags, const float* d_row0, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Reusable conv plan and packed weights (no counterpart call in the reference: they split
@@ -144,11 +147,8 @@ int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t n, int ci,
                              const void* d_packed_weight, const float* d_bias, int co,
                              void* d_out, int out_dtype, void* stream);
 
-/* tsp_subm_conv3x3_planned with flags (TSP_CONV_ZERO_PAD) and, optionally, d_row0: the f32
- * row 0 (ci floats) that a caller rounded d_feats from (ggml's F16 mul_mat rounds F32
- * activations, sparse.cpp:74, while the padding row 0 * feats[0] is formed before that, in F32,
- * sparse.cpp:81-85). Where d_row0 is given, the padding row's NaN channels are those of
- * 0 * d_row0; NULL tests feats row 0 itself. flags 0 and d_row0 NULL = the same call. */
+/* tsp_subm_conv3x3_planned with flags (TSP_CONV_ZERO_PAD) and, optionally, d_row0 (as for
+ * tsp_subm_conv3x3_ex). flags 0 and d_row0 NULL = the same call. */
 int tsp_subm_conv3x3_planned_ex(const void* d_feats, int dtype, int64_t n, int ci,
                                 const int32_t* d_nbr, const void* d_plan,
                                 const void* d_packed_weight, const float* d_bias, int co,

@@ -158,10 +158,24 @@ def subm_conv_f32_rows(feats, nbr, weight, bias, r0: int, r1: int, threads: int 
     return out
 
 
-def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0, zero_pad: bool = False) -> np.ndarray:
+def _pad_mode(zero_pad: bool, row0) -> bool:
+    """Whether the padding row is an exact zero row. row0: the float32 row 0 that 16-bit-rounded
+    feats came from (the reference pads before ggml's mul_mat rounds, sparse.cpp:74, 81-85). A
+    finite row0 gives a zero padding row even where its rounding overflows to Inf; a non-finite
+    channel of row0 stays non-finite in the rounded row, and any NaN channel of the padding row
+    makes every output channel of the rows that read it NaN, so the rounded row then stands for
+    row0."""
+    if zero_pad or row0 is None:
+        return zero_pad
+    return bool(np.isfinite(np.asarray(row0, np.float32)).all())
+
+
+def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0, zero_pad: bool = False,
+                  row0=None) -> np.ndarray:
     """The same sum in fp64 over active taps only: the tolerance judge. Absent taps read the
     padding row 0 * feats[0] (NaN rows where feats[0] is not finite), or with zero_pad an exact
-    zero row (the C2S conv2, sparse.cpp:289-306)."""
+    zero row (the C2S conv2, sparse.cpp:289-306); row0 as in _pad_mode."""
+    zero_pad = _pad_mode(zero_pad, row0)
     f = np.ascontiguousarray(feats, dtype=np.float32)
     n, ci = f.shape
     w = np.ascontiguousarray(weight, dtype=np.float32)
@@ -174,8 +188,9 @@ def subm_conv_f64(feats, nbr, weight, bias, threads: int = 0, zero_pad: bool = F
 
 
 def subm_conv_f64_rows(feats, nbr, weight, bias, rows, threads: int = 0,
-                      zero_pad: bool = False) -> np.ndarray:
+                      zero_pad: bool = False, row0=None) -> np.ndarray:
     """fp64 conv for the listed output rows only -> [len(rows), Co]."""
+    zero_pad = _pad_mode(zero_pad, row0)
     f = np.ascontiguousarray(feats, dtype=np.float32)
     n, ci = f.shape
     w = np.ascontiguousarray(weight, dtype=np.float32)
@@ -232,6 +247,34 @@ def subdivide_vectorised(mask, coords):
 # ----------------------------------------------------------------------------------------
 # Block arithmetic (float64)
 # ----------------------------------------------------------------------------------------
+def round_f16(x):
+    """x rounded to IEEE binary16 (nearest even) by way of float32, as a device rounds a float32
+    value; returned as float64."""
+    return np.asarray(x, np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+def round_bf16(x):
+    """x rounded to bfloat16 (nearest even on the float32 bit pattern; NaN stays NaN); float64."""
+    u = np.asarray(x, np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    out = r.view(np.float32).astype(np.float64)
+    nan = np.isnan(np.asarray(x, np.float64))
+    return np.where(nan, np.nan, out)
+
+
+def act_round(x, wtype, conv_weight: bool = False, cast_f32: bool = False):
+    """The input of a matrix product with weights stored as `wtype` ("f16", "bf16", "f32" or None),
+    rounded as ggml's mul_mat rounds it (sparse.cpp:74, 126, 128, 188; shape_decoder.cpp:71): to
+    the weights' 16-bit type (the CPU backend's vec_dot type), unchanged for f32 weights. F16 conv
+    weights under g_sparse_cast_f32 are cast to f32 first (w32, sparse.cpp:16-19) and leave the
+    input unrounded; linear weights are never cast. Returns float64."""
+    if wtype == "f16" and not (conv_weight and cast_f32):
+        return round_f16(x)
+    if wtype == "bf16":
+        return round_bf16(x)
+    return np.asarray(x, np.float64)
+
+
 def layer_norm(x, weight=None, bias=None, eps: float = 1e-6):
     """Row LayerNorm over channels with biased variance (ggml_norm, sparse.cpp:124)."""
     x = np.asarray(x, np.float64)
@@ -255,26 +298,42 @@ def linear(x, w, b):
     return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T + np.asarray(b, np.float64)
 
 
-def convnext_block(feats, nbr, p: dict, prefix: str):
+def _rounder(wt, cast_f32):
+    """r(x, name, conv): act_round by the stored type of weight `name` (wt: name -> type; None
+    rounds nothing)."""
+    def r(x, name, conv=False):
+        if wt is None:
+            return np.asarray(x, np.float64)
+        return act_round(x, wt.get(name), conv, cast_f32)
+    return r
+
+
+def convnext_block(feats, nbr, p: dict, prefix: str, wt=None, cast_f32: bool = False):
     """SparseConvNeXtBlock3d (sparse.cpp:102-137): conv -> LN(1e-6)+affine -> mlp.0 -> SiLU
-    -> mlp.2 -> + block input. Returns float64 [N, C]."""
+    -> mlp.2 -> + block input. wt (weight name -> stored type) rounds each product's input as
+    act_round says; p holds the weights' stored values. Returns float64 [N, C]."""
+    r = _rounder(wt, cast_f32)
     x = np.asarray(feats, np.float32)
-    h = subm_conv_f64(x, nbr, p[prefix + ".conv.weight"], p[prefix + ".conv.bias"])
+    xc = r(x, prefix + ".conv.weight", True).astype(np.float32)
+    h = subm_conv_f64(xc, nbr, p[prefix + ".conv.weight"], p[prefix + ".conv.bias"], row0=x[0])
     h = layer_norm(h, p[prefix + ".norm.weight"], p[prefix + ".norm.bias"], 1e-6)
-    h = linear(h, p[prefix + ".mlp.0.weight"], p[prefix + ".mlp.0.bias"])
+    h = linear(r(h, prefix + ".mlp.0.weight"), p[prefix + ".mlp.0.weight"], p[prefix + ".mlp.0.bias"])
     h = silu(h)
-    h = linear(h, p[prefix + ".mlp.2.weight"], p[prefix + ".mlp.2.bias"])
+    h = linear(r(h, prefix + ".mlp.2.weight"), p[prefix + ".mlp.2.weight"], p[prefix + ".mlp.2.bias"])
     return h + x.astype(np.float64)
 
 
-def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None):
-    """SparseResBlockC2S3d (sparse.cpp:172-336). Returns (out float64 [M,Cout],
-    child_coords [M,3], mask_used uint8 [8N])."""
+def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None, wt=None,
+              cast_f32: bool = False):
+    """SparseResBlockC2S3d (sparse.cpp:172-336). wt rounds each product's input as in
+    convnext_block. Returns (out float64 [M,Cout], child_coords [M,3], mask_used uint8 [8N])."""
+    rd = _rounder(wt, cast_f32)
     x = np.asarray(feats, np.float32)
     n, cin = x.shape
     c = _coords(coords)
     if ext_mask is None:
-        logits = linear(x, p[prefix + ".to_subdiv.weight"], p[prefix + ".to_subdiv.bias"])
+        logits = linear(rd(x, prefix + ".to_subdiv.weight"), p[prefix + ".to_subdiv.weight"],
+                        p[prefix + ".to_subdiv.bias"])
         mask = (logits > 0).astype(np.uint8).reshape(-1)        # sparse.cpp:215
     else:
         mask = (np.asarray(ext_mask).reshape(-1) != 0).astype(np.uint8)
@@ -283,34 +342,39 @@ def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None):
     r = cout // k
     nbr = neighbor_table(c)
     h = silu(layer_norm(x, p[prefix + ".norm1.weight"], p[prefix + ".norm1.bias"], 1e-6))
-    h = subm_conv_f64(h.astype(np.float32), nbr, p[prefix + ".conv1.weight"], p[prefix + ".conv1.bias"])
+    h = subm_conv_f64(rd(h, prefix + ".conv1.weight", True).astype(np.float32), nbr, p[prefix + ".conv1.weight"],
+                      p[prefix + ".conv1.bias"], row0=h[0].astype(np.float32))
     h = h.reshape(n * 8, cout)[gidx]                              # octant gather, :288
     h = silu(layer_norm(h, None, None, 1e-6))                     # norm2 without affine, :293
     nbr2 = neighbor_table(child)
     # conv2 reads hn padded with its zero column M (silu(norm(0)) = 0, :289-306), not 0 * hn[0]
-    h = subm_conv_f64(h.astype(np.float32), nbr2, p[prefix + ".conv2.weight"], p[prefix + ".conv2.bias"],
-                      zero_pad=True)
+    h = subm_conv_f64(rd(h, prefix + ".conv2.weight", True).astype(np.float32), nbr2, p[prefix + ".conv2.weight"],
+                      p[prefix + ".conv2.bias"], zero_pad=True)
     xs = x.reshape(n * 8, k)[gidx].astype(np.float64)             # skip gather, :307
     skip = np.repeat(xs, r, axis=1)                               # repeat_interleave, :322
     return h + skip, child, mask
 
 
-def decode_unet(latent, coords, p: dict, stages, out_ch: int, guide=None):
+def decode_unet(latent, coords, p: dict, stages, out_ch: int, guide=None, wt=None,
+                cast_f32: bool = False):
     """SparseUnetVaeDecoder (shape_decoder.cpp:79-117): from_latent -> per stage, its ConvNeXt
     blocks on the stage's table then its C2S block (masks from `guide` when given, else
     predicted) -> LayerNorm(eps 1e-5, no affine, :116) -> output_layer. `stages` lists
-    (block prefixes, (c2s prefix, cin, cout)). Returns (out float64 [M, out_ch], coords [M,3],
-    masks used per stage)."""
+    (block prefixes, (c2s prefix, cin, cout)); wt rounds each product's input as in
+    convnext_block. The stream between blocks is float32 (ggml's F32 tensors). Returns (out
+    float64 [M, out_ch], coords [M,3], masks used per stage)."""
+    r = _rounder(wt, cast_f32)
     c = _coords(coords)
-    h = linear(np.asarray(latent, np.float32), p["from_latent.weight"], p["from_latent.bias"])
+    h = linear(r(np.asarray(latent, np.float32), "from_latent.weight"), p["from_latent.weight"],
+               p["from_latent.bias"])
     masks = []
     for si, (blocks, (c2s, _cin, cout)) in enumerate(stages):
         nbr = neighbor_table(c)
         for b in blocks:
-            h = convnext_block(h.astype(np.float32), nbr, p, b)
+            h = convnext_block(h.astype(np.float32), nbr, p, b, wt, cast_f32)
         h, c, m = c2s_block(h.astype(np.float32), c, p, c2s, cout,
-                            None if guide is None else guide[si])
+                            None if guide is None else guide[si], wt, cast_f32)
         masks.append(m)
-    h = layer_norm(h, None, None, 1e-5)
-    out = linear(h, p["output_layer.weight"], p["output_layer.bias"])
+    h = layer_norm(h.astype(np.float32), None, None, 1e-5)
+    out = linear(r(h, "output_layer.weight"), p["output_layer.weight"], p["output_layer.bias"])
     return out, c, masks

@@ -65,37 +65,118 @@ def stored(params):
     return {k: (_f16(v) if v.ndim >= 2 else v) for k, v in params.items()}
 
 
-def write_conv_case(d, orc, coords, c, seed):
+def stored_types(params, wtype="f16"):
+    """Weight name -> the type the GGUF stores it in (the oracle's rounding rule reads it)."""
+    return {k: (wtype if np.asarray(v).ndim >= 2 else "f32") for k, v in params.items()}
+
+
+def write_conv_case(d, orc, coords, c, seed, cast_f32=False):
     """ConvNeXt block `blocks.3.0` with c channels on `coords` (the reference's
-    test_sparse_conv.cpp inputs: coords, feats_in, conv_out, block_out) plus the table and
-    conv_out16 (the conv of the F16-rounded features, what the matrix-core path computes)."""
+    test_sparse_conv.cpp inputs: coords, feats_in, conv_out, block_out) plus the table. The
+    expected outputs round every product's input as ggml's mul_mat does (F16 weights; under
+    cast_f32, the reference's g_sparse_cast_f32, the conv weights are cast and its input is not
+    rounded)."""
     rng = np.random.default_rng(seed)
     n = len(coords)
     x = rng.standard_normal((n, c)).astype(np.float32)
     p = convnext_params(rng, c)
     write_gguf(os.path.join(d, "model.gguf"), p)
-    q = stored(p)
+    q, wt = stored(p), stored_types(p)
     nbr = orc.neighbor_table(coords)
     w, b = q["blocks.3.0.conv.weight"], q["blocks.3.0.conv.bias"]
+    xc = orc.act_round(x, "f16", True, cast_f32).astype(np.float32)
     _save(d, coords=np.ascontiguousarray(coords, np.int32), feats_in=x, nbr=nbr,
-          conv_out=orc.subm_conv_f64(x, nbr, w, b).astype(np.float32),
-          conv_out16=orc.subm_conv_f64(_f16(x), nbr, w, b).astype(np.float32),
-          block_out=orc.convnext_block(x, nbr, q, "blocks.3.0").astype(np.float32))
+          conv_out=orc.subm_conv_f64(xc, nbr, w, b, row0=x[0]).astype(np.float32),
+          block_out=orc.convnext_block(x, nbr, q, "blocks.3.0", wt, cast_f32).astype(np.float32))
 
 
-def write_c2s_case(d, orc, coords, cin, cout, seed, ext=False):
+def write_c2s_case(d, orc, coords, cin, cout, seed, ext=False, cast_f32=False):
     """C2S up-block `blocks.3.4` (the reference's test_c2s.cpp inputs) with the expected
-    children, mask and features; with ext, a random ext_mask.npy drives the subdivision."""
+    children, mask and features (rounded as in write_conv_case); with ext, a random ext_mask.npy
+    drives the subdivision."""
     rng = np.random.default_rng(seed)
     n = len(coords)
     x = rng.standard_normal((n, cin)).astype(np.float32)
     p = c2s_params(rng, cin, cout)
     write_gguf(os.path.join(d, "model.gguf"), p)
-    q = stored(p)
+    q, wt = stored(p), stored_types(p)
     ext_mask = (rng.random(8 * n) < 0.3).astype(np.uint8) if ext else None
-    out, child, mask = orc.c2s_block(x, coords, q, "blocks.3.4", cout, ext_mask)
+    out, child, mask = orc.c2s_block(x, coords, q, "blocks.3.4", cout, ext_mask, wt, cast_f32)
     _save(d, coords=np.ascontiguousarray(coords, np.int32), feats_in=x,
           new_coords=np.ascontiguousarray(child, np.int32), out=np.asarray(out, np.float32),
           subdiv=np.asarray(mask, np.uint8))
     if ext:
         _save(d, ext_mask=ext_mask)
+
+
+def zero_weight_decoder(rng, channels, blocks):
+    """decoder parameters (f32) whose conv and MLP weights are zero: every ConvNeXt block adds its
+    mlp.2 bias, every C2S block gives a child conv2's bias + the skip, so the decoder reduces to
+    from_latent, the routing of the skips and the head."""
+    p, stages = decoder_params(rng, channels, blocks, latent=8, out_ch=6)
+    for k in p:
+        if k.endswith((".conv.weight", ".mlp.0.weight", ".mlp.2.weight", ".conv1.weight", ".conv2.weight")):
+            p[k] = np.zeros_like(p[k])
+    p["from_latent.weight"] = p["from_latent.weight"] * 0.01   # features ~ 0.01: the head's eps matters
+    p["from_latent.bias"] = p["from_latent.bias"] * 0.01
+    for k in p:
+        if k.endswith((".mlp.2.bias", ".conv2.bias")):
+            p[k] = p[k] * 0.05
+    return p, stages
+
+
+def decode_closed_form(latent, coords, p, stages, guide, eps=1e-5, octant_shift=0):
+    """The zero-weight decoder by explicit loops: h = latent W^T + b; each ConvNeXt block adds
+    mlp.2.bias; child (parent i, octant o, in parent order and ascending octant) of a C2S block is
+    conv2.bias + repeat(h[i, o k:(o+1) k], cout / k) at (2x + (o&1), 2y + (o>>1 & 1), 2z + (o>>2 & 1));
+    then LayerNorm with eps 1e-5 and no affine, and output_layer. eps and octant_shift (the skip
+    read from slice o ^ shift) plant mistakes."""
+    h = [np.asarray(latent[i], np.float64) @ p["from_latent.weight"].T.astype(np.float64) + p["from_latent.bias"]
+         for i in range(len(latent))]
+    c = [tuple(int(v) for v in row) for row in coords]
+    for si, (blocks, (c2s, cin, cout)) in enumerate(stages):
+        for b in blocks:
+            h = [hi + p[b + ".mlp.2.bias"] for hi in h]
+        k = cin // 8
+        nh, nc = [], []
+        for i, (x, y, z) in enumerate(c):
+            for o in range(8):
+                if guide[si][8 * i + o]:
+                    nc.append((2 * x + (o & 1), 2 * y + ((o >> 1) & 1), 2 * z + ((o >> 2) & 1)))
+                    os_ = o ^ octant_shift
+                    nh.append(p[c2s + ".conv2.bias"] + np.repeat(h[i][os_ * k:(os_ + 1) * k], cout // k))
+        h, c = nh, nc
+    out = []
+    for hi in h:
+        mu = hi.mean()
+        var = ((hi - mu) ** 2).mean()
+        y = (hi - mu) / np.sqrt(var + eps)
+        out.append(y @ p["output_layer.weight"].T.astype(np.float64) + p["output_layer.bias"])
+    return np.array(out), np.array(c, np.int32)
+
+
+def rounding_noise_floor(orc, run, runs=2, rel=1e-7, seed=0):
+    """How far two correct evaluations of the rounding semantics fall apart: the largest
+    max|d|/max|ref| between run() (an oracle computation returning an array) and run() again with
+    every matrix product's input perturbed by a relative `rel` before its rounding, as another
+    float32 evaluation order of what produced it would perturb it. A rounding step then falls on
+    the other side for some elements, as it does between the device and the oracle. run() returns
+    the array, or a tuple whose first item is it; the first result is returned with the floor."""
+    first = run()
+    pick = lambda r: np.asarray(r[0] if isinstance(r, tuple) else r, np.float64)
+    ref = pick(first)
+    exact = orc.act_round
+    rng = np.random.default_rng(seed)
+
+    def jittered(x, wtype, conv_weight=False, cast_f32=False):
+        x = np.asarray(x, np.float64)
+        return exact(x * (1 + rel * rng.uniform(-1, 1, x.shape)), wtype, conv_weight, cast_f32)
+
+    worst = 0.0
+    orc.act_round = jittered
+    try:
+        for _ in range(runs):
+            worst = max(worst, orc.rel_err(pick(run()), ref))
+    finally:
+        orc.act_round = exact
+    return first, worst

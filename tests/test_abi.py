@@ -199,9 +199,10 @@ def test_conv_ex_flags_validation(pkg):
     L = pkg.lib()
     O = ctypes.c_void_p(0x2000)
     f = lambda flags, **kw: L.tsp_subm_conv3x3_ex(
-        FAKE, 2, kw.get("n", 100), 64, FAKE, FAKE, 2, FAKE, 64, kw.get("out", O), 0, 0, flags, NULL)
+        FAKE, 2, kw.get("n", 100), 64, FAKE, FAKE, 2, FAKE, 64, kw.get("out", O), 0, 0, flags,
+        kw.get("row0", NULL), NULL)
     assert f(2) == 1 and "flags" in _err(pkg)
-    assert f(1, n=0) == 0 and f(0, n=0) == 0
+    assert f(1, n=0) == 0 and f(0, n=0) == 0 and f(0, n=0, row0=FAKE) == 0
     assert f(1, out=FAKE) == 1 and "alias" in _err(pkg)
     p = lambda flags, **kw: L.tsp_subm_conv3x3_planned_ex(
         FAKE, kw.get("dt", 2), kw.get("n", 100), 64, FAKE, FAKE, FAKE, FAKE, 64, O, 0, flags,

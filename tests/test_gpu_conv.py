@@ -442,12 +442,14 @@ def test_zero_padding_row(gpu_lib, orc, shells, path, bad):
     _nan_aware(out, ref, TOL_32 if key == "f32" else TOL_16)
 
 
-def test_padding_row_from_f32_source(gpu_lib, orc, shells):
+@pytest.mark.parametrize("path", ["planned", "mfma", "mfma_gather", "narrow"])
+def test_padding_row_from_f32_source(gpu_lib, orc, shells, path):
     """A finite f32 row 0 beyond the f16 range rounds to Inf. The reference forms its padding row
     0 * feats[0] in F32 before ggml's F16 mul_mat rounds the activations (sparse.cpp:74, 81-85), so
     the padding row is zero: given the f32 row 0 (row0=), only rows that reference row 0 turn
-    non-finite. Without it the rounded Inf row makes every row with an absent tap NaN."""
-    _case("padding row from the f32 source row")
+    non-finite. Without it the rounded Inf row makes every row with an absent tap NaN. On every
+    kernel path."""
+    _case(f"padding row from the f32 source row: {path}")
     import torch
     rng = np.random.default_rng(37)
     coords = np.ascontiguousarray(shells.sphere_shell(24, 12.0, 7.0, 9.0), np.int32)
@@ -464,9 +466,14 @@ def test_padding_row_from_f32_source(gpu_lib, orc, shells):
     plan = gpu_lib.conv_plan_build(nbr_d, n)
     pw = gpu_lib.conv_weight_pack(_dev(weight, torch.float16))
     f, b = _dev(feats16, torch.float16), _dev(bias, torch.float32)
-    with_src = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32,
-                                            row0=_dev(feats32[0], torch.float32))
-    without = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32)
+    r0 = _dev(feats32[0], torch.float32)
+    if path == "planned":
+        with_src = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32, row0=r0)
+        without = gpu_lib.subm_conv3x3_planned(f, nbr_d, plan, pw, b, co, out_dtype=torch.float32)
+    else:
+        w = _dev(weight, torch.float16)
+        with_src = gpu_lib.subm_conv3x3(f, nbr_d, w, b, out_dtype=torch.float32, algo=path, row0=r0)
+        without = gpu_lib.subm_conv3x3(f, nbr_d, w, b, out_dtype=torch.float32, algo=path)
     torch.cuda.synchronize()
     _nan_aware(with_src.cpu().numpy(), orc.subm_conv_f64(feats16, nbr, weight, bias, zero_pad=True), TOL_16)
     absent = (nbr.reshape(27, n) == n).any(axis=0)

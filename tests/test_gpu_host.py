@@ -3,10 +3,15 @@ synthetic weights through Model::load and run trellis::build_neighbor_table, spa
 sparse_convnext in a ggml graph, sparse_c2s, and the device-resident decoders (shape_decode,
 shape_upsample, tex_decode), against the oracle's outputs.
 
-Bars: table, children and masks exact. Features max|d|/max|ref|: <= 1e-3 on the matrix-core
-path (F32 activations rounded to F16 as ggml's F16 mul_mat does, fp32 accumulation); <= 2e-5
-for that conv against the oracle fed the same F16-rounded features; <= 1e-5 on the fp32 path
-(--f32, the reference's g_sparse_cast_f32)."""
+The oracle rounds the input of every matrix product to the weights' stored type where ggml's
+mul_mat does (oracle.act_round: F16 / BF16 weights; under --f32, the reference's
+g_sparse_cast_f32, the conv weights are cast to F32 and their input stays F32, the linears still
+round). Bars: table, children and masks exact. Features max|d|/max|ref|: <= 2e-5 for a conv (fp32
+accumulation against fp64 on the same rounded inputs); 2e-4 for a block, whose later products
+take inputs that both sides round from float32 values computed in another order, where one
+rounding step (2^-11 for F16) can fall on either side. Over a whole decoder such flips compound:
+its bar is 1.5x the oracle's own noise floor (host_cases.rounding_noise_floor: the oracle against
+itself with every product input perturbed by 1e-7 before rounding), measured in the test."""
 from __future__ import annotations
 
 import dataclasses
@@ -18,7 +23,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from host_cases import write_c2s_case, write_conv_case
+from host_cases import rounding_noise_floor, write_c2s_case, write_conv_case
 
 pytestmark = pytest.mark.gpu
 
@@ -50,46 +55,42 @@ def _val(out, key):
     return float(m.group(1))
 
 
-@pytest.mark.parametrize("c,f32", [(64, False), (64, True), (128, False), (48, False)])
+TOL_CONV = 2e-5
+TOL_BLOCK_F16 = 2e-4
+
+
+@pytest.mark.parametrize("c,f32", [(64, False), (64, True), (128, False), (48, False), (48, True)])
 def test_conv_and_convnext(gpu, orc, shells, tmp_path, c, f32):
+    """sparse_submconv and sparse_convnext in a ggml graph: C = 64 and 128 on the matrix cores, 48
+    on the VALU kernel (on F16-rounded input too), and --f32."""
     coords = shells.sphere_shell(40, 20.0, 12.0, 14.0)
-    write_conv_case(str(tmp_path), orc, coords, c, seed=c)
+    write_conv_case(str(tmp_path), orc, coords, c, seed=c, cast_f32=f32)
     args = [os.path.join(BIN, "sparse_conv_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0"]
     out = _run(args + (["--f32"] if f32 else []))
     assert _val(out, "nbr_exact") == 1
     conv, block = _val(out, "conv_out"), _val(out, "block_out")
-    mfma = not f32 and c % 64 == 0
-    tol = 1e-3 if mfma else 1e-5
-    assert conv < tol and block < tol, (conv, block)
-
-
-def test_conv_matches_rounded_features(gpu, orc, shells, tmp_path):
-    """On the matrix-core path the only difference from the closed form is the features'
-    rounding to F16: against the oracle fed F16-rounded features it agrees to fp32 accumulation."""
-    coords = shells.sphere_shell(40, 20.0, 12.0, 14.0)
-    write_conv_case(str(tmp_path), orc, coords, 64, seed=7)
-    os.replace(tmp_path / "conv_out16.npy", tmp_path / "conv_out.npy")
-    out = _run([os.path.join(BIN, "sparse_conv_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0"])
-    assert _val(out, "conv_out") < 2e-5
+    print(f"c={c} f32={f32} conv rel={conv:.3e} block rel={block:.3e}", flush=True)
+    assert conv < TOL_CONV and block < TOL_BLOCK_F16, (conv, block)
 
 
 @pytest.mark.parametrize("cin,cout,ext,f32", [(64, 32, False, False), (64, 32, True, False),
                                               (128, 64, False, False), (128, 64, True, True)])
 def test_c2s(gpu, orc, shells, tmp_path, cin, cout, ext, f32):
     coords = shells.random_distinct_voxels(700, 14, cin + cout)
-    write_c2s_case(str(tmp_path), orc, coords, cin, cout, seed=cin + cout, ext=ext)
+    write_c2s_case(str(tmp_path), orc, coords, cin, cout, seed=cin + cout, ext=ext, cast_f32=f32)
     args = [os.path.join(BIN, "c2s_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0"]
     out = _run(args + (["--ext"] if ext else []) + (["--f32"] if f32 else []))
     assert _val(out, "coords_exact") == 1
     assert _val(out, "mask_exact") == 1
-    tol = 1e-5 if f32 else 1e-3
-    assert _val(out, "feats") < tol
+    err = _val(out, "feats")
+    print(f"c2s {cin}->{cout} ext={ext} f32={f32} rel={err:.3e}", flush=True)
+    assert err < TOL_BLOCK_F16
 
 
 # ---- the device-resident decoders (shape_decode, shape_upsample, tex_decode) ----------------------
 def _decoder_case(tmp_path, orc, shells, out_ch, seed):
     from trellis_cpp_amd.gguf_writer import write as write_gguf
-    from host_cases import decoder_params, stored
+    from host_cases import decoder_params, stored, stored_types
     rng = np.random.default_rng(seed)
     coords = shells.random_distinct_voxels(200, 10, seed)
     latent = rng.standard_normal((len(coords), 32)).astype(np.float32)
@@ -97,20 +98,21 @@ def _decoder_case(tmp_path, orc, shells, out_ch, seed):
     write_gguf(str(tmp_path / f"model{out_ch}.gguf"), p)
     np.save(tmp_path / "latent.npy", latent)
     np.save(tmp_path / "coords.npy", np.ascontiguousarray(coords, np.int32))
-    return coords, latent, stored(p), stages
+    return coords, latent, stored(p), stages, stored_types(p)
 
 
 def test_shape_decode_fp32(gpu, orc, shells, tmp_path):
     """Predicted masks, fp32 paths: masks, children and output against the oracle decoder."""
-    coords, latent, q, stages = _decoder_case(tmp_path, orc, shells, 7, seed=11)
+    coords, latent, q, stages, wt = _decoder_case(tmp_path, orc, shells, 7, seed=11)
     _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model7.gguf"), str(tmp_path), "0", "--f32"])
-    ref, rcoords, rmasks = orc.decode_unet(latent, coords, q, stages, 7)
+    (ref, rcoords, rmasks), floor = rounding_noise_floor(
+        orc, lambda: orc.decode_unet(latent, coords, q, stages, 7, wt=wt, cast_f32=True))
     assert np.array_equal(np.load(tmp_path / "coords_out.npy"), rcoords)
     for s, m in enumerate(rmasks):
         assert np.array_equal(np.load(tmp_path / f"subs_out_{s}.npy"), m), s
     err = orc.rel_err(np.load(tmp_path / "out.npy"), ref)
-    print(f"shape_decode fp32 rel={err:.3e} M={len(rcoords)}", flush=True)
-    assert err < 1e-5
+    print(f"shape_decode fp32 rel={err:.3e} floor={floor:.3e} M={len(rcoords)}", flush=True)
+    assert err < max(TOL_BLOCK_F16, 1.5 * floor)
     _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model7.gguf"), str(tmp_path), "0", "--f32",
           "--upsample"])
     assert np.array_equal(np.load(tmp_path / "coords_out.npy"), rcoords)
@@ -118,7 +120,7 @@ def test_shape_decode_fp32(gpu, orc, shells, tmp_path):
 
 def test_tex_decode_guided(gpu, orc, shells, tmp_path):
     """Masks given (the texture decoder's route), matrix-core paths with 16-bit activations."""
-    coords, latent, q, stages = _decoder_case(tmp_path, orc, shells, 6, seed=12)
+    coords, latent, q, stages, wt = _decoder_case(tmp_path, orc, shells, 6, seed=12)
     rng = np.random.default_rng(5)
     guide, n = [], len(coords)
     for _ in stages:
@@ -127,13 +129,13 @@ def test_tex_decode_guided(gpu, orc, shells, tmp_path):
     for s, g in enumerate(guide):
         np.save(tmp_path / f"subs_{s}.npy", g)
     _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model6.gguf"), str(tmp_path), "0", "--tex"])
-    ref, rcoords, _ = orc.decode_unet(latent, coords, q, stages, 6, guide)
+    (ref, rcoords, _), floor = rounding_noise_floor(
+        orc, lambda: orc.decode_unet(latent, coords, q, stages, 6, guide, wt=wt))
     out = np.load(tmp_path / "out.npy")
     assert out.shape == ref.shape
     err = orc.rel_err(out, ref)
-    print(f"tex_decode 16-bit rel={err:.3e} M={len(rcoords)}", flush=True)
-    # every conv and linear of 3 stages rounds its input to F16 (measured 1.1e-3)
-    assert err < 3e-3
+    print(f"tex_decode 16-bit rel={err:.3e} floor={floor:.3e} M={len(rcoords)}", flush=True)
+    assert err < max(TOL_BLOCK_F16, 1.5 * floor)
 
 
 @pytest.mark.parametrize("channels", [None, (128, 64)])
@@ -143,7 +145,10 @@ def test_tex_decode_bf16_decoder_workload(gpu, orc, shells, tmp_path, channels):
     decoder fed the same bf16-rounded weights; every conv and linear rounds its input to bf16 (a
     2^-8 relative step, so the bar is looser than the F16 case's). channels (128, 64): one stage
     whose C2S conv1 stores its octants into the children and whose conv2 adds the skip as it
-    stores, and the fused LayerNorm + output head over 64 channels."""
+    stores, and the fused LayerNorm + output head over 64 channels. The oracle rounds every
+    product's input to bf16 where the device does; with bf16's 2^-8 step the flips between two
+    correct evaluation orders reach 3e-3 (one stage) to 8e-3 (three stages), so the bar is 1.5x
+    that floor, measured here."""
     from trellis_cpp_amd.gguf_writer import write as write_gguf
     w = shells.decoder_workload("decoder-shells16-c64")
     if channels is not None:
@@ -161,10 +166,40 @@ def test_tex_decode_bf16_decoder_workload(gpu, orc, shells, tmp_path, channels):
     q = {k: (shells.round_to(v, "bf16") if v.ndim >= 2 else v) for k, v in p.items()}
     stages = [([f"blocks.{s}.{j}" for j in range(w.blocks)], (f"blocks.{s}.{w.blocks}", ci, co))
               for s, (ci, co) in enumerate(zip(w.channels[:-1], w.channels[1:]))]
-    ref, rcoords, _ = orc.decode_unet(w.latent, w.coords, q, stages, w.out_ch, w.masks)
+    wt = {k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()}
+    (ref, rcoords, _), floor = rounding_noise_floor(
+        orc, lambda: orc.decode_unet(w.latent, w.coords, q, stages, w.out_ch, w.masks, wt=wt))
     assert len(rcoords) == w.counts[-1]
     out = np.load(tmp_path / "out.npy")
     assert out.shape == ref.shape
     err = orc.rel_err(out, ref)
-    print(f"tex_decode bf16 rel={err:.3e} M={len(rcoords)}", flush=True)
-    assert err < 3e-2
+    print(f"tex_decode bf16 rel={err:.3e} floor={floor:.3e} M={len(rcoords)}", flush=True)
+    assert err < 1.5 * floor
+
+
+def test_decoder_zero_weight_closed_form(gpu, shells, tmp_path):
+    """tex_decode on a model whose conv and MLP weights are zero (F32), against the closed form
+    that case reduces to (host_cases.decode_closed_form: from_latent, each block's mlp.2 bias, the
+    C2S skip's octant slices and child order, the head's LayerNorm with eps 1e-5 and no affine):
+    the decoder's stage structure checked without the oracle decoder."""
+    from trellis_cpp_amd.gguf_writer import write as write_gguf
+    from host_cases import decode_closed_form, zero_weight_decoder
+    rng = np.random.default_rng(31)
+    coords = shells.random_distinct_voxels(300, 10, 31)
+    latent = rng.standard_normal((300, 8)).astype(np.float32)
+    p, stages = zero_weight_decoder(rng, (32, 16, 8), (2, 1))
+    write_gguf(str(tmp_path / "model.gguf"), p, dtypes={k: "f32" for k in p})
+    np.save(tmp_path / "latent.npy", latent)
+    np.save(tmp_path / "coords.npy", np.ascontiguousarray(coords, np.int32))
+    guide, n = [], len(coords)
+    for s, _ in enumerate(stages):
+        guide.append((rng.random(8 * n) < 0.4).astype(np.uint8))
+        np.save(tmp_path / f"subs_{s}.npy", guide[-1])
+        n = int(guide[-1].sum())
+    _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0", "--tex"])
+    ref, rc = decode_closed_form(latent, coords, p, stages, guide)
+    out = np.load(tmp_path / "out.npy")     # the children's rows in the closed form's order
+    assert out.shape == ref.shape
+    err = np.abs(out - ref).max() / np.abs(ref).max()
+    print(f"zero-weight decoder rel={err:.3e} M={len(rc)}", flush=True)
+    assert err < 1e-5

@@ -9,6 +9,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from host_cases import decode_closed_form, zero_weight_decoder
+
 
 # ------------------------------------------------------------------------------------------
 # Rulebook
@@ -357,3 +359,100 @@ def test_c2s_block_vs_loops(orc, shells):
     h2 = p["c2s.conv2.bias"].astype(np.float64) + sum(hn_pad[nbr2[t]] @ w2[:, t, :].T for t in range(27))
     assert nbr2.shape[1] == m
     assert np.allclose(out, h2 + np.array(skips), atol=1e-9)
+
+
+def test_rounding_matches_library_conversions(orc):
+    """round_f16 / round_bf16 against numpy's float16 and torch's bfloat16 conversions of the
+    float32 values (round to nearest even), including ties, overflow, subnormals and NaN."""
+    rng = np.random.default_rng(21)
+    x = np.concatenate([rng.standard_normal(5000) * 10.0 ** rng.integers(-8, 6, 5000),
+                        [0.0, -0.0, 65504.0, 65520.0, 1e5, -1e5, 6e-8, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11,
+                         1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, np.inf, -np.inf, np.nan]]).astype(np.float32)
+    f16 = orc.round_f16(x)
+    assert np.array_equal(f16, x.astype(np.float16).astype(np.float64), equal_nan=True)
+    bf = orc.round_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).to(torch.float64).numpy()
+    assert np.array_equal(bf, ref, equal_nan=True)
+    assert orc.round_f16(np.float32(1.0 + 2.0 ** -11)) == 1.0              # tie to even
+    assert orc.round_bf16(np.float32(1.0 + 3 * 2.0 ** -8)) == 1.0 + 2.0 ** -6
+
+
+def test_act_round_rule(orc):
+    """ggml's mul_mat input rounding: F16/BF16 weights round to their type, F32 weights do not;
+    g_sparse_cast_f32 lifts it for F16 conv weights only (w32 casts F16, sparse.cpp:16-19)."""
+    x = np.float32(1.0 + 2.0 ** -10 + 2.0 ** -13)   # not representable in F16 or BF16
+    assert orc.act_round(x, "f16") == orc.round_f16(x) != x
+    assert orc.act_round(x, "bf16") == orc.round_bf16(x) != x
+    assert orc.act_round(x, "f32") == x and orc.act_round(x, None) == x
+    assert orc.act_round(x, "f16", conv_weight=True, cast_f32=True) == x
+    assert orc.act_round(x, "f16", conv_weight=False, cast_f32=True) == orc.round_f16(x)
+    assert orc.act_round(x, "bf16", conv_weight=True, cast_f32=True) == orc.round_bf16(x)
+
+
+def test_convnext_block_rounds_each_product_input(orc, shells):
+    """With wt, the block equals the same block on inputs rounded at the three products: the conv
+    (feats), mlp.0 (the LN + affine output) and mlp.2 (the SiLU output)."""
+    rng = np.random.default_rng(14)
+    coords = shells.random_distinct_voxels(150, 7, 14)
+    c = 16
+    x = rng.standard_normal((150, c)).astype(np.float32)
+    p = _block_params(rng, c)
+    wt = {k: ("f16" if v.ndim >= 2 else "f32") for k, v in p.items()}
+    nbr = orc.neighbor_table(coords)
+    out = orc.convnext_block(x, nbr, p, "blk", wt)
+    T = lambda a: torch.from_numpy(np.asarray(a)).double()
+    r16 = lambda a: T(np.asarray(a, np.float64).astype(np.float32).astype(np.float16).astype(np.float64))
+    h = T(orc.subm_conv_f64(r16(x).numpy().astype(np.float32), nbr, p["blk.conv.weight"], p["blk.conv.bias"]))
+    h = F.layer_norm(h, (c,), T(p["blk.norm.weight"]), T(p["blk.norm.bias"]), 1e-6)
+    h = F.silu(F.linear(r16(h), T(p["blk.mlp.0.weight"]), T(p["blk.mlp.0.bias"])))
+    h = F.linear(r16(h), T(p["blk.mlp.2.weight"]), T(p["blk.mlp.2.bias"])) + T(x)
+    assert np.allclose(out, h.numpy(), atol=1e-10)
+    assert not np.allclose(out, orc.convnext_block(x, nbr, p, "blk"), atol=1e-6)   # the rounding shows
+
+
+def test_decode_unet_zero_weight_closed_form(orc, shells):
+    """decode_unet pinned by the closed form its zero-weight case reduces to: the stage loop (2 and
+    1 blocks), the C2S skip's octant slice and repeat, the guide masks' routing and child order,
+    and the head's LayerNorm (eps 1e-5, no affine). A planted eps of 1e-6, a dropped block or a
+    swapped octant slice moves the closed form far beyond the bar."""
+    rng = np.random.default_rng(31)
+    coords = shells.random_distinct_voxels(60, 6, 31)
+    latent = rng.standard_normal((60, 8)).astype(np.float32)
+    p, stages = zero_weight_decoder(rng, (32, 16, 8), (2, 1))
+    guide, n = [], 60
+    for _ in stages:
+        guide.append((rng.random(8 * n) < 0.4).astype(np.uint8))
+        n = int(guide[-1].sum())
+    out, coords_out, masks = orc.decode_unet(latent, coords, p, stages, 6, guide)
+    ref, rc = decode_closed_form(latent, coords, p, stages, guide)
+    assert np.array_equal(coords_out, rc)
+    assert all(np.array_equal(m, g) for m, g in zip(masks, guide))
+    scale = np.abs(ref).max()
+    assert np.abs(out - ref).max() < 1e-5 * scale
+    far = lambda r: np.abs(r[0] - ref).max() > 1e-3 * scale
+    # (an earlier stage's block bias reaches the head as a constant per child, which the head's
+    # LayerNorm removes: the skip of the later stage repeats each element of its slice)
+    q = dict(p)
+    q[stages[1][0][0] + ".mlp.2.bias"] = np.zeros_like(p[stages[1][0][0] + ".mlp.2.bias"])
+    assert far(decode_closed_form(latent, coords, q, stages, guide))                 # a block dropped
+    assert far(decode_closed_form(latent, coords, p, stages, guide, eps=1e-6))       # the head's eps
+    assert far(decode_closed_form(latent, coords, p, stages, guide, octant_shift=1))  # the skip's slice
+
+
+def test_rounding_noise_floor_helper(orc, shells):
+    """The decoder tests' noise floor: nonzero where products round (flips appear), zero where
+    nothing rounds, and the oracle's rounding rule restored afterwards."""
+    from host_cases import rounding_noise_floor
+    rng = np.random.default_rng(15)
+    coords = shells.random_distinct_voxels(150, 7, 15)
+    x = rng.standard_normal((150, 16)).astype(np.float32)
+    p = _block_params(rng, 16)
+    nbr = orc.neighbor_table(coords)
+    wt = {k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()}
+    exact = orc.act_round
+    out, floor = rounding_noise_floor(orc, lambda: orc.convnext_block(x, nbr, p, "blk", wt), rel=1e-4)
+    assert orc.act_round is exact
+    assert np.array_equal(out, orc.convnext_block(x, nbr, p, "blk", wt))
+    assert 0 < floor < 1e-2
+    _, none = rounding_noise_floor(orc, lambda: orc.convnext_block(x, nbr, p, "blk"), rel=1e-4)
+    assert none == 0

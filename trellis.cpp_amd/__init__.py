@@ -73,7 +73,7 @@ def lib() -> ctypes.CDLL:
                                    c_vp, c_int, c_int, c_vp]
     L.tsp_subm_conv3x3_ex.restype = c_int
     L.tsp_subm_conv3x3_ex.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int,
-                                      c_vp, c_int, c_int, c_int, c_vp]
+                                      c_vp, c_int, c_int, c_int, c_vp, c_vp]
     L.tsp_conv_plan_bytes.restype = c_sz
     L.tsp_conv_plan_bytes.argtypes = [c_i64]
     L.tsp_conv_plan_build.restype = c_int
@@ -204,9 +204,10 @@ def _check_nbr(nbr, n: int, device):
 
 
 def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", out=None,
-                 zero_pad: bool = False, stream=None):
+                 zero_pad: bool = False, row0=None, stream=None):
     """feats [N,Ci], nbr int32 [27*N], weight [Co,27,Ci], bias f32 [Co] -> out [N,Co].
-    zero_pad: absent taps read an exact zero row instead of 0 * feats[0]."""
+    zero_pad: absent taps read an exact zero row instead of 0 * feats[0]; row0 (float32 [Ci]):
+    the unrounded row 0 the features were rounded from, whose 0 * row0 is the padding row."""
     torch = _torch()
     if feats.dim() != 2:
         raise ValueError("feats must be [N, Ci]")
@@ -217,18 +218,21 @@ def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", o
     _check_nbr(nbr, n, feats.device)
     if bias.dtype != torch.float32 or bias.numel() != co:
         raise ValueError("bias must be float32 [Co]")
+    if row0 is not None and (row0.dtype != torch.float32 or row0.numel() != ci):
+        raise ValueError("row0 must be float32 [Ci]")
     odt = out_dtype or feats.dtype
     if out is None:
         out = torch.empty((n, co), dtype=odt, device=feats.device)
     else:
         _check_out(out, n, co, odt, feats.device)
-    _require_cuda(feats, nbr, weight, bias, out)
+    _require_cuda(feats, nbr, weight, bias, out, row0)
     f, w, b = feats.contiguous(), weight.contiguous(), bias.contiguous()
+    r0 = row0.contiguous() if row0 is not None else None
     _check("tsp_subm_conv3x3_ex",
            lib().tsp_subm_conv3x3_ex(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr), _ptr(w),
                                      dtype_code(w.dtype), _ptr(b), co, _ptr(out),
                                      dtype_code(out.dtype), ALGO[algo], 1 if zero_pad else 0,
-                                     _stream(stream)))
+                                     _ptr(r0), _stream(stream)))
     return out
 
 

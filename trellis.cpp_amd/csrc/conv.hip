@@ -37,7 +37,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
     const typename Elem<FDT>::storage* __restrict__ feats, int64_t n, int ci,
     const int32_t* __restrict__ nbr, int taps,
     const typename Elem<WDT>::storage* __restrict__ weight, const float* __restrict__ bias,
-    int co, typename Elem<ODT>::storage* __restrict__ out, bool zero_pad) {
+    int co, typename Elem<ODT>::storage* __restrict__ out, PadRow pad) {
     __shared__ float sA[NB_K][NB_M + 4];
     __shared__ float sB[NB_K][NB_N + 4];
     __shared__ int32_t sRow[NB_M];
@@ -48,10 +48,11 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
     const int co0 = blockIdx.y * NB_N;
     const int32_t sentinel = (int32_t)n;
     // whether the padding row 0 * feats[0] (sparse.cpp:81-85) holds a NaN: then no tap is skipped
-    // (an exact zero padding row, zero_pad, never does)
+    // (an exact zero padding row, pad.zero, never does; with pad.row0 that f32 row is the source)
     bool row0_bad = false;
-    if (nbr && !zero_pad)
-        for (int k = tid; k < ci; k += NB_THREADS) row0_bad |= !__builtin_isfinite(Elem<FDT>::load(feats, k));
+    if (nbr && !pad.zero)
+        for (int k = tid; k < ci; k += NB_THREADS)
+            row0_bad |= !__builtin_isfinite(pad.row0 ? pad.row0[k] : Elem<FDT>::load(feats, k));
     row0_bad = __syncthreads_or(row0_bad);
 
     float acc[4][4];
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
                     // padding row 0 * feats[0] (sparse.cpp:81-85)
                     if (k < ci) {
                         if ((uint32_t)src < (uint32_t)n) v = Elem<FDT>::load(feats, (int64_t)src * ci + k);
-                        else if (row0_bad) v = 0.f * Elem<FDT>::load(feats, k);
+                        else if (row0_bad) v = 0.f * (pad.row0 ? pad.row0[k] : Elem<FDT>::load(feats, k));
                     }
                     sA[kk + j][r] = v;
                 }
@@ -138,7 +139,7 @@ template <bool BF16, int BN, int WAVES, int ODT>
 __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
-    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, int taps, bool zero_pad) {
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, int taps, PadRow pad) {
     constexpr int NT = WAVES * 64;
     constexpr int BM = 64 * WAVES;
     constexpr int CB = BN / 32;                       // 32-wide column blocks per wave
@@ -169,14 +170,21 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
     // Taps that some voxel of the workgroup has (wave ballots, OR in LDS). Absent taps read the
     // padding row 0 * feats[0] (sparse.cpp:81-85): zeros, unless row 0 holds an Inf or a NaN --
     // then every tap counts, as the padding row makes the sums of absent taps NaN. An exact zero
-    // padding row (zero_pad) reads zeros.
+    // padding row (pad.zero) reads zeros; with pad.row0 the padding row is 0 * that f32 row,
+    // rounded (a NaN where it is not finite, else 0).
     if (tid == 0) sMask = 0;
     bool row0_bad = false;
-    for (int k = tid * 8; k < ci && !zero_pad; k += NT * 8) {
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(feats + k);
-        const u32x4_t z = zero_times16<BF16>(v);
+    if (!pad.zero) {
+        if (pad.row0) {
+            for (int k = tid; k < ci; k += NT) row0_bad |= !__builtin_isfinite(pad.row0[k]);
+        } else {
+            for (int k = tid * 8; k < ci; k += NT * 8) {
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(feats + k);
+                const u32x4_t z = zero_times16<BF16>(v);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) row0_bad |= (z[e] & 0x7fff7fffu) != 0;
+                for (int e = 0; e < 4; ++e) row0_bad |= (z[e] & 0x7fff7fffu) != 0;
+            }
+        }
     }
     row0_bad = __syncthreads_or(row0_bad);
     {
@@ -231,8 +239,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_conv_mfma(
                     if ((uint32_t)r[rb] < (uint32_t)n) {   // sentinel N -> the padding row
                         a[rb][s] = *reinterpret_cast<const u32x4_t*>(
                             feats + (int64_t)r[rb] * ci + kc + s * 16 + g * 8);
-                    } else if (zero_pad) {
+                    } else if (pad.zero || !row0_bad) {
                         a[rb][s] = u32x4_t{0, 0, 0, 0};
+                    } else if (pad.row0) {
+                        // 16-bit NaN where the f32 source is not finite (either type's quiet NaN
+                        // pattern 0x7FC0 / 0x7E00), zero elsewhere
+                        constexpr uint32_t kNaN = BF16 ? 0x7FC0u : 0x7E00u;
+                        u32x4_t z;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int k = kc + s * 16 + g * 8 + 2 * e;
+                            z[e] = (__builtin_isfinite(pad.row0[k]) ? 0u : kNaN) |
+                                   ((__builtin_isfinite(pad.row0[k + 1]) ? 0u : kNaN) << 16);
+                        }
+                        a[rb][s] = z;
                     } else {
                         a[rb][s] = zero_times16<BF16>(
                             *reinterpret_cast<const u32x4_t*>(feats + kc + s * 16 + g * 8));
@@ -323,23 +343,23 @@ epilogue:
 // ---------------------------------------------------------------------------------------------
 template <int FDT, int WDT, int ODT>
 int launch_narrow(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
-                  const float* bias, int co, void* out, hipStream_t s, bool zero_pad) {
+                  const float* bias, int co, void* out, hipStream_t s, PadRow pad) {
     dim3 grid((unsigned)ceil_div(n, NB_M), (unsigned)ceil_div(co, NB_N));
     hipLaunchKernelGGL((k_conv_narrow<FDT, WDT, ODT>), grid, dim3(NB_THREADS), 0, s,
                        reinterpret_cast<const typename Elem<FDT>::storage*>(feats), n, ci, nbr,
                        nbr ? kTaps : 1, reinterpret_cast<const typename Elem<WDT>::storage*>(weight),
-                       bias, co, reinterpret_cast<typename Elem<ODT>::storage*>(out), zero_pad);
+                       bias, co, reinterpret_cast<typename Elem<ODT>::storage*>(out), pad);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
 
 template <int FDT, int WDT>
 int narrow_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
-               const void* weight, const float* bias, int co, void* out, hipStream_t s, bool zp) {
+               const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad) {
     switch (odt) {
-        case TSP_F32: return launch_narrow<FDT, WDT, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s, zp);
-        case TSP_F16: return launch_narrow<FDT, WDT, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s, zp);
-        case TSP_BF16: return launch_narrow<FDT, WDT, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s, zp);
+        case TSP_F32: return launch_narrow<FDT, WDT, TSP_F32>(feats, n, ci, nbr, weight, bias, co, out, s, pad);
+        case TSP_F16: return launch_narrow<FDT, WDT, TSP_F16>(feats, n, ci, nbr, weight, bias, co, out, s, pad);
+        case TSP_BF16: return launch_narrow<FDT, WDT, TSP_BF16>(feats, n, ci, nbr, weight, bias, co, out, s, pad);
     }
     set_error("tsp_subm_conv3x3: bad out dtype %d", odt);
     return TSP_ERR_INVALID;
@@ -347,19 +367,19 @@ int narrow_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr
 
 int dispatch_narrow(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci,
                     const int32_t* nbr, const void* weight, const float* bias, int co, void* out,
-                    hipStream_t s, bool zp = false) {
-    if (fdt == TSP_F32 && wdt == TSP_F32) return narrow_out<TSP_F32, TSP_F32>(odt, feats, n, ci, nbr, weight, bias, co, out, s, zp);
-    if (fdt == TSP_F32 && wdt == TSP_F16) return narrow_out<TSP_F32, TSP_F16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, zp);
-    if (fdt == TSP_F32 && wdt == TSP_BF16) return narrow_out<TSP_F32, TSP_BF16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, zp);
-    if (fdt == TSP_F16 && wdt == TSP_F16) return narrow_out<TSP_F16, TSP_F16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, zp);
-    if (fdt == TSP_BF16 && wdt == TSP_BF16) return narrow_out<TSP_BF16, TSP_BF16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, zp);
+                    hipStream_t s, PadRow pad = {}) {
+    if (fdt == TSP_F32 && wdt == TSP_F32) return narrow_out<TSP_F32, TSP_F32>(odt, feats, n, ci, nbr, weight, bias, co, out, s, pad);
+    if (fdt == TSP_F32 && wdt == TSP_F16) return narrow_out<TSP_F32, TSP_F16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, pad);
+    if (fdt == TSP_F32 && wdt == TSP_BF16) return narrow_out<TSP_F32, TSP_BF16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, pad);
+    if (fdt == TSP_F16 && wdt == TSP_F16) return narrow_out<TSP_F16, TSP_F16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, pad);
+    if (fdt == TSP_BF16 && wdt == TSP_BF16) return narrow_out<TSP_BF16, TSP_BF16>(odt, feats, n, ci, nbr, weight, bias, co, out, s, pad);
     set_error("tsp_subm_conv3x3: unsupported dtype pair feats=%d weight=%d", fdt, wdt);
     return TSP_ERR_UNSUPPORTED;
 }
 
 template <bool BF16, int BN, int WAVES, int ODT>
 int launch_gather(const void* feats, int64_t n, int ci, const int32_t* nbr, int taps,
-                  const void* weight, const float* bias, int co, void* out, hipStream_t s, bool zp) {
+                  const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad) {
     constexpr int BM = 64 * WAVES;
     const int64_t n_tiles = ceil_div(n, BM);
     const int n_ctiles = co / BN;
@@ -368,17 +388,17 @@ int launch_gather(const void* feats, int64_t n, int ci, const int32_t* nbr, int 
     hipLaunchKernelGGL((k_conv_mfma<BF16, BN, WAVES, ODT>), dim3((unsigned)(per_xcd * 8)),
                        dim3(WAVES * 64), 0, s, reinterpret_cast<const uint16_t*>(feats), n, ci,
                        nbr, reinterpret_cast<const uint16_t*>(weight), bias, co, out, n_tiles,
-                       n_ctiles, per_xcd, taps, zp);
+                       n_ctiles, per_xcd, taps, pad);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
 
 template <bool BF16, int BN>
 int gather_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr, int taps,
-               const void* weight, const float* bias, int co, void* out, hipStream_t s, bool zp) {
-    if (odt == TSP_F32) return launch_gather<BF16, BN, 4, TSP_F32>(feats, n, ci, nbr, taps, weight, bias, co, out, s, zp);
-    if (BF16 && odt == TSP_BF16) return launch_gather<BF16, BN, 4, TSP_BF16>(feats, n, ci, nbr, taps, weight, bias, co, out, s, zp);
-    if (!BF16 && odt == TSP_F16) return launch_gather<BF16, BN, 4, TSP_F16>(feats, n, ci, nbr, taps, weight, bias, co, out, s, zp);
+               const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad) {
+    if (odt == TSP_F32) return launch_gather<BF16, BN, 4, TSP_F32>(feats, n, ci, nbr, taps, weight, bias, co, out, s, pad);
+    if (BF16 && odt == TSP_BF16) return launch_gather<BF16, BN, 4, TSP_BF16>(feats, n, ci, nbr, taps, weight, bias, co, out, s, pad);
+    if (!BF16 && odt == TSP_F16) return launch_gather<BF16, BN, 4, TSP_F16>(feats, n, ci, nbr, taps, weight, bias, co, out, s, pad);
     set_error("tsp_subm_conv3x3: MFMA path writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
@@ -387,13 +407,13 @@ int gather_out(int odt, const void* feats, int64_t n, int ci, const int32_t* nbr
 // is a linear layer.
 int dispatch_gather(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                     int taps, const void* weight, const float* bias, int co, void* out,
-                    hipStream_t s, bool zp = false) {
+                    hipStream_t s, PadRow pad = {}) {
     const bool bn128 = co % 128 == 0;
     if (fdt == TSP_BF16)
-        return bn128 ? gather_out<true, 128>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, zp)
-                     : gather_out<true, 64>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, zp);
-    return bn128 ? gather_out<false, 128>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, zp)
-                 : gather_out<false, 64>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, zp);
+        return bn128 ? gather_out<true, 128>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, pad)
+                     : gather_out<true, 64>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, pad);
+    return bn128 ? gather_out<false, 128>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, pad)
+                 : gather_out<false, 64>(odt, feats, n, ci, nbr, taps, weight, bias, co, out, s, pad);
 }
 
 // MFMA kernels: 16-bit feats and weights of one dtype, out f32 or that dtype, ci % 32 == 0,
@@ -423,7 +443,7 @@ using namespace tsp;
 extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
                                    const int32_t* d_nbr, const void* d_weight, int weight_dtype,
                                    const float* d_bias, int co, void* d_out, int out_dtype, int algo,
-                                   int flags, void* stream) {
+                                   int flags, const float* d_row0, void* stream) {
     clear_error();
     TSP_CONV_COMMON_CHECKS("tsp_subm_conv3x3");
     TSP_REQUIRE(dtype_valid(feat_dtype) && dtype_valid(weight_dtype) && dtype_valid(out_dtype),
@@ -437,9 +457,9 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
                 "tsp_subm_conv3x3: null pointer");
     TSP_REQUIRE(d_out != d_feats, TSP_ERR_INVALID, "tsp_subm_conv3x3: out aliases feats");
     hipStream_t s = as_stream(stream);
-    const bool zp = (flags & TSP_CONV_ZERO_PAD) != 0;
     PadRow pad;
-    pad.zero = zp;
+    pad.zero = (flags & TSP_CONV_ZERO_PAD) != 0;
+    pad.row0 = pad.zero ? nullptr : d_row0;
     const bool eligible =
         mfma_eligible(feat_dtype, weight_dtype, out_dtype, ci, co, d_feats, d_weight, d_out);
     if (algo == TSP_ALGO_MFMA || algo == TSP_ALGO_MFMA_GATHER) {
@@ -450,15 +470,15 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
     }
     if (algo == TSP_ALGO_MFMA_GATHER)
         return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, kTaps, d_weight,
-                               d_bias, co, d_out, s, zp);
+                               d_bias, co, d_out, s, pad);
     if (algo == TSP_ALGO_AUTO && eligible && !halo_fits(n, ci))
         return dispatch_gather(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, kTaps, d_weight,
-                               d_bias, co, d_out, s, zp);
+                               d_bias, co, d_out, s, pad);
     if (algo == TSP_ALGO_MFMA || (algo == TSP_ALGO_AUTO && eligible))
         return halo_conv_launch(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, nullptr, d_weight,
                                 d_bias, co, d_out, s, OctantScatter{}, SkipAdd{}, pad);
     return dispatch_narrow(feat_dtype, weight_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight,
-                           d_bias, co, d_out, s, zp);
+                           d_bias, co, d_out, s, pad);
 }
 
 extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, int ci,
@@ -466,7 +486,7 @@ extern "C" int tsp_subm_conv3x3(const void* d_feats, int feat_dtype, int64_t n, 
                                 const float* d_bias, int co, void* d_out, int out_dtype, int algo,
                                 void* stream) {
     return tsp_subm_conv3x3_ex(d_feats, feat_dtype, n, ci, d_nbr, d_weight, weight_dtype, d_bias, co,
-                               d_out, out_dtype, algo, 0, stream);
+                               d_out, out_dtype, algo, 0, nullptr, stream);
 }
 
 extern "C" size_t tsp_conv_plan_bytes(int64_t n) { return n < 0 ? 0 : halo_plan_bytes(n); }

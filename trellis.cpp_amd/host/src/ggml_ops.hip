@@ -18,9 +18,11 @@ inline unsigned grid_for(int64_t total) {
 }
 
 template <int DT> struct Io;
+// ld / st: element i of a buffer of the type; rnd: v rounded to the type (as a float)
 template <> struct Io<TSP_F32> {
     static __device__ float ld(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
     static __device__ void st(void* p, int64_t i, float v) { static_cast<float*>(p)[i] = v; }
+    static __device__ float rnd(float v) { return v; }
 };
 template <> struct Io<TSP_F16> {
     static __device__ float ld(const void* p, int64_t i) {
@@ -29,6 +31,7 @@ template <> struct Io<TSP_F16> {
     static __device__ void st(void* p, int64_t i, float v) {
         static_cast<__half*>(p)[i] = __float2half_rn(v);
     }
+    static __device__ float rnd(float v) { return __half2float(__float2half_rn(v)); }
 };
 template <> struct Io<TSP_BF16> {
     static __device__ float ld(const void* p, int64_t i) {
@@ -42,6 +45,11 @@ template <> struct Io<TSP_BF16> {
         if ((u & 0x7fffffffu) > 0x7f800000u) r = (uint16_t)((u >> 16) | 0x40u);
         else r = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
         static_cast<uint16_t*>(p)[i] = r;
+    }
+    static __device__ float rnd(float v) {
+        const uint32_t u = __float_as_uint(v);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return v;
+        return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
     }
 };
 
@@ -269,6 +277,11 @@ __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x
             for (int off = L / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
         }
         const float rstd = 1.0f / sqrtf(q / (float)C + eps);
+        // the normalised row rounded to the weights' type, as ggml's mul_mat rounds its input
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j][e] = Io<WDT>::rnd(v[j][e] * rstd);
         float acc[kHeadMaxCo];
 #pragma unroll
         for (int o = 0; o < kHeadMaxCo; ++o) {
@@ -276,7 +289,7 @@ __global__ __launch_bounds__(256) void k_norm_linear(const float* __restrict__ x
 #pragma unroll
             for (int j = 0; j < V; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[o] += v[j][e] * rstd * wv[o][j][e];
+                for (int e = 0; e < 4; ++e) acc[o] += v[j][e] * wv[o][j][e];
         }
         if constexpr (L == 16) {
             // Reduce-scatter of the 8 sums over the row's 16 lanes in 8 DPP moves: each step

@@ -759,11 +759,25 @@ static void run_node(ggml_tensor* t, hipStream_t s) {
                 "norm");
             break;
         }
-        case GGML_OP_MUL_MAT:
-            lib(tsp_linear(b->data, tsp_dtype_of(b->type), b->ne[1], (int)b->ne[0], a->data,
-                           tsp_dtype_of(a->type), nullptr, (int)a->ne[1], t->data, TSP_F32, s),
+        case GGML_OP_MUL_MAT: {
+            // F16 / BF16 weights take their input rounded to their own type (the CPU backend's
+            // vec_dot type), F32 weights the input as it is
+            const int adt = tsp_dtype_of(a->type), bdt = tsp_dtype_of(b->type);
+            const int64_t nb = ggml_nelements(b);
+            const void* x = b->data;
+            int xdt = bdt;
+            DeviceBuffer rounded;
+            if (bdt == TSP_F32 && (adt == TSP_F16 || adt == TSP_BF16) && nb > 0) {
+                rounded = DeviceBuffer((size_t)nb * 2, s);
+                hip_check(launch_convert(b->data, TSP_F32, rounded.get(), adt, nb, s), "mul_mat rounding");
+                x = rounded.get();
+                xdt = adt;
+            }
+            lib(tsp_linear(x, xdt, b->ne[1], (int)b->ne[0], a->data, adt, nullptr, (int)a->ne[1], t->data,
+                           TSP_F32, s),
                 "mul_mat");
             break;
+        }
         case GGML_OP_GET_ROWS:
             hip_check(launch_get_rows(a, static_cast<const int32_t*>(b->data), b->ne[0], t->data, s),
                       "get_rows");

@@ -42,6 +42,11 @@ const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s) {
     return static_cast<const float*>(p);
 }
 
+int act_dtype(int wdt, bool conv_weight) {
+    if (wdt == TSP_F16) return conv_weight && g_sparse_cast_f32 ? TSP_F32 : TSP_F16;
+    return wdt;
+}
+
 // ---- conv --------------------------------------------------------------------------------------
 Conv conv_of(const Model& m, const std::string& prefix) {
     Conv c;
@@ -53,27 +58,32 @@ Conv conv_of(const Model& m, const std::string& prefix) {
     if (ggml_nelements(c.b) != c.co) fail(prefix + ".bias: expected " + std::to_string(c.co) + " elements");
     c.wdt = tgr::tsp_dtype_of(c.w->type);
     if (c.wdt < 0) fail(prefix + ".weight: unsupported tensor type");
-    c.mfma = !g_sparse_cast_f32 && (c.wdt == TSP_F16 || c.wdt == TSP_BF16) && c.ci % 16 == 0 &&
-             c.co % 64 == 0;
+    c.xdt = act_dtype(c.wdt, true);
+    c.mfma = c.xdt != TSP_F32 && c.ci % 16 == 0 && c.co % 64 == 0;
     return c;
 }
 
-// F32 activations are rounded to the weights' 16-bit type for the matrix-core kernel, as ggml's
-// F16 mul_mat rounds its F32 operand (sparse.cpp:74); under g_sparse_cast_f32 or for channel
-// counts the matrix-core tiles do not cover, the fp32 kernel runs on the weights' exact values.
-// The padding row is formed from the unrounded row 0 (sparse.cpp:81-85 pads the F32 input).
+// F32 activations are rounded to c.xdt, as ggml's mul_mat rounds its F32 operand to the weights'
+// type (sparse.cpp:74); the matrix-core kernel runs where the channel counts fit its tiles, the
+// VALU kernel elsewhere (on the rounded input, or under g_sparse_cast_f32 on the F32 input and
+// the weights' exact values). The padding row is formed from the unrounded row 0 (sparse.cpp:81-85
+// pads the F32 input). A caller that passes input already in c.xdt (rounded from F32 as it was
+// written) leaves the padding row to that row 0: the two differ only where a finite F32 value
+// overflows the 16-bit range.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
               float* out, Carve& sc, hipStream_t s, const ConvStores& st) {
     const float* bias = f32_param(c.b, sc, s);
     const int flags = st.zero_pad ? TSP_CONV_ZERO_PAD : 0;
+    const float* row0 = xdt == TSP_F32 && c.xdt != TSP_F32 ? static_cast<const float*>(x) : nullptr;
+    const void* xr = x;
+    if (xdt != c.xdt) {
+        if (xdt != TSP_F32) fail("sparse conv: 16-bit input of another type than the weights'");
+        void* p = sc.take((size_t)n * c.ci * 2);
+        if (sc.running()) hip_check(tgr::launch_convert(x, xdt, p, c.xdt, n * c.ci, s), "conv input rounding");
+        xr = p;
+    }
     if (c.mfma) {
-        const void* x16 = x;
-        const float* row0 = xdt == TSP_F32 ? static_cast<const float*>(x) : nullptr;
-        if (xdt != c.wdt) {
-            void* p = sc.take((size_t)n * c.ci * 2);
-            if (sc.running()) hip_check(tgr::launch_convert(x, xdt, p, c.wdt, n * c.ci, s), "conv input rounding");
-            x16 = p;
-        }
+        const void* x16 = xr;
         void* packed = sc.take((size_t)27 * c.ci * c.co * 2);
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
@@ -93,8 +103,8 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
     } else {
         if (st.ocout || st.skip_cin) fail("sparse conv: fused stores need the matrix-core path");
         if (!sc.running()) return;
-        lib(tsp_subm_conv3x3_ex(x, xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
-                                TSP_ALGO_AUTO, flags, s),
+        lib(tsp_subm_conv3x3_ex(xr, c.xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
+                                TSP_ALGO_NARROW, flags, row0, s),
             "sparse conv");
     }
 }
@@ -121,8 +131,8 @@ ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n) {
     a.c = c;
     // the [chunk, 4C] f32 hidden is bounded to 1 GiB
     a.chunk = std::max<int64_t>(1, std::min<int64_t>(n, (int64_t(1) << 30) / (16 * (int64_t)c)));
-    a.mlp16 = !g_sparse_cast_f32 && a.w0->type == a.w2->type &&
-              (a.w0->type == GGML_TYPE_F16 || a.w0->type == GGML_TYPE_BF16) && c % 64 == 0;
+    a.adt0 = act_dtype(tgr::tsp_dtype_of(a.w0->type), false);
+    a.adt2 = act_dtype(tgr::tsp_dtype_of(a.w2->type), false);
     return a;
 }
 
@@ -130,20 +140,20 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
                   float* out, Carve& sc, hipStream_t s) {
     const int c = a.c;
     const int w0dt = tgr::tsp_dtype_of(a.w0->type), w2dt = tgr::tsp_dtype_of(a.w2->type);
-    // the linears' inputs take the weights' 16-bit type so they run on the matrix cores
-    const int adt = a.mlp16 ? w0dt : TSP_F32;
-    const size_t aes = adt == TSP_F32 ? 4 : 2;
+    // each linear's input rounded to its act_dtype (LN + affine output -> adt0, SiLU output -> adt2)
+    const int adt0 = a.adt0, adt2 = a.adt2;
+    const size_t aes = adt0 == TSP_F32 ? 4 : 2;
     float* h = static_cast<float*>(sc.take((size_t)a.n * c * 4));
-    void* hn = a.mlp16 ? sc.take((size_t)a.n * c * 2) : h;
+    void* hn = adt0 != TSP_F32 ? sc.take((size_t)a.n * c * 2) : h;
     float* hid = static_cast<float*>(sc.take((size_t)a.chunk * 4 * c * 4));
-    void* hid_in = a.mlp16 ? sc.take((size_t)a.chunk * 4 * c * 2) : hid;
+    void* hid_in = adt2 != TSP_F32 ? sc.take((size_t)a.chunk * 4 * c * 2) : hid;
     const float* gamma = f32_param(a.nw, sc, s);
     const float* beta = f32_param(a.nb, sc, s);
     const float* bias0 = f32_param(a.b0, sc, s);
     const float* bias2 = f32_param(a.b2, sc, s);
     run_conv(a.conv, x, xdt, a.n, nbr, plan, h, sc, s);
     if (!sc.running()) return;
-    lib(tsp_layer_norm(h, TSP_F32, a.n, c, gamma, beta, 1e-6f, 0, hn, adt, s), "convnext norm");
+    lib(tsp_layer_norm(h, TSP_F32, a.n, c, gamma, beta, 1e-6f, 0, hn, adt0, s), "convnext norm");
     const size_t xes = xdt == TSP_F32 ? 4 : 2;
     for (int64_t r0 = 0; r0 < a.n; r0 += a.chunk) {
         const int64_t nr = std::min(a.chunk, a.n - r0);
@@ -153,23 +163,23 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
         // 16-bit MLP: mlp.0 with its bias and SiLU, and mlp.2 with its bias and the f32 block input,
         // each one library GEMM; the unfused sequence where a shape has no such GEMM
         int st = TSP_ERR_UNSUPPORTED;
-        if (a.mlp16)
-            st = tsp_linear_ex(hin, adt, nr, c, a.w0->data, w0dt, bias0, 4 * c, TSP_ACT_SILU, nullptr,
-                               hid_in, adt, s);
+        if (adt0 != TSP_F32 && adt2 != TSP_F32)
+            st = tsp_linear_ex(hin, adt0, nr, c, a.w0->data, w0dt, bias0, 4 * c, TSP_ACT_SILU, nullptr,
+                               hid_in, adt2, s);
         if (st != TSP_ERR_UNSUPPORTED) {
             lib(st, "convnext mlp.0");
         } else {
-            lib(tsp_linear(hin, adt, nr, c, a.w0->data, w0dt, bias0, 4 * c, hid, TSP_F32, s), "convnext mlp.0");
-            hip_check(tgr::launch_silu_to(hid, hid_in, adt, nr * 4 * c, s), "convnext silu");
+            lib(tsp_linear(hin, adt0, nr, c, a.w0->data, w0dt, bias0, 4 * c, hid, TSP_F32, s), "convnext mlp.0");
+            hip_check(tgr::launch_silu_to(hid, hid_in, adt2, nr * 4 * c, s), "convnext silu");
         }
         st = TSP_ERR_UNSUPPORTED;
-        if (a.mlp16 && xdt == TSP_F32)
-            st = tsp_linear_ex(hid_in, adt, nr, 4 * c, a.w2->data, w2dt, bias2, c, TSP_ACT_NONE,
+        if (adt2 != TSP_F32 && xdt == TSP_F32)
+            st = tsp_linear_ex(hid_in, adt2, nr, 4 * c, a.w2->data, w2dt, bias2, c, TSP_ACT_NONE,
                                static_cast<const float*>(xr), yr, TSP_F32, s);
         if (st != TSP_ERR_UNSUPPORTED) {
             lib(st, "convnext mlp.2");
         } else {
-            lib(tsp_linear(hid_in, adt, nr, 4 * c, a.w2->data, w2dt, bias2, c, yr, TSP_F32, s), "convnext mlp.2");
+            lib(tsp_linear(hid_in, adt2, nr, 4 * c, a.w2->data, w2dt, bias2, c, yr, TSP_F32, s), "convnext mlp.2");
             hip_check(tgr::launch_add_inplace(yr, xr, xdt, nr * c, s), "convnext residual");
         }
     }
@@ -251,10 +261,14 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     } else {
         const ggml_tensor* wsub = mat_param(m, prefix + ".to_subdiv.weight", cin, 8);
         const ggml_tensor* bsub = vec_param(m, prefix + ".to_subdiv.bias", 8);
+        const int wsdt = tgr::tsp_dtype_of(wsub->type), xsdt = act_dtype(wsdt, false);
         DeviceBuffer d_logits((size_t)8 * n * 4, s), d_b(256, s);
+        DeviceBuffer d_xs(xsdt != TSP_F32 ? (size_t)n * cin * 2 : 0, s);
         Carve sc(d_b.get());
-        lib(tsp_linear(d_x, TSP_F32, n, cin, wsub->data, tgr::tsp_dtype_of(wsub->type), f32_param(bsub, sc, s),
-                       8, d_logits.get(), TSP_F32, s),
+        if (xsdt != TSP_F32)
+            hip_check(tgr::launch_convert(d_x, TSP_F32, d_xs.get(), xsdt, n * cin, s), "to_subdiv rounding");
+        lib(tsp_linear(xsdt != TSP_F32 ? d_xs.get() : static_cast<const void*>(d_x), xsdt, n, cin, wsub->data,
+                       wsdt, f32_param(bsub, sc, s), 8, d_logits.get(), TSP_F32, s),
             prefix + ".to_subdiv");
         lib(tsp_mask_positive(d_logits.as<float>(), 8 * n, d_mask.as<uint8_t>(), s), prefix + " mask");
     }
@@ -287,7 +301,8 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     // conv1 on the parents: LN(norm1)+SiLU written straight in the conv's input dtype. On the
     // matrix cores (cout % 64 == 0) its stores do the octant gather, and the [n][8 cout]
     // intermediate is never written.
-    const int in1 = conv1.mfma ? conv1.wdt : TSP_F32, in2 = conv2.mfma ? conv2.wdt : TSP_F32;
+    // norm1 / norm2 (+ SiLU) write the convs' inputs rounded as the convs take them
+    const int in1 = conv1.xdt, in2 = conv2.xdt;
     const size_t es1 = in1 == TSP_F32 ? 4 : 2, es2 = in2 == TSP_F32 ? 4 : 2;
     const size_t s1 = conv_scratch(conv1, n, in1), s2 = conv_scratch(conv2, mm, in2);
     const bool octant_stores = conv1.mfma && cout % 64 == 0;
@@ -356,25 +371,25 @@ void run_linear(const Model& m, const std::string& prefix, const float* d_x, int
     const ggml_tensor* w = mat_param(m, prefix + ".weight", ci, co);
     const ggml_tensor* b = vec_param(m, prefix + ".bias", co);
     const int wdt = tgr::tsp_dtype_of(w->type);
-    const bool mfma = !g_sparse_cast_f32 && (wdt == TSP_F16 || wdt == TSP_BF16) && ci % 32 == 0 && co % 64 == 0;
-    const int xdt = mfma ? wdt : TSP_F32;
+    const int xdt = act_dtype(wdt, false);
     DeviceBuffer pb((size_t)co * 4 + 256, s);
     Carve sc(pb.get());
     const float* bias = f32_param(b, sc, s);
-    // a narrow head after a LayerNorm runs as one pass over x (shapes it does not take fall back)
-    if (pre_norm && !mfma && co <= 8) {
+    // a narrow head after a LayerNorm runs as one pass over x (shapes it does not take fall back);
+    // it rounds the normalised values to xdt as the LN's output would be
+    if (pre_norm && co <= 8) {
         const hipError_t e = tgr::launch_norm_linear(d_x, n, ci, eps, w->data, wdt, bias, co, d_out, s);
         if (e != hipErrorInvalidValue) {
             hip_check(e, (prefix + " head").c_str());
             return;
         }
     }
-    DeviceBuffer tmp((pre_norm || mfma) ? (size_t)n * ci * (mfma ? 2 : 4) : 0, s);
+    DeviceBuffer tmp((pre_norm || xdt != TSP_F32) ? (size_t)n * ci * (xdt != TSP_F32 ? 2 : 4) : 0, s);
     const void* x = d_x;
     if (pre_norm) {
         lib(tsp_layer_norm(d_x, TSP_F32, n, ci, nullptr, nullptr, eps, 0, tmp.get(), xdt, s), prefix + " norm");
         x = tmp.get();
-    } else if (mfma) {
+    } else if (xdt != TSP_F32) {
         hip_check(tgr::launch_convert(d_x, TSP_F32, tmp.get(), xdt, n * ci, s), (prefix + " rounding").c_str());
         x = tmp.get();
     }

@@ -36,12 +36,19 @@ const ggml_tensor* mat_param(const Model& m, const std::string& name, int64_t k,
 // f32 view of a 1-D parameter (converted into scratch when stored in 16 bits)
 const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s);
 
+// The dtype ggml's mul_mat rounds an F32 activation to before its product with weights of
+// dtype wdt (the CPU backend's vec_dot type): F16 and BF16 weights round it to their own type,
+// F32 weights take it as it is. Conv weights under g_sparse_cast_f32 are F32 casts of F16 ones
+// (w32, sparse.cpp:16-19; BF16 conv weights are not cast); linear weights are never cast.
+int act_dtype(int wdt, bool conv_weight);
+
 // A submanifold conv's weights (`prefix.weight` ggml [Ci, 27, Co], `prefix.bias` [Co]).
 struct Conv {
     const ggml_tensor* w = nullptr;
     const ggml_tensor* b = nullptr;
     int ci = 0, co = 0, wdt = 0;
-    bool mfma = false;   // matrix-core kernel (16-bit weights, Ci % 16 == 0, Co % 64 == 0)
+    int xdt = 0;         // the dtype the input is rounded to (act_dtype)
+    bool mfma = false;   // matrix-core kernel (16-bit xdt, Ci % 16 == 0, Co % 64 == 0)
 };
 Conv conv_of(const Model& m, const std::string& prefix);
 // What a matrix-core conv's stores do besides writing its rows (the C2S block's fusions).
@@ -71,7 +78,7 @@ struct ConvNext {
     int64_t n = 0;
     int c = 0;
     int64_t chunk = 0;
-    bool mlp16 = false;   // the linears run on 16-bit activations (matrix cores)
+    int adt0 = 0, adt2 = 0;   // the dtypes mlp.0's and mlp.2's inputs are rounded to
 };
 ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n);
 // out [n][c] f32 = block(x [n][c]); out must not alias x.
@@ -115,7 +122,7 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
                int32_t* d_status = nullptr, bool want_mask = true, int64_t ext_count = -1);
 
 // out [n][co] f32 = (optionally LN(eps, no affine) of) x [n][ci] . W^T + b for `prefix.weight`
-// ggml [ci, co]; the input is rounded to the weight's 16-bit type when the matrix cores can run it.
+// ggml [ci, co]; the input (the LN's output) is rounded to act_dtype of the weight.
 void run_linear(const Model& m, const std::string& prefix, const float* d_x, int64_t n, int ci, int co,
                 bool pre_norm, float eps, float* d_out, hipStream_t s);
 
