@@ -257,6 +257,73 @@ int tsp_c2s_skip_add(const void* d_x, int x_dtype, const int32_t* d_gidx, int64_
 /* mask[e] = logits[e] > 0 (the predicted subdivision, sparse.cpp:215). */
 int tsp_mask_positive(const float* d_logits, int64_t n, uint8_t* d_mask, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Composite blocks: one call each for the ConvNeXt block and the C2S block's features, over the
+ * entry points above, on caller-owned buffers (temporaries in the caller's workspace; nothing is
+ * allocated). Every matrix product takes its input rounded as ggml's mul_mat rounds it: to the
+ * weights' type for F16 and BF16 weights, unrounded for F32 weights and, with
+ * TSP_BLOCK_CAST_F32 (the reference's g_sparse_cast_f32, sparse.cpp:16-19), for F16 conv weights.
+ * Matrices in the reference's layouts (ggml ne reversed), vectors f32, all device pointers.
+ * A *_packed pointer, optional, holds its conv weight packed by tsp_conv_weight_pack; NULL packs
+ * it into the workspace on each call that runs the planned kernel.
+ * ------------------------------------------------------------------------------------- */
+enum { TSP_BLOCK_CAST_F32 = 2 };
+
+typedef struct {
+    const void* conv_weight;   /* [C][27][C] */
+    int conv_dtype;
+    const float* conv_bias;    /* [C] */
+    const void* conv_packed;
+    const float* norm_weight;  /* [C] */
+    const float* norm_bias;    /* [C] */
+    const void* mlp0_weight;   /* [4C][C] */
+    int mlp0_dtype;
+    const float* mlp0_bias;    /* [4C] */
+    const void* mlp2_weight;   /* [C][4C] */
+    int mlp2_dtype;
+    const float* mlp2_bias;    /* [C] */
+} tsp_convnext_weights;
+
+/* Workspace tsp_convnext needs (only the dtypes and conv_packed of w are read). */
+size_t tsp_convnext_workspace_bytes(int64_t n, int c, int x_dtype, const tsp_convnext_weights* w,
+                                    int has_plan, int flags);
+/* SparseConvNeXtBlock3d (replaces trellis::sparse_convnext, include/sparse.h:24-25,
+ * src/sparse.cpp:94-137): out f32 [n][c] = x + mlp.2(SiLU(mlp.0(LN(conv(x)) * norm.weight +
+ * norm.bias))), LN eps 1e-6. x f32, or 16-bit of the conv input's type; d_plan (of d_nbr) may be
+ * NULL; out must not alias x. */
+int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, const int32_t* d_nbr,
+                 const void* d_plan, const tsp_convnext_weights* w, float* d_out,
+                 void* d_workspace, size_t workspace_bytes, int flags, void* stream);
+
+typedef struct {
+    const float* norm1_weight;  /* [Cin] */
+    const float* norm1_bias;    /* [Cin] */
+    const void* conv1_weight;   /* [8 Cout][27][Cin] */
+    int conv1_dtype;
+    const float* conv1_bias;    /* [8 Cout] */
+    const void* conv1_packed;
+    const void* conv2_weight;   /* [Cout][27][Cout] */
+    int conv2_dtype;
+    const float* conv2_bias;    /* [Cout] */
+    const void* conv2_packed;
+} tsp_c2s_weights;
+
+/* Workspace tsp_c2s needs (only the dtypes and *_packed of w are read). */
+size_t tsp_c2s_workspace_bytes(int64_t n, int64_t m, int cin, int cout, const tsp_c2s_weights* w,
+                               int has_plan, int has_child_plan, int flags);
+/* The features of SparseResBlockC2S3d (replaces the feature half of trellis::sparse_c2s,
+ * include/sparse.h:27-35, src/sparse.cpp:256-336) once its subdivision is known: the caller has
+ * the mask (its own, or tsp_linear of to_subdiv + tsp_mask_positive), ran tsp_subdivide (mstart,
+ * gidx, M children) and tsp_rulebook_build on the children. out f32 [m][cout] =
+ * conv2(SiLU(LN(gather(conv1(SiLU(LN(x) * norm1.weight + norm1.bias))))), absent taps of conv2
+ * reading an exact zero row) + the repeat-interleaved skip of x. d_plan (of d_nbr, for conv1)
+ * and d_child_plan (of d_child_nbr, for conv2) may each be NULL. out must not alias x. */
+int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+            const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m,
+            int cout, const int32_t* d_child_nbr, const void* d_child_plan,
+            const tsp_c2s_weights* w, float* d_out, void* d_workspace, size_t workspace_bytes,
+            int flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -247,3 +247,31 @@ def test_python_conv_argument_checks(pkg):
         pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed, b, co, row0=torch.zeros(ci - 1))
     with pytest.raises(ValueError, match="GPU"):   # every check passed: only the device is wrong
         pkg.subm_conv3x3_planned(f, nbr, plan_ok, packed, b, co)
+
+
+def test_composite_validation(pkg):
+    """tsp_convnext / tsp_c2s reject bad arguments before any device work: no weights, unknown
+    flags, a 16-bit x of another type than the conv input, a short workspace, mismatched plans."""
+    L = pkg.lib()
+    w = pkg.ConvNextWeights(FAKE, 2, FAKE, None, FAKE, FAKE, FAKE, 2, FAKE, FAKE, 2, FAKE)
+    nb = L.tsp_convnext_workspace_bytes(1000, 64, 0, ctypes.byref(w), 1, 0)
+    assert nb >= 1000 * 64 * (2 + 4 + 2) and nb % 256 == 0
+    assert L.tsp_convnext_workspace_bytes(1000, 64, 0, ctypes.byref(w), 0, 0) < nb   # no packing without a plan
+    cn = lambda **kw: L.tsp_convnext(FAKE, kw.get("xdt", 0), 1000, 64, FAKE, kw.get("plan", FAKE),
+                                     kw.get("w", ctypes.byref(w)), ctypes.c_void_p(0x2000), FAKE,
+                                     kw.get("ws", nb), kw.get("flags", 0), NULL)
+    assert cn(w=None) == 1
+    assert cn(flags=4) == 1 and "flags" in _err(pkg)
+    assert cn(xdt=1) == 4                     # f16 x for bf16 conv weights
+    assert cn(ws=nb - 1) == 5 and "workspace" in _err(pkg)
+    c = pkg.C2SWeights(FAKE, FAKE, FAKE, 2, FAKE, None, FAKE, 2, FAKE, None)
+    cb = L.tsp_c2s_workspace_bytes(500, 1200, 128, 64, ctypes.byref(c), 1, 1, 0)
+    assert cb > 0
+    cs = lambda **kw: L.tsp_c2s(FAKE, 500, kw.get("cin", 128), FAKE, kw.get("plan", FAKE), FAKE, FAKE, FAKE,
+                                kw.get("m", 1200), 64, FAKE, kw.get("cplan", FAKE), ctypes.byref(c),
+                                ctypes.c_void_p(0x2000), FAKE, kw.get("ws", cb), 0, NULL)
+    assert cs(cin=60) == 1                    # Cin % 8
+    assert cs(m=4001) == 1                    # M > 8 N
+    assert L.tsp_c2s_workspace_bytes(500, 1200, 128, 64, ctypes.byref(c), 1, 0, 0) != cb
+    assert cs(ws=cb - 1) == 5
+    assert cs(m=0) == 0

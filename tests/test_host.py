@@ -1,7 +1,7 @@
 """CPU tests of the C++ host side (trellis.cpp_amd/host): its GGUF reader against files the test
 writer produces, its host fp16 conversion against numpy, the symbols it exports, and -- where the
 reference checkout is present -- that the reference's own callers of the sparse path compile
-unchanged against its headers."""
+unchanged against its headers and link against its libraries."""
 from __future__ import annotations
 
 import ctypes
@@ -131,10 +131,20 @@ def test_host_library_exports():
                     reason="the reference checkout is not present")
 @pytest.mark.parametrize("src", ["shape_decoder.cpp", "test_sparse_conv.cpp", "test_c2s.cpp",
                                  "test_bigop.cpp"])
-def test_reference_callers_compile_against_the_shim(src):
+def test_reference_callers_compile_and_link_against_the_shim(src, tmp_path):
     """The reference's callers of the sparse path compile unchanged against this build's
-    sparse.h, trellis_model.h and ggml-compatible headers (syntax only: nothing is written)."""
-    r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", os.path.join(HOST, "include"),
-                        "-I", os.path.join(REF, "include"), os.path.join(REF, "src", src)],
-                       capture_output=True, text=True, timeout=120)
+    sparse.h, trellis_model.h and ggml-compatible headers and link against libtrellis_host.so
+    (and through it libtrellis_sparse.so): the programs with a main() into executables, the
+    decoder into a shared object with no undefined symbol left. Nothing is run."""
+    lib_dir = os.path.join(ROOT, "trellis.cpp_amd", "host")
+    if not os.path.exists(os.path.join(lib_dir, "libtrellis_host.so")):
+        pytest.fail("libtrellis_host.so is not built")
+    out = str(tmp_path / os.path.splitext(src)[0])
+    shared = ["-shared", "-fPIC", "-Wl,--no-undefined"] if src == "shape_decoder.cpp" else []
+    r = subprocess.run(["g++", "-std=c++17", *shared, "-I", os.path.join(HOST, "include"),
+                        "-I", os.path.join(REF, "include"), os.path.join(REF, "src", src), "-o", out,
+                        "-L", lib_dir, "-ltrellis_host",
+                        "-Wl,-rpath-link," + os.path.join(ROOT, "trellis.cpp_amd") + ":/opt/rocm/lib"],
+                       capture_output=True, text=True, timeout=180)
     assert r.returncode == 0, r.stderr[-3000:]
+    assert os.path.getsize(out) > 0

@@ -32,7 +32,27 @@ EXPORTS = (
     "tsp_subdivide_workspace_bytes", "tsp_subdivide", "tsp_subdivide_noalloc",
     "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
+    "tsp_convnext_workspace_bytes", "tsp_convnext", "tsp_c2s_workspace_bytes", "tsp_c2s",
 )
+
+BLOCK_CAST_F32 = 2
+
+
+class ConvNextWeights(ctypes.Structure):
+    """tsp_convnext_weights: device pointers, dtypes as tsp_dtype codes."""
+    _fields_ = [("conv_weight", ctypes.c_void_p), ("conv_dtype", ctypes.c_int), ("conv_bias", ctypes.c_void_p),
+                ("conv_packed", ctypes.c_void_p), ("norm_weight", ctypes.c_void_p),
+                ("norm_bias", ctypes.c_void_p), ("mlp0_weight", ctypes.c_void_p), ("mlp0_dtype", ctypes.c_int),
+                ("mlp0_bias", ctypes.c_void_p), ("mlp2_weight", ctypes.c_void_p), ("mlp2_dtype", ctypes.c_int),
+                ("mlp2_bias", ctypes.c_void_p)]
+
+
+class C2SWeights(ctypes.Structure):
+    """tsp_c2s_weights: device pointers, dtypes as tsp_dtype codes."""
+    _fields_ = [("norm1_weight", ctypes.c_void_p), ("norm1_bias", ctypes.c_void_p),
+                ("conv1_weight", ctypes.c_void_p), ("conv1_dtype", ctypes.c_int), ("conv1_bias", ctypes.c_void_p),
+                ("conv1_packed", ctypes.c_void_p), ("conv2_weight", ctypes.c_void_p), ("conv2_dtype", ctypes.c_int),
+                ("conv2_bias", ctypes.c_void_p), ("conv2_packed", ctypes.c_void_p)]
 
 
 class TspError(RuntimeError):
@@ -115,6 +135,16 @@ def lib() -> ctypes.CDLL:
     L.tsp_subdivide.argtypes = [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]
     L.tsp_subdivide_noalloc.restype = c_int
     L.tsp_subdivide_noalloc.argtypes = [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]
+    cnw, c2w = ctypes.POINTER(ConvNextWeights), ctypes.POINTER(C2SWeights)
+    L.tsp_convnext_workspace_bytes.restype = c_sz
+    L.tsp_convnext_workspace_bytes.argtypes = [c_i64, c_int, c_int, cnw, c_int, c_int]
+    L.tsp_convnext.restype = c_int
+    L.tsp_convnext.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, cnw, c_vp, c_vp, c_sz, c_int, c_vp]
+    L.tsp_c2s_workspace_bytes.restype = c_sz
+    L.tsp_c2s_workspace_bytes.argtypes = [c_i64, c_i64, c_int, c_int, c2w, c_int, c_int, c_int]
+    L.tsp_c2s.restype = c_int
+    L.tsp_c2s.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c2w,
+                          c_vp, c_vp, c_sz, c_int, c_vp]
     _lib = L
     return L
 
@@ -485,3 +515,93 @@ def mask_positive(logits, stream=None):
     _check("tsp_mask_positive",
            lib().tsp_mask_positive(_ptr(lc), lc.numel(), _ptr(mask), _stream(stream)))
     return mask
+
+
+def _vec(t, n: int, name: str):
+    torch = _torch()
+    if t.dtype != torch.float32 or t.numel() != n:
+        raise ValueError(f"{name} must be float32 [{n}]")
+    return t.contiguous()
+
+
+def _mat(t, shape, name: str):
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must be {list(shape)}, got {list(t.shape)}")
+    return t.contiguous()
+
+
+def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None):
+    """SparseConvNeXtBlock3d through tsp_convnext: x [N, C] (f32, or 16-bit of the conv input's
+    type), p the block's tensors by their reference names without the prefix ("conv.weight"
+    [C,27,C], "conv.bias", "norm.weight", "norm.bias", "mlp.0.weight" [4C,C], "mlp.0.bias",
+    "mlp.2.weight" [C,4C], "mlp.2.bias"); optional "conv.packed". -> f32 [N, C]."""
+    torch = _torch()
+    n, c = x.shape
+    _check_nbr(nbr, n, x.device)
+    t = {"conv.weight": _mat(p["conv.weight"], (c, 27, c), "conv.weight"),
+         "mlp.0.weight": _mat(p["mlp.0.weight"], (4 * c, c), "mlp.0.weight"),
+         "mlp.2.weight": _mat(p["mlp.2.weight"], (c, 4 * c), "mlp.2.weight")}
+    for k, m in (("conv.bias", c), ("norm.weight", c), ("norm.bias", c), ("mlp.0.bias", 4 * c), ("mlp.2.bias", c)):
+        t[k] = _vec(p[k], m, k)
+    packed = p.get("conv.packed")
+    if packed is not None and (packed.numel() * packed.element_size() != 27 * c * c * 2):
+        raise ValueError("conv.packed must hold 27*C*C 16-bit values")
+    if plan is not None and (plan.dtype != torch.uint8 or plan.numel() < lib().tsp_conv_plan_bytes(n)):
+        raise ValueError("plan must be a uint8 buffer of tsp_conv_plan_bytes(N)")
+    _require_cuda(x, nbr, plan, packed, *t.values())
+    w = ConvNextWeights(_ptr(t["conv.weight"]), dtype_code(t["conv.weight"].dtype), _ptr(t["conv.bias"]),
+                        _ptr(packed), _ptr(t["norm.weight"]), _ptr(t["norm.bias"]), _ptr(t["mlp.0.weight"]),
+                        dtype_code(t["mlp.0.weight"].dtype), _ptr(t["mlp.0.bias"]), _ptr(t["mlp.2.weight"]),
+                        dtype_code(t["mlp.2.weight"].dtype), _ptr(t["mlp.2.bias"]))
+    flags = BLOCK_CAST_F32 if cast_f32 else 0
+    xc = x.contiguous()
+    out = torch.empty((n, c), dtype=torch.float32, device=x.device)
+    nb = lib().tsp_convnext_workspace_bytes(n, c, dtype_code(xc.dtype), ctypes.byref(w), int(plan is not None), flags)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
+    _check("tsp_convnext", lib().tsp_convnext(_ptr(xc), dtype_code(xc.dtype), n, c, _ptr(nbr), _ptr(plan),
+                                              ctypes.byref(w), _ptr(out), _ptr(ws), nb, flags, _stream(stream)))
+    return out
+
+
+def c2s(x, nbr, mask, mstart, gidx, m: int, cout: int, child_nbr, p: dict, plan=None, child_plan=None,
+        cast_f32: bool = False, stream=None):
+    """The C2S block's features through tsp_c2s, after its subdivision (mask uint8 [8N], mstart
+    and gidx from subdivide, child_nbr the children's table): x f32 [N, Cin], p by reference
+    names without the prefix ("norm1.weight", "norm1.bias", "conv1.weight" [8 Cout,27,Cin],
+    "conv1.bias", "conv2.weight" [Cout,27,Cout], "conv2.bias"; optional "conv1.packed",
+    "conv2.packed"). -> f32 [M, Cout]."""
+    torch = _torch()
+    n, cin = x.shape
+    if x.dtype != torch.float32:
+        raise ValueError("x must be float32")
+    _check_nbr(nbr, n, x.device)
+    _check_nbr(child_nbr, m, x.device)
+    if mask.dtype != torch.uint8 or mask.numel() != 8 * n:
+        raise ValueError("mask must be uint8 with 8*N entries")
+    if mstart.dtype != torch.int32 or mstart.numel() != n + 1 or gidx.dtype != torch.int32 or gidx.numel() < m:
+        raise ValueError("mstart must be int32 [N+1] and gidx int32 [>= M]")
+    t = {"conv1.weight": _mat(p["conv1.weight"], (8 * cout, 27, cin), "conv1.weight"),
+         "conv2.weight": _mat(p["conv2.weight"], (cout, 27, cout), "conv2.weight")}
+    for k, k_n in (("norm1.weight", cin), ("norm1.bias", cin), ("conv1.bias", 8 * cout), ("conv2.bias", cout)):
+        t[k] = _vec(p[k], k_n, k)
+    p1, p2 = p.get("conv1.packed"), p.get("conv2.packed")
+    for pk, numel, name in ((p1, 27 * cin * 8 * cout, "conv1.packed"), (p2, 27 * cout * cout, "conv2.packed")):
+        if pk is not None and pk.numel() * pk.element_size() != 2 * numel:
+            raise ValueError(f"{name} must hold the packed 16-bit weight")
+    for pl, rows, name in ((plan, n, "plan"), (child_plan, m, "child_plan")):
+        if pl is not None and (pl.dtype != torch.uint8 or pl.numel() < lib().tsp_conv_plan_bytes(rows)):
+            raise ValueError(f"{name} must be a uint8 buffer of tsp_conv_plan_bytes")
+    _require_cuda(x, nbr, mask, mstart, gidx, child_nbr, plan, child_plan, p1, p2, *t.values())
+    w = C2SWeights(_ptr(t["norm1.weight"]), _ptr(t["norm1.bias"]), _ptr(t["conv1.weight"]),
+                   dtype_code(t["conv1.weight"].dtype), _ptr(t["conv1.bias"]), _ptr(p1), _ptr(t["conv2.weight"]),
+                   dtype_code(t["conv2.weight"].dtype), _ptr(t["conv2.bias"]), _ptr(p2))
+    flags = BLOCK_CAST_F32 if cast_f32 else 0
+    xc = x.contiguous()
+    out = torch.empty((m, cout), dtype=torch.float32, device=x.device)
+    nb = lib().tsp_c2s_workspace_bytes(n, m, cin, cout, ctypes.byref(w), int(plan is not None),
+                                       int(child_plan is not None), flags)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
+    _check("tsp_c2s", lib().tsp_c2s(_ptr(xc), n, cin, _ptr(nbr), _ptr(plan), _ptr(mask.reshape(-1).contiguous()),
+                                    _ptr(mstart), _ptr(gidx), m, cout, _ptr(child_nbr), _ptr(child_plan),
+                                    ctypes.byref(w), _ptr(out), _ptr(ws), nb, flags, _stream(stream)))
+    return out

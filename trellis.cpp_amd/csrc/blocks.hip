@@ -5,9 +5,12 @@
 //   * the channel-to-spatial octant gather: child m takes the Cout-channel block (gidx[m] % 8)
 //     of parent gidx[m] / 8 of conv1's [N][8 Cout] output (sparse.cpp:263-291);
 //   * the C2S skip: child m adds parent x's K = Cin/8 channel block (gidx[m] % 8), each channel
-//     repeated R = Cout/K times (repeat_interleave, sparse.cpp:302-323).
+//     repeated R = Cout/K times (repeat_interleave, sparse.cpp:302-323);
+//   * the elementwise steps the composite blocks need between library calls: rounding an f32
+//     tensor to a product's input type, SiLU into that type, and a residual add.
 #include <algorithm>
 
+#include "blocks_internal.hpp"
 #include "common.hpp"
 
 namespace tsp {
@@ -211,6 +214,24 @@ __global__ void k_c2s_skip_add(const void* __restrict__ x, const int32_t* __rest
     }
 }
 
+// y = f(x) stored as DT (round to nearest even for 16-bit types), f = identity or SiLU
+template <int DT, bool SILU>
+__global__ void k_f32_to(const float* __restrict__ x, int64_t n, void* __restrict__ y) {
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        float v = x[e];
+        if constexpr (SILU) v = v / (1.0f + expf(-v));
+        st<DT>(y, e, v);
+    }
+}
+
+template <int XDT>
+__global__ void k_add_to(float* __restrict__ y, const void* __restrict__ x, int64_t n) {
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+         e += (int64_t)gridDim.x * blockDim.x)
+        y[e] += ld<XDT>(x, e);
+}
+
 __global__ void k_mask_positive(const float* __restrict__ logits, int64_t n,
                                 uint8_t* __restrict__ mask) {
     for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
@@ -223,6 +244,31 @@ inline unsigned grid_for(int64_t total) {
 }
 
 }  // namespace
+
+int f32_to(const float* x, int64_t n, void* y, int ydt, bool silu, hipStream_t s) {
+    if (n <= 0) return TSP_OK;
+    const dim3 g(grid_for(n)), b(256);
+#define TSP_F32_TO(DT)                                                                     \
+    if (silu) hipLaunchKernelGGL((k_f32_to<DT, true>), g, b, 0, s, x, n, y);               \
+    else hipLaunchKernelGGL((k_f32_to<DT, false>), g, b, 0, s, x, n, y);
+    if (ydt == TSP_F32) { TSP_F32_TO(TSP_F32) }
+    else if (ydt == TSP_F16) { TSP_F32_TO(TSP_F16) }
+    else { TSP_F32_TO(TSP_BF16) }
+#undef TSP_F32_TO
+    TSP_CHECK_LAUNCH();
+    return TSP_OK;
+}
+
+int add_to(float* y, const void* x, int xdt, int64_t n, hipStream_t s) {
+    if (n <= 0) return TSP_OK;
+    const dim3 g(grid_for(n)), b(256);
+    if (xdt == TSP_F32) hipLaunchKernelGGL(k_add_to<TSP_F32>, g, b, 0, s, y, x, n);
+    else if (xdt == TSP_F16) hipLaunchKernelGGL(k_add_to<TSP_F16>, g, b, 0, s, y, x, n);
+    else hipLaunchKernelGGL(k_add_to<TSP_BF16>, g, b, 0, s, y, x, n);
+    TSP_CHECK_LAUNCH();
+    return TSP_OK;
+}
+
 }  // namespace tsp
 
 using namespace tsp;

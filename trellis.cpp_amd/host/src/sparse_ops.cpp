@@ -67,13 +67,10 @@ Conv conv_of(const Model& m, const std::string& prefix) {
 // type (sparse.cpp:74); the matrix-core kernel runs where the channel counts fit its tiles, the
 // VALU kernel elsewhere (on the rounded input, or under g_sparse_cast_f32 on the F32 input and
 // the weights' exact values). The padding row is formed from the unrounded row 0 (sparse.cpp:81-85
-// pads the F32 input). A caller that passes input already in c.xdt (rounded from F32 as it was
-// written) leaves the padding row to that row 0: the two differ only where a finite F32 value
-// overflows the 16-bit range.
+// pads the F32 input).
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
-              float* out, Carve& sc, hipStream_t s, const ConvStores& st) {
+              float* out, Carve& sc, hipStream_t s) {
     const float* bias = f32_param(c.b, sc, s);
-    const int flags = st.zero_pad ? TSP_CONV_ZERO_PAD : 0;
     const float* row0 = xdt == TSP_F32 && c.xdt != TSP_F32 ? static_cast<const float*>(x) : nullptr;
     const void* xr = x;
     if (xdt != c.xdt) {
@@ -83,28 +80,16 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
         xr = p;
     }
     if (c.mfma) {
-        const void* x16 = xr;
         void* packed = sc.take((size_t)27 * c.ci * c.co * 2);
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
         lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, packed, s), "weight pack");
-        if (st.ocout)
-            lib(tsp_subm_conv3x3_planned_octants(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, st.ocout,
-                                                 st.omask, st.omstart, out, s),
-                "sparse conv (octant stores)");
-        else if (st.skip_cin)   // always an exact zero padding row: the C2S conv2
-            lib(tsp_subm_conv3x3_planned_skip(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, st.skip_x,
-                                              st.skip_cin, st.skip_gidx, out, s),
-                "sparse conv (skip stores)");
-        else
-            lib(tsp_subm_conv3x3_planned_ex(x16, c.wdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32,
-                                            flags, row0, s),
-                "sparse conv");
+        lib(tsp_subm_conv3x3_planned_ex(xr, c.xdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, 0, row0, s),
+            "sparse conv");
     } else {
-        if (st.ocout || st.skip_cin) fail("sparse conv: fused stores need the matrix-core path");
         if (!sc.running()) return;
-        lib(tsp_subm_conv3x3_ex(xr, c.xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32,
-                                TSP_ALGO_NARROW, flags, row0, s),
+        lib(tsp_subm_conv3x3_ex(xr, c.xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32, TSP_ALGO_NARROW,
+                                0, row0, s),
             "sparse conv");
     }
 }
@@ -129,60 +114,32 @@ ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n) {
     a.b2 = vec_param(m, prefix + ".mlp.2.bias", c);
     a.n = n;
     a.c = c;
-    // the [chunk, 4C] f32 hidden is bounded to 1 GiB
-    a.chunk = std::max<int64_t>(1, std::min<int64_t>(n, (int64_t(1) << 30) / (16 * (int64_t)c)));
-    a.adt0 = act_dtype(tgr::tsp_dtype_of(a.w0->type), false);
-    a.adt2 = act_dtype(tgr::tsp_dtype_of(a.w2->type), false);
     return a;
 }
 
+// The block is one tsp_convnext call; 16-bit vectors are converted to f32 in the scratch first.
 void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr, const void* plan,
                   float* out, Carve& sc, hipStream_t s) {
-    const int c = a.c;
-    const int w0dt = tgr::tsp_dtype_of(a.w0->type), w2dt = tgr::tsp_dtype_of(a.w2->type);
-    // each linear's input rounded to its act_dtype (LN + affine output -> adt0, SiLU output -> adt2)
-    const int adt0 = a.adt0, adt2 = a.adt2;
-    const size_t aes = adt0 == TSP_F32 ? 4 : 2;
-    float* h = static_cast<float*>(sc.take((size_t)a.n * c * 4));
-    void* hn = adt0 != TSP_F32 ? sc.take((size_t)a.n * c * 2) : h;
-    float* hid = static_cast<float*>(sc.take((size_t)a.chunk * 4 * c * 4));
-    void* hid_in = adt2 != TSP_F32 ? sc.take((size_t)a.chunk * 4 * c * 2) : hid;
-    const float* gamma = f32_param(a.nw, sc, s);
-    const float* beta = f32_param(a.nb, sc, s);
-    const float* bias0 = f32_param(a.b0, sc, s);
-    const float* bias2 = f32_param(a.b2, sc, s);
-    run_conv(a.conv, x, xdt, a.n, nbr, plan, h, sc, s);
+    tsp_convnext_weights w{};
+    w.conv_weight = a.conv.w->data;
+    w.conv_dtype = a.conv.wdt;
+    w.conv_bias = f32_param(a.conv.b, sc, s);
+    w.norm_weight = f32_param(a.nw, sc, s);
+    w.norm_bias = f32_param(a.nb, sc, s);
+    w.mlp0_weight = a.w0->data;
+    w.mlp0_dtype = tgr::tsp_dtype_of(a.w0->type);
+    w.mlp0_bias = f32_param(a.b0, sc, s);
+    w.mlp2_weight = a.w2->data;
+    w.mlp2_dtype = tgr::tsp_dtype_of(a.w2->type);
+    w.mlp2_bias = f32_param(a.b2, sc, s);
+    const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
+    // a plan comes with every matrix-core conv (the callers build it where conv.mfma)
+    const size_t nb = tsp_convnext_workspace_bytes(a.n, a.c, xdt, &w, a.conv.mfma, flags);
+    void* ws = sc.take(nb);
     if (!sc.running()) return;
-    lib(tsp_layer_norm(h, TSP_F32, a.n, c, gamma, beta, 1e-6f, 0, hn, adt0, s), "convnext norm");
-    const size_t xes = xdt == TSP_F32 ? 4 : 2;
-    for (int64_t r0 = 0; r0 < a.n; r0 += a.chunk) {
-        const int64_t nr = std::min(a.chunk, a.n - r0);
-        const void* hin = static_cast<const char*>(hn) + (size_t)r0 * c * aes;
-        const void* xr = static_cast<const char*>(x) + (size_t)r0 * c * xes;
-        float* yr = out + r0 * c;
-        // 16-bit MLP: mlp.0 with its bias and SiLU, and mlp.2 with its bias and the f32 block input,
-        // each one library GEMM; the unfused sequence where a shape has no such GEMM
-        int st = TSP_ERR_UNSUPPORTED;
-        if (adt0 != TSP_F32 && adt2 != TSP_F32)
-            st = tsp_linear_ex(hin, adt0, nr, c, a.w0->data, w0dt, bias0, 4 * c, TSP_ACT_SILU, nullptr,
-                               hid_in, adt2, s);
-        if (st != TSP_ERR_UNSUPPORTED) {
-            lib(st, "convnext mlp.0");
-        } else {
-            lib(tsp_linear(hin, adt0, nr, c, a.w0->data, w0dt, bias0, 4 * c, hid, TSP_F32, s), "convnext mlp.0");
-            hip_check(tgr::launch_silu_to(hid, hid_in, adt2, nr * 4 * c, s), "convnext silu");
-        }
-        st = TSP_ERR_UNSUPPORTED;
-        if (adt2 != TSP_F32 && xdt == TSP_F32)
-            st = tsp_linear_ex(hid_in, adt2, nr, 4 * c, a.w2->data, w2dt, bias2, c, TSP_ACT_NONE,
-                               static_cast<const float*>(xr), yr, TSP_F32, s);
-        if (st != TSP_ERR_UNSUPPORTED) {
-            lib(st, "convnext mlp.2");
-        } else {
-            lib(tsp_linear(hid_in, adt2, nr, 4 * c, a.w2->data, w2dt, bias2, c, yr, TSP_F32, s), "convnext mlp.2");
-            hip_check(tgr::launch_add_inplace(yr, xr, xdt, nr * c, s), "convnext residual");
-        }
-    }
+    if (a.conv.mfma && !plan) fail("sparse_convnext: the matrix-core path needs a conv plan");
+    lib(tsp_convnext(x, xdt, a.n, a.c, nbr, a.conv.mfma ? plan : nullptr, &w, out, ws, nb, flags, s),
+        "sparse_convnext");
 }
 
 size_t convnext_scratch(const ConvNext& a, int xdt) {
@@ -298,70 +255,32 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     hip_check(hipMemcpyAsync(r.coords.get(), d_child.get(), (size_t)mm * 12, hipMemcpyDeviceToDevice, s),
               "c2s");
 
-    // conv1 on the parents: LN(norm1)+SiLU written straight in the conv's input dtype. On the
-    // matrix cores (cout % 64 == 0) its stores do the octant gather, and the [n][8 cout]
-    // intermediate is never written.
-    // norm1 / norm2 (+ SiLU) write the convs' inputs rounded as the convs take them
-    const int in1 = conv1.xdt, in2 = conv2.xdt;
-    const size_t es1 = in1 == TSP_F32 ? 4 : 2, es2 = in2 == TSP_F32 ? 4 : 2;
-    const size_t s1 = conv_scratch(conv1, n, in1), s2 = conv_scratch(conv2, mm, in2);
-    const bool octant_stores = conv1.mfma && cout % 64 == 0;
-    Carve sz;
-    sz.take((size_t)n * cin * es1);
-    sz.take(octant_stores ? 0 : (size_t)n * 8 * cout * 4);
-    sz.take(s1);
-    sz.take((size_t)mm * cout * 4);
-    sz.take((size_t)mm * cout * es2);
-    sz.take(s2);
-    sz.take(2 * (size_t)cin * 4);
-    DeviceBuffer work(sz.off, s);
-    Carve w(work.get());
-    void* h0 = w.take((size_t)n * cin * es1);
-    float* h1 = static_cast<float*>(w.take(octant_stores ? 0 : (size_t)n * 8 * cout * 4));
-    Carve sc1(w.take(s1));
-    float* g = static_cast<float*>(w.take((size_t)mm * cout * 4));
-    void* h2 = w.take((size_t)mm * cout * es2);
-    Carve sc2(w.take(s2));
-    Carve scp(w.take(2 * (size_t)cin * 4));
-    const float* g1 = f32_param(n1w, scp, s);
-    const float* b1 = f32_param(n1b, scp, s);
-
-    lib(tsp_layer_norm(d_x, TSP_F32, n, cin, g1, b1, 1e-6f, 1, h0, in1, s), prefix + ".norm1");
-    if (conv1.mfma) parent.ensure_plan(s);
-    if (octant_stores) {
-        ConvStores st;
-        st.omask = d_mask.as<uint8_t>();
-        st.omstart = d_mstart.as<int32_t>();
-        st.ocout = cout;
-        run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), g, sc1, s, st);
-    } else {
-        run_conv(conv1, h0, in1, n, parent.nbr.as<int32_t>(), parent.plan.get(), h1, sc1, s);
-        // channel -> spatial gather
-        lib(tsp_c2s_gather(h1, TSP_F32, d_gidx.as<int32_t>(), mm, cout, g, s), prefix + " gather");
-    }
-
-    // norm2 (no affine) + SiLU, conv2 on the children, skip
-    lib(tsp_layer_norm(g, TSP_F32, mm, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s), prefix + " norm2");
+    // the children's table (and plans where a conv runs on the matrix cores), then the block's
+    // features in one tsp_c2s call: norm1 + SiLU, conv1 with the octant gather, norm2 + SiLU,
+    // conv2 (its absent taps read hn's zero padding column, sparse.cpp:289-306) with the skip
     build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status);
+    if (conv1.mfma) parent.ensure_plan(s);
     if (conv2.mfma) r.table.ensure_plan(s);
-    // the skip: added by conv2's stores on the matrix cores (repeat R % 4 == 0), else its own pass
-    // conv2's absent taps read hn's zero padding column (sparse.cpp:289-306)
-    if (conv2.mfma && (cout / (cin / 8)) % 4 == 0) {
-        ConvStores st;
-        st.skip_x = d_x;
-        st.skip_gidx = d_gidx.as<int32_t>();
-        st.skip_cin = cin;
-        st.zero_pad = true;
-        run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s,
-                 st);
-    } else {
-        ConvStores st;
-        st.zero_pad = true;
-        run_conv(conv2, h2, in2, mm, r.table.nbr.as<int32_t>(), r.table.plan.get(), r.feats.as<float>(), sc2, s,
-                 st);
-        lib(tsp_c2s_skip_add(d_x, TSP_F32, d_gidx.as<int32_t>(), mm, cin, cout, r.feats.get(), TSP_F32, s),
-            prefix + " skip");
-    }
+    const ggml_tensor* c1b = conv1.b;
+    const ggml_tensor* c2b = conv2.b;
+    DeviceBuffer pbuf((size_t)(2 * cin + 9 * cout) * 4 + 4 * 256, s);
+    Carve scp(pbuf.get());
+    tsp_c2s_weights w{};
+    w.norm1_weight = f32_param(n1w, scp, s);
+    w.norm1_bias = f32_param(n1b, scp, s);
+    w.conv1_weight = conv1.w->data;
+    w.conv1_dtype = conv1.wdt;
+    w.conv1_bias = f32_param(c1b, scp, s);
+    w.conv2_weight = conv2.w->data;
+    w.conv2_dtype = conv2.wdt;
+    w.conv2_bias = f32_param(c2b, scp, s);
+    const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
+    const size_t nb = tsp_c2s_workspace_bytes(n, mm, cin, cout, &w, conv1.mfma, conv2.mfma, flags);
+    DeviceBuffer work(nb, s);
+    lib(tsp_c2s(d_x, n, cin, parent.nbr.as<int32_t>(), conv1.mfma ? parent.plan.get() : nullptr, d_mask.as<uint8_t>(),
+                d_mstart.as<int32_t>(), d_gidx.as<int32_t>(), mm, cout, r.table.nbr.as<int32_t>(),
+                conv2.mfma ? r.table.plan.get() : nullptr, &w, r.feats.as<float>(), work.get(), nb, flags, s),
+        prefix);
     return r;
 }
 

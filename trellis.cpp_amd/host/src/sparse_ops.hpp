@@ -51,23 +51,9 @@ struct Conv {
     bool mfma = false;   // matrix-core kernel (16-bit xdt, Ci % 16 == 0, Co % 64 == 0)
 };
 Conv conv_of(const Model& m, const std::string& prefix);
-// What a matrix-core conv's stores do besides writing its rows (the C2S block's fusions).
-struct ConvStores {
-    // ocout > 0: rows go to the children, out [M][ocout] as tsp_subm_conv3x3_planned_octants
-    // writes it (co = 8 * ocout, ocout % 64 == 0), from the subdivision's mask and mstart
-    const uint8_t* omask = nullptr;
-    const int32_t* omstart = nullptr;
-    int ocout = 0;
-    // skip_cin > 0: the skip of tsp_subm_conv3x3_planned_skip is added (x f32 [N][skip_cin])
-    const float* skip_x = nullptr;
-    const int32_t* skip_gidx = nullptr;
-    int skip_cin = 0;
-    // absent taps read an exact zero row (the C2S conv2, sparse.cpp:289-306), not 0 * x[0]
-    bool zero_pad = false;
-};
 // out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
-              float* out, Carve& sc, hipStream_t s, const ConvStores& st = {});
+              float* out, Carve& sc, hipStream_t s);
 size_t conv_scratch(const Conv& c, int64_t n, int xdt);
 
 // SparseConvNeXtBlock3d weights and the launch shape of one block over n voxels.
@@ -77,11 +63,10 @@ struct ConvNext {
                       *b2 = nullptr;
     int64_t n = 0;
     int c = 0;
-    int64_t chunk = 0;
-    int adt0 = 0, adt2 = 0;   // the dtypes mlp.0's and mlp.2's inputs are rounded to
 };
 ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n);
-// out [n][c] f32 = block(x [n][c]); out must not alias x.
+// out [n][c] f32 = block(x [n][c]) by tsp_convnext (plan needed where conv.mfma); out must not
+// alias x.
 void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr, const void* plan,
                   float* out, Carve& sc, hipStream_t s);
 size_t convnext_scratch(const ConvNext& a, int xdt);
