@@ -32,22 +32,32 @@ struct TensorInfo {
     uint64_t offset = 0;
 };
 
+// Every length read from the file is checked against the bytes the file has left before it is
+// used, so a corrupt count is rejected instead of allocated or skipped past the end.
 class Reader {
 public:
-    explicit Reader(FILE* f) : f_(f) {}
+    explicit Reader(FILE* f) : f_(f) {
+        if (fseeko(f_, 0, SEEK_END) == 0) size_ = (uint64_t)ftello(f_);
+        fseeko(f_, 0, SEEK_SET);
+    }
     bool bytes(void* p, size_t n) { return fread(p, 1, n, f_) == n; }
     template <class T> bool pod(T& v) { return bytes(&v, sizeof(T)); }
     bool str(std::string& s) {
         uint64_t n;
-        if (!pod(n) || n > (1ull << 32)) return false;
+        if (!pod(n) || n > left()) return false;
         s.resize(n);
         return n == 0 || bytes(&s[0], n);
     }
-    bool skip(uint64_t n) { return fseeko(f_, (off_t)n, SEEK_CUR) == 0; }
+    bool skip(uint64_t n) { return n <= left() && fseeko(f_, (off_t)n, SEEK_CUR) == 0; }
     uint64_t tell() { return (uint64_t)ftello(f_); }
+    uint64_t left() {
+        const uint64_t t = tell();
+        return t <= size_ ? size_ - t : 0;
+    }
 
 private:
     FILE* f_;
+    uint64_t size_ = 0;
 };
 
 size_t scalar_size(uint32_t t) {
@@ -107,11 +117,13 @@ struct gguf_context* gguf_init_from_file(const char* fname, struct gguf_init_par
             if (!r.pod(et) || !r.pod(n)) return bad("truncated array");
             if (et == T_STRING) {
                 std::string s;
+                if (n > r.left() / 8) return bad("truncated string array");   // 8 length bytes each
                 for (uint64_t j = 0; j < n; ++j)
                     if (!r.str(s)) return bad("truncated string array");
             } else {
                 const size_t es = scalar_size(et);
-                if (!es || !r.skip(es * n)) return bad("bad array element type");
+                if (!es) return bad("bad array element type");
+                if (n > r.left() / es || !r.skip(es * n)) return bad("truncated array");
             }
         } else {
             const size_t es = scalar_size(kv.type);
