@@ -75,14 +75,7 @@ def cpu_baseline(w, nbr, budget_s: float):
     t = time.perf_counter()
     orc.neighbor_table(w.coords)
     rb_s = time.perf_counter() - t
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu = host_cpu()
     return {
         "value": rows / dt, "unit": "voxels/s", "cores": threads, "kind": "port",
         "sample": f"output rows [{r0}, {r0 + rows}) of {n}: median of {reps} runs "
@@ -91,8 +84,40 @@ def cpu_baseline(w, nbr, budget_s: float):
                   f"(CPU restatement of sparse.cpp; ggml unavailable)",
         "value_1core": rows1 / dt1, "sample_1core": f"{rows1} rows in {dt1:.2f} s on 1 thread",
         "rulebook_s_1thread": rb_s,
-        "cpu_model": cpu_model,
+        "cpu_model": cpu["model"],
+        "host_cpu": cpu,
     }
+
+
+def host_cpu() -> dict:
+    """The host CPU as lscpu reports it (model, sockets, cores, threads, flags of note), the
+    logical CPUs this process may use, and /proc/cpuinfo's model string."""
+    import subprocess
+    info = {"model": "", "logical_cpus_usable": len(os.sched_getaffinity(0))}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["cpuinfo_model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+                "Thread(s) per core": "threads_per_core", "CPU(s)": "logical_cpus", "CPU max MHz": "max_mhz",
+                "Vendor ID": "vendor", "CPU family": "family", "Model": "model_number",
+                "Hypervisor vendor": "hypervisor"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keys:
+                info[keys[k.strip()]] = v.strip()
+        flags = next((l.split(":", 1)[1].split() for l in out.splitlines() if l.startswith("Flags")), [])
+        info["simd"] = [f for f in ("avx2", "fma", "avx512f", "avx512_bf16") if f in flags]
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not info["model"]:
+        info["model"] = info.get("cpuinfo_model", "")
+    return info
 
 
 def decoder_bench(args) -> dict:
@@ -217,7 +242,8 @@ def decoder_cpu_baseline(w, flops_dense: float, budget_s: float) -> dict:
             "sample": f"extrapolated: the oracle's conv ({c} -> {c} channels, rows [{r0}, {r0 + rows}) of "
                       f"{n}, median of 3: {dt:.2f} s) runs {rate / 1e9:.1f} dense-27 GFLOP/s; the "
                       f"decoder's {flops_dense / 1e12:.1f} dense-27 TFLOP at that rate take {est:.0f} s "
-                      f"(LayerNorm, SiLU and gathers not counted)"}
+                      f"(LayerNorm, SiLU and gathers not counted)",
+            "host_cpu": host_cpu()}
 
 
 def main():
@@ -229,6 +255,7 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the ~640K-voxel variant of the C=128 set")
     ap.add_argument("--plan-order", default="morton", choices=["morton", "rows"],
                     help="conv plan tiles: Morton order of 8^3 cells, or consecutive rows")
     ap.add_argument("--prepare-only", default="", metavar="DIR",
@@ -247,7 +274,6 @@ def main():
         print(json.dumps(decoder_bench(args)))
         return
 
-    import numpy as np
     import torch
 
     if args.copy_calibration:
@@ -263,97 +289,51 @@ def main():
     pkg = load_package()
     import trellis_cpp_amd.shells as shells
     pkg.lib()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
+    torch.cuda.set_device(torch.device("cuda:0"))
 
     w = shells.workload(args.workload)
-    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w.dtype]
-    coords = torch.from_numpy(w.coords).to(dev)
-    feats = torch.from_numpy(w.feats).to(tdt).to(dev)
-    weight = torch.from_numpy(w.weight).to(tdt).to(dev)
-    bias = torch.from_numpy(w.bias).to(dev)
-    out = torch.empty((w.n, w.co), dtype=tdt, device=dev)
-    stream = torch.cuda.current_stream()
-
-    # neighbour table: built once, timed on its own
-    nbr = pkg.rulebook_build(coords)
-    torch.cuda.synchronize()
-    rb_ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    rb_ev[0].record(stream)
-    for _ in range(5):
-        nbr = pkg.rulebook_build(coords, check=False)
-    rb_ev[1].record(stream)
-    torch.cuda.synchronize()
-    rulebook_ms = rb_ev[0].elapsed_time(rb_ev[1]) / 5
-    pairs = pkg.count_pairs(nbr, w.n)
-
-    # The MFMA path runs with a conv plan of the table and packed weights, both built once
-    # (like the table, a plan serves every conv of a stage; weights are packed at model load).
-    planned = (args.algo in ("auto", "mfma") and w.dtype in ("bf16", "f16")
-               and w.ci % 16 == 0 and w.co % 64 == 0)
-    plan_ms = None
-    if planned:
-        # tiles in the Morton order of the voxels' 8^3 cells (or, with --plan-order rows, runs of
-        # consecutive rows)
-        pcoords = coords if args.plan_order == "morton" else None
-        plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
-        packed = pkg.conv_weight_pack(weight)
-        torch.cuda.synchronize()
-        rb_ev[0].record(stream)
-        for _ in range(5):
-            plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
-        rb_ev[1].record(stream)
-        torch.cuda.synchronize()
-        plan_ms = rb_ev[0].elapsed_time(rb_ev[1]) / 5
-
-        def step():
-            pkg.subm_conv3x3_planned(feats, nbr, plan, packed, bias, w.co, out=out)
-    else:
-        def step():
-            pkg.subm_conv3x3(feats, nbr, weight, bias, out=out, algo=args.algo)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    t0 = time.perf_counter()
-    ev[0].record(stream)
-    for _ in range(args.steps):
-        step()
-    ev[1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = ev[0].elapsed_time(ev[1]) / args.steps
-
+    r = time_conv(pkg, w, args, args.steps, args.warmup)
+    ms, pairs, planned = r["ms"], r["pairs"], r["planned"]
     flops = 2.0 * w.ci * w.co * pairs
     flops_dense = 2.0 * w.ci * w.co * 27 * w.n
-    es = 2 if w.dtype != "f32" else 4
-    compulsory = w.n * w.ci * es + w.n * w.co * es + 27 * w.ci * w.co * es + 4 * w.co + 108 * w.n
-    tflops = flops / (ms * 1e-3) / 1e12
-    peak = PEAK_TFLOPS[w.dtype]
-    bound = "mfma" if flops / compulsory > peak * 1e12 / (PEAK_HBM_GBS * 1e9) else "hbm"
-    if bound == "mfma":
-        roof = {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s",
-                "frac": tflops / peak}
-    else:
-        gbs = compulsory / (ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": gbs / PEAK_HBM_GBS}
+    compulsory = compulsory_bytes(w)
+    roof = roofline(w, flops, compulsory, ms)
     # HBM bytes per launch of the conv kernel, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # passes scaled by a copy kernel of known size (profiles/traffic_<workload>.md)
+    # passes scaled by a copy kernel of known size (profiles/traffic_<workload>.md); used only
+    # while the kernel's sources are the ones that profile measured
     roof["traffic"] = None
     tj = os.path.join(ROOT, "profiles", "traffic.json")
     if planned and os.path.exists(tj):
         rec = json.load(open(tj)).get(w.name)
-        if rec:
+        if rec and rec.get("sources_sha256") == kernel_sources_sha():
             roof["traffic"] = rec["bytes_per_launch"]
             roof["traffic_source"] = rec["source"]
+        elif rec:
+            roof["traffic_note"] = "profile predates the current kernel sources; re-measure"
     roof["algorithmic_flops_per_launch"] = flops
     roof["compulsory_bytes_per_launch"] = compulsory
 
+    # the same conv with f32 output (what the decoders and the parity tests read), and for the
+    # 256^3 C=128 configuration the same shells at ~640K voxels (the size the target names)
+    extra = {}
+    if w.dtype != "f32" and planned:
+        rf = time_conv(pkg, w, args, max(5, args.steps // 2), 2, out_dtype=torch.float32, reuse=r)
+        extra["f32_out"] = {"ms_per_step": rf["ms"], "tflops": flops / (rf["ms"] * 1e-3) / 1e12,
+                            "frac": flops / (rf["ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[w.dtype]}
+    if w.name == "shells256-c128-bf16" and not args.no_extra:
+        w6 = shells.workload("shells600k-c128-bf16")
+        r6 = time_conv(pkg, w6, args, max(5, args.steps // 2), 2)
+        f6 = 2.0 * w6.ci * w6.co * r6["pairs"]
+        extra["shells600k-c128-bf16"] = {
+            "n_voxels": w6.n, "active_pairs": r6["pairs"], "ms_per_step": r6["ms"],
+            "voxels_per_s": w6.n / (r6["ms"] * 1e-3), "tflops": f6 / (r6["ms"] * 1e-3) / 1e12,
+            "frac": f6 / (r6["ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[w6.dtype],
+            "rulebook_ms": r6["rulebook_ms"], "plan_ms": r6["plan_ms"]}
+        del r6
+
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(w, nbr.cpu().numpy(), args.cpu_seconds)
+        cpu = cpu_baseline(w, r["nbr"].cpu().numpy(), args.cpu_seconds)
 
     res = {
         "metric": "active voxels/s & TFLOP/s per sparse conv layer; % MFMA/HBM roofline",
@@ -376,15 +356,113 @@ def main():
             "plan_order": args.plan_order if planned else None,
             "parallelism": "single-gpu",
         },
-        "tflops": tflops,
+        "tflops": flops / (ms * 1e-3) / 1e12,
         "tflops_dense27_equivalent": flops_dense / (ms * 1e-3) / 1e12,
-        "rulebook_ms": rulebook_ms,
-        "plan_ms": plan_ms,
-        "wall_s_timed_region": wall,
+        "rulebook_ms": r["rulebook_ms"],
+        "plan_ms": r["plan_ms"],
+        "wall_s_timed_region": r["wall"],
+        "gpu": torch.cuda.get_device_name(0),
         "roofline": roof,
+        "extra": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))
+
+
+def kernel_sources_sha() -> str:
+    """sha256 over the conv kernel's sources: a traffic profile is valid for these only."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in ("conv_halo.hip", "tile_plan.hpp", "plan.hip", "conv_internal.hpp", "common.hpp"):
+        with open(os.path.join(ROOT, "trellis.cpp_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
+def compulsory_bytes(w) -> float:
+    es = 2 if w.dtype != "f32" else 4
+    return w.n * w.ci * es + w.n * w.co * es + 27 * w.ci * w.co * es + 4 * w.co + 108 * w.n
+
+
+def roofline(w, flops: float, compulsory: float, ms: float) -> dict:
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[w.dtype]
+    if flops / compulsory > peak * 1e12 / (PEAK_HBM_GBS * 1e9):
+        return {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s", "frac": tflops / peak}
+    gbs = compulsory / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}
+
+
+def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None) -> dict:
+    """Times one conv of workload w: the neighbour table and (16-bit, matrix-core shapes) the
+    conv plan are built and timed first, each on its own (reuse: the table and plan of an
+    earlier call on the same workload); then `steps` convs between two HIP events on the
+    stream the kernel runs on."""
+    import torch
+    dev = torch.device("cuda:0")
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w.dtype]
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    if reuse is None:
+        coords = torch.from_numpy(w.coords).to(dev)
+        feats = torch.from_numpy(w.feats).to(tdt).to(dev)
+        weight = torch.from_numpy(w.weight).to(tdt).to(dev)
+        bias = torch.from_numpy(w.bias).to(dev)
+        # neighbour table: built once, timed on its own
+        nbr = pkg.rulebook_build(coords)
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        for _ in range(5):
+            nbr = pkg.rulebook_build(coords, check=False)
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        rulebook_ms = ev[0].elapsed_time(ev[1]) / 5
+        pairs = pkg.count_pairs(nbr, w.n)
+    else:
+        coords, feats, weight, bias, nbr = (reuse[k] for k in ("coords", "feats", "weight", "bias", "nbr"))
+        rulebook_ms, pairs = reuse["rulebook_ms"], reuse["pairs"]
+    out = torch.empty((w.n, w.co), dtype=out_dtype or tdt, device=dev)
+
+    # The MFMA path runs with a conv plan of the table and packed weights, both built once
+    # (like the table, a plan serves every conv of a stage; weights are packed at model load).
+    planned = (args.algo in ("auto", "mfma") and w.dtype in ("bf16", "f16")
+               and w.ci % 16 == 0 and w.co % 64 == 0)
+    plan = packed = plan_ms = None
+    if planned and reuse is not None:
+        plan, packed, plan_ms = reuse["plan"], reuse["packed"], reuse["plan_ms"]
+    elif planned:
+        # tiles in the Morton order of the voxels' 8^3 cells (or, with --plan-order rows, runs of
+        # consecutive rows)
+        pcoords = coords if args.plan_order == "morton" else None
+        plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
+        packed = pkg.conv_weight_pack(weight)
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        for _ in range(5):
+            plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        plan_ms = ev[0].elapsed_time(ev[1]) / 5
+    if planned:
+        def step():
+            pkg.subm_conv3x3_planned(feats, nbr, plan, packed, bias, w.co, out=out, out_dtype=out.dtype)
+    else:
+        def step():
+            pkg.subm_conv3x3(feats, nbr, weight, bias, out=out, out_dtype=out.dtype, algo=args.algo)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for _ in range(steps):
+        step()
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return {"ms": ev[0].elapsed_time(ev[1]) / steps, "wall": wall, "pairs": pairs, "planned": planned,
+            "rulebook_ms": rulebook_ms, "plan_ms": plan_ms, "coords": coords, "feats": feats,
+            "weight": weight, "bias": bias, "nbr": nbr, "plan": plan, "packed": packed}
 
 
 if __name__ == "__main__":

@@ -547,11 +547,14 @@ __device__ __forceinline__ void conv_tiles(
                 // all 27 taps unrolled: register rings stay static and every wait is exact
 #pragma unroll
                 for (int t = 0; t < kTaps; ++t) {
-                    // The higher issue priority on odd taps, the lower on even ones (every wave
-                    // alike), so that waves at different taps of the slice are not served
-                    // alike. Against equal priorities this measured 3.5 % faster at 128 output
-                    // channels and the same at 64; priority on the even taps instead, 0.5 % slower.
-                    if (t & 1) __builtin_amdgcn_s_setprio(1);
+                    // The higher issue priority on alternate taps, so that waves at different
+                    // taps of the slice are not served alike: at 128 output channels even and
+                    // odd waves alternate it (neighbouring SIMDs in turn), at 64 every wave takes
+                    // it on the odd taps. Against equal priorities, 3.5 % faster at 128 and the
+                    // same at 64. (At 128 the wave-uniform branch also keeps the scheduler from
+                    // interleaving taps: the every-wave-alike form there doubles the spills and
+                    // runs 2.3 % slower; at 64, with no spills, it is 1 % faster.)
+                    if ((BN == 128 ? t + wave : t) & 1) __builtin_amdgcn_s_setprio(1);
                     else __builtin_amdgcn_s_setprio(0);
                     // weights PD taps ahead (the first taps of the next slice at the end)
                     if (t + PD < kTaps) load_b(t + PD, kc, bR[(R0 + t + PD) % (PD + 1)]);

@@ -22,8 +22,7 @@ constexpr int RS_ROUNDS = 16;               // items per thread and pass
 constexpr int RS_TILE = RS_NT * RS_ROUNDS;  // items per sort workgroup
 constexpr int RS_BINS = 256;
 constexpr int RS_PASSES = 3;                // 24-bit keys
-constexpr int RS_SCAN_NT = 1024;
-constexpr int RS_SCAN_PER = 8;
+constexpr int RS_SCAN_NT = 256;
 
 // bits of v (8 used) spread to every third position
 __device__ __forceinline__ uint32_t spread3(uint32_t v) {
@@ -61,21 +60,18 @@ __global__ __launch_bounds__(RS_NT) void k_rs_hist(const uint32_t* __restrict__ 
     if (tid < RS_BINS) hist[(int64_t)tid * nblk + blockIdx.x] = sH[tid];
 }
 
-// exclusive prefix sum of a[0, m) in place (one workgroup, RS_SCAN_PER consecutive values per thread)
-__global__ __launch_bounds__(RS_SCAN_NT) void k_rs_scan(int32_t* __restrict__ a, int64_t m) {
+// Exclusive prefix sum of one digit's row hist[digit * nblk + 0 .. nblk) in place (a workgroup per
+// digit), its total into tot[digit]. The digits' bases are added by the scatter.
+__global__ __launch_bounds__(RS_SCAN_NT) void k_rs_scan_rows(int32_t* __restrict__ hist, int nblk,
+                                                             int32_t* __restrict__ tot) {
     __shared__ int sW[RS_SCAN_NT / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int32_t* a = hist + (int64_t)blockIdx.x * nblk;
     int carry = 0;
-    for (int64_t t0 = 0; t0 < m; t0 += (int64_t)RS_SCAN_NT * RS_SCAN_PER) {
-        const int64_t i0 = t0 + (int64_t)tid * RS_SCAN_PER;
-        int v[RS_SCAN_PER];
-        int sum = 0;
-#pragma unroll
-        for (int k = 0; k < RS_SCAN_PER; ++k) {
-            v[k] = i0 + k < m ? a[i0 + k] : 0;
-            sum += v[k];
-        }
-        int x = sum;   // inclusive scan over the wave
+    for (int t0 = 0; t0 < nblk; t0 += RS_SCAN_NT) {
+        const int i = t0 + tid;
+        const int v = i < nblk ? a[i] : 0;
+        int x = v;   // inclusive scan over the wave
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int y = __shfl_up(x, off, 64);
@@ -89,15 +85,11 @@ __global__ __launch_bounds__(RS_SCAN_NT) void k_rs_scan(int32_t* __restrict__ a,
             before += w < wave ? sW[w] : 0;
             total += sW[w];
         }
-        int run = carry + before + x - sum;
-#pragma unroll
-        for (int k = 0; k < RS_SCAN_PER; ++k) {
-            if (i0 + k < m) a[i0 + k] = run;
-            run += v[k];
-        }
+        if (i < nblk) a[i] = carry + before + x - v;
         carry += total;
-        __syncthreads();   // sW is rewritten by the next tile
+        __syncthreads();   // sW is rewritten by the next round
     }
+    if (tid == 0) tot[blockIdx.x] = carry;
 }
 
 // Stable scatter of each workgroup's RS_TILE (key, value) pairs to their digit's range. Pairs are
@@ -105,16 +97,34 @@ __global__ __launch_bounds__(RS_SCAN_NT) void k_rs_scan(int32_t* __restrict__ a,
 // lane's rank among its wave's lanes of the same digit comes from ballots of the digit's 8 bits.
 __global__ __launch_bounds__(RS_NT) void k_rs_scatter(const uint32_t* __restrict__ kin,
                                                       const int32_t* __restrict__ vin, int64_t n, int shift,
-                                                      const int32_t* __restrict__ off, int nblk,
-                                                      uint32_t* __restrict__ kout, int32_t* __restrict__ vout) {
+                                                      const int32_t* __restrict__ off, const int32_t* __restrict__ tot,
+                                                      int nblk, uint32_t* __restrict__ kout,
+                                                      int32_t* __restrict__ vout) {
     constexpr int NW = RS_NT / 64;
+    static_assert(RS_BINS == 4 * 64 && NW >= 4, "digit bases: four waves of 64 digits");
     __shared__ int sCnt[NW][RS_BINS];   // a round's count (then first rank) per (wave, digit)
     __shared__ int sRun[RS_BINS];       // pairs of each digit placed by earlier rounds
     __shared__ int sGlob[RS_BINS];      // the workgroup's first position per digit
+    __shared__ int sTot[4];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the digit's base (exclusive scan of the digit totals) + this workgroup's offset in its row
+    int dbase = 0;
     if (tid < RS_BINS) {
+        const int t = tot[tid];
+        int x = t;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) sTot[wave] = x;
+        dbase = x - t;
+    }
+    __syncthreads();
+    if (tid < RS_BINS) {
+        for (int w = 0; w < wave; ++w) dbase += sTot[w];
         sRun[tid] = 0;
-        sGlob[tid] = off[(int64_t)tid * nblk + blockIdx.x];
+        sGlob[tid] = dbase + off[(int64_t)tid * nblk + blockIdx.x];
     }
     const int64_t base = (int64_t)blockIdx.x * RS_TILE;
     const uint64_t below = (1ull << lane) - 1ull;
@@ -159,11 +169,12 @@ struct SortScratch {
     uint32_t* keys[2];
     int32_t* vals[2];
     int32_t* hist;
+    int32_t* tot;
     int nblk;
 };
 size_t sort_scratch_bytes(int64_t n) {
     const int64_t nblk = ceil_div(std::max<int64_t>(n, 1), RS_TILE);
-    return 4 * align256((size_t)n * 4) + align256((size_t)nblk * RS_BINS * 4);
+    return 4 * align256((size_t)n * 4) + align256((size_t)nblk * RS_BINS * 4) + align256(RS_BINS * 4);
 }
 SortScratch carve_sort(void* p, int64_t n) {
     char* c = reinterpret_cast<char*>(p);
@@ -176,6 +187,8 @@ SortScratch carve_sort(void* p, int64_t n) {
     }
     s.hist = reinterpret_cast<int32_t*>(c);
     s.nblk = (int)ceil_div(std::max<int64_t>(n, 1), RS_TILE);
+    c += align256((size_t)s.nblk * RS_BINS * 4);
+    s.tot = reinterpret_cast<int32_t*>(c);
     return s;
 }
 
@@ -185,16 +198,15 @@ int morton_order(const int32_t* coords, int64_t n, const SortScratch& ss, hipStr
     hipLaunchKernelGGL(k_order_keys, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, coords, n,
                        ss.keys[0], ss.vals[0]);
     TSP_CHECK_LAUNCH();
-    const int64_t m = (int64_t)RS_BINS * ss.nblk;
     int cur = 0;
     for (int pass = 0; pass < RS_PASSES; ++pass, cur ^= 1) {
         const int shift = 8 * pass;
         hipLaunchKernelGGL(k_rs_hist, dim3(ss.nblk), dim3(RS_NT), 0, s, ss.keys[cur], n, shift, ss.hist, ss.nblk);
         TSP_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_rs_scan, dim3(1), dim3(RS_SCAN_NT), 0, s, ss.hist, m);
+        hipLaunchKernelGGL(k_rs_scan_rows, dim3(RS_BINS), dim3(RS_SCAN_NT), 0, s, ss.hist, ss.nblk, ss.tot);
         TSP_CHECK_LAUNCH();
         hipLaunchKernelGGL(k_rs_scatter, dim3(ss.nblk), dim3(RS_NT), 0, s, ss.keys[cur], ss.vals[cur], n, shift,
-                           ss.hist, ss.nblk, ss.keys[cur ^ 1], ss.vals[cur ^ 1]);
+                           ss.hist, ss.tot, ss.nblk, ss.keys[cur ^ 1], ss.vals[cur ^ 1]);
         TSP_CHECK_LAUNCH();
     }
     *order = ss.vals[cur];

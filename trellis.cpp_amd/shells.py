@@ -217,6 +217,8 @@ def workload(name: str) -> ConvWorkload:
                              in 256^3; C=128 bf16, Kaiming W ~ N(0, sqrt(2/(27*128))), seed 2
     band512-c64-bf16         the seed-3 256^3 shell set subdivided 2x and pruned to the
                              thickness-2 band at 512^3; C=64 bf16, W ~ N(0, 1/sqrt(27*64))
+    shells600k-c128-bf16     shells256-c128-bf16 with the semi-axes drawn from U[24,66] (0.6x),
+                             so the set has ~640K voxels, the size the 256^3 C=128 target names
     """
     if name == "shell64-c64-f32":
         rng = np.random.default_rng(0)
@@ -231,6 +233,11 @@ def workload(name: str) -> ConvWorkload:
     if name == "shells256-c128-bf16":
         rng = np.random.default_rng(2)
         coords = band_voxels(random_shapes(rng, 256, 8, 40, 110, boxes=True), 256, 2.0)
+        f, w, b = conv_inputs(rng, len(coords), 128, 128, np.sqrt(2 / (27 * 128)), "bf16", 0.1)
+        return ConvWorkload(name, coords, f, w, b, "bf16", 256, workload.__doc__)
+    if name == "shells600k-c128-bf16":
+        rng = np.random.default_rng(2)
+        coords = band_voxels(random_shapes(rng, 256, 8, 24, 66, boxes=True), 256, 2.0)
         f, w, b = conv_inputs(rng, len(coords), 128, 128, np.sqrt(2 / (27 * 128)), "bf16", 0.1)
         return ConvWorkload(name, coords, f, w, b, "bf16", 256, workload.__doc__)
     if name == "band512-c64-bf16":
@@ -254,7 +261,7 @@ def band512_parents():
 
 
 WORKLOADS = ("shell64-c64-f32", "ellipsoids128-c256-bf16", "shells256-c128-bf16",
-             "band512-c64-bf16")
+             "band512-c64-bf16", "shells600k-c128-bf16")
 
 
 def random_distinct_voxels(n: int, extent: int, seed: int) -> np.ndarray:
