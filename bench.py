@@ -28,6 +28,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 
 PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # MI355X dense, datasheet
 PEAK_HBM_GBS = 8000.0
+# fp32 FMA on the VALU without packed-fp32 instructions (which this build does not emit):
+# 256 CUs x 4 SIMDs x 16 lanes x 2 FLOP x 2.4 GHz
+PEAK_VALU_TFLOPS = 78.6
 
 
 def _load(name, path, pkg_dir=None):
@@ -252,7 +255,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="shells256-c128-bf16")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather", "thin"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the ~640K-voxel variant of the C=128 set")
@@ -297,7 +300,10 @@ def main():
     flops = 2.0 * w.ci * w.co * pairs
     flops_dense = 2.0 * w.ci * w.co * 27 * w.n
     compulsory = compulsory_bytes(w)
-    roof = roofline(w, flops, compulsory, ms)
+    # the matrix-core kernels take 16-bit features with Ci % 16 (planned) / 32 and Co % 64 == 0;
+    # everything else runs on a VALU kernel (the thin one for Co <= 32)
+    mfma_shape = w.dtype in ("bf16", "f16") and w.co % 64 == 0 and w.ci % 16 == 0
+    roof = roofline(w, flops, compulsory, ms, valu=not mfma_shape)
     # HBM bytes per launch of the conv kernel, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
     # passes scaled by a copy kernel of known size (profiles/traffic_<workload>.md); used only
     # while the kernel's sources are the ones that profile measured
@@ -352,7 +358,9 @@ def main():
             "workload": w.name, "grid": w.grid, "n_voxels": w.n, "active_pairs": pairs,
             "pairs_per_voxel": pairs / max(w.n, 1), "c_in": w.ci, "c_out": w.co,
             "accumulate": "f32", "out_dtype": w.dtype,
-            "algo": "mfma-planned" if planned else args.algo,
+            "algo": "mfma-planned" if planned else (
+                "thin" if args.algo in ("auto", "thin") and w.co in (4, 8, 16, 32) and w.ci % 4 == 0
+                and w.ci * w.co <= 512 else args.algo),
             "plan_order": args.plan_order if planned else None,
             "parallelism": "single-gpu",
         },
@@ -384,8 +392,16 @@ def compulsory_bytes(w) -> float:
     return w.n * w.ci * es + w.n * w.co * es + 27 * w.ci * w.co * es + 4 * w.co + 108 * w.n
 
 
-def roofline(w, flops: float, compulsory: float, ms: float) -> dict:
+def roofline(w, flops: float, compulsory: float, ms: float, valu: bool = False) -> dict:
+    """The bound of the conv kernel: the matrix cores (or, for the VALU kernels, fp32 FMA issue)
+    when its FLOPs over the compulsory bytes exceed the ridge of that peak over HBM's, else HBM."""
     tflops = flops / (ms * 1e-3) / 1e12
+    if valu:
+        peak = PEAK_VALU_TFLOPS
+        if flops / compulsory > peak * 1e12 / (PEAK_HBM_GBS * 1e9):
+            return {"bound": "valu", "achieved": tflops, "peak": peak, "unit": "TFLOP/s", "frac": tflops / peak}
+        gbs = compulsory / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}
     peak = PEAK_TFLOPS[w.dtype]
     if flops / compulsory > peak * 1e12 / (PEAK_HBM_GBS * 1e9):
         return {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s", "frac": tflops / peak}

@@ -636,3 +636,73 @@ def test_nonfinite_weight_runs_every_tap(gpu_lib, shells, bad):
     assert np.isnan(want[:, 5]).any()
     assert np.array_equal(np.isnan(got), np.isnan(want))
     assert np.array_equal(got[~np.isnan(want)], want[~np.isnan(want)])
+
+
+@pytest.mark.parametrize("ci,co", [(4, 4), (8, 8), (16, 16), (32, 16), (16, 32), (64, 8), (128, 4)])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16", "f32xf16"])
+def test_thin_vs_oracle(gpu_lib, orc, shells, ci, co, dt):
+    """The thin-channel VALU kernel (one voxel's output row per thread) at every width it takes,
+    for f32, bf16, f16 and f32 features with f16 weights; chosen by AUTO for these shapes and
+    by algo="thin" explicitly (the same results)."""
+    _case(f"thin ci={ci} co={co} {dt}")
+    import torch
+    rng = np.random.default_rng(ci * 7 + co)
+    fkey, wkey = {"f32": ("f32", "f32"), "bf16": ("bf16", "bf16"), "f16": ("f16", "f16"),
+                  "f32xf16": ("f32", "f16")}[dt]
+    coords, feats, weight, bias = _rand_case(shells, rng, 3000, ci, co, "f32")
+    feats, weight = shells.round_to(feats, fkey), shells.round_to(weight, wkey)
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    out, nbr = _run(gpu_lib, coords, feats, weight, bias, tdt[fkey], wdtype=tdt[wkey])
+    tol = TOL_32 if fkey == "f32" and wkey == "f32" else (TOL_32 if fkey == "f32" else TOL_16)
+    assert orc.rel_err(out, ref) < tol
+    out2, _ = _run(gpu_lib, coords, feats, weight, bias, tdt[fkey], wdtype=tdt[wkey], algo="thin")
+    assert np.array_equal(out, out2)
+    if fkey != "f32":   # 16-bit output: one rounding more
+        o16, _ = _run(gpu_lib, coords, feats, weight, bias, tdt[fkey], out_dtype=tdt[fkey], algo="thin")
+        assert orc.rel_err(o16, ref) < TOL_16_OUT
+
+
+@pytest.mark.parametrize("mode", ["nan_row0", "zero_pad", "row0_source"])
+def test_thin_padding_row(gpu_lib, orc, shells, mode):
+    """The thin kernel's padding row: a NaN in row 0 makes every row with an absent tap NaN;
+    TSP_CONV_ZERO_PAD reads an exact zero row (only row 0's neighbours turn non-finite); an f32
+    source row that is finite gives a zero padding row although its f16 rounding overflows."""
+    _case(f"thin padding {mode}")
+    import torch
+    rng = np.random.default_rng(41)
+    coords = np.ascontiguousarray(np.concatenate([shells.sphere_shell(24, 12.0, 7.0, 9.0),
+                                                  np.stack(np.meshgrid(*[np.arange(40, 45)] * 3, indexing="ij"),
+                                                           -1).reshape(-1, 3)]), np.int32)
+    n, ci, co = len(coords), 16, 16
+    feats = rng.standard_normal((n, ci)).astype(np.float32)
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / 20).astype(np.float32), "f16")
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    t = nbr.reshape(27, n)
+    absent, refs0 = (t == n).any(axis=0), (t == 0).any(axis=0)
+    c = torch.from_numpy(coords).cuda()
+    nbr_d = gpu_lib.rulebook_build(c)
+    w, b = _dev(weight, torch.float16), _dev(bias, torch.float32)
+    if mode == "nan_row0":
+        feats[0, 3] = np.nan
+        f16 = shells.round_to(feats, "f16")
+        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo="thin")
+        out = out.cpu().numpy()
+        assert np.isnan(out[absent]).all()
+        keep = ~absent & ~refs0
+        assert orc.rel_err(out[keep], orc.subm_conv_f64(f16, nbr, weight, bias)[keep]) < TOL_16
+    elif mode == "zero_pad":
+        feats[0, 3] = np.inf
+        f16 = shells.round_to(feats, "f16")
+        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo="thin",
+                                   zero_pad=True).cpu().numpy()
+        assert np.isfinite(out[~refs0]).all()
+        _nan_aware(out, orc.subm_conv_f64(f16, nbr, weight, bias, zero_pad=True), TOL_16)
+    else:
+        feats[0, 3] = 1.0e5                         # finite, > 65504: rounds to Inf
+        f16 = shells.round_to(feats, "f16")
+        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo="thin",
+                                   row0=_dev(feats[0], torch.float32)).cpu().numpy()
+        assert np.isfinite(out[~refs0]).all()
+        _nan_aware(out, orc.subm_conv_f64(f16, nbr, weight, bias, row0=feats[0]), TOL_16)

@@ -63,7 +63,7 @@ int run_conv(const void* x, int xdt, int64_t n, int ci, const int32_t* nbr, cons
         return tsp_subm_conv3x3_planned_ex(x, xdt, n, ci, nbr, plan, packed, bias, co, out, TSP_F32, flags, row0, s);
     }
     return tsp_subm_conv3x3_ex(x, xdt, n, ci, nbr, w, wdt, bias, co, out, TSP_F32,
-                               is16(xdt) && xdt == wdt ? TSP_ALGO_AUTO : TSP_ALGO_NARROW, flags, row0, s);
+                               TSP_ALGO_AUTO, flags, row0, s);
 }
 
 // the rows of one MLP chunk: its f32 hidden layer [chunk][4C] stays within 1 GiB
@@ -162,7 +162,7 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
                                              nullptr, s);
         else
             st = tsp_subm_conv3x3_ex(h0, in1, n, cin, nbr, w.conv1_weight, w.conv1_dtype, w.conv1_bias, 8 * cout, h1,
-                                     TSP_F32, is16(in1) && in1 == w.conv1_dtype ? TSP_ALGO_AUTO : TSP_ALGO_NARROW, 0,
+                                     TSP_F32, TSP_ALGO_AUTO, 0,
                                      nullptr, s);
         if (!st) st = tsp_c2s_gather(h1, TSP_F32, gidx, m, cout, g, s);
     }
@@ -181,7 +181,7 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
                                          TSP_CONV_ZERO_PAD, nullptr, s);
     else
         st = tsp_subm_conv3x3_ex(h2, in2, m, cout, cnbr, w.conv2_weight, w.conv2_dtype, w.conv2_bias, cout, out,
-                                 TSP_F32, is16(in2) && in2 == w.conv2_dtype ? TSP_ALGO_AUTO : TSP_ALGO_NARROW,
+                                 TSP_F32, TSP_ALGO_AUTO,
                                  TSP_CONV_ZERO_PAD, nullptr, s);
     if (st) return st;
     return tsp_c2s_skip_add(x, TSP_F32, gidx, m, cin, cout, out, TSP_F32, s);

@@ -84,4 +84,11 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                      const void* plan, const void* weight, const float* bias, int co, void* out,
                      hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {});
 
+// The thin-channel VALU conv (conv_thin.hip): Co in {4, 8, 16, 32}, Ci % 4 == 0, Ci * Co <= 512,
+// a neighbour table, 16-byte aligned features. Returns TSP_ERR_UNSUPPORTED (with no message) for
+// anything else.
+bool thin_fits(int ci, int co);
+int thin_conv_launch(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+                     const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad);
+
 }  // namespace tsp

@@ -88,7 +88,7 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
             "sparse conv");
     } else {
         if (!sc.running()) return;
-        lib(tsp_subm_conv3x3_ex(xr, c.xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32, TSP_ALGO_NARROW,
+        lib(tsp_subm_conv3x3_ex(xr, c.xdt, n, c.ci, nbr, c.w->data, c.wdt, bias, c.co, out, TSP_F32, TSP_ALGO_AUTO,
                                 0, row0, s),
             "sparse conv");
     }

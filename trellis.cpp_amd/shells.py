@@ -219,6 +219,8 @@ def workload(name: str) -> ConvWorkload:
                              thickness-2 band at 512^3; C=64 bf16, W ~ N(0, 1/sqrt(27*64))
     shells600k-c128-bf16     shells256-c128-bf16 with the semi-axes drawn from U[24,66] (0.6x),
                              so the set has ~640K voxels, the size the 256^3 C=128 target names
+    shells256-c8-bf16        the shells256 voxel set with C=8 bf16 (a thin layer: the VALU path),
+                             W ~ N(0, 1/sqrt(27*8)), seed 2
     """
     if name == "shell64-c64-f32":
         rng = np.random.default_rng(0)
@@ -234,6 +236,11 @@ def workload(name: str) -> ConvWorkload:
         rng = np.random.default_rng(2)
         coords = band_voxels(random_shapes(rng, 256, 8, 40, 110, boxes=True), 256, 2.0)
         f, w, b = conv_inputs(rng, len(coords), 128, 128, np.sqrt(2 / (27 * 128)), "bf16", 0.1)
+        return ConvWorkload(name, coords, f, w, b, "bf16", 256, workload.__doc__)
+    if name == "shells256-c8-bf16":
+        rng = np.random.default_rng(2)
+        coords = band_voxels(random_shapes(rng, 256, 8, 40, 110, boxes=True), 256, 2.0)
+        f, w, b = conv_inputs(rng, len(coords), 8, 8, 1 / np.sqrt(27 * 8), "bf16", 0.1)
         return ConvWorkload(name, coords, f, w, b, "bf16", 256, workload.__doc__)
     if name == "shells600k-c128-bf16":
         rng = np.random.default_rng(2)
@@ -261,7 +268,7 @@ def band512_parents():
 
 
 WORKLOADS = ("shell64-c64-f32", "ellipsoids128-c256-bf16", "shells256-c128-bf16",
-             "band512-c64-bf16", "shells600k-c128-bf16")
+             "band512-c64-bf16", "shells600k-c128-bf16", "shells256-c8-bf16")
 
 
 def random_distinct_voxels(n: int, extent: int, seed: int) -> np.ndarray:
