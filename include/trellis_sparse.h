@@ -120,12 +120,14 @@ int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
  * the neighbour table -- shared by every conv of a decoder stage, shape_decoder.cpp:93-103 --
  * and what depends only on the weights, loaded once per model, trellis_model.cpp:96-142).
  *
- * A plan splits the voxels into tiles of 512 and holds, for each tile, its voxels' rows (in
- * increasing order inside the tile), the sorted set of input rows their table entries reference
- * and each entry's rank in that set (the planned conv stages those rows in LDS once per tile).
+ * A plan splits the voxels into tiles of 512 and holds, for each tile, its voxels' rows (grouped
+ * by their set of present taps inside the tile), which taps each 32-row block of them has, the
+ * sorted set of input rows their table entries reference and each entry's rank in that set (the
+ * planned conv stages those rows in LDS once per tile).
  * Packed weights hold W [Co][27][Ci] in the order the matrix-core operands are read. Both are
- * plain device buffers owned by the caller; every tap of every voxel is computed, so the results
- * of a planned conv do not depend on how the plan grouped the voxels.
+ * plain device buffers owned by the caller. Every present tap of every voxel is computed, in the
+ * same order, so the results of a planned conv do not depend on how the plan grouped the voxels
+ * (a skipped absent tap only adds exact zeros, see tsp_conv_weight_pack).
  * ------------------------------------------------------------------------------------- */
 size_t tsp_conv_plan_bytes(int64_t n);
 /* Tiles of 512 consecutive rows. d_plan 16-byte aligned, plan_bytes >= tsp_conv_plan_bytes(n). */
@@ -138,9 +140,16 @@ int tsp_conv_plan_build(const int32_t* d_nbr, int64_t n, void* d_plan, size_t pl
 int tsp_conv_plan_build_ordered(const int32_t* d_nbr, const int32_t* d_coords, int64_t n,
                                 void* d_plan, size_t plan_bytes, void* stream);
 
-/* W [co][27][ci] (f16 or bf16; ci % 16 == 0, co % 32 == 0) -> d_packed, same byte size. */
+/* W [co][27][ci] (f16 or bf16; ci % 16 == 0, co % 32 == 0) -> d_packed, which must hold
+ * tsp_conv_weight_packed_bytes(ci, co) bytes: the 27*ci*co values in operand order, then a
+ * 256-byte trailer that records whether some weight is an Inf or a NaN. With finite weights the
+ * planned convs skip the matrix-core work of a tap that is absent from a whole 32-row block of a
+ * tile (it would add exact zeros); with a non-finite weight they compute it, since the padding
+ * row times an Inf or a NaN is NaN, as in the reference's mul_mat. */
 int tsp_conv_weight_pack(const void* d_weight, int dtype, int ci, int co, void* d_packed,
                          void* stream);
+/* Bytes of packed weights for ci input and co output channels (0 for non-positive sizes). */
+size_t tsp_conv_weight_packed_bytes(int ci, int co);
 
 /* The conv of tsp_subm_conv3x3 (MFMA kernel) with a plan of d_nbr and packed weights:
  * f16/bf16 features, ci % 16 == 0, co % 64 == 0, out f32 or the feature dtype. d_nbr is still

@@ -101,6 +101,9 @@ def test_plan_and_pack_validation(pkg):
     assert L.tsp_conv_weight_pack(FAKE, 2, 40, 64, ctypes.c_void_p(0x2000), NULL) == 4   # ci%16
     assert L.tsp_conv_weight_pack(FAKE, 2, 64, 48, ctypes.c_void_p(0x2000), NULL) == 4   # co%32
     assert L.tsp_conv_weight_pack(FAKE, 2, 64, 64, FAKE, NULL) == 1                      # aliased
+    # the packed values, then the 256-byte trailer (the non-finite flag)
+    assert L.tsp_conv_weight_packed_bytes(64, 128) == 27 * 64 * 128 * 2 + 256
+    assert L.tsp_conv_weight_packed_bytes(0, 64) == 0 and L.tsp_conv_weight_packed_bytes(64, -1) == 0
     p = lambda **kw: L.tsp_subm_conv3x3_planned(
         kw.get("feats", FAKE), kw.get("dt", 2), kw.get("n", 100), kw.get("ci", 64), FAKE,
         FAKE, FAKE, FAKE, kw.get("co", 64), kw.get("out", ctypes.c_void_p(0x2000)),
@@ -234,7 +237,7 @@ def test_python_conv_argument_checks(pkg):
     with pytest.raises(ValueError, match="27\\*N"):
         pkg.subm_conv3x3(f, nbr.to(torch.int64), w, b)
     plan_ok = torch.zeros(pkg.lib().tsp_conv_plan_bytes(n), dtype=torch.uint8)
-    packed = torch.zeros(co * 27 * ci, dtype=torch.bfloat16)
+    packed = torch.zeros(pkg.lib().tsp_conv_weight_packed_bytes(ci, co) // 2, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="plan holds"):
         pkg.subm_conv3x3_planned(f, nbr, plan_ok[:-1], packed, b, co)
     with pytest.raises(ValueError, match="packed weight is"):

@@ -247,9 +247,34 @@ def test_weight_pack_layout(gpu_lib):
     ci, co = 48, 96
     w = torch.arange(co * 27 * ci, dtype=torch.float32).reshape(co, 27, ci)
     w16 = (w % 2048).to(torch.float16)        # exactly representable, all distinct per 2048
-    packed = gpu_lib.conv_weight_pack(w16.cuda()).cpu().reshape(co // 32, ci // 16, 27, 2, 32, 8)
+    flat = gpu_lib.conv_weight_pack(w16.cuda()).cpu()
+    assert flat.numel() == co * 27 * ci + 128                 # + the 256-byte trailer
+    packed = flat[:co * 27 * ci].reshape(co // 32, ci // 16, 27, 2, 32, 8)
     ref = w16.reshape(co // 32, 32, 27, ci // 16, 2, 8).permute(0, 3, 2, 4, 1, 5)
     assert torch.equal(packed, ref)
+    trailer = flat[co * 27 * ci:].view(torch.int32)
+    assert int(trailer[0]) == 0 and not trailer.any()         # finite weights
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("bad", ["none", "inf", "-inf", "nan", "max"])
+def test_weight_pack_nonfinite_flag(gpu_lib, dt, bad):
+    """The trailer's first word is nonzero exactly when some weight is an Inf or a NaN (the
+    largest finite value does not count), wherever it sits."""
+    _case(f"weight pack trailer {dt} {bad}")
+    import torch
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    ci, co = 32, 64
+    w = torch.randn(co, 27, ci).to(tdt)
+    if bad != "none":
+        val = {"inf": float("inf"), "-inf": float("-inf"), "nan": float("nan"),
+               "max": torch.finfo(tdt).max}[bad]
+        w[co - 1, 26, ci - 1] = val            # the last element of the last pack block
+        w[3, 13, 17] = val
+    flat = gpu_lib.conv_weight_pack(w.cuda()).cpu()
+    flag = int(flat[co * 27 * ci:].view(torch.int32)[0])
+    assert (flag != 0) == (bad in ("inf", "-inf", "nan"))
+
 
 
 @pytest.mark.parametrize("n_shell", ["r14", "r22"])
@@ -488,26 +513,44 @@ def _plan_parts(plan, n):
     off, parts = 0, {}
     for name, nbytes, dt, shape in (("hdr", t * 16, np.int32, (t, 4)), ("rowof", t * 2048 * 4, np.int32, (t, 2048)),
                                     ("slots", t * 27 * 512 * 2, np.uint16, (t, 27, 4, 32, 4)),
-                                    ("vox", t * 512 * 4, np.int32, (t, 512))):
+                                    ("vox", t * 512 * 4, np.int32, (t, 512)),
+                                    ("act", t * 64, np.uint32, (t, 4, 4))):
         parts[name] = raw[off:off + nbytes].view(dt).reshape(shape)
         off += al(nbytes)
     return parts
 
 
 def _check_plan(p, table, n, order):
-    """What a plan promises the conv: the tiles' positions hold every voxel once, in row order
-    inside a tile (consecutive rows for a plan without coordinates); each (tap, position) slot
-    names the row the table gives, through the tile's sorted row list, or the zero slot."""
+    """What a plan promises the conv: the tiles' positions hold every voxel once (a tile of a
+    plan without coordinates holds consecutive rows); inside each 32-row block the voxels come
+    first, ordered by (set of present taps, row), then the empty positions; the act bits of each
+    (row group, block, tap) say exactly whether a voxel of the block has the tap; each (tap,
+    position) slot names the row the table gives, through the tile's sorted row list, or the zero
+    slot. Returns the tiles' distinct-row counts and the number of clear act bits."""
     vox = p["vox"].reshape(-1)
     assert np.array_equal(np.sort(vox[vox >= 0]), np.arange(n))
     assert (vox < 0).sum() == p["vox"].size - n
     H = p["hdr"][:, 0]
+    present = table != n                                   # [27, n]
+    taps = (present.astype(np.int64) << np.arange(27)[:, None]).sum(0)
+    clear = 0
     for t in range(p["vox"].shape[0]):
         v = p["vox"][t]
         k = int((v >= 0).sum())
-        assert (v[:k] >= 0).all() and np.all(np.diff(v[:k]) > 0)
         if order == "rows":
-            assert np.array_equal(v[:k], np.arange(512 * t, 512 * t + k))
+            assert np.array_equal(np.sort(v[v >= 0]), np.arange(512 * t, 512 * t + k))
+        for g in range(4):
+            bits = sum(int(p["act"][t, g, w]) << (32 * w) for w in range(4))
+            for b in range(4):
+                blk = v[g * 128 + b * 32: g * 128 + b * 32 + 32]
+                m = int((blk >= 0).sum())
+                assert (blk[:m] >= 0).all() and (blk[m:] < 0).all()
+                key = (taps[blk[:m]] << 32) | blk[:m]
+                assert np.all(np.diff(key) > 0)
+                for tap in range(27):
+                    want = bool(m) and bool(present[tap, blk[:m]].any())
+                    assert ((bits >> (4 * tap + b)) & 1) == want, (t, g, b, tap)
+                    clear += not want
         if p["hdr"][t, 1]:
             continue
         rows = p["rowof"][t, :H[t]]
@@ -517,13 +560,14 @@ def _check_plan(p, table, n, order):
             got = np.where(sl == 2048, n, rows[np.minimum(sl, max(H[t] - 1, 0))])
             want = np.where(v >= 0, table[tap][np.maximum(v, 0)], n)
             assert np.array_equal(got, want), (t, tap)
-    return H
+    return H, clear
 
 
 @pytest.mark.parametrize("order", ["rows", "morton"])
 def test_plan_records(gpu_lib, orc, shells, order):
     """The plan's records checked on the host (see _check_plan); Morton tiles reference fewer
-    distinct rows than row tiles on a thin shell, and every tile fits the LDS stage."""
+    distinct rows than row tiles on a thin shell, every tile fits the LDS stage, and grouping
+    voxels by tap set clears act bits (absent taps skipped by whole blocks)."""
     _case(f"plan records {order}")
     import torch
     coords = np.ascontiguousarray(shells.sphere_shell(64, 32.0, 20.0, 22.0), np.int32)
@@ -533,9 +577,11 @@ def test_plan_records(gpu_lib, orc, shells, order):
     plan = gpu_lib.conv_plan_build(nbr, n, coords=c if order == "morton" else None)
     torch.cuda.synchronize()
     p = _plan_parts(plan, n)
-    H = _check_plan(p, nbr.cpu().numpy().reshape(27, n), n, order)
+    H, clear = _check_plan(p, nbr.cpu().numpy().reshape(27, n), n, order)
     assert (p["hdr"][:, 1] == 0).all()
-    print(f"{order}: distinct rows per voxel {H.sum() / n:.2f}", flush=True)
+    print(f"{order}: distinct rows per voxel {H.sum() / n:.2f}, (block, tap) pairs skipped "
+          f"{clear / (len(H) * 16 * 27):.3f}", flush=True)
+    assert clear > 0.05 * len(H) * 16 * 27
     if order == "morton":
         rplan = gpu_lib.conv_plan_build(nbr, n)
         assert H.sum() < 0.8 * _plan_parts(rplan, n)["hdr"][:, 0].sum()

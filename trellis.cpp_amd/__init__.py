@@ -26,7 +26,7 @@ EXPORTS = (
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
     "tsp_subm_conv3x3", "tsp_subm_conv3x3_ex",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_plan_build_ordered",
-    "tsp_conv_weight_pack",
+    "tsp_conv_weight_pack", "tsp_conv_weight_packed_bytes",
     "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_ex", "tsp_subm_conv3x3_planned_octants",
     "tsp_subm_conv3x3_planned_skip",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide", "tsp_subdivide_noalloc",
@@ -102,6 +102,8 @@ def lib() -> ctypes.CDLL:
     L.tsp_conv_plan_build_ordered.argtypes = [c_vp, c_vp, c_i64, c_vp, c_sz, c_vp]
     L.tsp_conv_weight_pack.restype = c_int
     L.tsp_conv_weight_pack.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
+    L.tsp_conv_weight_packed_bytes.restype = c_sz
+    L.tsp_conv_weight_packed_bytes.argtypes = [c_int, c_int]
     L.tsp_subm_conv3x3_planned.restype = c_int
     L.tsp_subm_conv3x3_planned.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
                                            c_int, c_vp, c_int, c_vp]
@@ -288,12 +290,13 @@ def conv_plan_build(nbr, n: int, coords=None, stream=None):
 
 
 def conv_weight_pack(weight, stream=None):
-    """W [Co,27,Ci] f16/bf16 -> packed copy (same dtype and byte size, flat)."""
+    """W [Co,27,Ci] f16/bf16 -> packed copy (same dtype, flat): the values in operand order, then
+    the 256-byte trailer (tsp_conv_weight_packed_bytes(Ci, Co) bytes in all)."""
     torch = _torch()
     _require_cuda(weight)
     w = weight.contiguous()
     co, _, ci = w.shape
-    packed = torch.empty(w.numel(), dtype=w.dtype, device=w.device)
+    packed = torch.empty(lib().tsp_conv_weight_packed_bytes(ci, co) // 2, dtype=w.dtype, device=w.device)
     _check("tsp_conv_weight_pack",
            lib().tsp_conv_weight_pack(_ptr(w), dtype_code(w.dtype), ci, co, _ptr(packed),
                                       _stream(stream)))
@@ -309,8 +312,8 @@ def _check_planned(feats, nbr, plan, packed_weight, ci: int, co: int):
                          f"voxels needs {need}")
     if packed_weight.dtype != feats.dtype:
         raise ValueError(f"packed weight is {packed_weight.dtype}, features are {feats.dtype}")
-    if packed_weight.numel() != co * 27 * ci:
-        raise ValueError("packed weight size does not match [Co,27,Ci]")
+    if packed_weight.numel() * packed_weight.element_size() != lib().tsp_conv_weight_packed_bytes(ci, co):
+        raise ValueError("packed weight size does not match [Co,27,Ci] (see conv_weight_pack)")
     if not packed_weight.is_contiguous():
         raise ValueError("packed weight must be contiguous")
 
@@ -544,8 +547,8 @@ def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None):
     for k, m in (("conv.bias", c), ("norm.weight", c), ("norm.bias", c), ("mlp.0.bias", 4 * c), ("mlp.2.bias", c)):
         t[k] = _vec(p[k], m, k)
     packed = p.get("conv.packed")
-    if packed is not None and (packed.numel() * packed.element_size() != 27 * c * c * 2):
-        raise ValueError("conv.packed must hold 27*C*C 16-bit values")
+    if packed is not None and (packed.numel() * packed.element_size() != lib().tsp_conv_weight_packed_bytes(c, c)):
+        raise ValueError("conv.packed must be conv.weight packed by conv_weight_pack")
     if plan is not None and (plan.dtype != torch.uint8 or plan.numel() < lib().tsp_conv_plan_bytes(n)):
         raise ValueError("plan must be a uint8 buffer of tsp_conv_plan_bytes(N)")
     _require_cuda(x, nbr, plan, packed, *t.values())
@@ -585,9 +588,9 @@ def c2s(x, nbr, mask, mstart, gidx, m: int, cout: int, child_nbr, p: dict, plan=
     for k, k_n in (("norm1.weight", cin), ("norm1.bias", cin), ("conv1.bias", 8 * cout), ("conv2.bias", cout)):
         t[k] = _vec(p[k], k_n, k)
     p1, p2 = p.get("conv1.packed"), p.get("conv2.packed")
-    for pk, numel, name in ((p1, 27 * cin * 8 * cout, "conv1.packed"), (p2, 27 * cout * cout, "conv2.packed")):
-        if pk is not None and pk.numel() * pk.element_size() != 2 * numel:
-            raise ValueError(f"{name} must hold the packed 16-bit weight")
+    for pk, (ci_, co_), name in ((p1, (cin, 8 * cout), "conv1.packed"), (p2, (cout, cout), "conv2.packed")):
+        if pk is not None and pk.numel() * pk.element_size() != lib().tsp_conv_weight_packed_bytes(ci_, co_):
+            raise ValueError(f"{name} must hold the weight packed by conv_weight_pack")
     for pl, rows, name in ((plan, n, "plan"), (child_plan, m, "child_plan")):
         if pl is not None and (pl.dtype != torch.uint8 or pl.numel() < lib().tsp_conv_plan_bytes(rows)):
             raise ValueError(f"{name} must be a uint8 buffer of tsp_conv_plan_bytes")

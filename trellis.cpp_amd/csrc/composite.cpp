@@ -53,7 +53,7 @@ int run_conv(const void* x, int xdt, int64_t n, int ci, const int32_t* nbr, cons
              const void* w, int wdt, const void* packed, const float* bias, int co, float* out, int flags,
              const float* row0, Carve& ws, hipStream_t s) {
     const ConvPlan cp = conv_plan(xdt, ci, co, plan, packed);
-    void* pk = cp.pack_here ? ws.take((size_t)27 * ci * co * 2) : nullptr;
+    void* pk = cp.pack_here ? ws.take(tsp_conv_weight_packed_bytes(ci, co)) : nullptr;
     if (!ws.base) return TSP_OK;
     if (cp.planned) {
         if (cp.pack_here) {
@@ -144,8 +144,8 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
     float* h1 = octants ? nullptr : static_cast<float*>(ws.take((size_t)n * 8 * cout * 4));
     float* g = static_cast<float*>(ws.take((size_t)m * cout * 4));
     void* h2 = ws.take((size_t)m * cout * dtype_size(in2));
-    void* pk1 = cp1.pack_here ? ws.take((size_t)27 * cin * 8 * cout * 2) : nullptr;
-    void* pk2 = cp2.pack_here ? ws.take((size_t)27 * cout * cout * 2) : nullptr;
+    void* pk1 = cp1.pack_here ? ws.take(tsp_conv_weight_packed_bytes(cin, 8 * cout)) : nullptr;
+    void* pk2 = cp2.pack_here ? ws.take(tsp_conv_weight_packed_bytes(cout, cout)) : nullptr;
     if (!ws.base) return TSP_OK;
     int st;
     if ((st = tsp_layer_norm(x, TSP_F32, n, cin, w.norm1_weight, w.norm1_bias, 1e-6f, 1, h0, in1, s))) return st;

@@ -545,7 +545,12 @@ extern "C" int tsp_conv_weight_pack(const void* d_weight, int dtype, int ci, int
     TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_weight) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(d_packed) % 16 == 0,
                 TSP_ERR_INVALID, "tsp_conv_weight_pack: buffers must be 16-byte aligned");
-    return halo_weight_pack(d_weight, ci, co, d_packed, as_stream(stream));
+    return halo_weight_pack(d_weight, dtype, ci, co, d_packed, as_stream(stream));
+}
+
+extern "C" size_t tsp_conv_weight_packed_bytes(int ci, int co) {
+    if (ci <= 0 || co <= 0) return 0;
+    return packed_weight_bytes(ci, co);
 }
 
 extern "C" int tsp_subm_conv3x3_planned_ex(const void* d_feats, int dtype, int64_t n, int ci,

@@ -1,0 +1,11 @@
+// LDS-staged MFMA conv: the bf16 features / 128-output-channel-tile instantiations.
+#include "conv_halo_kernel.hpp"
+
+namespace tsp {
+
+int halo_launch_bf16_128(TSP_HALO_LAUNCH_ARGS) {
+    return launch_out<true, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s,
+                                     osc, skip, pad);
+}
+
+}  // namespace tsp

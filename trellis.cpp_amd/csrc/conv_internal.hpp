@@ -45,8 +45,14 @@ int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, cons
 // Builds the plan of neighbour table `nbr` into `plan`: tiles in the Morton order of the voxels'
 // 8^3 cells when `coords` is given, else tiles of consecutive rows.
 int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s);
-// Packs [co][27][ci] 16-bit weights into the MFMA operand order (ci % 16 == 0, co % 32 == 0).
-int halo_weight_pack(const void* w, int ci, int co, void* packed, hipStream_t s);
+// Packed weights: the [co][27][ci] 16-bit values in the MFMA operand order, then a trailer of
+// HB_PACK_TRAILER bytes whose first word is nonzero when some weight is an Inf or a NaN. With
+// finite weights the planned conv skips the MFMAs of taps absent from a whole 32-row block (their
+// products with the zero padding row are exact zeros); otherwise it computes them, as 0 * W is NaN.
+constexpr int HB_PACK_TRAILER = 256;
+inline size_t packed_weight_bytes(int ci, int co) { return (size_t)kTaps * ci * co * 2 + HB_PACK_TRAILER; }
+// Packs [co][27][ci] 16-bit weights of dtype wdt (ci % 16 == 0, co % 32 == 0) and writes the trailer.
+int halo_weight_pack(const void* w, int wdt, int ci, int co, void* packed, hipStream_t s);
 // Output rows scattered to the children of a 2x subdivision: with cout > 0, the conv's output
 // channel c = o * cout + k of row i goes to row mstart[i] + (octants of parent i kept before o)
 // of an [M][cout] output when mask[8 i + o] != 0, and nowhere otherwise (the octant gather of

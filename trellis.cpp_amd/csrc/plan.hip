@@ -6,9 +6,10 @@
 // Morton code of their 8^3 cell (a stable radix sort, so voxels of one cell keep their row order)
 // and each run of HB_M voxels is a tile -- a compact patch of the surface, whose neighbours are
 // ~1.7 distinct rows per voxel on thin shells instead of ~3.3 for HB_M consecutive rows of an
-// x-major set. Inside a tile the voxels are placed in row order. Without coordinates tiles are
-// consecutive rows. The conv's results do not depend on the grouping: every output row sums the
-// same products in the same order wherever it sits.
+// x-major set. Without coordinates tiles are consecutive rows. Inside a tile the voxels are
+// grouped by their set of present taps (see k_plan_build). The conv's results do not depend on
+// the grouping: every output row sums the same products in the same order wherever it sits (a
+// skipped absent tap would only have added exact zeros).
 #include <algorithm>
 
 #include "tile_plan.hpp"
@@ -214,39 +215,109 @@ int morton_order(const int32_t* coords, int64_t n, const SortScratch& ss, hipStr
 }
 
 // ---- the plan of one tile per workgroup (HB_PLAN_NT threads, one voxel each) ------------------------
+// Positions inside the tile: the voxels sorted by (set of present taps, row) -- a bitonic sort of
+// 64-bit keys in LDS -- so that voxels with the same taps share 32-row MFMA blocks and a tap absent
+// from a whole block costs no MFMA; then the 16 blocks are dealt to the 4 row groups (one per
+// SIMD) largest first, each to the group with the fewest present (tap, block) pairs so far that
+// still has room, which keeps the groups' MFMA counts within a block of each other.
 __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __restrict__ nbr, int64_t n,
                                                            const int32_t* __restrict__ order,
                                                            int64_t n_tiles, PlanView plan) {
     static_assert(HB_PLAN_NT == HB_M, "one thread per tile position");
+    constexpr int NB = HB_M / 32;                 // MFMA row blocks of a tile
     __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
-    __shared__ int32_t sRowOf[HB_SLOTS];
+    __shared__ __attribute__((aligned(16))) int32_t sRowOf[HB_SLOTS];
     __shared__ uint32_t sScratch[HB_PLAN_SCRATCH];
     __shared__ int sRed[2 * HB_PLAN_NT / 64];
-    // before tile_plan_core, its scratch holds the rows to rank
-    int32_t* sRow = reinterpret_cast<int32_t*>(sScratch);
+    __shared__ uint32_t sBlk[NB];                 // present taps of each sorted block
+    __shared__ int sBase[NB];                     // first position of each sorted block
+    __shared__ int sIdx[NB];                      // sorted blocks, most present taps first
+    __shared__ int sWho[NB];                      // sorted block at (row group, block) 4 g + s
+    // before tile_plan_core, sRowOf holds the sort: keys, then the thread of each sorted key, then
+    // the position of each thread
+    static_assert(HB_SLOTS * 4 >= HB_M * 8 + HB_M * 2 + HB_M * 2, "sort fits the row list");
+    uint64_t* sKey = reinterpret_cast<uint64_t*>(sRowOf);
+    uint16_t* sTid = reinterpret_cast<uint16_t*>(sKey + HB_M);
+    uint16_t* sPos = sTid + HB_M;
 
     const int64_t tile = blockIdx.x;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int64_t q = tile * HB_M + tid;
     int64_t i[1] = {q < n ? (order ? (int64_t)order[q] : q) : -1};
     int32_t nv[kTaps][1];
     load_entries<1>(nbr, n, i, nv);
-    // the tile's voxels in row order (rows past n last): consecutive positions then mostly read
-    // consecutive rows at each tap, so the slots an MFMA operand reads are near each other
-    int pos[1] = {tid};
-    if (order) {
-        const int32_t key = i[0] >= 0 ? (int32_t)i[0] : INT32_MAX;
-        sRow[tid] = key;
-        __syncthreads();
-        int rank = 0;
-        for (int j = 0; j < HB_M; ++j) {
-            const int32_t o = sRow[j];
-            rank += o < key || (o == key && j < tid);
+    uint32_t taps = 0;
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) taps |= (nv[t][0] >= 0 ? 1u : 0u) << t;
+    // empty positions (past n) sort last
+    sKey[tid] = i[0] >= 0 ? ((uint64_t)taps << 32) | (uint32_t)i[0] : ~0ull;
+    sTid[tid] = (uint16_t)tid;
+    __syncthreads();
+    for (int k = 2; k <= HB_M; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const int p = tid ^ j;
+            if (p > tid) {
+                const uint64_t a = sKey[tid], b = sKey[p];
+                if ((a > b) == ((tid & k) == 0)) {
+                    sKey[tid] = b;
+                    sKey[p] = a;
+                    const uint16_t ta = sTid[tid];
+                    sTid[tid] = sTid[p];
+                    sTid[p] = ta;
+                }
+            }
+            __syncthreads();
         }
-        pos[0] = rank;
-        __syncthreads();   // sRow is the planner's scratch from here on
+    // thread tid now stands for sorted index tid: the present taps of its 32-row block
+    uint32_t bt = sKey[tid] == ~0ull ? 0u : (uint32_t)(sKey[tid] >> 32);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) bt |= __shfl_xor(bt, off, 64);
+    if ((lane & 31) == 0) sBlk[tid >> 5] = bt;
+    __syncthreads();
+    // blocks by present taps, most first (ties: sorted order)
+    if (tid < NB) {
+        const int c = __popc(sBlk[tid]);
+        int rank = 0;
+        for (int b = 0; b < NB; ++b) {
+            const int cb = __popc(sBlk[b]);
+            rank += (cb > c) || (cb == c && b < tid);
+        }
+        sIdx[rank] = tid;
     }
+    __syncthreads();
+    if (tid == 0) {
+        // each block to the least-loaded group with room (ties: the lower group)
+        int load[4] = {0, 0, 0, 0}, fill[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int a = 0; a < NB; ++a) {
+            const int b = sIdx[a];
+            int g = 0, best = INT32_MAX, slot = 0;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                if (fill[h] < 4 && load[h] < best) { g = h; best = load[h]; slot = fill[h]; }
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                if (h == g) { ++fill[h]; load[h] += __popc(sBlk[b]); }
+            sBase[b] = g * 128 + slot * 32;
+            sWho[g * 4 + slot] = b;
+        }
+    }
+    __syncthreads();
+    if (tid < 4 * HB_ACT_WORDS) {
+        // word w of row group g: bit 4 t + s = tap t present in the group's block s
+        const int g = tid / HB_ACT_WORDS, w = tid % HB_ACT_WORDS;
+        uint32_t word = 0;
+        for (int k = 0; k < 32; ++k) {
+            const int bit = 32 * w + k, t = bit >> 2;
+            if (t < kTaps) word |= ((sBlk[sWho[4 * g + (bit & 3)]] >> t) & 1u) << k;
+        }
+        plan.act[tile * 4 * HB_ACT_WORDS + tid] = word;
+    }
+    sPos[sTid[tid]] = (uint16_t)(sBase[tid >> 5] + (tid & 31));
+    __syncthreads();
+    int pos[1] = {sPos[tid]};
     plan.vox[tile * HB_M + pos[0]] = (int32_t)i[0];
+    __syncthreads();   // sRowOf is the planner's row list from here on
 
     int H;
     bool direct;

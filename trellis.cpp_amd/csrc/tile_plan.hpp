@@ -30,14 +30,21 @@ __device__ __forceinline__ int wave_max(int v) {
 //   rowof int32 [HB_SLOTS]     input row of each slot (slots sorted by row)
 //   slots uint16 [27][4][32][4] slot of each (tap, position / 128, position % 32, position / 32 % 4)
 //   vox   int32 [HB_M]         output row at each tile position, -1 for none
+//   act   uint32 [4][4]        per row group g: bit 4 t + b set when some voxel of MFMA block b of
+//                              the group has tap t (HB_ACT_WORDS words per group)
 // Position p of a tile is row p % 32 of MFMA block (p / 32) % 4 of row group p / 128. The tiles
 // partition the voxels in an order chosen by the build (compact regions of space when coordinates
-// are given); inside a tile the voxels are in row order.
+// are given); inside a tile the voxels are grouped by their set of present taps, so that a 32-row
+// block often has a tap absent for all its rows (act bit clear: the conv skips that block's MFMAs
+// when the weights are finite), and the blocks are dealt to the four row groups so that each
+// group has about the same number of present (tap, block) pairs.
+constexpr int HB_ACT_WORDS = 4;            // act words per row group: 27 taps x 4 blocks <= 128 bits
 struct PlanView {
     int32_t* hdr;
     int32_t* rowof;
     uint16_t* slots;
     int32_t* vox;
+    uint32_t* act;
 };
 inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 __host__ __device__ inline PlanView carve_plan(void* p, int64_t n_tiles) {
@@ -50,12 +57,15 @@ __host__ __device__ inline PlanView carve_plan(void* p, int64_t n_tiles) {
     v.slots = reinterpret_cast<uint16_t*>(c);
     c += align256((size_t)n_tiles * HB_SLOT_TABLE * 2);
     v.vox = reinterpret_cast<int32_t*>(c);
+    c += align256((size_t)n_tiles * HB_M * 4);
+    v.act = reinterpret_cast<uint32_t*>(c);
     return v;
 }
 // bytes of the tile records (without the build's sort scratch)
 inline size_t plan_tile_bytes(int64_t n_tiles) {
     return align256((size_t)n_tiles * 16) + align256((size_t)n_tiles * HB_SLOTS * 4) +
-           align256((size_t)n_tiles * HB_SLOT_TABLE * 2) + align256((size_t)n_tiles * HB_M * 4);
+           align256((size_t)n_tiles * HB_SLOT_TABLE * 2) + align256((size_t)n_tiles * HB_M * 4) +
+           align256((size_t)n_tiles * 4 * HB_ACT_WORDS * 4);
 }
 
 // Exclusive scan of the popcounts of words[0..nwords) (nwords <= HB_SLOTS) into pre[];

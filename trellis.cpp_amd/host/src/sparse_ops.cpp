@@ -80,7 +80,7 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
         xr = p;
     }
     if (c.mfma) {
-        void* packed = sc.take((size_t)27 * c.ci * c.co * 2);
+        void* packed = sc.take(tsp_conv_weight_packed_bytes(c.ci, c.co));
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
         lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, packed, s), "weight pack");
