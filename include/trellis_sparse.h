@@ -121,7 +121,7 @@ int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
  * and what depends only on the weights, loaded once per model, trellis_model.cpp:96-142).
  *
  * A plan splits the voxels into tiles of 512 and holds, for each tile, its voxels' rows (grouped
- * by their set of present taps inside the tile), which taps each 32-row block of them has, the
+ * by which of the 8 corner taps they have inside the tile), which taps each 32-row block has, the
  * sorted set of input rows their table entries reference and each entry's rank in that set (the
  * planned conv stages those rows in LDS once per tile).
  * Packed weights hold W [Co][27][Ci] in the order the matrix-core operands are read. Both are

@@ -523,7 +523,8 @@ def _plan_parts(plan, n):
 def _check_plan(p, table, n, order):
     """What a plan promises the conv: the tiles' positions hold every voxel once (a tile of a
     plan without coordinates holds consecutive rows); inside each 32-row block the voxels come
-    first, ordered by (set of present taps, row), then the empty positions; the act bits of each
+    first, ordered by their set of present corner taps (then by row, for a plan without
+    coordinates), then the empty positions; the act bits of each
     (row group, block, tap) say exactly whether a voxel of the block has the tap; each (tap,
     position) slot names the row the table gives, through the tile's sorted row list, or the zero
     slot. Returns the tiles' distinct-row counts and the number of clear act bits."""
@@ -532,7 +533,8 @@ def _check_plan(p, table, n, order):
     assert (vox < 0).sum() == p["vox"].size - n
     H = p["hdr"][:, 0]
     present = table != n                                   # [27, n]
-    taps = (present.astype(np.int64) << np.arange(27)[:, None]).sum(0)
+    corners = [0, 2, 6, 8, 18, 20, 24, 26]                 # taps (+-1, +-1, +-1)
+    cset = (present[corners].astype(np.int64) << np.arange(8)[:, None]).sum(0)
     clear = 0
     for t in range(p["vox"].shape[0]):
         v = p["vox"][t]
@@ -545,8 +547,9 @@ def _check_plan(p, table, n, order):
                 blk = v[g * 128 + b * 32: g * 128 + b * 32 + 32]
                 m = int((blk >= 0).sum())
                 assert (blk[:m] >= 0).all() and (blk[m:] < 0).all()
-                key = (taps[blk[:m]] << 32) | blk[:m]
-                assert np.all(np.diff(key) > 0)
+                assert np.all(np.diff(cset[blk[:m]]) >= 0)
+                if order == "rows":
+                    assert np.all(np.diff((cset[blk[:m]] << 32) | blk[:m]) > 0)
                 for tap in range(27):
                     want = bool(m) and bool(present[tap, blk[:m]].any())
                     assert ((bits >> (4 * tap + b)) & 1) == want, (t, g, b, tap)

@@ -7,7 +7,7 @@
 // and each run of HB_M voxels is a tile -- a compact patch of the surface, whose neighbours are
 // ~1.7 distinct rows per voxel on thin shells instead of ~3.3 for HB_M consecutive rows of an
 // x-major set. Without coordinates tiles are consecutive rows. Inside a tile the voxels are
-// grouped by their set of present taps (see k_plan_build). The conv's results do not depend on
+// grouped by which corner taps they have (see k_plan_build). The conv's results do not depend on
 // the grouping: every output row sums the same products in the same order wherever it sits (a
 // skipped absent tap would only have added exact zeros).
 #include <algorithm>
@@ -215,33 +215,38 @@ int morton_order(const int32_t* coords, int64_t n, const SortScratch& ss, hipStr
 }
 
 // ---- the plan of one tile per workgroup (HB_PLAN_NT threads, one voxel each) ------------------------
-// Positions inside the tile: the voxels sorted by (set of present taps, row) -- a bitonic sort of
-// 64-bit keys in LDS -- so that voxels with the same taps share 32-row MFMA blocks and a tap absent
-// from a whole block costs no MFMA; then the 16 blocks are dealt to the 4 row groups (one per
-// SIMD) largest first, each to the group with the fewest present (tap, block) pairs so far that
-// still has room, which keeps the groups' MFMA counts within a block of each other.
+// Positions inside the tile: the voxels grouped by which of the 8 corner taps they have (a stable
+// counting sort of 9-bit digits in LDS: voxels with the same corners mostly share their other
+// taps too, so a tap is often absent from all 32 rows of an MFMA block and costs no MFMA there);
+// then the 16 blocks are dealt to the 4 row groups (one per SIMD) so that the groups' MFMA counts
+// stay close.
 __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __restrict__ nbr, int64_t n,
                                                            const int32_t* __restrict__ order,
                                                            int64_t n_tiles, PlanView plan) {
     static_assert(HB_PLAN_NT == HB_M, "one thread per tile position");
     constexpr int NB = HB_M / 32;                 // MFMA row blocks of a tile
+    constexpr int NW = HB_PLAN_NT / 64;
+    constexpr int ND = 257;                       // digits: corner sets 0..255, 256 = no voxel
     __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
     __shared__ __attribute__((aligned(16))) int32_t sRowOf[HB_SLOTS];
     __shared__ uint32_t sScratch[HB_PLAN_SCRATCH];
     __shared__ int sRed[2 * HB_PLAN_NT / 64];
     __shared__ uint32_t sBlk[NB];                 // present taps of each sorted block
     __shared__ int sBase[NB];                     // first position of each sorted block
-    __shared__ int sIdx[NB];                      // sorted blocks, most present taps first
-    __shared__ int sWho[NB];                      // sorted block at (row group, block) 4 g + s
-    // before tile_plan_core, sRowOf holds the sort: keys, then the thread of each sorted key, then
-    // the position of each thread
-    static_assert(HB_SLOTS * 4 >= HB_M * 8 + HB_M * 2 + HB_M * 2, "sort fits the row list");
-    uint64_t* sKey = reinterpret_cast<uint64_t*>(sRowOf);
-    uint16_t* sTid = reinterpret_cast<uint16_t*>(sKey + HB_M);
+    __shared__ uint32_t sAct[4 * HB_ACT_WORDS];   // the tile's act words
+    // Until tile_plan_core, sRowOf holds the taps and the thread of each sorted index and the
+    // position of each thread, and the scratch the sort's counts.
+    static_assert(HB_SLOTS * 4 >= HB_M * 4 + HB_M * 2 + HB_M * 2, "sort records fit the row list");
+    static_assert(HB_PLAN_SCRATCH >= NW * ND + ND + 64, "sort counts fit the scratch");
+    uint32_t* sTaps = reinterpret_cast<uint32_t*>(sRowOf);
+    uint16_t* sTid = reinterpret_cast<uint16_t*>(sTaps + HB_M);
     uint16_t* sPos = sTid + HB_M;
+    int* sCnt = reinterpret_cast<int*>(sScratch);            // [NW][ND]: count, then first rank
+    int* sDig = sCnt + NW * ND;                               // [ND]: first sorted index of a digit
+    int* sWsum = sDig + ND;                                   // scan of the digit totals
 
     const int64_t tile = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t q = tile * HB_M + tid;
     int64_t i[1] = {q < n ? (order ? (int64_t)order[q] : q) : -1};
     int32_t nv[kTaps][1];
@@ -249,75 +254,90 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
     uint32_t taps = 0;
 #pragma unroll
     for (int t = 0; t < kTaps; ++t) taps |= (nv[t][0] >= 0 ? 1u : 0u) << t;
-    // empty positions (past n) sort last
-    sKey[tid] = i[0] >= 0 ? ((uint64_t)taps << 32) | (uint32_t)i[0] : ~0ull;
-    sTid[tid] = (uint16_t)tid;
+    constexpr int kCorner[8] = {0, 2, 6, 8, 18, 20, 24, 26};   // taps (+-1, +-1, +-1)
+    int d = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) d |= ((taps >> kCorner[k]) & 1u) << k;
+    if (i[0] < 0) d = ND - 1;                     // empty positions sort last
+    for (int k = tid; k < NW * ND; k += HB_PLAN_NT) sCnt[k] = 0;
+    if (tid < 4 * HB_ACT_WORDS) sAct[tid] = 0u;
+    // rank among this wave's lanes with the same digit (lanes in order)
+    uint64_t peers = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 9; ++b) {
+        const uint64_t set = __ballot((d >> b) & 1);
+        peers &= ((d >> b) & 1) ? set : ~set;
+    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
     __syncthreads();
-    for (int k = 2; k <= HB_M; k <<= 1)
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const int p = tid ^ j;
-            if (p > tid) {
-                const uint64_t a = sKey[tid], b = sKey[p];
-                if ((a > b) == ((tid & k) == 0)) {
-                    sKey[tid] = b;
-                    sKey[p] = a;
-                    const uint16_t ta = sTid[tid];
-                    sTid[tid] = sTid[p];
-                    sTid[p] = ta;
-                }
-            }
-            __syncthreads();
+    if (rank == 0) sCnt[wave * ND + d] = __popcll(peers);
+    __syncthreads();
+    // per digit: counts of the waves before, and the digit's total
+    int tot = 0;
+    if (tid < ND) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int c = sCnt[w * ND + tid];
+            sCnt[w * ND + tid] = tot;
+            tot += c;
         }
+    }
+    // exclusive scan of the digit totals (digits tid < ND, waves 0..4)
+    int x = tot;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) sWsum[wave] = x;
+    __syncthreads();
+    if (tid < ND) {
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += sWsum[w];
+        sDig[tid] = before + x - tot;
+    }
+    __syncthreads();
+    const int sidx = sDig[d] + sCnt[wave * ND + d] + rank;   // this voxel's sorted index
+    sTaps[sidx] = i[0] >= 0 ? taps : 0u;
+    sTid[sidx] = (uint16_t)tid;
+    __syncthreads();
     // thread tid now stands for sorted index tid: the present taps of its 32-row block
-    uint32_t bt = sKey[tid] == ~0ull ? 0u : (uint32_t)(sKey[tid] >> 32);
+    uint32_t bt = sTaps[tid];
 #pragma unroll
     for (int off = 1; off < 32; off <<= 1) bt |= __shfl_xor(bt, off, 64);
     if ((lane & 31) == 0) sBlk[tid >> 5] = bt;
     __syncthreads();
-    // blocks by present taps, most first (ties: sorted order)
+    // The blocks, ranked by present taps (most first; ties: sorted order), are dealt to the row
+    // groups in snake order (ranks 0-3 to groups 0-3, 4-7 to groups 3-0, ...; slot = rank / 4),
+    // which keeps the groups' MFMA counts close; each block ORs its act bits into its group's words.
     if (tid < NB) {
-        const int c = __popc(sBlk[tid]);
-        int rank = 0;
-        for (int b = 0; b < NB; ++b) {
-            const int cb = __popc(sBlk[b]);
-            rank += (cb > c) || (cb == c && b < tid);
+        const uint32_t blk = sBlk[tid];
+        const int c = __popc(blk);
+        int r = 0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int cj = __popc(sBlk[j]);
+            r += (cj > c) || (cj == c && j < tid);
         }
-        sIdx[rank] = tid;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        // each block to the least-loaded group with room (ties: the lower group)
-        int load[4] = {0, 0, 0, 0}, fill[4] = {0, 0, 0, 0};
+        const int slot = r >> 2, g = (slot & 1) ? 3 - (r & 3) : (r & 3);
+        sBase[tid] = g * 128 + slot * 32;
+        // word w of row group g: bit 4 t + slot (t in [8 w, 8 w + 8)) = tap t present in the block
 #pragma unroll
-        for (int a = 0; a < NB; ++a) {
-            const int b = sIdx[a];
-            int g = 0, best = INT32_MAX, slot = 0;
-#pragma unroll
-            for (int h = 0; h < 4; ++h)
-                if (fill[h] < 4 && load[h] < best) { g = h; best = load[h]; slot = fill[h]; }
-#pragma unroll
-            for (int h = 0; h < 4; ++h)
-                if (h == g) { ++fill[h]; load[h] += __popc(sBlk[b]); }
-            sBase[b] = g * 128 + slot * 32;
-            sWho[g * 4 + slot] = b;
+        for (int w = 0; w < HB_ACT_WORDS; ++w) {
+            uint32_t v = (blk >> (8 * w)) & 0xffu;   // the 8 tap bits spread to every fourth bit
+            v = (v | (v << 12)) & 0x000F000Fu;
+            v = (v | (v << 6)) & 0x03030303u;
+            v = (v | (v << 3)) & 0x11111111u;
+            if (v) atomicOr(&sAct[g * HB_ACT_WORDS + w], v << slot);
         }
     }
     __syncthreads();
-    if (tid < 4 * HB_ACT_WORDS) {
-        // word w of row group g: bit 4 t + s = tap t present in the group's block s
-        const int g = tid / HB_ACT_WORDS, w = tid % HB_ACT_WORDS;
-        uint32_t word = 0;
-        for (int k = 0; k < 32; ++k) {
-            const int bit = 32 * w + k, t = bit >> 2;
-            if (t < kTaps) word |= ((sBlk[sWho[4 * g + (bit & 3)]] >> t) & 1u) << k;
-        }
-        plan.act[tile * 4 * HB_ACT_WORDS + tid] = word;
-    }
+    if (tid < 4 * HB_ACT_WORDS) plan.act[tile * 4 * HB_ACT_WORDS + tid] = sAct[tid];
     sPos[sTid[tid]] = (uint16_t)(sBase[tid >> 5] + (tid & 31));
     __syncthreads();
     int pos[1] = {sPos[tid]};
     plan.vox[tile * HB_M + pos[0]] = (int32_t)i[0];
-    __syncthreads();   // sRowOf is the planner's row list from here on
+    __syncthreads();   // sRowOf and the scratch are the planner's from here on
 
     int H;
     bool direct;

@@ -34,7 +34,7 @@ __device__ __forceinline__ int wave_max(int v) {
 //                              the group has tap t (HB_ACT_WORDS words per group)
 // Position p of a tile is row p % 32 of MFMA block (p / 32) % 4 of row group p / 128. The tiles
 // partition the voxels in an order chosen by the build (compact regions of space when coordinates
-// are given); inside a tile the voxels are grouped by their set of present taps, so that a 32-row
+// are given); inside a tile the voxels are grouped by which corner taps they have, so that a 32-row
 // block often has a tap absent for all its rows (act bit clear: the conv skips that block's MFMAs
 // when the weights are finite), and the blocks are dealt to the four row groups so that each
 // group has about the same number of present (tap, block) pairs.
