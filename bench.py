@@ -381,7 +381,9 @@ def kernel_sources_sha() -> str:
     """sha256 over the conv kernel's sources: a traffic profile is valid for these only."""
     import hashlib
     h = hashlib.sha256()
-    for f in ("conv_halo.hip", "tile_plan.hpp", "plan.hip", "conv_internal.hpp", "common.hpp"):
+    for f in ("conv_halo.hip", "conv_halo_kernel.hpp", "conv_halo_bf16_128.hip", "conv_halo_bf16_64.hip",
+              "conv_halo_f16_128.hip", "conv_halo_f16_64.hip", "tile_plan.hpp", "plan.hip",
+              "conv_internal.hpp", "common.hpp"):
         with open(os.path.join(ROOT, "trellis.cpp_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()
