@@ -194,6 +194,19 @@ int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int
                                   const float* d_x, int cin, const int32_t* d_gidx, float* d_out,
                                   void* stream);
 
+/* The ConvNeXt block's conv and the LayerNorm after it in one kernel (sparse.cpp:121-128:
+ * h = conv(x) + bias, then norm(h) * norm.weight + norm.bias, eps 1e-6 there): the conv of
+ * tsp_subm_conv3x3_planned_ex (d_row0 as there, flags 0) whose stores normalise each output row
+ * over its co channels -- mean, biased variance, (h - mean) / sqrt(var + eps) * w + b, in f32 --
+ * and write it in the feature dtype (the ggml mul_mat after the norm rounds its input to that
+ * type, sparse.cpp:128). The f32 conv output and the separate norm pass are never needed.
+ * co = 64 or 128 (one workgroup holds a whole row); norm weight and bias f32 [co]. */
+int tsp_subm_conv3x3_planned_ln(const void* d_feats, int dtype, int64_t n, int ci,
+                                const int32_t* d_nbr, const void* d_plan,
+                                const void* d_packed_weight, const float* d_bias, int co,
+                                const float* d_norm_weight, const float* d_norm_bias, float eps,
+                                void* d_out, const float* d_row0, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * 2x subdivision (channel-to-spatial) index math.
  * Replaces the host loop of trellis::sparse_c2s (src/sparse.cpp:205-222): parent i keeps

@@ -258,8 +258,13 @@ def test_composite_validation(pkg):
     L = pkg.lib()
     w = pkg.ConvNextWeights(FAKE, 2, FAKE, None, FAKE, FAKE, FAKE, 2, FAKE, FAKE, 2, FAKE)
     nb = L.tsp_convnext_workspace_bytes(1000, 64, 0, ctypes.byref(w), 1, 0)
-    assert nb >= 1000 * 64 * (2 + 4 + 2) and nb % 256 == 0
-    assert L.tsp_convnext_workspace_bytes(1000, 64, 0, ctypes.byref(w), 0, 0) < nb   # no packing without a plan
+    plain = L.tsp_convnext_workspace_bytes(1000, 64, 0, ctypes.byref(w), 0, 0)
+    # without a plan: the rounded conv input, the f32 conv output and the norm's output (+ the MLP
+    # chunk); with one, the conv and the norm are one kernel (no f32 conv output) and the weights
+    # are packed into the workspace
+    assert plain >= 1000 * 64 * (2 + 4 + 2) and nb % 256 == 0 and plain % 256 == 0
+    a256 = lambda b: (b + 255) // 256 * 256
+    assert nb == plain - a256(1000 * 64 * 4) + a256(L.tsp_conv_weight_packed_bytes(64, 64))
     cn = lambda **kw: L.tsp_convnext(FAKE, kw.get("xdt", 0), 1000, 64, FAKE, kw.get("plan", FAKE),
                                      kw.get("w", ctypes.byref(w)), ctypes.c_void_p(0x2000), FAKE,
                                      kw.get("ws", nb), kw.get("flags", 0), NULL)

@@ -755,3 +755,83 @@ def test_thin_padding_row(gpu_lib, orc, shells, mode):
                                    row0=_dev(feats[0], torch.float32)).cpu().numpy()
         assert np.isfinite(out[~refs0]).all()
         _nan_aware(out, orc.subm_conv_f64(f16, nbr, weight, bias, row0=feats[0]), TOL_16)
+
+
+@pytest.mark.parametrize("ci,co", [(64, 64), (32, 128), (128, 128)])
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_planned_ln_vs_oracle(gpu_lib, orc, shells, ci, co, dtype_name):
+    """The conv with its LayerNorm done by the stores (the ConvNeXt block's conv + norm,
+    sparse.cpp:121-128) against the fp64 oracle's conv followed by its norm (eps 1e-6, affine),
+    both through a plan; one 16-bit rounding of the output."""
+    _case(f"planned conv+norm ci={ci} co={co} {dtype_name}")
+    import torch
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(ci + 3 * co)
+    coords, feats, weight, bias = _rand_case(shells, rng, 0, ci, co, key)
+    nw = (1 + 0.1 * rng.standard_normal(co)).astype(np.float32)
+    nb = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    nbr = orc.neighbor_table(coords)
+    ref = orc.layer_norm(orc.subm_conv_f64(feats, nbr, weight, bias), nw, nb, 1e-6)
+    c = torch.from_numpy(coords).cuda()
+    nbr_d = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr_d, len(coords), coords=c)
+    pw = gpu_lib.conv_weight_pack(_dev(weight, dt))
+    out = gpu_lib.subm_conv3x3_planned_ln(_dev(feats, dt), nbr_d, plan, pw, _dev(bias, torch.float32), co,
+                                          _dev(nw, torch.float32), _dev(nb, torch.float32))
+    assert out.dtype == dt
+    assert orc.rel_err(out.float().cpu().numpy(), ref) < TOL_16_OUT
+
+
+@pytest.mark.parametrize("co", [64, 128])
+def test_planned_ln_vs_separate_full_size(gpu_lib, shells, co):
+    """On the ~640K-voxel shell set (1,257 tiles: several per workgroup of the persistent grid, so
+    the row-norm stores also run after the cross-tile prefetch): the fused conv + norm against the
+    planned conv's f32 rows normalised by the LayerNorm kernel, within one 16-bit rounding."""
+    _case(f"planned conv+norm full size co={co}")
+    import torch
+    w = shells.workload("shells600k-c128-bf16")
+    rng = np.random.default_rng(co)
+    n, ci = w.n, 128
+    c = torch.from_numpy(w.coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    f = torch.from_numpy(w.feats).to(torch.bfloat16).cuda()
+    wt = torch.from_numpy(w.weight[:co]).to(torch.bfloat16).cuda()
+    pw = gpu_lib.conv_weight_pack(wt)
+    b = torch.from_numpy(w.bias[:co]).cuda()
+    nw = torch.from_numpy((1 + 0.1 * rng.standard_normal(co)).astype(np.float32)).cuda()
+    nb = torch.from_numpy((0.1 * rng.standard_normal(co)).astype(np.float32)).cuda()
+    fused = gpu_lib.subm_conv3x3_planned_ln(f, nbr, plan, pw, b, co, nw, nb).float()
+    h = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, co, out_dtype=torch.float32)
+    ref = gpu_lib.layer_norm(h, nw, nb, eps=1e-6, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    d = (fused - ref).abs()
+    # a bf16 rounding moves a value by at most 2^-9 of it; the two f32 norms differ by far less
+    assert bool((d <= ref.abs() * 2.0 ** -8 + 1e-6).all()), float((d / (ref.abs() + 1e-6)).max())
+
+
+def test_planned_ln_nonfinite_row0(gpu_lib, orc, shells):
+    """A NaN in feature row 0 makes every row with an absent tap NaN before the norm (the
+    reference's padding row 0 * feats[0]), so those rows are NaN after it; the rest match the
+    oracle."""
+    _case("planned conv+norm non-finite row 0")
+    import torch
+    rng = np.random.default_rng(77)
+    coords, feats, weight, bias = _rand_case(shells, rng, 0, 64, 64, "bf16")
+    feats[0, 3] = np.nan
+    n = len(coords)
+    nbr = orc.neighbor_table(coords)
+    t = nbr.reshape(27, n)
+    absent, refs0 = (t == n).any(axis=0), (t == 0).any(axis=0)
+    c = torch.from_numpy(coords).cuda()
+    nbr_d = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr_d, n, coords=c)
+    pw = gpu_lib.conv_weight_pack(_dev(weight, torch.bfloat16))
+    nw, nb = np.ones(64, np.float32), np.zeros(64, np.float32)
+    out = gpu_lib.subm_conv3x3_planned_ln(_dev(feats, torch.bfloat16), nbr_d, plan, pw, _dev(bias, torch.float32),
+                                          64, _dev(nw, torch.float32), _dev(nb, torch.float32)).float().cpu().numpy()
+    assert np.isnan(out[absent]).all()
+    keep = ~absent & ~refs0
+    ref = orc.layer_norm(orc.subm_conv_f64(feats, nbr, weight, bias), nw, nb, 1e-6)
+    assert orc.rel_err(out[keep], ref[keep]) < TOL_16_OUT

@@ -26,7 +26,7 @@ EXPORTS = (
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
     "tsp_subm_conv3x3", "tsp_subm_conv3x3_ex",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_plan_build_ordered",
-    "tsp_conv_weight_pack", "tsp_conv_weight_packed_bytes",
+    "tsp_conv_weight_pack", "tsp_conv_weight_packed_bytes", "tsp_subm_conv3x3_planned_ln",
     "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_ex", "tsp_subm_conv3x3_planned_octants",
     "tsp_subm_conv3x3_planned_skip",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide", "tsp_subdivide_noalloc",
@@ -104,6 +104,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_conv_weight_pack.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
     L.tsp_conv_weight_packed_bytes.restype = c_sz
     L.tsp_conv_weight_packed_bytes.argtypes = [c_int, c_int]
+    L.tsp_subm_conv3x3_planned_ln.restype = c_int
+    L.tsp_subm_conv3x3_planned_ln.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_vp, c_vp,
+                                              ctypes.c_float, c_vp, c_vp, c_vp]
     L.tsp_subm_conv3x3_planned.restype = c_int
     L.tsp_subm_conv3x3_planned.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp,
                                            c_int, c_vp, c_int, c_vp]
@@ -345,6 +348,35 @@ def subm_conv3x3_planned(feats, nbr, plan, packed_weight, bias, co: int, out_dty
                                              _ptr(plan), _ptr(packed_weight), _ptr(bias), co,
                                              _ptr(out), dtype_code(out.dtype),
                                              1 if zero_pad else 0, _ptr(r0), _stream(stream)))
+    return out
+
+
+def subm_conv3x3_planned_ln(feats, nbr, plan, packed_weight, bias, co: int, norm_weight, norm_bias,
+                            eps: float = 1e-6, out=None, row0=None, stream=None):
+    """The planned conv with each output row layer-normalised by its stores (co = 64 or 128):
+    (h - mean) / sqrt(var + eps) * norm_weight + norm_bias for h = conv + bias, in the feature
+    dtype."""
+    torch = _torch()
+    if feats.dim() != 2:
+        raise ValueError("feats must be [N, Ci]")
+    n, ci = feats.shape
+    _check_planned(feats, nbr, plan, packed_weight, ci, co)
+    for name, t in (("bias", bias), ("norm_weight", norm_weight), ("norm_bias", norm_bias)):
+        if t.dtype != torch.float32 or t.numel() != co:
+            raise ValueError(f"{name} must be float32 [Co]")
+    if row0 is not None and (row0.dtype != torch.float32 or row0.numel() != ci):
+        raise ValueError("row0 must be float32 [Ci]")
+    if out is None:
+        out = torch.empty((n, co), dtype=feats.dtype, device=feats.device)
+    else:
+        _check_out(out, n, co, feats.dtype, feats.device)
+    _require_cuda(feats, nbr, plan, packed_weight, bias, norm_weight, norm_bias, out, row0)
+    f = feats.contiguous()
+    r0 = row0.contiguous() if row0 is not None else None
+    _check("tsp_subm_conv3x3_planned_ln",
+           lib().tsp_subm_conv3x3_planned_ln(_ptr(f), dtype_code(f.dtype), n, ci, _ptr(nbr), _ptr(plan),
+                                             _ptr(packed_weight), _ptr(bias), co, _ptr(norm_weight),
+                                             _ptr(norm_bias), float(eps), _ptr(out), _ptr(r0), _stream(stream)))
     return out
 
 

@@ -87,25 +87,6 @@ __device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {
     }
 }
 
-// Sum over aligned groups of L lanes (16 <= L <= 64); every lane of a group ends with the same
-// value. Within a 16-lane DPP row the moves are lane ^ 1, lane ^ 2, 7 - lane within each 8 and
-// 15 - lane, each pairing lanes whose partial sums cover disjoint lanes; across rows, shuffles.
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int L>
-__device__ __forceinline__ float group_sum(float v) {
-    static_assert(L == 16 || L == 32 || L == 64, "group of 16, 32 or 64 lanes");
-    v += dpp_move<0xB1>(v);    // quad_perm [1, 0, 3, 2]
-    v += dpp_move<0x4E>(v);    // quad_perm [2, 3, 0, 1]
-    v += dpp_move<0x141>(v);   // row_half_mirror
-    v += dpp_move<0x140>(v);   // row_mirror
-    if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
-    if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
-    return v;
-}
-
 // Rows of c = 4 L V channels held in registers: L lanes per row (64 / L rows per wave), each lane
 // V groups of 4 channels, interleaved so that a row's lanes read consecutive 16 bytes. One read of
 // x, one write of out; every lane takes part in the group reductions, rows past n store nothing.

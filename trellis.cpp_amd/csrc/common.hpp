@@ -113,4 +113,23 @@ constexpr int kTaps = 27;
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Sum over aligned groups of L lanes (16 <= L <= 64); every lane of a group ends with the same
+// value. Within a 16-lane DPP row the moves are lane ^ 1, lane ^ 2, 7 - lane within each 8 and
+// 15 - lane, each pairing lanes whose partial sums cover disjoint lanes; across rows, shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(L == 16 || L == 32 || L == 64, "group of 16, 32 or 64 lanes");
+    v += dpp_move<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    v += dpp_move<0x141>(v);   // row_half_mirror
+    v += dpp_move<0x140>(v);   // row_mirror
+    if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 }  // namespace tsp

@@ -10,6 +10,7 @@
 
 #include "blocks_internal.hpp"
 #include "common.hpp"
+#include "conv_internal.hpp"
 
 namespace tsp {
 namespace {
@@ -66,6 +67,39 @@ int run_conv(const void* x, int xdt, int64_t n, int ci, const int32_t* nbr, cons
                                TSP_ALGO_AUTO, flags, row0, s);
 }
 
+// The ConvNeXt conv and the LayerNorm after it in one kernel (the planned kernel's row-norm
+// stores, straight into the norm's 16-bit output) when a plan is given, the conv's rows fit one
+// workgroup (C = 64 or 128) and the norm's output type is the conv input's; the f32 conv output
+// and the separate norm pass are then never needed.
+bool ln_fused(int cdt, int adt0, int c, const void* plan) {
+    return plan && is16(cdt) && adt0 == cdt && (c == 64 || c == 128);
+}
+
+int run_conv_ln(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, const void* plan, const void* w,
+                int wdt, const void* packed, const float* bias, const float* norm_w, const float* norm_b,
+                const float* row0, void* hn, Carve& ws, hipStream_t s) {
+    void* pk = packed ? nullptr : ws.take(tsp_conv_weight_packed_bytes(c, c));
+    if (!ws.base) return TSP_OK;
+    if (n == 0) return TSP_OK;
+    if (!packed) {
+        if (int st = tsp_conv_weight_pack(w, wdt, c, c, pk, s)) return st;
+        packed = pk;
+    }
+    TSP_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(hn) % 16 == 0,
+                TSP_ERR_INVALID, "tsp_convnext: conv buffers must be 16-byte aligned");
+    TSP_REQUIRE(halo_fits(n, c), TSP_ERR_UNSUPPORTED, "tsp_convnext: %lld rows of %d channels exceed the "
+                "planned conv's 4 GiB of features", (long long)n, c);
+    PadRow pad;
+    pad.row0 = row0;
+    RowNorm ln;
+    ln.w = norm_w;
+    ln.b = norm_b;
+    ln.eps = 1e-6f;
+    return halo_conv_launch(xdt, xdt, x, n, c, nbr, plan, packed, bias, c, hn, s, OctantScatter{}, SkipAdd{},
+                            pad, ln);
+}
+
 // the rows of one MLP chunk: its f32 hidden layer [chunk][4C] stays within 1 GiB
 int64_t mlp_chunk(int64_t n, int c) {
     return std::max<int64_t>(1, std::min<int64_t>(n, (int64_t(1) << 30) / (16 * (int64_t)c)));
@@ -84,16 +118,24 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
             if (int st = f32_to(static_cast<const float*>(x), n * c, p, cdt, false, s)) return st;
         xc = p;
     }
-    float* h = static_cast<float*>(ws.take((size_t)n * c * 4));
+    const bool fuse = ln_fused(cdt, adt0, c, plan);
+    float* h = fuse ? nullptr : static_cast<float*>(ws.take((size_t)n * c * 4));
     void* hn = ws.take((size_t)n * c * dtype_size(adt0));
     float* hid = static_cast<float*>(ws.take((size_t)chunk * 4 * c * 4));
     void* hid_in = adt2 == TSP_F32 ? hid : ws.take((size_t)chunk * 4 * c * 2);
     const float* row0 = xdt == TSP_F32 && cdt != TSP_F32 ? static_cast<const float*>(x) : nullptr;
-    if (int st = run_conv(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed, w.conv_bias,
-                          c, h, 0, row0, ws, s))
-        return st;
-    if (!ws.base) return TSP_OK;
-    if (int st = tsp_layer_norm(h, TSP_F32, n, c, w.norm_weight, w.norm_bias, 1e-6f, 0, hn, adt0, s)) return st;
+    if (fuse) {
+        if (int st = run_conv_ln(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed, w.conv_bias,
+                                 w.norm_weight, w.norm_bias, row0, hn, ws, s))
+            return st;
+        if (!ws.base) return TSP_OK;
+    } else {
+        if (int st = run_conv(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed, w.conv_bias,
+                              c, h, 0, row0, ws, s))
+            return st;
+        if (!ws.base) return TSP_OK;
+        if (int st = tsp_layer_norm(h, TSP_F32, n, c, w.norm_weight, w.norm_bias, 1e-6f, 0, hn, adt0, s)) return st;
+    }
     const size_t aes = dtype_size(adt0), xes = dtype_size(xdt);
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {
         const int64_t nr = std::min(chunk, n - r0);

@@ -669,6 +669,39 @@ extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int
                             d_out, as_stream(stream), OctantScatter{}, skip, pad);
 }
 
+extern "C" int tsp_subm_conv3x3_planned_ln(const void* d_feats, int dtype, int64_t n, int ci,
+                                           const int32_t* d_nbr, const void* d_plan,
+                                           const void* d_packed_weight, const float* d_bias, int co,
+                                           const float* d_norm_weight, const float* d_norm_bias, float eps,
+                                           void* d_out, const float* d_row0, void* stream) {
+    clear_error();
+    TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && ci > 0 && co > 0, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_ln: n=%lld ci=%d co=%d", (long long)n, ci, co);
+    TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_ln: features are f16 or bf16, not dtype %d", dtype);
+    TSP_REQUIRE(ci % 16 == 0 && (co == 64 || co == 128), TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_ln: needs ci %% 16 == 0 and co = 64 or 128 (ci=%d co=%d)", ci, co);
+    TSP_REQUIRE(eps >= 0.f, TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_ln: eps < 0");
+    if (n == 0) return TSP_OK;
+    TSP_REQUIRE(d_feats && d_nbr && d_plan && d_packed_weight && d_bias && d_norm_weight && d_norm_bias && d_out,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_ln: null pointer");
+    TSP_REQUIRE(d_out != d_feats, TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_ln: out aliases feats");
+    TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_feats) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_packed_weight) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_out) % 16 == 0,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_ln: buffers must be 16-byte aligned");
+    TSP_REQUIRE(halo_fits(n, ci), TSP_ERR_UNSUPPORTED,
+                "tsp_subm_conv3x3_planned_ln: %lld rows of %d channels exceed 4 GiB of features", (long long)n, ci);
+    PadRow pad;
+    pad.row0 = d_row0;
+    RowNorm ln;
+    ln.w = d_norm_weight;
+    ln.b = d_norm_bias;
+    ln.eps = eps;
+    return halo_conv_launch(dtype, dtype, d_feats, n, ci, d_nbr, d_plan, d_packed_weight, d_bias, co, d_out,
+                            as_stream(stream), OctantScatter{}, SkipAdd{}, pad, ln);
+}
+
 extern "C" int tsp_linear(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
                           int weight_dtype, const float* d_bias, int co, void* d_out,
                           int out_dtype, void* stream) {

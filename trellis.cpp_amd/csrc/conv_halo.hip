@@ -50,8 +50,13 @@ int halo_weight_pack(const void* w, int wdt, int ci, int co, void* packed, hipSt
 
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad) {
+                     hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
     const bool planned = plan != nullptr;
+    if (ln.w && (!planned || !(co == 64 || co == 128) || odt != fdt || osc.cout || skip.cin)) {
+        set_error("MFMA conv: a row norm needs a plan, co = 64 or 128 and output in the feature type "
+                  "(co=%d)", co);
+        return TSP_ERR_UNSUPPORTED;
+    }
     const bool bn128 = co % 128 == 0;
     if (osc.cout && (!planned || osc.cout % (bn128 ? 64 : 32) != 0 || (int64_t)osc.cout * 8 != co)) {
         set_error("MFMA conv: an octant scatter needs a plan, co = 8 * cout and cout %% %d == 0 "
@@ -71,7 +76,7 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
     }
     auto* fn = fdt == TSP_BF16 ? (bn128 ? halo_launch_bf16_128 : halo_launch_bf16_64)
                                : (bn128 ? halo_launch_f16_128 : halo_launch_f16_64);
-    return fn(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
+    return fn(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
 }
 
 }  // namespace tsp

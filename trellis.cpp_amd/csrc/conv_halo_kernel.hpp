@@ -42,7 +42,8 @@
 
 #include "tile_plan.hpp"
 
-namespace tsp {namespace {
+namespace tsp {
+namespace {
 
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00); }
 
@@ -79,14 +80,14 @@ __device__ __forceinline__ void conv_tiles(
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip, PadRow pad);
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln);
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG, int EPI>
 __device__ __forceinline__ void conv_grid(
     const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
-    SkipAdd skip, PadRow pad) {
+    SkipAdd skip, PadRow pad, RowNorm ln) {
     // wave w owns voxels [32 RB rg, +32 RB) x channels [32 CB cg, +32 CB) of the tile, with
     // rg = w % NRG and cg = w / NRG
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
@@ -112,7 +113,7 @@ __device__ __forceinline__ void conv_grid(
     const int64_t xlo = xcd * per_xcd, xhi = xlo + per_xcd < total ? xlo + per_xcd : total;
     conv_tiles<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, EPI>(
         feats, n, ci, nbr, plan, weight, bias, co, out, n_ctiles, xlo + blockIdx.x / 8,
-        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc, skip, pad);
+        gridDim.x / 8, xhi, sH0, sH1, sL, sRed, osc, skip, pad, ln);
 }
 
 template <bool BF16, int BN, int ODT, bool PLANNED, int RB, int CB, int PD, int SP, int STG>
@@ -122,7 +123,7 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo(
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, PadRow pad) {
     conv_grid<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG, 0>(
         feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{},
-        SkipAdd{}, pad);
+        SkipAdd{}, pad, RowNorm{});
 }
 
 // The same conv with f32 output rows scattered to the children of a 2x subdivision (stored plan).
@@ -133,7 +134,8 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
     PadRow pad) {
     conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, 1>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{}, pad);
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{}, pad,
+        RowNorm{});
 }
 
 // The same conv with f32 output and the C2S skip added by its stores (stored plan).
@@ -144,8 +146,19 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_
     void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, SkipAdd skip,
     PadRow pad) {
     conv_grid<BF16, BN, TSP_F32, true, RB, CB, PD, SP, STG, 2>(
-        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{}, skip,
-        pad);
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{}, skip, pad, RowNorm{});
+}
+
+// The same conv with the ConvNeXt block's LayerNorm done by its stores (stored plan, co == BN,
+// output in the feature type).
+template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
+__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_ln(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, PadRow pad, RowNorm ln) {
+    conv_grid<BF16, BN, BF16 ? TSP_BF16 : TSP_F16, true, RB, CB, PD, SP, STG, 3>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, OctantScatter{}, SkipAdd{},
+        pad, ln);
 }
 
 // The tiles lin0, lin0 + stride, ... (< xhi) of one workgroup. With a stored plan and an even
@@ -159,7 +172,7 @@ __device__ __forceinline__ void conv_tiles(
     PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
     void* __restrict__ out, int n_ctiles, int64_t lin0, int64_t stride, int64_t xhi,
     uint16_t (&sH0)[2][HB_ROWS][8], uint16_t (&sH1)[2][HB_ROWS][8],
-    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip, PadRow pad) {
+    uint16_t (&sL)[kTaps][4][32][4], int* sRed, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
     constexpr int NRG = HB_M / (32 * RB), NCG = BN / (32 * CB);
     constexpr int WAVES = NRG * NCG;
     constexpr int NT = WAVES * 64;
@@ -469,6 +482,104 @@ __device__ __forceinline__ void conv_tiles(
         }
     };
 
+    // ---- row-norm epilogue (EPI 3: co == BN, so the workgroup holds every channel of its rows):
+    // in rounds of 16 rows of each row group, both column waves stage their halves of the rows
+    // (f32, + bias) in sH1 as whole rows; then each wave normalises 8 of the rows, 16 lanes a row
+    // (BN / 16 consecutive channels each), with the row's sums reduced over those lanes: the mean,
+    // then the mean square deviation, rstd = 1 / sqrt(var + eps), y = (x - mean) rstd w + b,
+    // stored in the 16-bit output type, one contiguous row segment per lane.
+    auto epilogue_ln = [&](f32x16_t (&acc)[RB][CB], int64_t tile) {
+        constexpr int RR = 16;                   // rows per round and row group
+        constexpr int RSW = BN * 4 + 16;         // staged row stride in bytes
+        constexpr int CPL = BN / 16;             // channels per lane
+        static_assert(EPI != 3 || (NCG == 2 && RB == 4 && NRG * RR * RSW <= (int)sizeof(sH1)), "row-norm staging");
+        static_assert(EPI != 3 || ODT == TSP_BF16 || ODT == TSP_F16, "row norm stores 16-bit rows");
+        char* stage = reinterpret_cast<char*>(&sH1[0][0][0]) + rg * RR * RSW;
+        const int cg = wave / NRG;
+        int vrow[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) vrow[k] = plan.vox[tile * HB_M + 32 * RB * rg + 2 * lane + k];
+        auto row_at = [&](int lr) {
+            const int a = __shfl(vrow[0], lr >> 1, 64), b = __shfl(vrow[1], lr >> 1, 64);
+            return (lr & 1) ? b : a;
+        };
+        const int lc = (lane & 15) * CPL;        // this lane's first channel
+        float gw[CPL], gb[CPL];
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            gw[e] = ln.w[lc + e];
+            gb[e] = ln.b[lc + e];
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                // element j of a block holds row 8 (j / 4) + 4 g + j % 4: rows 16 h .. 16 h + 15
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                    for (int j = 8 * h; j < 8 * h + 8; ++j) {
+                        const int r = 8 * (j / 4) + 4 * g + (j % 4) - 16 * h;
+                        *reinterpret_cast<float*>(stage + r * RSW + (cg * WN + cb * 32 + r32) * 4) =
+                            acc[rb][cb][j] + bv[cb];
+                    }
+                __syncthreads();
+#pragma unroll
+                for (int bt = 0; bt < 2; ++bt) {
+                    const int r = 8 * cg + 4 * bt + (lane >> 4);          // row of the round
+                    float v[CPL];
+#pragma unroll
+                    for (int e = 0; e < CPL; e += 4) {
+                        const f32x4_t q = *reinterpret_cast<const f32x4_t*>(stage + r * RSW + (lc + e) * 4);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) v[e + k] = q[k];
+                    }
+                    float sum = 0.f;
+#pragma unroll
+                    for (int e = 0; e < CPL; ++e) sum += v[e];
+                    const float mean = group_sum<16>(sum) / (float)BN;
+                    float sq = 0.f;
+#pragma unroll
+                    for (int e = 0; e < CPL; ++e) {
+                        const float d = v[e] - mean;
+                        sq += d * d;
+                    }
+                    const float rstd = 1.0f / sqrtf(group_sum<16>(sq) / (float)BN + ln.eps);
+                    float y[CPL];
+#pragma unroll
+                    for (int e = 0; e < CPL; ++e) y[e] = (v[e] - mean) * rstd * gw[e] + gb[e];
+                    const int64_t i = row_at(32 * rb + 16 * h + r);
+                    if (row0_bad && i >= 0) {
+                        bool absent = false;
+                        for (int t = 0; t < kTaps; ++t) absent |= nbr[(int64_t)t * n + i] == (int32_t)n;
+                        if (absent) {
+#pragma unroll
+                            for (int e = 0; e < CPL; ++e) y[e] = NAN;
+                        }
+                    }
+                    if (i >= 0) {
+                        uint32_t wd[CPL / 2];
+#pragma unroll
+                        for (int e = 0; e < CPL / 2; ++e)
+                            wd[e] = (ODT == TSP_BF16) ? f32x2_to_bf16x2_bits(y[2 * e], y[2 * e + 1])
+                                                      : f32_to_f16_bits(y[2 * e]) |
+                                                            ((uint32_t)f32_to_f16_bits(y[2 * e + 1]) << 16);
+                        uint16_t* dst = reinterpret_cast<uint16_t*>(out) + i * co + lc;
+                        if constexpr (CPL == 8)
+                            *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+                        else
+                            *reinterpret_cast<uint2*>(dst) = uint2{wd[0], wd[1]};
+                    }
+                }
+                __syncthreads();                 // the next round overwrites the staging
+            }
+        }
+    };
+    auto finish = [&](auto nr_c, f32x16_t (&acc)[RB][CB], int64_t tile) {
+        if constexpr (EPI == 3) epilogue_ln(acc, tile);
+        else epilogue(nr_c, acc, tile);
+    };
+
     // Vector-memory loads return in issue order, so waiting for a weight load also waits for
     // every slice piece issued before it: the weights run PD taps ahead and the slice pieces go
     // out every SP-th tap, which leaves each piece >= PD+1 taps to land. The weight ring has
@@ -664,7 +775,7 @@ __device__ __forceinline__ void conv_tiles(
                     if (p < HB_SLOT_TABLE * 2 / 1024)
                         *reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(&sL[0][0][0][0]) + p * 1024 + lane * 16) = stg[k];
                 }
-                epilogue(std::integral_constant<int, 16>{}, acc, tile);
+                finish(std::integral_constant<int, 16>{}, acc, tile);
                 __syncthreads();       // the next tile's slot table; every wave's staging is done
                 zero_slot(sH1);        // the staging covered it; first read after the next barrier
                 pre = nlin != lin && !ndirect;
@@ -682,7 +793,7 @@ __device__ __forceinline__ void conv_tiles(
                     if (kc + 1 < nkc)
                         run_slice(acc, I1{}, NO{}, sH1, sH0, kc + 1, kc + 2 < nkc ? kc + 2 : kc + 1, nullptr);
                 }
-                epilogue(std::integral_constant<int, 32>{}, acc, tile);
+                finish(std::integral_constant<int, 32>{}, acc, tile);
                 __syncthreads();       // staging reads end before the next tile's loads
                 pre = false;
             }
@@ -712,7 +823,7 @@ __device__ __forceinline__ void conv_tiles(
                         for (int cb = 0; cb < CB; ++cb)
                             acc[rb][cb] = mfma32x32x16<BF16>(a[rb], bq[cb], acc[rb][cb]);
                 }
-            epilogue(std::integral_constant<int, 32>{}, acc, tile);
+            finish(std::integral_constant<int, 32>{}, acc, tile);
             __syncthreads();           // staging reads end before the next tile's loads
             pre = false;
         }
@@ -736,7 +847,7 @@ int cu_count() {
 template <bool BF16, int BN, int ODT, bool PLANNED>
 int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* plan,
            const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc,
-           SkipAdd skip, PadRow pad) {
+           SkipAdd skip, PadRow pad, RowNorm ln) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     const int n_ctiles = co / BN;
     const int64_t total = n_tiles * n_ctiles;
@@ -771,8 +882,17 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
             return TSP_OK;
         }
     }
-    if (osc.cout || skip.cin) {
-        set_error("MFMA conv: octant stores and the skip add write f32 from a stored plan");
+    if constexpr (PLANNED && ODT == (BF16 ? TSP_BF16 : TSP_F16)) {
+        if (ln.w) {
+            hipLaunchKernelGGL((k_conv_halo_ln<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
+                               f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, pad, ln);
+            TSP_CHECK_LAUNCH();
+            return TSP_OK;
+        }
+    }
+    if (osc.cout || skip.cin || ln.w) {
+        set_error("MFMA conv: octant stores and the skip add write f32 from a stored plan, a row norm "
+                  "the feature type");
         return TSP_ERR_UNSUPPORTED;
     }
     hipLaunchKernelGGL((k_conv_halo<BF16, BN, ODT, PLANNED, RB, CB, PD, SP, STG>), grid, block, 0, s,
@@ -784,21 +904,21 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
 template <bool BF16, int BN, int ODT>
 int launch_planned(bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                    const void* plan, const void* weight, const float* bias, int co, void* out,
-                   hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad) {
-    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
-    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip, pad);
+                   hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
+    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
+    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip, pad, ln);
 }
 
 template <bool BF16, int BN>
 int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                const void* plan, const void* weight, const float* bias, int co, void* out,
-               hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad) {
+               hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
     if (odt == TSP_F32)
-        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
+        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
     if (BF16 && odt == TSP_BF16)
-        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
+        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
     if (!BF16 && odt == TSP_F16)
-        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad);
+        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
     set_error("MFMA conv writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
@@ -809,7 +929,7 @@ int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, cons
 // output dtype odt, octant or skip stores when given.
 #define TSP_HALO_LAUNCH_ARGS int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr, \
     const void* plan, const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc, \
-    SkipAdd skip, PadRow pad
+    SkipAdd skip, PadRow pad, RowNorm ln
 int halo_launch_bf16_128(TSP_HALO_LAUNCH_ARGS);
 int halo_launch_bf16_64(TSP_HALO_LAUNCH_ARGS);
 int halo_launch_f16_128(TSP_HALO_LAUNCH_ARGS);

@@ -82,13 +82,25 @@ struct PadRow {
     bool zero = false;
 };
 
+// A LayerNorm over each output row done by the conv's stores (the ConvNeXt block's norm after
+// its conv, sparse.cpp:121-135): with w set, row i of the output is
+// (y - mean(y)) / sqrt(var(y) + eps) * w + b for y = conv row i (f32, bias added), the mean and
+// the biased variance over its co channels, stored in the 16-bit feature type.
+struct RowNorm {
+    const float* w = nullptr;
+    const float* b = nullptr;
+    float eps = 0.f;
+};
+
 // The conv. With plan == nullptr the tile plan is built inside the kernel and `weight` is in
 // the [co][27][ci] layout; with a plan, `weight` must be packed by halo_weight_pack. An
 // OctantScatter or a SkipAdd needs a plan and f32 output; an OctantScatter needs cout a multiple
-// of the channels one wave owns (64 when co % 128 == 0, else 32).
+// of the channels one wave owns (64 when co % 128 == 0, else 32). A RowNorm needs a plan,
+// co == 64 or 128 (one workgroup holds whole rows) and odt == fdt.
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {});
+                     hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {},
+                     RowNorm ln = {});
 
 // The thin-channel VALU conv (conv_thin.hip): Co in {4, 8, 16, 32}, Ci % 4 == 0, Ci * Co <= 512,
 // a neighbour table, 16-byte aligned features. Returns TSP_ERR_UNSUPPORTED (with no message) for

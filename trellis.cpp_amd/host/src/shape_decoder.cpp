@@ -89,7 +89,8 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     // coordinate range checks of every table of the pass, read once at the end
     DeviceBuffer status(4, s);
     hip_check(hipMemsetAsync(status.get(), 0, 4, s), "decoder");
-    ops::build_table(dc.as<int32_t>(), n, table, s, status.as<int32_t>());
+    // Morton-ordered plans: dc holds each level's coordinates until that level's plans are built
+    ops::build_table(dc.as<int32_t>(), n, table, s, status.as<int32_t>(), /*morton_plan=*/true);
     DeviceBuffer scratch, h2;
     // The result's host memory is touched on threads of their own while the device works: from
     // the start when the masks fix the final voxel count, else once the last subdivision is known.
@@ -136,7 +137,7 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         h = std::move(o.feats);
         dc = std::move(o.coords);
         table = std::move(o.table);
-        if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s, status.as<int32_t>());
+        if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s, status.as<int32_t>(), true);
         n = o.m;
         c = g.cout;
         if (!result_started && si + 1 == stages.size()) start_result(n);

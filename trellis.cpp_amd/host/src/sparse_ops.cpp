@@ -149,9 +149,10 @@ size_t convnext_scratch(const ConvNext& a, int xdt) {
 }
 
 // ---- tables --------------------------------------------------------------------------------------
-void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status) {
+void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status,
+                 bool morton_plan) {
     t.n = n;
-    t.coords = nullptr;
+    t.coords = morton_plan ? d_coords : nullptr;
     t.plan = DeviceBuffer();
     t.nbr = DeviceBuffer((size_t)27 * n * 4, s);
     if (n == 0) return;
@@ -258,7 +259,7 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     // the children's table (and plans where a conv runs on the matrix cores), then the block's
     // features in one tsp_c2s call: norm1 + SiLU, conv1 with the octant gather, norm2 + SiLU,
     // conv2 (its absent taps read hn's zero padding column, sparse.cpp:289-306) with the skip
-    build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status);
+    build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status, /*morton_plan=*/true);   // r.coords outlives it
     if (conv1.mfma) parent.ensure_plan(s);
     if (conv2.mfma) r.table.ensure_plan(s);
     const ggml_tensor* c1b = conv1.b;

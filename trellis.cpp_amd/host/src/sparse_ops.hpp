@@ -77,16 +77,19 @@ struct Table {
     tgr::DeviceBuffer nbr;    // int32 [27 n]
     tgr::DeviceBuffer plan;   // empty until ensure_plan
     // Set to the coordinates the table was built from (the caller's buffer, alive until the plan
-    // is built) for a plan whose tiles follow their Morton order: about 3 % off each conv, for a
-    // build about three times as long (0.4 ms more at 2.6 M voxels), so it pays from about ten
-    // convs per table. Left null (row tiles) by build_table.
+    // is built) for a plan whose tiles follow their Morton order: 6-8 % off each conv against
+    // tiles of consecutive rows, for a build about 0.1 ms longer per million voxels. Null: row
+    // tiles.
     const int32_t* coords = nullptr;
     void ensure_plan(hipStream_t s);
 };
 // Builds the table of d_coords [n][3] (its buffers stream-ordered on s). Without d_status it
 // waits for the build and throws for coordinates outside [0, 2^21-3]; with d_status (a device
-// int32 the caller zeroed) it ORs the range check into it and returns without waiting.
-void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status = nullptr);
+// int32 the caller zeroed) it ORs the range check into it and returns without waiting. With
+// morton_plan the table's plan will be built from d_coords, which must then stay alive until
+// ensure_plan has run.
+void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status = nullptr,
+                 bool morton_plan = false);
 
 // Nonzero bytes of p[0, n) (the children a subdivision mask asks for).
 int64_t count_nonzero(const uint8_t* p, size_t n);
