@@ -62,14 +62,17 @@ int tsp_version(void);
 /* ---------------------------------------------------------------------------------------
  * Coordinate hash and neighbour table.
  * Replaces trellis::build_neighbor_table (include/sparse.h:17, src/sparse.cpp:21-39),
- * which builds a std::unordered_map on the host; here the map is an open-addressing table in
- * device memory and the 27 probes per voxel run on the GPU. The table is bit-identical to
+ * which builds a std::unordered_map on the host; here the map lives in device memory -- a
+ * Morton-ordered grid of 8^3-voxel cells when the voxels' bounding box is compact enough for
+ * the workspace, otherwise an open-addressing hash of 2x2x2 bricks (chosen on the device) --
+ * and the 27 probes per voxel run on the GPU. The table is bit-identical to
  * the reference's: row of the voxel at each offset, N when absent, and for duplicate
  * coordinates the largest row index (the reference's last insert wins, sparse.cpp:26).
  * ------------------------------------------------------------------------------------- */
 
 /* Device workspace (bytes) tsp_rulebook_build needs for n voxels (64 bytes per bucket of a
- * 2x2x2-brick hash with 1.5 n + 1024 buckets); the workspace must be 64-byte aligned. */
+ * 2x2x2-brick hash with 1.5 n + 1024 buckets, which the cell grid reuses, plus 32 KiB); the
+ * workspace must be 64-byte aligned. */
 size_t tsp_rulebook_workspace_bytes(int64_t n);
 
 /* d_coords int32 [n][3] -> d_nbr int32 [27*n]. d_status, if not NULL, is a device int32 that

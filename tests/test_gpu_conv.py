@@ -526,8 +526,9 @@ def _check_plan(p, table, n, order):
     first, ordered by their set of present corner taps (then by row, for a plan without
     coordinates), then the empty positions; the act bits of each
     (row group, block, tap) say exactly whether a voxel of the block has the tap; each (tap,
-    position) slot names the row the table gives, through the tile's sorted row list, or the zero
-    slot. Returns the tiles' distinct-row counts and the number of clear act bits."""
+    position) slot names the row the table gives, through the tile's list of distinct rows (sorted
+    for row tiles; in cell-grid position order for Morton tiles), or the zero slot. Returns the
+    tiles' distinct-row counts and the number of clear act bits."""
     vox = p["vox"].reshape(-1)
     assert np.array_equal(np.sort(vox[vox >= 0]), np.arange(n))
     assert (vox < 0).sum() == p["vox"].size - n
@@ -557,7 +558,10 @@ def _check_plan(p, table, n, order):
         if p["hdr"][t, 1]:
             continue
         rows = p["rowof"][t, :H[t]]
-        assert np.all(np.diff(rows) > 0)
+        if order == "rows":
+            assert np.all(np.diff(rows) > 0)
+        else:
+            assert len(np.unique(rows)) == H[t] and rows.min() >= 0 and rows.max() < n
         for tap in (0, 4, 13, 22, 26):
             sl = p["slots"][t, tap].transpose(0, 2, 1).reshape(512)   # [group][block][row] = position order
             got = np.where(sl == 2048, n, rows[np.minimum(sl, max(H[t] - 1, 0))])
@@ -590,13 +594,16 @@ def test_plan_records(gpu_lib, orc, shells, order):
         assert H.sum() < 0.8 * _plan_parts(rplan, n)["hdr"][:, 0].sum()
 
 
-def test_plan_wide_row_span(gpu_lib, orc, shells):
-    """A tile whose voxels lie at both ends of a 2.2M-row range (half a compact cube in the first
-    rows, the other half in the last, a dense box in between): its rows span more than the
-    two-level bitmap's 2^21, so the planner cuts the empty stretch out and the tile still stages
-    its rows in LDS. Records checked as in test_plan_records; the conv equals the unplanned one bit
-    for bit and the oracle on the cube's rows."""
-    _case("plan: wide row span")
+@pytest.mark.parametrize("order", ["rows", "morton"])
+def test_plan_wide_row_span(gpu_lib, orc, shells, order):
+    """Half a compact cube in the first rows, the other half in the last, a dense box of 2.2M
+    voxels in between. Row tiles: the first tile (the cube's first half and the box's first rows)
+    references rows at both ends of the range, more than the two-level bitmap's 2^21, so the
+    planner cuts the empty stretch out and the tile still stages its rows in LDS. Morton tiles: the
+    cube is one 8^3 cell and one tile of its own, with the first and the last rows. Records of that
+    tile checked as in test_plan_records; the conv equals the unplanned one bit for bit and the
+    oracle on the cube's rows."""
+    _case(f"plan: wide row span, {order}")
     import torch
     cube = np.stack(np.meshgrid(*[np.arange(8)] * 3, indexing="ij"), -1).reshape(-1, 3).astype(np.int32)
     box = (np.stack(np.meshgrid(*[np.arange(131)] * 3, indexing="ij"), -1).reshape(-1, 3) + 100).astype(np.int32)
@@ -605,16 +612,18 @@ def test_plan_wide_row_span(gpu_lib, orc, shells):
     assert n - 256 > (1 << 21)
     c = torch.from_numpy(coords).cuda()
     nbr = gpu_lib.rulebook_build(c)
-    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c if order == "morton" else None)
     torch.cuda.synchronize()
     p = _plan_parts(plan, n)
     table = nbr.cpu().numpy().reshape(27, n)
     first = np.nonzero((p["vox"] == 0).any(axis=1))[0][0]          # the tile holding row 0
-    assert (p["vox"][first] == n - 1).any()                         # ... and the last row
-    assert (p["hdr"][:, 1] == 0).all()
+    assert p["hdr"][first, 1] == 0
+    if order == "morton":
+        assert (p["vox"][first] == n - 1).any()                     # ... and the last row
+        assert (p["hdr"][:, 1] == 0).all()
     H = p["hdr"][first, 0]
     rows = p["rowof"][first, :H]
-    assert rows[0] == 0 and rows[-1] == n - 1 and np.all(np.diff(rows) > 0)
+    assert rows[0] == 0 and rows[-1] >= n - 256 and np.all(np.diff(rows) > 0)
     v = p["vox"][first]
     for tap in range(27):
         sl = p["slots"][first, tap].transpose(0, 2, 1).reshape(512)
@@ -632,6 +641,74 @@ def test_plan_wide_row_span(gpu_lib, orc, shells):
     rows_chk = np.concatenate([np.arange(256), np.arange(n - 256, n)])
     ref = orc.subm_conv_f64_rows(feats, nbr.cpu().numpy(), weight, bias, rows_chk)
     assert orc.rel_err(out.cpu().numpy()[rows_chk], ref) < TOL_16
+
+
+def test_ordered_plan_duplicates_unsorted(gpu_lib, orc, shells):
+    """Morton tiles of an unsorted shell with duplicated coordinates: the cell walk places each
+    coordinate's largest row in its cell and the other duplicates after all cells; every voxel
+    sits in the plan once, each slot names the table's row, and the planned conv equals the
+    unplanned one bit for bit."""
+    _case("ordered plan: duplicates, unsorted")
+    import torch
+    rng = np.random.default_rng(31)
+    shell = shells.sphere_shell(48, 24.0, 14.0, 16.0)
+    dup = shell[rng.choice(len(shell), size=700, replace=False)]
+    coords = np.ascontiguousarray(rng.permutation(np.concatenate([shell, dup])), np.int32)
+    n = len(coords)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    torch.cuda.synchronize()
+    table = nbr.cpu().numpy().reshape(27, n)
+    assert np.array_equal(table, orc.neighbor_table(coords).reshape(27, n))
+    p = _plan_parts(plan, n)
+    H, _ = _check_plan(p, table, n, "morton")
+    # the largest row of each coordinate is placed by its cell; the duplicates' other rows fill the
+    # last walk positions [n - 700, n), so tiles past the one holding position n - 700 hold only them
+    _, last = np.unique(coords[::-1], axis=0, return_index=True)
+    losers = np.setdiff1d(np.arange(n), n - 1 - last)
+    assert len(losers) == 700
+    t0 = (n - 700) // 512
+    tail = p["vox"][t0 + 1:].reshape(-1)
+    assert np.isin(tail[tail >= 0], losers).all()
+    head = p["vox"][:t0].reshape(-1)
+    assert not np.isin(head[head >= 0], losers).any()
+    assert (p["hdr"][:t0, 1] == 0).all()       # the cells' tiles stage their rows in LDS
+    feats = shells.round_to(rng.standard_normal((n, 64)).astype(np.float32), "bf16")
+    weight = shells.round_to((rng.standard_normal((64, 27, 64)) / 40).astype(np.float32), "bf16")
+    bias = (rng.standard_normal(64) * 0.1).astype(np.float32)
+    f, w, b = _dev(feats, torch.bfloat16), _dev(weight, torch.bfloat16), _dev(bias, torch.float32)
+    out = gpu_lib.subm_conv3x3_planned(f, nbr, plan, gpu_lib.conv_weight_pack(w), b, 64, out_dtype=torch.float32)
+    ref_d = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_d)
+
+
+@pytest.mark.parametrize("kind", ["far-flung", "scattered-box"])
+def test_ordered_plan_fallback(gpu_lib, shells, kind):
+    """Coordinates whose cell grid does not fit the plan's space -- a bounding box wider than the
+    directory allows (far-flung), or more occupied cells than the blocks' space (scattered-box):
+    the ordered build falls back to row tiles on the device, and its records equal the plan
+    without coordinates."""
+    _case(f"ordered plan fallback: {kind}")
+    import torch
+    rng = np.random.default_rng(41)
+    if kind == "far-flung":
+        coords = rng.integers(0, (1 << 21) - 3, size=(3000, 3)).astype(np.int32)
+    else:
+        coords = rng.integers(0, 400, size=(20000, 3)).astype(np.int32)
+    n = len(coords)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    a = _plan_parts(gpu_lib.conv_plan_build(nbr, n, coords=c), n)
+    b = _plan_parts(gpu_lib.conv_plan_build(nbr, n), n)
+    for k in ("hdr", "vox", "act"):
+        assert np.array_equal(a[k], b[k]), k
+    for t in range(a["hdr"].shape[0]):
+        if a["hdr"][t, 1] == 0:
+            H = a["hdr"][t, 0]
+            assert np.array_equal(a["rowof"][t, :H], b["rowof"][t, :H])
+            assert np.array_equal(a["slots"][t], b["slots"][t])
 
 
 @pytest.mark.parametrize("ci,co", [(128, 128), (64, 64), (256, 64)])

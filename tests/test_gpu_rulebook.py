@@ -40,6 +40,10 @@ def test_edge_cases(gpu_lib, orc, shells):
         "shell-255": shells.sphere_shell(40, 20.0, 10.0, 11.0)[:255],
         "shell-257": shells.sphere_shell(40, 20.0, 10.0, 11.0)[:257],
         "unsorted": rng.permutation(shells.sphere_shell(40, 20.0, 12.0, 14.0)),
+        # a cell directory fits the workspace but the occupied cells' blocks do not: the hash
+        "scattered-box": rng.integers(0, 400, size=(20000, 3)).astype(np.int32),
+        # duplicates spread over many cells of the grid
+        "shell-duplicates": np.concatenate([shells.sphere_shell(40, 20.0, 12.0, 14.0)] * 2)[::-1].copy(),
     }
     import torch
     for name, c in cases.items():

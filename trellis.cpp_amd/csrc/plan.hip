@@ -2,216 +2,183 @@
 //
 // A plan splits the output voxels into tiles of HB_M and records, per tile, the input rows its
 // table entries reference and the LDS slot of every (tap, voxel) (tile_plan.hpp). Which voxels
-// share a tile decides how many rows a tile stages: with coordinates, voxels are ordered by the
-// Morton code of their 8^3 cell (a stable radix sort, so voxels of one cell keep their row order)
-// and each run of HB_M voxels is a tile -- a compact patch of the surface, whose neighbours are
-// ~1.7 distinct rows per voxel on thin shells instead of ~3.3 for HB_M consecutive rows of an
-// x-major set. Without coordinates tiles are consecutive rows. Inside a tile the voxels are
+// share a tile decides how many rows a tile stages: with coordinates, the plan builds a cell grid
+// of the voxels (grid.hpp), lists them in Morton order of their 8^3 cells (then x, y, z inside a
+// cell) and each run of HB_M voxels is a tile -- a compact patch of the surface, whose neighbours
+// are ~1.7 distinct rows per voxel on thin shells instead of ~3.3 for HB_M consecutive rows of an
+// x-major set -- and the tiles read their neighbours from the grid, where a Morton-ordered tile's
+// neighbourhood is a few cells, instead of gathering them from the tap-major table. Without
+// coordinates, or when the grid does not fit, tiles are consecutive rows. Inside a tile the voxels are
 // grouped by which corner taps they have (see k_plan_build). The conv's results do not depend on
 // the grouping: every output row sums the same products in the same order wherever it sits (a
 // skipped absent tap would only have added exact zeros).
 #include <algorithm>
 
+#include "grid.hpp"
 #include "tile_plan.hpp"
 
 namespace tsp {
 namespace {
 
-// ---- Morton order of 8^3 cells: stable LSD radix sort, 8-bit digits -----------------------------
-constexpr int RS_NT = 512;                  // threads per sort workgroup
-constexpr int RS_ROUNDS = 16;               // items per thread and pass
-constexpr int RS_TILE = RS_NT * RS_ROUNDS;  // items per sort workgroup
-constexpr int RS_BINS = 256;
-constexpr int RS_PASSES = 3;                // 24-bit keys
-constexpr int RS_SCAN_NT = 256;
+// ---- Morton order from the cell grid -----------------------------------------------------------
+// The cell walk lists the voxels block by block (blocks are numbered in Morton order of their
+// cells), each block's voxels in x, y, z order inside the cell; then the voxels that hold no
+// block word -- duplicates of a coordinate other than its largest row, and coordinates out of
+// range -- in row order. Three launches: counts, their scan (one workgroup), the stores.
+constexpr int WK_NT = 256;
 
-// bits of v (8 used) spread to every third position
-__device__ __forceinline__ uint32_t spread3(uint32_t v) {
-    uint32_t r = 0;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) r |= ((v >> b) & 1u) << (3 * b);
-    return r;
+__device__ __forceinline__ int wave_sum_i(int v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
 }
 
-// key = Morton code of the voxel's 8^3 cell (8 bits per axis, x most significant; coordinates past
-// 2^11 wrap, which only costs locality), value = row
-__global__ void k_order_keys(const int32_t* __restrict__ coords, int64_t n, uint32_t* __restrict__ keys,
-                             int32_t* __restrict__ vals) {
-    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t x = (uint32_t)coords[3 * i] >> 3, y = (uint32_t)coords[3 * i + 1] >> 3,
-                   z = (uint32_t)coords[3 * i + 2] >> 3;
-    keys[i] = (spread3(x & 255u) << 2) | (spread3(y & 255u) << 1) | spread3(z & 255u);
-    vals[i] = (int32_t)i;
+// voxel i holds no block word
+__device__ __forceinline__ bool left_out(const int32_t* __restrict__ coords, const GridRef& g, int64_t i) {
+    const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+    if (!coords_ok(x, y, z)) return true;
+    const int32_t blk = grid_block(g, x >> 3, y >> 3, z >> 3);
+    return g.blocks[(int64_t)blk * 512 + cell_local(x, y, z)] != (int32_t)(i + 1);
 }
 
-// digit counts of each workgroup's RS_TILE keys: hist[digit * nblk + workgroup]
-__global__ __launch_bounds__(RS_NT) void k_rs_hist(const uint32_t* __restrict__ kin, int64_t n, int shift,
-                                                   int32_t* __restrict__ hist, int nblk) {
-    __shared__ int sH[RS_BINS];
-    const int tid = threadIdx.x;
-    if (tid < RS_BINS) sH[tid] = 0;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * RS_TILE;
-    for (int r = 0; r < RS_ROUNDS; ++r) {
-        const int64_t i = base + r * RS_NT + tid;
-        if (i < n) atomicAdd(&sH[(kin[i] >> shift) & (RS_BINS - 1)], 1);
-    }
-    __syncthreads();
-    if (tid < RS_BINS) hist[(int64_t)tid * nblk + blockIdx.x] = sH[tid];
-}
-
-// Exclusive prefix sum of one digit's row hist[digit * nblk + 0 .. nblk) in place (a workgroup per
-// digit), its total into tot[digit]. The digits' bases are added by the scatter.
-__global__ __launch_bounds__(RS_SCAN_NT) void k_rs_scan_rows(int32_t* __restrict__ hist, int nblk,
-                                                             int32_t* __restrict__ tot) {
-    __shared__ int sW[RS_SCAN_NT / 64];
+// Workgroup p: the voxel counts of blocks [p bchunk, +bchunk) into counts[] and their sum into
+// parts[p]; each block's presence bitmap (byte (x & 7) * 8 + (y & 7) holds the z bits) into
+// pres[64 b ..]; the left-out voxels of rows [p vchunk, +vchunk) into parts[GRID_PARTS + p].
+__global__ __launch_bounds__(WK_NT) void k_walk_count(const int32_t* __restrict__ coords, int64_t n,
+                                                      const int32_t* __restrict__ dir, const GridHdr* __restrict__ hdr,
+                                                      int32_t* __restrict__ counts, uint8_t* __restrict__ pres,
+                                                      int32_t* __restrict__ parts) {
+    __shared__ int sW[WK_NT / 64];
+    __shared__ int sB[WK_NT / 64];
+    if (hdr->mode != GRID_MODE_CELLS) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    int32_t* a = hist + (int64_t)blockIdx.x * nblk;
-    int carry = 0;
-    for (int t0 = 0; t0 < nblk; t0 += RS_SCAN_NT) {
-        const int i = t0 + tid;
-        const int v = i < nblk ? a[i] : 0;
-        int x = v;   // inclusive scan over the wave
+    const GridRef g = grid_ref(dir, hdr);
+    const int64_t nb = hdr->nblocks, bchunk = (nb + GRID_PARTS - 1) / GRID_PARTS;
+    const int64_t b0 = blockIdx.x * bchunk, b1 = min(nb, b0 + bchunk);
+    int bsum = 0;
+    for (int64_t b = b0 + wave; b < b1; b += WK_NT / 64) {
+        // lane L holds words 4 L .. 4 L + 3 (x = L / 16, y = L / 2 % 8, z = 4 (L & 1) ..) and the
+        // same 256 words further
+        const u32x4_t* w = reinterpret_cast<const u32x4_t*>(g.blocks + b * 512);
+        const u32x4_t a = w[lane], c = w[64 + lane];
+        uint32_t na = 0, nc = 0;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(x, off, 64);
-            if (lane >= off) x += y;
+        for (int e = 0; e < 4; ++e) {
+            na |= (a[e] != 0u ? 1u : 0u) << e;
+            nc |= (c[e] != 0u ? 1u : 0u) << e;
         }
-        if (lane == 63) sW[wave] = x;
-        __syncthreads();
-        int before = 0, total = 0;
-#pragma unroll
-        for (int w = 0; w < RS_SCAN_NT / 64; ++w) {
-            before += w < wave ? sW[w] : 0;
-            total += sW[w];
+        const uint32_t pa = __shfl_xor(na, 1, 64), pc = __shfl_xor(nc, 1, 64);
+        if ((lane & 1) == 0) {
+            pres[b * 64 + (lane >> 1)] = (uint8_t)(na | (pa << 4));
+            pres[b * 64 + 32 + (lane >> 1)] = (uint8_t)(nc | (pc << 4));
         }
-        if (i < nblk) a[i] = carry + before + x - v;
-        carry += total;
-        __syncthreads();   // sW is rewritten by the next round
+        const int k = wave_sum_i(__popc(na) + __popc(nc));
+        if (lane == 0) counts[b] = k;
+        bsum += k;
     }
-    if (tid == 0) tot[blockIdx.x] = carry;
+    const int64_t vchunk = (n + GRID_PARTS - 1) / GRID_PARTS;
+    const int64_t v0 = blockIdx.x * vchunk, v1 = min(n, v0 + vchunk);
+    int lc = 0;
+    for (int64_t i = v0 + tid; i < v1; i += WK_NT) lc += left_out(coords, g, i);
+    lc = wave_sum_i(lc);
+    if (lane == 0) { sW[wave] = lc; sB[wave] = bsum; }
+    __syncthreads();
+    if (tid == 0) {
+        int tb = 0, tl = 0;
+        for (int w = 0; w < WK_NT / 64; ++w) { tb += sB[w]; tl += sW[w]; }
+        parts[blockIdx.x] = tb;
+        parts[GRID_PARTS + blockIdx.x] = tl;
+    }
 }
 
-// Stable scatter of each workgroup's RS_TILE (key, value) pairs to their digit's range. Pairs are
-// ranked in index order: round by round (RS_NT consecutive pairs), wave by wave, lane by lane. A
-// lane's rank among its wave's lanes of the same digit comes from ballots of the digit's 8 bits.
-__global__ __launch_bounds__(RS_NT) void k_rs_scatter(const uint32_t* __restrict__ kin,
-                                                      const int32_t* __restrict__ vin, int64_t n, int shift,
-                                                      const int32_t* __restrict__ off, const int32_t* __restrict__ tot,
-                                                      int nblk, uint32_t* __restrict__ kout,
-                                                      int32_t* __restrict__ vout) {
-    constexpr int NW = RS_NT / 64;
-    static_assert(RS_BINS == 4 * 64 && NW >= 4, "digit bases: four waves of 64 digits");
-    __shared__ int sCnt[NW][RS_BINS];   // a round's count (then first rank) per (wave, digit)
-    __shared__ int sRun[RS_BINS];       // pairs of each digit placed by earlier rounds
-    __shared__ int sGlob[RS_BINS];      // the workgroup's first position per digit
-    __shared__ int sTot[4];
+// One workgroup: both partial arrays into exclusive prefixes; nplaced = the block voxels.
+__global__ __launch_bounds__(GRID_PARTS) void k_walk_top(GridHdr* __restrict__ hdr, int32_t* __restrict__ parts) {
+    __shared__ int sW[GRID_PARTS / 64];
+    if (hdr->mode != GRID_MODE_CELLS) return;
+    int total;
+    const int vb = parts[threadIdx.x], vl = parts[GRID_PARTS + threadIdx.x];
+    parts[threadIdx.x] = block_exclusive_scan<GRID_PARTS>(vb, sW, total);
+    if (threadIdx.x == 0) hdr->nplaced = total;
+    parts[GRID_PARTS + threadIdx.x] = block_exclusive_scan<GRID_PARTS>(vl, sW, total);
+}
+
+// The stores of the walk: block voxels from their block's start, then the left-out voxels after
+// the nplaced block voxels.
+__global__ __launch_bounds__(WK_NT) void k_walk_emit(const int32_t* __restrict__ coords, int64_t n,
+                                                     const int32_t* __restrict__ dir, const GridHdr* __restrict__ hdr,
+                                                     const int32_t* __restrict__ counts,
+                                                     const int32_t* __restrict__ parts, int32_t* __restrict__ order) {
+    __shared__ int sW[WK_NT / 64];
+    __shared__ int sStart[WK_NT];
+    if (hdr->mode != GRID_MODE_CELLS) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // the digit's base (exclusive scan of the digit totals) + this workgroup's offset in its row
-    int dbase = 0;
-    if (tid < RS_BINS) {
-        const int t = tot[tid];
-        int x = t;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(x, o, 64);
-            if (lane >= o) x += y;
-        }
-        if (lane == 63) sTot[wave] = x;
-        dbase = x - t;
-    }
-    __syncthreads();
-    if (tid < RS_BINS) {
-        for (int w = 0; w < wave; ++w) dbase += sTot[w];
-        sRun[tid] = 0;
-        sGlob[tid] = dbase + off[(int64_t)tid * nblk + blockIdx.x];
-    }
-    const int64_t base = (int64_t)blockIdx.x * RS_TILE;
+    const GridRef g = grid_ref(dir, hdr);
+    const int64_t nb = hdr->nblocks, bchunk = (nb + GRID_PARTS - 1) / GRID_PARTS;
+    const int64_t b0 = blockIdx.x * bchunk, b1 = min(nb, b0 + bchunk);
+    int base = parts[blockIdx.x];
     const uint64_t below = (1ull << lane) - 1ull;
-    for (int r = 0; r < RS_ROUNDS; ++r) {
-        for (int k = tid; k < NW * RS_BINS; k += RS_NT) (&sCnt[0][0])[k] = 0;
+    for (int64_t r0 = b0; r0 < b1; r0 += WK_NT) {
+        const int64_t b = r0 + tid;
+        int total;
+        const int pre = block_exclusive_scan<WK_NT>(b < b1 ? counts[b] : 0, sW, total);
+        sStart[tid] = base + pre;
+        base += total;
         __syncthreads();
-        const int64_t i = base + r * RS_NT + tid;
-        const bool valid = i < n;
-        const uint32_t key = valid ? kin[i] : 0u;
-        const int32_t val = valid ? vin[i] : 0;
-        const int d = (int)((key >> shift) & (RS_BINS - 1));
-        uint64_t peers = __ballot(valid);
+        const int nr = (int)min<int64_t>(WK_NT, b1 - r0);
+        for (int j = wave; j < nr; j += WK_NT / 64) {
+            const int32_t* w = g.blocks + (r0 + j) * 512;
+            int at = sStart[j];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const uint64_t set = __ballot((d >> b) & 1);
-            peers &= ((d >> b) & 1) ? set : ~set;
-        }
-        const int rank = __popcll(peers & below);
-        if (valid && rank == 0) sCnt[wave][d] = __popcll(peers);
-        __syncthreads();
-        if (tid < RS_BINS) {
-            int run = sRun[tid];
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const int c = sCnt[w][tid];
-                sCnt[w][tid] = run;
-                run += c;
+            for (int r = 0; r < 8; ++r) {
+                const int32_t v = w[r * 64 + lane];
+                const uint64_t bal = __ballot(v != 0);
+                if (v != 0) order[at + __popcll(bal & below)] = v - 1;
+                at += __popcll(bal);
             }
-            sRun[tid] = run;
         }
-        __syncthreads();
-        if (valid) {
-            const int64_t pos = (int64_t)sGlob[d] + sCnt[wave][d] + rank;
-            kout[pos] = key;
-            vout[pos] = val;
-        }
-        __syncthreads();   // sCnt is cleared by the next round
+        __syncthreads();   // sStart is rewritten by the next round
+    }
+    const int64_t vchunk = (n + GRID_PARTS - 1) / GRID_PARTS;
+    const int64_t v0 = blockIdx.x * vchunk, v1 = min(n, v0 + vchunk);
+    int lbase = hdr->nplaced + parts[GRID_PARTS + blockIdx.x];
+    for (int64_t r0 = v0; r0 < v1; r0 += WK_NT) {
+        const int64_t i = r0 + tid;
+        const bool out = i < v1 && left_out(coords, g, i);
+        int total;
+        const int pre = block_exclusive_scan<WK_NT>(out ? 1 : 0, sW, total);
+        if (out) order[lbase + pre] = (int32_t)i;
+        lbase += total;
     }
 }
 
-struct SortScratch {
-    uint32_t* keys[2];
-    int32_t* vals[2];
-    int32_t* hist;
-    int32_t* tot;
-    int nblk;
+struct PlanScratch {
+    int32_t* order;
+    int32_t* counts;
+    uint8_t* pres;
+    void* tail;
+    void* region;
+    size_t region_bytes;
 };
-size_t sort_scratch_bytes(int64_t n) {
-    const int64_t nblk = ceil_div(std::max<int64_t>(n, 1), RS_TILE);
-    return 4 * align256((size_t)n * 4) + align256((size_t)nblk * RS_BINS * 4) + align256(RS_BINS * 4);
+// the grid may use 32 bytes per voxel + 16 MiB (surface-like sets need ~20-25 bytes per voxel);
+// presence bitmaps take 64 bytes per block of 2 KiB
+size_t grid_region_bytes(int64_t n) { return align256((size_t)n * 32 + ((size_t)16 << 20)); }
+size_t plan_scratch_bytes(int64_t n) {
+    return align256((size_t)n * 4) + align256((size_t)std::max<int64_t>(n, 1) * 4) +
+           align256(grid_region_bytes(n) / 32) + GRID_TAIL + grid_region_bytes(n);
 }
-SortScratch carve_sort(void* p, int64_t n) {
-    char* c = reinterpret_cast<char*>(p);
-    SortScratch s;
-    for (int b = 0; b < 2; ++b) {
-        s.keys[b] = reinterpret_cast<uint32_t*>(c);
-        c += align256((size_t)n * 4);
-        s.vals[b] = reinterpret_cast<int32_t*>(c);
-        c += align256((size_t)n * 4);
-    }
-    s.hist = reinterpret_cast<int32_t*>(c);
-    s.nblk = (int)ceil_div(std::max<int64_t>(n, 1), RS_TILE);
-    c += align256((size_t)s.nblk * RS_BINS * 4);
-    s.tot = reinterpret_cast<int32_t*>(c);
+PlanScratch carve_scratch(void* p, int64_t n) {
+    char* c = static_cast<char*>(p);
+    PlanScratch s;
+    s.order = reinterpret_cast<int32_t*>(c);
+    c += align256((size_t)n * 4);
+    s.counts = reinterpret_cast<int32_t*>(c);
+    c += align256((size_t)std::max<int64_t>(n, 1) * 4);
+    s.pres = reinterpret_cast<uint8_t*>(c);
+    c += align256(grid_region_bytes(n) / 32);
+    s.tail = c;
+    c += GRID_TAIL;
+    s.region = c;
+    s.region_bytes = grid_region_bytes(n);
     return s;
-}
-
-// Voxel rows in Morton order of their 8^3 cells; returns the buffer holding them.
-int morton_order(const int32_t* coords, int64_t n, const SortScratch& ss, hipStream_t s,
-                 const int32_t** order) {
-    hipLaunchKernelGGL(k_order_keys, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, coords, n,
-                       ss.keys[0], ss.vals[0]);
-    TSP_CHECK_LAUNCH();
-    int cur = 0;
-    for (int pass = 0; pass < RS_PASSES; ++pass, cur ^= 1) {
-        const int shift = 8 * pass;
-        hipLaunchKernelGGL(k_rs_hist, dim3(ss.nblk), dim3(RS_NT), 0, s, ss.keys[cur], n, shift, ss.hist, ss.nblk);
-        TSP_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_rs_scan_rows, dim3(RS_BINS), dim3(RS_SCAN_NT), 0, s, ss.hist, ss.nblk, ss.tot);
-        TSP_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_rs_scatter, dim3(ss.nblk), dim3(RS_NT), 0, s, ss.keys[cur], ss.vals[cur], n, shift,
-                           ss.hist, ss.tot, ss.nblk, ss.keys[cur ^ 1], ss.vals[cur ^ 1]);
-        TSP_CHECK_LAUNCH();
-    }
-    *order = ss.vals[cur];
-    return TSP_OK;
 }
 
 // ---- the plan of one tile per workgroup (HB_PLAN_NT threads, one voxel each) ------------------------
@@ -220,8 +187,66 @@ int morton_order(const int32_t* coords, int64_t n, const SortScratch& ss, hipStr
 // taps too, so a tap is often absent from all 32 rows of an MFMA block and costs no MFMA there);
 // then the 16 blocks are dealt to the 4 row groups (one per SIMD) so that the groups' MFMA counts
 // stay close.
+//
+// Distinct rows and slots, two ways:
+//   * window (cell grid, the tile's voxels within a box of at most WIN_COLS columns of <= 64
+//     voxels in z, with a voxel of margin): a bitmap over the box, one 64-bit word of z bits per
+//     (x, y) column. The tile's voxels are marked (one LDS OR each), dilated by one voxel along
+//     every axis with word shifts and ORs of the neighbouring columns, and ANDed with the grid's
+//     presence bits: the set bits are exactly the distinct rows the tile's taps reference. Their
+//     ranks in (x, y, z) order are the slots -- row order for coordinate-sorted sets -- and a
+//     voxel's 27 taps are 9 column reads (3 z bits each). No table entries are read; the box's
+//     cells are looked up once (a block number per cell in LDS).
+//   * otherwise (no grid, or a tile spread too wide): the table's 27 entries of each voxel,
+//     ranked by tile_plan_core.
+// With a grid tile q holds voxels order[512 q ..] of the cell walk; otherwise rows 512 q ...
+constexpr int WIN_COLS = 1280;                                   // columns of a window
+constexpr int WIN_CELLS = HB_PLAN_SCRATCH - 7 * WIN_COLS;        // cells of a window's box
+
+// Exclusive scan of the popcounts of the 64-bit words[0..nw) (nw <= WIN_COLS) into pre[];
+// returns the total. sRed: NT / 64 ints.
+template <int NT>
+__device__ int scan_popcounts64(const uint64_t* words, int nw, int32_t* pre, int* sRed) {
+    constexpr int CPT = (WIN_COLS + NT - 1) / NT;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int cnt[CPT], mine = 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        const int c = tid * CPT + k;
+        cnt[k] = c < nw ? __popcll(words[c]) : 0;
+        mine += cnt[k];
+    }
+    int x = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) sRed[wave] = x;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+        if (w < wave) base += sRed[w];
+        total += sRed[w];
+    }
+    base += x - mine;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        const int c = tid * CPT + k;
+        if (c < nw) pre[c] = base;
+        base += cnt[k];
+    }
+    __syncthreads();
+    return total;
+}
+
 __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __restrict__ nbr, int64_t n,
                                                            const int32_t* __restrict__ order,
+                                                           const int32_t* __restrict__ coords,
+                                                           const int32_t* __restrict__ dir,
+                                                           const uint8_t* __restrict__ pres,
+                                                           const GridHdr* __restrict__ hdr,
                                                            int64_t n_tiles, PlanView plan) {
     static_assert(HB_PLAN_NT == HB_M, "one thread per tile position");
     constexpr int NB = HB_M / 32;                 // MFMA row blocks of a tile
@@ -229,31 +254,173 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
     constexpr int ND = 257;                       // digits: corner sets 0..255, 256 = no voxel
     __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
     __shared__ __attribute__((aligned(16))) int32_t sRowOf[HB_SLOTS];
-    __shared__ uint32_t sScratch[HB_PLAN_SCRATCH];
+    __shared__ __attribute__((aligned(16))) uint32_t sScratch[HB_PLAN_SCRATCH];
     __shared__ int sRed[2 * HB_PLAN_NT / 64];
+    __shared__ int sBox[6][NW];                   // the tile's coordinate box, per wave
     __shared__ uint32_t sBlk[NB];                 // present taps of each sorted block
     __shared__ int sBase[NB];                     // first position of each sorted block
     __shared__ uint32_t sAct[4 * HB_ACT_WORDS];   // the tile's act words
-    // Until tile_plan_core, sRowOf holds the taps and the thread of each sorted index and the
-    // position of each thread, and the scratch the sort's counts.
+    // Until the slots are ranked (tile_plan_core), sRowOf holds the taps and the thread of each
+    // sorted index and the position of each thread, and the scratch the sort's counts; the
+    // window's bitmaps use the scratch before the sort.
     static_assert(HB_SLOTS * 4 >= HB_M * 4 + HB_M * 2 + HB_M * 2, "sort records fit the row list");
     static_assert(HB_PLAN_SCRATCH >= NW * ND + ND + 64, "sort counts fit the scratch");
+    static_assert(WIN_CELLS >= 512, "window bitmaps and cells fit the scratch");
     uint32_t* sTaps = reinterpret_cast<uint32_t*>(sRowOf);
     uint16_t* sTid = reinterpret_cast<uint16_t*>(sTaps + HB_M);
     uint16_t* sPos = sTid + HB_M;
     int* sCnt = reinterpret_cast<int*>(sScratch);            // [NW][ND]: count, then first rank
     int* sDig = sCnt + NW * ND;                               // [ND]: first sorted index of a digit
     int* sWsum = sDig + ND;                                   // scan of the digit totals
+    uint64_t* wT = reinterpret_cast<uint64_t*>(sScratch);                   // window: the tile's voxels
+    uint64_t* wP = wT + WIN_COLS;                                            //   referenced and present
+    uint64_t* wPres = wP + WIN_COLS;                                         //   present voxels
+    int32_t* wPre = reinterpret_cast<int32_t*>(wPres + WIN_COLS);            //   slot of a column's first bit
+    int32_t* wCell = wPre + WIN_COLS;                                        //   block of each cell of the box
 
     const int64_t tile = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t q = tile * HB_M + tid;
-    int64_t i[1] = {q < n ? (order ? (int64_t)order[q] : q) : -1};
-    int32_t nv[kTaps][1];
-    load_entries<1>(nbr, n, i, nv);
-    uint32_t taps = 0;
+    const bool cells = hdr != nullptr && hdr->mode == GRID_MODE_CELLS;
+    int64_t i[1] = {q < n ? (cells ? (int64_t)order[q] : q) : -1};
+
+    // the window, when the grid is there and the tile's box fits
+    GridRef g{};
+    int32_t x = 0, y = 0, z = 0;
+    bool valid = false, win = false;
+    int wx0 = 0, wy0 = 0, wz0 = 0, WY = 1, ncol = 0;
+    int ox = 0, oy = 0, oz = 0, CY = 1, CZ = 1;   // the box's first cell and cells along y, z
+    if (cells) {
+        g = grid_ref(dir, hdr);
+        if (i[0] >= 0) {
+            x = coords[3 * i[0]]; y = coords[3 * i[0] + 1]; z = coords[3 * i[0] + 2];
+            valid = coords_ok(x, y, z);
+        }
+        int b[6] = {valid ? x : INT32_MAX, valid ? y : INT32_MAX, valid ? z : INT32_MAX,
+                    valid ? x : -1, valid ? y : -1, valid ? z : -1};
 #pragma unroll
-    for (int t = 0; t < kTaps; ++t) taps |= (nv[t][0] >= 0 ? 1u : 0u) << t;
+        for (int a = 0; a < 6; ++a) {
+            b[a] = a < 3 ? wave_min(b[a]) : wave_max(b[a]);
+            if (lane == 0) sBox[a][wave] = b[a];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int a = 0; a < 6; ++a) {
+            int v = sBox[a][0];
+            for (int w = 1; w < NW; ++w) v = a < 3 ? min(v, sBox[a][w]) : max(v, sBox[a][w]);
+            b[a] = v;
+        }
+        if (b[3] >= 0) {
+            wx0 = b[0] - 1; wy0 = b[1] - 1; wz0 = b[2] - 1;
+            const int64_t WX = (int64_t)b[3] - b[0] + 3, WYl = (int64_t)b[4] - b[1] + 3, WZ = (int64_t)b[5] - b[2] + 3;
+            ox = wx0 >> 3; oy = wy0 >> 3; oz = wz0 >> 3;
+            const int64_t CX = ((wx0 + WX - 1) >> 3) - ox + 1, CYl = ((wy0 + WYl - 1) >> 3) - oy + 1,
+                          CZl = ((wz0 + WZ - 1) >> 3) - oz + 1;
+            win = WZ <= 64 && WX * WYl <= WIN_COLS && CX * CYl * CZl <= WIN_CELLS;
+            if (win) {
+                WY = (int)WYl;
+                CY = (int)CYl;
+                CZ = (int)CZl;
+                ncol = (int)(WX * WYl);
+                const int ncell = (int)(CX * CYl * CZl);
+                // the block of every cell of the box
+                for (int k = tid; k < ncell; k += HB_PLAN_NT)
+                    wCell[k] = grid_block(g, ox + k / (CY * CZ), oy + (k / CZ) % CY, oz + k % CZ);
+                __syncthreads();
+                // presence words of the columns, from the blocks' presence bytes
+                const uint64_t zmask = WZ == 64 ? ~0ull : ((1ull << WZ) - 1ull);
+                for (int c = tid; c < ncol; c += HB_PLAN_NT) {
+                    const int cx = wx0 + c / WY, cy = wy0 + c % WY;
+                    const int32_t* cc = wCell + ((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ;
+                    const int po = (cx & 7) * 8 + (cy & 7);
+                    uint64_t word = 0;
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) {
+                        if (k >= CZ) break;
+                        const int32_t blk = cc[k];
+                        const uint64_t byte = blk >= 0 ? pres[(int64_t)blk * 64 + po] : 0u;
+                        const int sh = (oz + k) * 8 - wz0;
+                        word |= sh >= 0 ? byte << sh : byte >> -sh;
+                    }
+                    wPres[c] = word & zmask;
+                    wT[c] = 0ull;
+                }
+                __syncthreads();
+                if (valid)
+                    atomicOr(reinterpret_cast<unsigned long long*>(&wT[(x - wx0) * WY + (y - wy0)]), 1ull << (z - wz0));
+                __syncthreads();
+                // dilate by one voxel, keep the present ones
+                for (int c = tid; c < ncol; c += HB_PLAN_NT) {
+                    const int cx = c / WY, cy = c % WY;
+                    uint64_t d = 0;
+#pragma unroll
+                    for (int dx = -1; dx <= 1; ++dx)
+#pragma unroll
+                        for (int dy = -1; dy <= 1; ++dy) {
+                            const int ax = cx + dx, ay = cy + dy;
+                            if (ax < 0 || ay < 0 || ax >= (int)WX || ay >= WY) continue;
+                            const uint64_t t = wT[ax * WY + ay];
+                            d |= t | (t << 1) | (t >> 1);
+                        }
+                    wP[c] = d & wPres[c];
+                }
+                __syncthreads();
+            }
+        }
+    }
+    // window and direct are uniform over the workgroup from here on
+    int H = 0;
+    bool direct = false;
+    uint32_t taps = 0;
+    uint16_t wsl[kTaps];
+    int32_t nv[kTaps][1];
+    if (win) {
+        H = scan_popcounts64<HB_PLAN_NT>(wP, ncol, wPre, sRed);
+        direct = H > HB_ZERO;
+        if (!direct) {
+            // the row of every slot s: column = the last one whose first slot is <= s, then the
+            // (s - first)-th set bit of its word
+            int32_t* ro = plan.rowof + tile * HB_SLOTS;
+            for (int sl = tid; sl < H; sl += HB_PLAN_NT) {
+                int lo = 0, hi = ncol - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (wPre[mid] <= sl) lo = mid; else hi = mid - 1;
+                }
+                uint64_t bits = wP[lo];
+                for (int k = sl - wPre[lo]; k > 0; --k) bits &= bits - 1ull;
+                const int cx = wx0 + lo / WY, cy = wy0 + lo % WY, cz = wz0 + __builtin_ctzll(bits);
+                const int32_t blk = wCell[((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ + ((cz >> 3) - oz)];
+                ro[sl] = g.blocks[(int64_t)blk * 512 + cell_local(cx, cy, cz)] - 1;
+            }
+        }
+        // taps and slots of this voxel: 3 z bits of each of its 9 neighbouring columns
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) wsl[t] = HB_ZERO;
+        if (valid) {
+            const int zz = z - wz0;   // in [1, WZ - 2]
+#pragma unroll
+            for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+                for (int dy = 0; dy < 3; ++dy) {
+                    const int c = (x - wx0 + dx - 1) * WY + (y - wy0 + dy - 1);
+                    const uint64_t w = wP[c];
+                    const uint32_t b3 = (uint32_t)(w >> (zz - 1)) & 7u;
+                    const int base = wPre[c] + __popcll(w & ((1ull << (zz - 1)) - 1ull));
+                    const int t0 = dx * 9 + dy * 3;
+                    taps |= b3 << t0;
+                    const int b0 = b3 & 1u, b1 = (b3 >> 1) & 1u;
+                    if (b3 & 1u) wsl[t0] = (uint16_t)base;
+                    if (b3 & 2u) wsl[t0 + 1] = (uint16_t)(base + b0);
+                    if (b3 & 4u) wsl[t0 + 2] = (uint16_t)(base + b0 + b1);
+                }
+        }
+        __syncthreads();   // the scratch is the sort's from here on
+    } else {
+        load_entries<1>(nbr, n, i, nv);
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) taps |= (nv[t][0] >= 0 ? 1u : 0u) << t;
+    }
     constexpr int kCorner[8] = {0, 2, 6, 8, 18, 20, 24, 26};   // taps (+-1, +-1, +-1)
     int d = 0;
 #pragma unroll
@@ -283,18 +450,18 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
         }
     }
     // exclusive scan of the digit totals (digits tid < ND, waves 0..4)
-    int x = tot;
+    int xs = tot;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
+        const int yv = __shfl_up(xs, off, 64);
+        if (lane >= off) xs += yv;
     }
-    if (lane == 63) sWsum[wave] = x;
+    if (lane == 63) sWsum[wave] = xs;
     __syncthreads();
     if (tid < ND) {
         int before = 0;
         for (int w = 0; w < wave; ++w) before += sWsum[w];
-        sDig[tid] = before + x - tot;
+        sDig[tid] = before + xs - tot;
     }
     __syncthreads();
     const int sidx = sDig[d] + sCnt[wave * ND + d] + rank;   // this voxel's sorted index
@@ -319,16 +486,16 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
             const int cj = __popc(sBlk[j]);
             r += (cj > c) || (cj == c && j < tid);
         }
-        const int slot = r >> 2, g = (slot & 1) ? 3 - (r & 3) : (r & 3);
-        sBase[tid] = g * 128 + slot * 32;
-        // word w of row group g: bit 4 t + slot (t in [8 w, 8 w + 8)) = tap t present in the block
+        const int slot = r >> 2, grp = (slot & 1) ? 3 - (r & 3) : (r & 3);
+        sBase[tid] = grp * 128 + slot * 32;
+        // word w of row group grp: bit 4 t + slot (t in [8 w, 8 w + 8)) = tap t present in the block
 #pragma unroll
         for (int w = 0; w < HB_ACT_WORDS; ++w) {
             uint32_t v = (blk >> (8 * w)) & 0xffu;   // the 8 tap bits spread to every fourth bit
             v = (v | (v << 12)) & 0x000F000Fu;
             v = (v | (v << 6)) & 0x03030303u;
             v = (v | (v << 3)) & 0x11111111u;
-            if (v) atomicOr(&sAct[g * HB_ACT_WORDS + w], v << slot);
+            if (v) atomicOr(&sAct[grp * HB_ACT_WORDS + w], v << slot);
         }
     }
     __syncthreads();
@@ -339,16 +506,25 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
     plan.vox[tile * HB_M + pos[0]] = (int32_t)i[0];
     __syncthreads();   // sRowOf and the scratch are the planner's from here on
 
-    int H;
-    bool direct;
-    tile_plan_core<HB_PLAN_NT, 1>(nv, pos, sL, sRowOf, sScratch, sRed, H, direct);
+    if (win) {
+        if (!direct) {
+            const int rr = pos[0];
+#pragma unroll
+            for (int t = 0; t < kTaps; ++t) sL[t][rr >> 7][rr & 31][(rr >> 5) & 3] = wsl[t];
+        }
+        __syncthreads();
+    } else {
+        tile_plan_core<HB_PLAN_NT, 1>(nv, pos, sL, sRowOf, sScratch, sRed, H, direct);
+    }
     if (tid == 0) {
         int32_t* h = plan.hdr + tile * 4;
         h[0] = H; h[1] = direct ? 1 : 0; h[2] = 0; h[3] = 0;
     }
     if (direct) return;
-    int32_t* ro = plan.rowof + tile * HB_SLOTS;
-    for (int s = tid; s < H; s += HB_PLAN_NT) ro[s] = sRowOf[s];
+    if (!win) {
+        int32_t* ro = plan.rowof + tile * HB_SLOTS;
+        for (int s = tid; s < H; s += HB_PLAN_NT) ro[s] = sRowOf[s];
+    }
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(&sL[0][0][0][0]);
     u32x4_t* dst = reinterpret_cast<u32x4_t*>(plan.slots + tile * HB_SLOT_TABLE);
     for (int p = tid; p < HB_SLOT_TABLE / 8; p += HB_PLAN_NT) dst[p] = src[p];
@@ -358,20 +534,38 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
 
 size_t halo_plan_bytes(int64_t n) {
     const int64_t n_tiles = std::max<int64_t>(1, ceil_div(n, HB_M));
-    return plan_tile_bytes(n_tiles) + sort_scratch_bytes(n);
+    return plan_tile_bytes(n_tiles) + plan_scratch_bytes(n);
 }
 
+// With coordinates: the cell grid, the cell walk, then the tiles (which fall back to row tiles and
+// the table on the device when the grid did not fit its space).
 int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     if (n_tiles == 0) return TSP_OK;
     const int32_t* order = nullptr;
+    const int32_t* dir = nullptr;
+    const uint8_t* pres = nullptr;
+    const GridHdr* hdr = nullptr;
     if (coords) {
-        const SortScratch ss = carve_sort(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
-        const int st = morton_order(coords, n, ss, s, &order);
+        const PlanScratch ps = carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
+        const GridTail gt = carve_grid_tail(ps.tail);
+        int st = grid_build(coords, n, ps.region, ps.region_bytes, ps.tail, nullptr, s);
         if (st != TSP_OK) return st;
+        dir = static_cast<const int32_t*>(ps.region);
+        hipLaunchKernelGGL(k_walk_count, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
+                           ps.pres, gt.parts);
+        TSP_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_walk_top, dim3(1), dim3(GRID_PARTS), 0, s, gt.hdr, gt.parts);
+        TSP_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_walk_emit, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
+                           gt.parts, ps.order);
+        TSP_CHECK_LAUNCH();
+        order = ps.order;
+        pres = ps.pres;
+        hdr = gt.hdr;
     }
-    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, order, n_tiles,
-                       carve_plan(plan, n_tiles));
+    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, order, coords,
+                       dir, pres, hdr, n_tiles, carve_plan(plan, n_tiles));
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }

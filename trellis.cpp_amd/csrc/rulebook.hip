@@ -1,9 +1,18 @@
-// Coordinate hash and tap-major neighbour table on the GPU.
+// Tap-major neighbour table on the GPU.
 //
 // Replaces trellis::build_neighbor_table (src/sparse.cpp:21-39). The reference inserts every
 // voxel into a host std::unordered_map (later rows overwrite earlier ones, :26) and probes the
-// 27 offsets of each voxel (:28-37). Here the map is an open-addressing table in HBM whose
-// entries are bricks, not voxels:
+// 27 offsets of each voxel (:28-37). Here the map is one of two structures in HBM:
+//   * the cell grid (grid.hpp) when the voxels' bounding box is compact enough for the
+//     workspace: a Morton-ordered directory of 8^3 cells and a 512-word block per occupied
+//     cell, built without atomics on the hot path (plain stores, then a max-fix pass for
+//     duplicated coordinates). A voxel's 27 neighbours are 8 directory reads and 27 block reads,
+//     mostly from L2 since neighbouring voxels share cells;
+//   * otherwise (scattered or far-flung voxels) a coordinate hash described below.
+// Both are built in the same workspace; which one runs is decided on the device, and the
+// kernels of the other return at once.
+//
+// The hash is an open-addressing table whose entries are bricks, not voxels:
 //   * with X = x + 1 (so that the x - 1 probes stay non-negative), voxel (X, Y, Z) lives in
 //     brick (X>>1, Y>>1, Z>>1) at octant (X&1) | (Y&1)<<1 | (Z&1)<<2. A bucket is one 64-byte
 //     line: the rows of its 8 voxels (row + 1, 0 = absent) in words 0-7, then the brick's key;
@@ -19,12 +28,11 @@
 // own (scattered sets); surface shells fill about a third of a brick's octants.
 #include <algorithm>
 
-#include "common.hpp"
+#include "grid.hpp"
 
 namespace tsp {
 namespace {
 
-constexpr int32_t kCoordMax = (1 << 21) - 3;   // voxel coords in [0, kCoordMax]
 constexpr int kBucketWords = 16;               // uint32 words of a bucket (64 bytes)
 constexpr int kKeyWord = 8;                    // the key's first word; rows are words 0-7
 
@@ -55,25 +63,22 @@ __device__ __forceinline__ uint64_t home(const HashView& h, uint64_t key) {
 __device__ __forceinline__ uint64_t next(const HashView& h, uint64_t s) {
     return s + 1 == h.cap ? 0 : s + 1;
 }
-__device__ __forceinline__ bool coords_ok(int32_t x, int32_t y, int32_t z) {
-    return x >= 0 && y >= 0 && z >= 0 && x <= kCoordMax && y <= kCoordMax && z <= kCoordMax;
-}
+__device__ __forceinline__ bool hash_mode(const GridHdr* hdr) { return hdr->mode != GRID_MODE_CELLS; }
 
-__global__ void k_hash_clear(u32x4_t* __restrict__ words, int64_t n16) {
+__global__ void k_hash_clear(u32x4_t* __restrict__ words, int64_t n16, const GridHdr* __restrict__ hdr) {
+    if (!hash_mode(hdr)) return;
     for (int64_t s = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; s < n16;
          s += (int64_t)gridDim.x * blockDim.x)
         words[s] = u32x4_t{0, 0, 0, 0};
 }
 
 __global__ void k_hash_insert(const int32_t* __restrict__ coords, int64_t n, HashView h,
-                              int32_t* status) {
+                              const GridHdr* __restrict__ hdr) {
+    if (!hash_mode(hdr)) return;
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
-    if (!coords_ok(x, y, z)) {
-        if (status) atomicOr(status, 1);
-        return;
-    }
+    if (!coords_ok(x, y, z)) return;   // reported by the bounding-box pass
     const uint32_t X = x + 1, Y = y + 1, Z = z + 1;
     const uint64_t key = brick_key(X >> 1, Y >> 1, Z >> 1);
     const int oct = (X & 1) | (Y & 1) << 1 | (Z & 1) << 2;
@@ -112,7 +117,9 @@ constexpr int kProbeThreads = 256;
 
 __global__ __launch_bounds__(kProbeThreads) void k_probe(const int32_t* __restrict__ coords,
                                                          int64_t n, HashView h,
-                                                         int32_t* __restrict__ nbr) {
+                                                         int32_t* __restrict__ nbr,
+                                                         const GridHdr* __restrict__ hdr) {
+    if (!hash_mode(hdr)) return;
     const int64_t i = blockIdx.x * (int64_t)kProbeThreads + threadIdx.x;
     if (i >= n) return;
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
@@ -180,6 +187,28 @@ __global__ __launch_bounds__(kProbeThreads) void k_probe(const int32_t* __restri
     for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = r[t] ? (int32_t)(r[t] - 1) : miss;
 }
 
+// The table from the cell grid: one thread per voxel, 27 coalesced tap-major stores.
+__global__ __launch_bounds__(kProbeThreads) void k_grid_probe(const int32_t* __restrict__ coords,
+                                                              int64_t n, const int32_t* __restrict__ dir,
+                                                              const GridHdr* __restrict__ hdr,
+                                                              int32_t* __restrict__ nbr) {
+    if (hdr->mode != GRID_MODE_CELLS) return;
+    const int64_t i = blockIdx.x * (int64_t)kProbeThreads + threadIdx.x;
+    if (i >= n) return;
+    const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+    const int32_t miss = (int32_t)n;
+    if (!coords_ok(x, y, z)) {
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = miss;
+        return;
+    }
+    const GridRef g = grid_ref(dir, hdr);
+    int32_t key[kTaps], word[kTaps];
+    grid_neighbours(g, x, y, z, key, word);
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = word[t] ? word[t] - 1 : miss;
+}
+
 __global__ void k_count_pairs(const int32_t* __restrict__ nbr, int64_t total, int32_t sentinel,
                               unsigned long long* count) {
     unsigned long long local = 0;
@@ -196,9 +225,10 @@ __global__ void k_count_pairs(const int32_t* __restrict__ nbr, int64_t total, in
 
 using namespace tsp;
 
+// workspace: the hash buckets (also the cell grid's directory and blocks), then the grid's tail
 extern "C" size_t tsp_rulebook_workspace_bytes(int64_t n) {
     if (n < 0) return 0;
-    return table_capacity(n) * kBucketWords * 4;
+    return table_capacity(n) * kBucketWords * 4 + GRID_TAIL;
 }
 
 extern "C" int tsp_rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d_nbr,
@@ -217,16 +247,25 @@ extern "C" int tsp_rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d
     HashView h{reinterpret_cast<uint32_t*>(d_workspace), table_capacity(n)};
     TSP_REQUIRE((reinterpret_cast<uintptr_t>(d_workspace) & 63) == 0, TSP_ERR_INVALID,
                 "tsp_rulebook_build: workspace must be 64-byte aligned");
+    const size_t region = h.cap * kBucketWords * 4;
+    void* tail = static_cast<char*>(d_workspace) + region;
+    const GridHdr* hdr = carve_grid_tail(tail).hdr;
+    const int st = grid_build(d_coords, n, d_workspace, region, tail, d_status, s);
+    if (st != TSP_OK) return st;
+    const unsigned nvb = (unsigned)ceil_div(n, kProbeThreads);
+    hipLaunchKernelGGL(k_grid_probe, dim3(nvb), dim3(kProbeThreads), 0, s, d_coords, n,
+                       static_cast<const int32_t*>(d_workspace), hdr, d_nbr);
+    TSP_CHECK_LAUNCH();
+    // the hash, when the grid did not fit
     const int64_t n16 = (int64_t)h.cap * (kBucketWords / 4);
     const int clear_blocks = (int)std::min<int64_t>(ceil_div(n16, 256), 8192);
     hipLaunchKernelGGL(k_hash_clear, dim3(clear_blocks), dim3(256), 0, s,
-                       reinterpret_cast<u32x4_t*>(d_workspace), n16);
+                       reinterpret_cast<u32x4_t*>(d_workspace), n16, hdr);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_hash_insert, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s,
-                       d_coords, n, h, d_status);
+                       d_coords, n, h, hdr);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_probe, dim3((unsigned)ceil_div(n, kProbeThreads)), dim3(kProbeThreads),
-                       0, s, d_coords, n, h, d_nbr);
+    hipLaunchKernelGGL(k_probe, dim3(nvb), dim3(kProbeThreads), 0, s, d_coords, n, h, d_nbr, hdr);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
