@@ -125,7 +125,7 @@ int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t n, int ci,
  *
  * A plan splits the voxels into tiles of 512 and holds, for each tile, its voxels' rows (grouped
  * by which of the 8 corner taps they have inside the tile), which taps each 32-row block has, the
- * sorted set of input rows their table entries reference and each entry's rank in that set (the
+ * set of input rows their table entries reference and each entry's rank in that set (the
  * planned conv stages those rows in LDS once per tile).
  * Packed weights hold W [Co][27][Ci] in the order the matrix-core operands are read. Both are
  * plain device buffers owned by the caller. Every present tap of every voxel is computed, in the
@@ -139,9 +139,18 @@ int tsp_conv_plan_build(const int32_t* d_nbr, int64_t n, void* d_plan, size_t pl
 /* Tiles of 512 voxels in the Morton order of their 8^3 cells (d_coords int32 [n][3], the
  * coordinates d_nbr was built from): compact patches of a surface, whose 27-neighbourhoods
  * overlap, so a tile stages about half the rows of one made of consecutive rows. The plan's
- * buffer also serves the ordering's sort. */
+ * buffer also holds the build's cell grid of the coordinates; where that grid does not fit
+ * (scattered or far-flung voxels) the tiles are consecutive rows. The slot sets are in (x, y, z)
+ * order of the referenced voxels -- row order for coordinate-sorted sets. */
 int tsp_conv_plan_build_ordered(const int32_t* d_nbr, const int32_t* d_coords, int64_t n,
                                 void* d_plan, size_t plan_bytes, void* stream);
+/* tsp_rulebook_build and tsp_conv_plan_build_ordered in one call, on one cell grid of the
+ * coordinates (the table's workspace holds it; no counterpart in the reference, whose decoder
+ * builds a table per level, shape_decoder.cpp:93, that every conv of the level then uses). The
+ * table and the plan are those of the two separate calls. */
+int tsp_rulebook_build_planned(const int32_t* d_coords, int64_t n, int32_t* d_nbr, void* d_workspace,
+                               size_t workspace_bytes, int32_t* d_status, void* d_plan, size_t plan_bytes,
+                               void* stream);
 
 /* W [co][27][ci] (f16 or bf16; ci % 16 == 0, co % 32 == 0) -> d_packed, which must hold
  * tsp_conv_weight_packed_bytes(ci, co) bytes: the 27*ci*co values in operand order, then a

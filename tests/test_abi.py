@@ -59,6 +59,16 @@ def test_rulebook_validation(pkg):
     assert L.tsp_rulebook_build(FAKE, 1000, FAKE, FAKE, ws - 1, NULL, NULL) == 5
     assert "workspace" in _err(pkg)
     assert L.tsp_rulebook_count_pairs(FAKE, -3, FAKE, NULL) == 1
+    # the table and the ordered plan in one call: the plan buffer is checked first
+    pb = L.tsp_conv_plan_bytes(1000)
+    assert L.tsp_rulebook_build_planned(FAKE, -1, FAKE, FAKE, ws, NULL, FAKE, pb, NULL) == 1
+    assert L.tsp_rulebook_build_planned(NULL, 0, NULL, NULL, 0, NULL, NULL, 0, NULL) == 0
+    assert L.tsp_rulebook_build_planned(FAKE, 1000, FAKE, FAKE, ws, NULL, NULL, pb, NULL) == 1
+    assert "null plan" in _err(pkg)
+    assert L.tsp_rulebook_build_planned(FAKE, 1000, FAKE, FAKE, ws, NULL, FAKE, pb - 1, NULL) == 5
+    assert "plan buffer" in _err(pkg)
+    assert L.tsp_rulebook_build_planned(FAKE, 1000, FAKE, FAKE, ws - 1, NULL, FAKE, pb, NULL) == 5
+    assert "workspace" in _err(pkg)
 
 
 def test_workspace_sizes(pkg):

@@ -684,6 +684,42 @@ def test_ordered_plan_duplicates_unsorted(gpu_lib, orc, shells):
     assert torch.equal(out, ref_d)
 
 
+@pytest.mark.parametrize("kind", ["shell", "duplicates", "scattered-box"])
+def test_table_and_plan_in_one_call(gpu_lib, shells, kind):
+    """tsp_rulebook_build_planned: the table of tsp_rulebook_build and the records of
+    tsp_conv_plan_build_ordered, from one cell grid (a brick hash and row tiles for the scattered
+    set), also when the buffers are reused."""
+    _case(f"table + plan in one call: {kind}")
+    import torch
+    rng = np.random.default_rng(43)
+    if kind == "shell":
+        coords = shells.sphere_shell(80, 40.0, 30.0, 32.0)
+    elif kind == "duplicates":
+        sh = shells.sphere_shell(48, 24.0, 14.0, 16.0)
+        coords = rng.permutation(np.concatenate([sh, sh[rng.choice(len(sh), 500, replace=False)]]))
+    else:
+        coords = rng.integers(0, 400, size=(20000, 3))
+    coords = np.ascontiguousarray(coords, np.int32)
+    n = len(coords)
+    c = torch.from_numpy(coords).cuda()
+    nbr, plan = gpu_lib.rulebook_build_planned(c)
+    ref_nbr = gpu_lib.rulebook_build(c)
+    ref_plan = gpu_lib.conv_plan_build(ref_nbr, n, coords=c)
+    nbr2, plan2 = gpu_lib.rulebook_build_planned(c, nbr=torch.full_like(nbr, -7),
+                                                 plan=torch.full_like(plan, 255))
+    torch.cuda.synchronize()
+    assert torch.equal(nbr, ref_nbr) and torch.equal(nbr2, ref_nbr)
+    b = _plan_parts(ref_plan, n)
+    for got in (_plan_parts(plan, n), _plan_parts(plan2, n)):
+        for k in ("hdr", "vox", "act"):
+            assert np.array_equal(got[k], b[k]), k
+        for t in range(b["hdr"].shape[0]):
+            if b["hdr"][t, 1] == 0:
+                H = b["hdr"][t, 0]
+                assert np.array_equal(got["rowof"][t, :H], b["rowof"][t, :H])
+                assert np.array_equal(got["slots"][t], b["slots"][t])
+
+
 @pytest.mark.parametrize("kind", ["far-flung", "scattered-box"])
 def test_ordered_plan_fallback(gpu_lib, shells, kind):
     """Coordinates whose cell grid does not fit the plan's space -- a bounding box wider than the

@@ -23,7 +23,7 @@ STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "RANGE", 4: "UNSUPPORTED", 5: "WOR
 # Every extern "C" entry point the header declares (checked by the CPU test suite).
 EXPORTS = (
     "tsp_last_error", "tsp_version",
-    "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_count_pairs",
+    "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_build_planned", "tsp_rulebook_count_pairs",
     "tsp_subm_conv3x3", "tsp_subm_conv3x3_ex",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_plan_build_ordered",
     "tsp_conv_weight_pack", "tsp_conv_weight_packed_bytes", "tsp_subm_conv3x3_planned_ln",
@@ -86,6 +86,8 @@ def lib() -> ctypes.CDLL:
     L.tsp_rulebook_workspace_bytes.argtypes = [c_i64]
     L.tsp_rulebook_build.restype = c_int
     L.tsp_rulebook_build.argtypes = [c_vp, c_i64, c_vp, c_vp, c_sz, c_vp, c_vp]
+    L.tsp_rulebook_build_planned.restype = c_int
+    L.tsp_rulebook_build_planned.argtypes = [c_vp, c_i64, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp]
     L.tsp_rulebook_count_pairs.restype = c_int
     L.tsp_rulebook_count_pairs.argtypes = [c_vp, c_i64, c_vp, c_vp]
     L.tsp_subm_conv3x3.restype = c_int
@@ -206,6 +208,41 @@ def rulebook_build(coords, check: bool = True, stream=None):
     if check and n and int(status.item()) != 0:
         raise TspError("tsp_rulebook_build", 3, "coordinate outside [0, 2^21-3]")
     return nbr
+
+
+def rulebook_build_planned(coords, check: bool = True, nbr=None, workspace=None, plan=None, stream=None):
+    """coords int32 [N,3] on the GPU -> (neighbour table int32 [27*N], Morton-ordered conv plan
+    uint8 buffer): rulebook_build and conv_plan_build(coords=...) in one call on one cell grid.
+    nbr, workspace (uint8, tsp_rulebook_workspace_bytes(N)) and plan (uint8, tsp_conv_plan_bytes(N))
+    may be given to reuse buffers."""
+    torch = _torch()
+    _require_cuda(coords)
+    c = coords.contiguous()
+    if c.dtype != torch.int32 or c.dim() != 2 or c.shape[1] != 3:
+        raise ValueError("coords must be int32 [N, 3]")
+    n = c.shape[0]
+    ws_bytes = lib().tsp_rulebook_workspace_bytes(n)
+    nb = lib().tsp_conv_plan_bytes(n)
+    if nbr is None:
+        nbr = torch.empty(27 * n, dtype=torch.int32, device=c.device)
+    elif nbr.dtype != torch.int32 or nbr.numel() != 27 * n or not nbr.is_contiguous():
+        raise ValueError("nbr must be a contiguous int32 buffer of 27*N")
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c.device)
+    elif workspace.dtype != torch.uint8 or workspace.numel() < ws_bytes:
+        raise ValueError("workspace must be a uint8 buffer of tsp_rulebook_workspace_bytes(N)")
+    if plan is None:
+        plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=c.device)
+    elif plan.dtype != torch.uint8 or plan.numel() < nb:
+        raise ValueError("plan must be a uint8 buffer of tsp_conv_plan_bytes(N)")
+    status = torch.zeros(1, dtype=torch.int32, device=c.device) if check else None
+    _check("tsp_rulebook_build_planned",
+           lib().tsp_rulebook_build_planned(_ptr(c), n, _ptr(nbr), _ptr(workspace), ws_bytes,
+                                            _ptr(status) if check else None, _ptr(plan), nb,
+                                            _stream(stream)))
+    if check and n and int(status.item()) != 0:
+        raise TspError("tsp_rulebook_build_planned", 3, "coordinate outside [0, 2^21-3]")
+    return nbr, plan
 
 
 def count_pairs(nbr, n: int, stream=None) -> int:

@@ -45,6 +45,11 @@ int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, cons
 // Builds the plan of neighbour table `nbr` into `plan`: tiles in the Morton order of the voxels'
 // 8^3 cells when `coords` is given, else tiles of consecutive rows.
 int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s);
+// The same Morton-ordered plan on a cell grid already built from `coords` (region and tail of
+// grid_build, with cell_of = plan_cell_of(plan, n)), e.g. the neighbour table's.
+int32_t* plan_cell_of(void* plan, int64_t n);
+int halo_plan_build_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan,
+                            const void* region, void* tail, hipStream_t s);
 // Packed weights: the [co][27][ci] 16-bit values in the MFMA operand order, then a trailer of
 // HB_PACK_TRAILER bytes whose first word is nonzero when some weight is an Inf or a NaN. With
 // finite weights the planned conv skips the MFMAs of taps absent from a whole 32-row block (their

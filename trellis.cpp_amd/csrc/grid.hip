@@ -1,13 +1,15 @@
-// Cell grid build (grid.hpp): bounding box, directory, blocks -- nine launches, no host round
-// trip. Every kernel after the set-up returns at once when the header says the grid does not fit.
+// Cell grid build (grid.hpp): bounding box, directory, blocks -- seven launches, no host round
+// trip. When the grid does not fit and a brick hash is given, the same launches build the hash
+// instead (its buckets cleared by the numbering launch, its voxels inserted by the insert launch).
 #include <algorithm>
 
-#include "grid.hpp"
+#include "brick_hash.hpp"
 
 namespace tsp {
 namespace {
 
-constexpr int GB_NT = 256;   // threads of the grid-build workgroups
+constexpr int GB_NT = 256;        // threads of the grid-build workgroups
+constexpr int BBOX_PARTS = GRID_PARTS;   // workgroups of the bounding-box pass
 
 __device__ __forceinline__ int wave_min_i(int v) {
     for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, 64));
@@ -54,58 +56,63 @@ __global__ __launch_bounds__(GB_NT) void k_grid_bbox(const int32_t* __restrict__
     }
 }
 
-// One workgroup: reduce the partials, size the directory, decide the mode.
-__global__ __launch_bounds__(1024) void k_grid_setup(const int32_t* __restrict__ parts, int nparts,
-                                                     GridHdr* hdr, int64_t region_words) {
-    __shared__ int sR[6][16];
+// Every workgroup reduces the bounding-box partials and sizes the directory (the same answer in
+// each; workgroup 0 writes the header), then the directory is cleared.
+__global__ __launch_bounds__(GB_NT) void k_grid_clear(const int32_t* __restrict__ parts, GridHdr* __restrict__ hdr,
+                                                      int32_t* __restrict__ dir, int64_t region_words) {
+    static_assert(BBOX_PARTS % GB_NT == 0, "whole partials per thread");
+    __shared__ int sR[6][GB_NT / 64];
+    __shared__ GridHdr sH;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    int v[6];
-#pragma unroll
-    for (int a = 0; a < 6; ++a) v[a] = tid < nparts ? parts[6 * tid + a] : (a < 3 ? INT32_MAX : -1);
 #pragma unroll
     for (int a = 0; a < 6; ++a) {
-        const int r = a < 3 ? wave_min_i(v[a]) : wave_max_i(v[a]);
+        int v = parts[6 * tid + a];
+        for (int p = tid + GB_NT; p < BBOX_PARTS; p += GB_NT) {
+            const int u = parts[6 * p + a];
+            v = a < 3 ? min(v, u) : max(v, u);
+        }
+        const int r = a < 3 ? wave_min_i(v) : wave_max_i(v);
         if (lane == 0) sR[a][wave] = r;
     }
     __syncthreads();
-    if (tid != 0) return;
-    int lo[3], hi[3];
+    if (tid == 0) {
+        int lo[3], hi[3];
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        lo[a] = sR[a][0];
-        hi[a] = sR[3 + a][0];
-        for (int w = 1; w < 16; ++w) { lo[a] = min(lo[a], sR[a][w]); hi[a] = max(hi[a], sR[3 + a][w]); }
-    }
-    GridHdr h{};
-    h.mode = GRID_MODE_CELLS;
-    if (hi[0] < 0) {                  // no valid voxel: a one-cell directory that stays empty
-        lo[0] = lo[1] = lo[2] = 0;
-        hi[0] = hi[1] = hi[2] = 0;
-    }
-    int ext = 1;
+        for (int a = 0; a < 3; ++a) {
+            lo[a] = sR[a][0];
+            hi[a] = sR[3 + a][0];
+            for (int w = 1; w < GB_NT / 64; ++w) { lo[a] = min(lo[a], sR[a][w]); hi[a] = max(hi[a], sR[3 + a][w]); }
+        }
+        GridHdr h{};
+        h.mode = GRID_MODE_CELLS;
+        if (hi[0] < 0) {                  // no valid voxel: a one-cell directory that stays empty
+            lo[0] = lo[1] = lo[2] = 0;
+            hi[0] = hi[1] = hi[2] = 0;
+        }
+        int ext = 1;
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        h.clo[a] = lo[a] >> 3;
-        ext = max(ext, (hi[a] >> 3) - h.clo[a] + 1);
+        for (int a = 0; a < 3; ++a) {
+            h.clo[a] = lo[a] >> 3;
+            ext = max(ext, (hi[a] >> 3) - h.clo[a] + 1);
+        }
+        int bits = 0;
+        while ((1 << bits) < ext) ++bits;
+        h.bits = bits;
+        if (bits > GRID_MAX_BITS) {
+            h.mode = GRID_MODE_FALLBACK;
+            h.bits = 0;
+        }
+        h.dir_n = (int64_t)1 << (3 * h.bits);
+        h.blocks_off = (h.dir_n + 63) & ~int64_t(63);
+        h.region_words = region_words;
+        if (h.blocks_off > region_words) h.mode = GRID_MODE_FALLBACK;
+        sH = h;
+        if (blockIdx.x == 0) *hdr = h;
     }
-    int bits = 0;
-    while ((1 << bits) < ext) ++bits;
-    h.bits = bits;
-    if (bits > GRID_MAX_BITS) {
-        h.mode = GRID_MODE_FALLBACK;
-        h.bits = 0;
-    }
-    h.dir_n = (int64_t)1 << (3 * h.bits);
-    h.blocks_off = (h.dir_n + 63) & ~int64_t(63);
-    h.region_words = region_words;
-    if (h.blocks_off > region_words) h.mode = GRID_MODE_FALLBACK;
-    *hdr = h;
-}
-
-__global__ __launch_bounds__(GB_NT) void k_grid_dir_clear(const GridHdr* __restrict__ hdr, int32_t* __restrict__ dir) {
-    if (hdr->mode != GRID_MODE_CELLS) return;
-    const int64_t nw = hdr->dir_n;
-    for (int64_t i = blockIdx.x * (int64_t)GB_NT + threadIdx.x; i < nw; i += (int64_t)gridDim.x * GB_NT) dir[i] = 0;
+    __syncthreads();
+    if (sH.mode != GRID_MODE_CELLS) return;
+    const int64_t nw = sH.dir_n;
+    for (int64_t i = blockIdx.x * (int64_t)GB_NT + tid; i < nw; i += (int64_t)gridDim.x * GB_NT) dir[i] = 0;
 }
 
 __global__ __launch_bounds__(GB_NT) void k_grid_mark(const int32_t* __restrict__ coords, int64_t n,
@@ -115,9 +122,17 @@ __global__ __launch_bounds__(GB_NT) void k_grid_mark(const int32_t* __restrict__
     if (i >= n) return;
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
     if (!coords_ok(x, y, z)) return;
-    const uint32_t m = cell_morton((uint32_t)((x >> 3) - hdr->clo[0]), (uint32_t)((y >> 3) - hdr->clo[1]),
-                                   (uint32_t)((z >> 3) - hdr->clo[2]));
-    dir[m] = 1;
+    const uint32_t rx = (uint32_t)((x >> 3) - hdr->clo[0]), ry = (uint32_t)((y >> 3) - hdr->clo[1]),
+                   rz = (uint32_t)((z >> 3) - hdr->clo[2]);
+    dir[cell_morton(rx, ry, rz)] = 1;
+    // A voxel at the bottom (top) of its cell is the halo word of the cell below (above), which
+    // must then have a block even when it holds no voxel: the neighbours of voxels in that
+    // z-layer of cells are read from it.
+    const int lz = z & 7;
+    if (lz == 0 || lz == 7) {
+        const uint32_t hz = lz == 0 ? rz - 1 : rz + 1;
+        if (hz < (1u << hdr->bits)) dir[cell_morton(rx, ry, hz)] = 1;
+    }
 }
 
 // Occupied directory words of each of GRID_PARTS chunks into parts[].
@@ -140,64 +155,118 @@ __global__ __launch_bounds__(GB_NT) void k_grid_scan(const GridHdr* __restrict__
     }
 }
 
-// One workgroup of GRID_PARTS threads: the partials into exclusive prefixes, nblocks, and whether
-// the blocks fit.
-__global__ __launch_bounds__(GRID_PARTS) void k_grid_scan_top(GridHdr* __restrict__ hdr, int32_t* __restrict__ parts) {
-    __shared__ int sW[GRID_PARTS / 64];
-    if (hdr->mode != GRID_MODE_CELLS) return;
-    int total;
-    const int v = parts[threadIdx.x];
-    parts[threadIdx.x] = block_exclusive_scan<GRID_PARTS>(v, sW, total);
-    if (threadIdx.x == 0) {
-        hdr->nblocks = total;
-        if ((int64_t)total * 512 >= ((int64_t)1 << 31) || hdr->blocks_off + (int64_t)total * 512 > hdr->region_words)
-            hdr->mode = GRID_MODE_FALLBACK;
-    }
-}
-
-// Block numbers into the directory (Morton order), and the blocks cleared.
-__global__ __launch_bounds__(GB_NT) void k_grid_apply(const GridHdr* __restrict__ hdr, int32_t* __restrict__ dir,
-                                                      const int32_t* __restrict__ parts) {
-    __shared__ int sW[GB_NT / 64];
-    if (hdr->mode != GRID_MODE_CELLS) return;
+// Every workgroup sums the GRID_PARTS partials for its own prefix and the block count, and
+// decides whether the blocks fit (the same answer in each; workgroup 0 records it). Then: block
+// numbers into the directory (Morton order; cell_of, when given, gets each block's directory
+// index) and the blocks cleared; or, when the grid does not fit and a hash is given, the hash's
+// buckets cleared.
+__global__ __launch_bounds__(GB_NT) void k_grid_apply(GridHdr* __restrict__ hdr, int32_t* __restrict__ dir,
+                                                      const int32_t* __restrict__ parts, HashView hash,
+                                                      int32_t* __restrict__ cell_of) {
+    constexpr int PPT = GRID_PARTS / GB_NT;
+    __shared__ int sW[2][GB_NT / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    bool cells = hdr->mode == GRID_MODE_CELLS;
+    int64_t nblocks = 0;
+    int run = 0;
+    if (cells) {
+        int v = 0, before = 0;
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int p = tid * PPT + k;
+            const int x = parts[p];
+            if (p < (int)blockIdx.x) before += x;
+            v += x;
+        }
+        v = wave_sum_i(v);
+        before = wave_sum_i(before);
+        if (lane == 0) { sW[0][wave] = v; sW[1][wave] = before; }
+        __syncthreads();
+        int tot = 0;
+        for (int w = 0; w < GB_NT / 64; ++w) { tot += sW[0][w]; run += sW[1][w]; }
+        __syncthreads();   // sW is reused by the numbering below
+        nblocks = tot;
+        cells = nblocks * GRID_BLOCK_WORDS < ((int64_t)1 << 31) &&
+                hdr->blocks_off + nblocks * GRID_BLOCK_WORDS <= hdr->region_words;
+        if (blockIdx.x == 0 && tid == 0) {
+            hdr->nblocks = (int32_t)nblocks;
+            if (!cells) hdr->mode = GRID_MODE_FALLBACK;
+        }
+    }
+    if (!cells) {
+        if (hash.cap == 0) return;
+        u32x4_t* w = reinterpret_cast<u32x4_t*>(hash.words);
+        const int64_t n16 = (int64_t)hash.cap * (kBucketWords / 4);
+        for (int64_t s = blockIdx.x * (int64_t)GB_NT + tid; s < n16; s += (int64_t)gridDim.x * GB_NT)
+            w[s] = u32x4_t{0u, 0u, 0u, 0u};
+        return;
+    }
     const int64_t nw = hdr->dir_n, chunk = (nw + GRID_PARTS - 1) / GRID_PARTS;
     const int64_t b = blockIdx.x * chunk, e = min(nw, b + chunk);
-    int run = parts[blockIdx.x];
     for (int64_t r0 = b; r0 < e; r0 += GB_NT) {
         const int64_t i = r0 + tid;
         const bool occ = i < e && dir[i] != 0;
         const uint64_t bal = __ballot(occ);
-        if (lane == 0) sW[wave] = __popcll(bal);
+        if (lane == 0) sW[0][wave] = __popcll(bal);
         __syncthreads();
         int before = 0, total = 0;
         for (int w = 0; w < GB_NT / 64; ++w) {
-            if (w < wave) before += sW[w];
-            total += sW[w];
+            if (w < wave) before += sW[0][w];
+            total += sW[0][w];
         }
-        if (occ) dir[i] = run + before + __popcll(bal & ((1ull << lane) - 1ull)) + 1;
+        if (occ) {
+            const int id = run + before + __popcll(bal & ((1ull << lane) - 1ull));
+            dir[i] = id + 1;
+            if (cell_of) cell_of[id] = (int32_t)i;
+        }
         run += total;
         __syncthreads();
     }
-    // clear the blocks: nblocks * 512 words, 16 bytes per store
+    // clear the blocks, 16 bytes per store
     u32x4_t* blk = reinterpret_cast<u32x4_t*>(dir + hdr->blocks_off);
-    const int64_t n16 = (int64_t)hdr->nblocks * 128;
+    const int64_t n16 = nblocks * (GRID_BLOCK_WORDS / 4);
     for (int64_t i = blockIdx.x * (int64_t)GB_NT + tid; i < n16; i += (int64_t)gridDim.x * GB_NT)
         blk[i] = u32x4_t{0u, 0u, 0u, 0u};
 }
 
-// row + 1 of each voxel into its block word; duplicates: some writer wins, k_grid_fix raises it
-// to the largest row
+// The words a voxel's row goes to: its own cell's block, and the halo word of the cell below
+// (z & 7 == 7) or above (z & 7 == 0) when that cell has a block. Returns how many (1 or 2).
+__device__ __forceinline__ int voxel_words(const GridRef& g, int32_t x, int32_t y, int32_t z, int64_t (&w)[2]) {
+    const int32_t cx = x >> 3, cy = y >> 3, cz = z >> 3;
+    const int col = ((x & 7) * 8 + (y & 7)) * GRID_COL_WORDS;
+    w[0] = (int64_t)grid_block(g, cx, cy, cz) * GRID_BLOCK_WORDS + col + (z & 7) + 1;
+    if ((z & 7) == 0 || (z & 7) == 7) {
+        const bool low = (z & 7) == 0;
+        const int32_t b = grid_block(g, cx, cy, low ? cz - 1 : cz + 1);
+        if (b >= 0) {
+            w[1] = (int64_t)b * GRID_BLOCK_WORDS + col + (low ? GRID_COL_WORDS - 1 : 0);
+            return 2;
+        }
+    }
+    return 1;
+}
+
+// row + 1 of each voxel into its block words (duplicates: some writer wins, k_grid_fix raises it
+// to the largest row); or the voxel into the hash
 __global__ __launch_bounds__(GB_NT) void k_grid_insert(const int32_t* __restrict__ coords, int64_t n,
-                                                       const GridHdr* __restrict__ hdr, int32_t* __restrict__ dir) {
-    if (hdr->mode != GRID_MODE_CELLS) return;
+                                                       const GridHdr* __restrict__ hdr, int32_t* __restrict__ dir,
+                                                       HashView hash) {
+    const bool cells = hdr->mode == GRID_MODE_CELLS;
+    if (!cells && hash.cap == 0) return;
     const int64_t i = blockIdx.x * (int64_t)GB_NT + threadIdx.x;
     if (i >= n) return;
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
     if (!coords_ok(x, y, z)) return;
+    if (!cells) {
+        hash_insert(hash, i, x, y, z);
+        return;
+    }
     const GridRef g = grid_ref(dir, hdr);
-    const int32_t blk = grid_block(g, x >> 3, y >> 3, z >> 3);
-    dir[hdr->blocks_off + (int64_t)blk * 512 + cell_local(x, y, z)] = (int32_t)(i + 1);
+    int64_t w[2];
+    const int k = voxel_words(g, x, y, z, w);
+    int32_t* blocks = dir + hdr->blocks_off;
+    blocks[w[0]] = (int32_t)(i + 1);
+    if (k == 2) blocks[w[1]] = (int32_t)(i + 1);
 }
 
 __global__ __launch_bounds__(GB_NT) void k_grid_fix(const int32_t* __restrict__ coords, int64_t n,
@@ -208,34 +277,32 @@ __global__ __launch_bounds__(GB_NT) void k_grid_fix(const int32_t* __restrict__ 
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
     if (!coords_ok(x, y, z)) return;
     const GridRef g = grid_ref(dir, hdr);
-    const int32_t blk = grid_block(g, x >> 3, y >> 3, z >> 3);
-    int32_t* w = dir + hdr->blocks_off + (int64_t)blk * 512 + cell_local(x, y, z);
-    if (*w < (int32_t)(i + 1)) atomicMax(w, (int32_t)(i + 1));
+    int64_t w[2];
+    const int k = voxel_words(g, x, y, z, w);
+    int32_t* blocks = dir + hdr->blocks_off;
+    for (int j = 0; j < k; ++j)
+        if (blocks[w[j]] < (int32_t)(i + 1)) atomicMax(&blocks[w[j]], (int32_t)(i + 1));
 }
 
 }  // namespace
 
 int grid_build(const int32_t* coords, int64_t n, void* region, size_t region_bytes, void* tail,
-               int32_t* status, hipStream_t s) {
+               int32_t* status, HashView hash, int32_t* cell_of, hipStream_t s) {
     const GridTail gt = carve_grid_tail(tail);
     int32_t* dir = static_cast<int32_t*>(region);
     const unsigned nvb = (unsigned)std::max<int64_t>(1, ceil_div(n, GB_NT));
-    hipLaunchKernelGGL(k_grid_bbox, dim3(GRID_PARTS), dim3(GB_NT), 0, s, coords, n, gt.parts, status);
+    hipLaunchKernelGGL(k_grid_bbox, dim3(BBOX_PARTS), dim3(GB_NT), 0, s, coords, n, gt.parts, status);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_setup, dim3(1), dim3(1024), 0, s, gt.parts, GRID_PARTS, gt.hdr,
+    hipLaunchKernelGGL(k_grid_clear, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.parts, gt.hdr, dir,
                        (int64_t)(region_bytes / 4));
-    TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_dir_clear, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_grid_mark, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_grid_scan, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir, gt.parts);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_scan_top, dim3(1), dim3(GRID_PARTS), 0, s, gt.hdr, gt.parts);
+    hipLaunchKernelGGL(k_grid_apply, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir, gt.parts, hash, cell_of);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_apply, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir, gt.parts);
-    TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_insert, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir);
+    hipLaunchKernelGGL(k_grid_insert, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir, hash);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_grid_fix, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir);
     TSP_CHECK_LAUNCH();

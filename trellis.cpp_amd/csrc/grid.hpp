@@ -3,11 +3,14 @@
 //
 // Space is cut into cells of 8^3 voxels. A directory, indexed by the Morton code of a cell
 // relative to the bounding box's first cell, holds for each occupied cell the index of its block
-// (+1, 0 = empty); blocks are numbered in Morton order of their cells. A block is 512 words, one
-// per voxel of the cell at (x & 7) << 6 | (y & 7) << 3 | (z & 7), holding row + 1 (0 = absent;
-// the largest row for duplicated coordinates, as the reference's map keeps the last insert).
-// Position key = block * 512 + local index: the word of the voxel in the block array, unique per
-// coordinate, ordered by cell (Morton) and then x, y, z inside the cell.
+// (+1, 0 = empty); blocks are numbered in Morton order of their cells. A block holds the cell's
+// 64 (x, y) columns, column (x & 7) * 8 + (y & 7) as 10 words: the voxel below the cell (the
+// z-neighbouring cell's top voxel), the cell's 8 voxels, the voxel above. A word holds row + 1
+// (0 = absent; the largest row for duplicated coordinates, as the reference's map keeps the last
+// insert). With the two halo words a voxel's three z-neighbours in any column are three
+// consecutive words of one block, read together. A cell directly above or below an occupied
+// cell's top or bottom voxel gets a block (holding only halo words if it has no voxel), so that
+// the halo word has somewhere to live.
 //
 // The build runs on the device without a host round trip; when the directory or the blocks would
 // not fit the space the caller gave (scattered or far-flung voxels), the header's mode says so
@@ -29,8 +32,7 @@ struct GridHdr {
     int32_t bits;           // Morton bits per axis of the directory
     int32_t clo[3];         // first cell of the bounding box
     int32_t nblocks;        // occupied cells
-    int32_t nplaced;        // voxels placed by the plan's cell walk (plan builds only)
-    int32_t pad0;
+    int32_t pad0, pad1;
     int64_t dir_n;          // directory words: 8^bits
     int64_t blocks_off;     // words from the directory to the first block
     int64_t region_words;   // words available for directory + blocks
@@ -87,8 +89,18 @@ __device__ __forceinline__ uint32_t spread3_10(uint32_t v) {
 __device__ __forceinline__ uint32_t cell_morton(uint32_t cx, uint32_t cy, uint32_t cz) {
     return (spread3_10(cx) << 2) | (spread3_10(cy) << 1) | spread3_10(cz);
 }
-__device__ __forceinline__ int cell_local(int32_t x, int32_t y, int32_t z) {
-    return ((x & 7) << 6) | ((y & 7) << 3) | (z & 7);
+constexpr int GRID_COL_WORDS = 10;                     // words of a block column
+constexpr int GRID_BLOCK_WORDS = 64 * GRID_COL_WORDS;  // words of a block
+// word of voxel (x, y, z) in its own cell's block
+__device__ __forceinline__ int cell_word(int32_t x, int32_t y, int32_t z) {
+    return ((x & 7) * 8 + (y & 7)) * GRID_COL_WORDS + (z & 7) + 1;
+}
+// bits 0, 3, 6, ..., 27 of v gathered into bits 0..9
+__device__ __forceinline__ uint32_t compact3_10(uint32_t v) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int b = 0; b < GRID_MAX_BITS; ++b) r |= ((v >> (3 * b)) & 1u) << b;
+    return r;
 }
 
 // A read-only view of a built grid.
@@ -117,30 +129,48 @@ __device__ __forceinline__ int32_t grid_block(const GridRef& g, int32_t cx, int3
 }
 
 // The 27 neighbours of voxel (x, y, z) (valid coordinates), tap t = 9 (dx + 1) + 3 (dy + 1) +
-// (dz + 1): key[t] = position key (-1 where the cell is absent) and the block word there (row + 1,
-// 0 = absent). The neighbourhood spans at most 2 cells per axis, so 8 directory reads serve it.
+// (dz + 1): word[t] = row + 1, 0 when absent. The neighbourhood's columns lie in at most 2 x 2
+// cells of the voxel's z-layer of cells, so 4 directory reads and 9 three-word reads serve it.
 __device__ __forceinline__ void grid_neighbours(const GridRef& g, int32_t x, int32_t y, int32_t z,
-                                                int32_t (&key)[kTaps], int32_t (&word)[kTaps]) {
-    const int32_t cx0 = (x - 1) >> 3, cy0 = (y - 1) >> 3, cz0 = (z - 1) >> 3;
-    const int32_t cx1 = (x + 1) >> 3, cy1 = (y + 1) >> 3, cz1 = (z + 1) >> 3;
-    int32_t blk[8];
+                                                int32_t (&word)[kTaps]) {
+    const int32_t cx0 = (x - 1) >> 3, cy0 = (y - 1) >> 3, cx1 = (x + 1) >> 3, cy1 = (y + 1) >> 3;
+    const int32_t cz = z >> 3;
+    const int32_t b00 = grid_block(g, cx0, cy0, cz), b10 = grid_block(g, cx1, cy0, cz);
+    const int32_t b01 = grid_block(g, cx0, cy1, cz), b11 = grid_block(g, cx1, cy1, cz);
+    // offset d of an axis lies in the upper of its two cells: h[d + 1] (never for d = -1); the
+    // block of a column is picked with selects, so that the four stay in registers
+    const bool hx[3] = {false, (x >> 3) != cx0, ((x + 1) >> 3) != cx0};
+    const bool hy[3] = {false, (y >> 3) != cy0, ((y + 1) >> 3) != cy0};
+    const int pz = z & 7;   // the three words start at the word below the voxel's own
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-        blk[c] = grid_block(g, (c & 1) ? cx1 : cx0, (c & 2) ? cy1 : cy0, (c & 4) ? cz1 : cz0);
+    for (int dx = 0; dx < 3; ++dx)
 #pragma unroll
-    for (int t = 0; t < kTaps; ++t) {
-        const int32_t nx = x + t / 9 - 1, ny = y + (t / 3) % 3 - 1, nz = z + t % 3 - 1;
-        const int c = ((nx >> 3) != cx0 ? 1 : 0) | ((ny >> 3) != cy0 ? 2 : 0) | ((nz >> 3) != cz0 ? 4 : 0);
-        key[t] = blk[c] >= 0 ? blk[c] * 512 + cell_local(nx, ny, nz) : -1;
-    }
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t) word[t] = key[t] >= 0 ? g.blocks[key[t]] : 0;
+        for (int dy = 0; dy < 3; ++dy) {
+            const int32_t b = hy[dy] ? (hx[dx] ? b11 : b01) : (hx[dx] ? b10 : b00);
+            const int32_t nx = x + dx - 1, ny = y + dy - 1;
+            const int t = dx * 9 + dy * 3;
+            if (b >= 0) {
+                const int32_t* w = g.blocks + (int64_t)b * GRID_BLOCK_WORDS + ((nx & 7) * 8 + (ny & 7)) * GRID_COL_WORDS + pz;
+                word[t] = w[0]; word[t + 1] = w[1]; word[t + 2] = w[2];
+            } else {
+                word[t] = word[t + 1] = word[t + 2] = 0;
+            }
+        }
 }
 
+// The brick hash (brick_hash.hpp) that stands in for the grid when it does not fit: cap buckets
+// of 16 words -- rows of octants 0..7 (8 words), key (2 words), unused. cap = 0: none.
+struct HashView {
+    uint32_t* words;
+    uint64_t cap;
+};
+
 // Builds the grid of coords[0..n) in `region` (region_bytes, 16-byte aligned) with header and
-// partials in `tail` (GRID_TAIL bytes). Coordinates outside [0, kCoordMax] are left out and set
-// bit 0 of *status when status is given. Returns a tsp_status of the launches.
+// partials in `tail` (GRID_TAIL bytes), or, when it does not fit and a hash is given (its
+// buckets are `region`), the hash. Coordinates outside [0, kCoordMax] are left out and set bit 0
+// of *status when status is given. Returns a tsp_status of the launches.
+// cell_of (optional, one int per block): each block's directory index (its cell's Morton code).
 int grid_build(const int32_t* coords, int64_t n, void* region, size_t region_bytes, void* tail,
-               int32_t* status, hipStream_t s);
+               int32_t* status, HashView hash, int32_t* cell_of, hipStream_t s);
 
 }  // namespace tsp

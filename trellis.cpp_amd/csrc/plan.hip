@@ -24,7 +24,7 @@ namespace {
 // The cell walk lists the voxels block by block (blocks are numbered in Morton order of their
 // cells), each block's voxels in x, y, z order inside the cell; then the voxels that hold no
 // block word -- duplicates of a coordinate other than its largest row, and coordinates out of
-// range -- in row order. Three launches: counts, their scan (one workgroup), the stores.
+// range -- in row order. Two launches: counts, then the stores.
 constexpr int WK_NT = 256;
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -37,12 +37,18 @@ __device__ __forceinline__ bool left_out(const int32_t* __restrict__ coords, con
     const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
     if (!coords_ok(x, y, z)) return true;
     const int32_t blk = grid_block(g, x >> 3, y >> 3, z >> 3);
-    return g.blocks[(int64_t)blk * 512 + cell_local(x, y, z)] != (int32_t)(i + 1);
+    return g.blocks[(int64_t)blk * GRID_BLOCK_WORDS + cell_word(x, y, z)] != (int32_t)(i + 1);
+}
+
+// coordinates packed 21 bits each (all ones: out of range)
+__device__ __forceinline__ uint64_t pack_xyz(int32_t x, int32_t y, int32_t z) {
+    return (uint64_t)x | ((uint64_t)y << 21) | ((uint64_t)z << 42);
 }
 
 // Workgroup p: the voxel counts of blocks [p bchunk, +bchunk) into counts[] and their sum into
-// parts[p]; each block's presence bitmap (byte (x & 7) * 8 + (y & 7) holds the z bits) into
-// pres[64 b ..]; the left-out voxels of rows [p vchunk, +vchunk) into parts[GRID_PARTS + p].
+// parts[p]; each block's presence bitmap (byte (x & 7) * 8 + (y & 7) holds the z bits of that
+// column) into pres[64 b ..]; the left-out voxels of rows [p vchunk, +vchunk) into
+// parts[GRID_PARTS + p]. A wave takes a block, a lane a column.
 __global__ __launch_bounds__(WK_NT) void k_walk_count(const int32_t* __restrict__ coords, int64_t n,
                                                       const int32_t* __restrict__ dir, const GridHdr* __restrict__ hdr,
                                                       int32_t* __restrict__ counts, uint8_t* __restrict__ pres,
@@ -56,22 +62,12 @@ __global__ __launch_bounds__(WK_NT) void k_walk_count(const int32_t* __restrict_
     const int64_t b0 = blockIdx.x * bchunk, b1 = min(nb, b0 + bchunk);
     int bsum = 0;
     for (int64_t b = b0 + wave; b < b1; b += WK_NT / 64) {
-        // lane L holds words 4 L .. 4 L + 3 (x = L / 16, y = L / 2 % 8, z = 4 (L & 1) ..) and the
-        // same 256 words further
-        const u32x4_t* w = reinterpret_cast<const u32x4_t*>(g.blocks + b * 512);
-        const u32x4_t a = w[lane], c = w[64 + lane];
-        uint32_t na = 0, nc = 0;
+        const int32_t* col = g.blocks + b * GRID_BLOCK_WORDS + lane * GRID_COL_WORDS + 1;
+        uint32_t byte = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            na |= (a[e] != 0u ? 1u : 0u) << e;
-            nc |= (c[e] != 0u ? 1u : 0u) << e;
-        }
-        const uint32_t pa = __shfl_xor(na, 1, 64), pc = __shfl_xor(nc, 1, 64);
-        if ((lane & 1) == 0) {
-            pres[b * 64 + (lane >> 1)] = (uint8_t)(na | (pa << 4));
-            pres[b * 64 + 32 + (lane >> 1)] = (uint8_t)(nc | (pc << 4));
-        }
-        const int k = wave_sum_i(__popc(na) + __popc(nc));
+        for (int k = 0; k < 8; ++k) byte |= (col[k] != 0 ? 1u : 0u) << k;
+        pres[b * 64 + lane] = (uint8_t)byte;
+        const int k = wave_sum_i(__popc(byte));
         if (lane == 0) counts[b] = k;
         bsum += k;
     }
@@ -90,32 +86,40 @@ __global__ __launch_bounds__(WK_NT) void k_walk_count(const int32_t* __restrict_
     }
 }
 
-// One workgroup: both partial arrays into exclusive prefixes; nplaced = the block voxels.
-__global__ __launch_bounds__(GRID_PARTS) void k_walk_top(GridHdr* __restrict__ hdr, int32_t* __restrict__ parts) {
-    __shared__ int sW[GRID_PARTS / 64];
-    if (hdr->mode != GRID_MODE_CELLS) return;
-    int total;
-    const int vb = parts[threadIdx.x], vl = parts[GRID_PARTS + threadIdx.x];
-    parts[threadIdx.x] = block_exclusive_scan<GRID_PARTS>(vb, sW, total);
-    if (threadIdx.x == 0) hdr->nplaced = total;
-    parts[GRID_PARTS + threadIdx.x] = block_exclusive_scan<GRID_PARTS>(vl, sW, total);
-}
-
-// The stores of the walk: block voxels from their block's start, then the left-out voxels after
-// the nplaced block voxels.
+// The stores of the walk: the row (order) and packed coordinates (wc) of every voxel -- block
+// voxels from their block's start, column by column, then the left-out voxels after all block
+// voxels. Every workgroup sums the partials before it (and all block partials) itself.
 __global__ __launch_bounds__(WK_NT) void k_walk_emit(const int32_t* __restrict__ coords, int64_t n,
                                                      const int32_t* __restrict__ dir, const GridHdr* __restrict__ hdr,
-                                                     const int32_t* __restrict__ counts,
-                                                     const int32_t* __restrict__ parts, int32_t* __restrict__ order) {
+                                                     const int32_t* __restrict__ counts, const uint8_t* __restrict__ pres,
+                                                     const int32_t* __restrict__ cell_of,
+                                                     const int32_t* __restrict__ parts, int32_t* __restrict__ order,
+                                                     uint64_t* __restrict__ wc) {
     __shared__ int sW[WK_NT / 64];
+    __shared__ int sS[3][WK_NT / 64];
     __shared__ int sStart[WK_NT];
     if (hdr->mode != GRID_MODE_CELLS) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const GridRef g = grid_ref(dir, hdr);
     const int64_t nb = hdr->nblocks, bchunk = (nb + GRID_PARTS - 1) / GRID_PARTS;
     const int64_t b0 = blockIdx.x * bchunk, b1 = min(nb, b0 + bchunk);
-    int base = parts[blockIdx.x];
-    const uint64_t below = (1ull << lane) - 1ull;
+    int base = 0, placed = 0, lbase = 0;
+    {
+        constexpr int PPT = GRID_PARTS / WK_NT;
+        int bb = 0, ball = 0, lb = 0;
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int p = tid * PPT + k;
+            const int vb = parts[p], vl = parts[GRID_PARTS + p];
+            ball += vb;
+            if (p < (int)blockIdx.x) { bb += vb; lb += vl; }
+        }
+        bb = wave_sum_i(bb); ball = wave_sum_i(ball); lb = wave_sum_i(lb);
+        if (lane == 0) { sS[0][wave] = bb; sS[1][wave] = ball; sS[2][wave] = lb; }
+        __syncthreads();
+        for (int w = 0; w < WK_NT / 64; ++w) { base += sS[0][w]; placed += sS[1][w]; lbase += sS[2][w]; }
+        lbase += placed;
+    }
     for (int64_t r0 = b0; r0 < b1; r0 += WK_NT) {
         const int64_t b = r0 + tid;
         int total;
@@ -125,53 +129,77 @@ __global__ __launch_bounds__(WK_NT) void k_walk_emit(const int32_t* __restrict__
         __syncthreads();
         const int nr = (int)min<int64_t>(WK_NT, b1 - r0);
         for (int j = wave; j < nr; j += WK_NT / 64) {
-            const int32_t* w = g.blocks + (r0 + j) * 512;
-            int at = sStart[j];
+            const int64_t blk = r0 + j;
+            const uint32_t m = (uint32_t)cell_of[blk];
+            const int32_t cx = (int32_t)compact3_10(m >> 2) + g.clo[0], cy = (int32_t)compact3_10(m >> 1) + g.clo[1],
+                          cz = (int32_t)compact3_10(m) + g.clo[2];
+            const uint32_t byte = pres[blk * 64 + lane];
+            const int cnt = __popc(byte);
+            int x = cnt;   // inclusive scan of the columns' counts
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const int32_t v = w[r * 64 + lane];
-                const uint64_t bal = __ballot(v != 0);
-                if (v != 0) order[at + __popcll(bal & below)] = v - 1;
-                at += __popcll(bal);
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(x, off, 64);
+                if (lane >= off) x += y;
             }
+            int at = sStart[j] + x - cnt;
+            const int32_t* col = g.blocks + blk * GRID_BLOCK_WORDS + lane * GRID_COL_WORDS + 1;
+            const int32_t vx = cx * 8 + (lane >> 3), vy = cy * 8 + (lane & 7);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if ((byte >> k) & 1u) {
+                    order[at] = col[k] - 1;
+                    wc[at] = pack_xyz(vx, vy, cz * 8 + k);
+                    ++at;
+                }
         }
         __syncthreads();   // sStart is rewritten by the next round
     }
     const int64_t vchunk = (n + GRID_PARTS - 1) / GRID_PARTS;
     const int64_t v0 = blockIdx.x * vchunk, v1 = min(n, v0 + vchunk);
-    int lbase = hdr->nplaced + parts[GRID_PARTS + blockIdx.x];
     for (int64_t r0 = v0; r0 < v1; r0 += WK_NT) {
         const int64_t i = r0 + tid;
         const bool out = i < v1 && left_out(coords, g, i);
         int total;
         const int pre = block_exclusive_scan<WK_NT>(out ? 1 : 0, sW, total);
-        if (out) order[lbase + pre] = (int32_t)i;
+        if (out) {
+            const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+            order[lbase + pre] = (int32_t)i;
+            wc[lbase + pre] = coords_ok(x, y, z) ? pack_xyz(x, y, z) : ~0ull;
+        }
         lbase += total;
     }
 }
 
 struct PlanScratch {
     int32_t* order;
+    uint64_t* wc;
     int32_t* counts;
+    int32_t* cell_of;
     uint8_t* pres;
     void* tail;
     void* region;
     size_t region_bytes;
 };
-// the grid may use 32 bytes per voxel + 16 MiB (surface-like sets need ~20-25 bytes per voxel);
-// presence bitmaps take 64 bytes per block of 2 KiB
+// the grid may use 32 bytes per voxel + 16 MiB (surface-like sets need ~25-30 bytes per voxel);
+// presence bitmaps take 64 bytes per block of 2.5 KiB
 size_t grid_region_bytes(int64_t n) { return align256((size_t)n * 32 + ((size_t)16 << 20)); }
 size_t plan_scratch_bytes(int64_t n) {
-    return align256((size_t)n * 4) + align256((size_t)std::max<int64_t>(n, 1) * 4) +
-           align256(grid_region_bytes(n) / 32) + GRID_TAIL + grid_region_bytes(n);
+    const size_t n1 = (size_t)std::max<int64_t>(n, 1);
+    return align256(n1 * 4) + align256(n1 * 8) + 2 * align256(n1 * 4) + align256(grid_region_bytes(n) / 32) +
+           GRID_TAIL + grid_region_bytes(n);
 }
 PlanScratch carve_scratch(void* p, int64_t n) {
+    const size_t n1 = (size_t)std::max<int64_t>(n, 1);
     char* c = static_cast<char*>(p);
     PlanScratch s;
     s.order = reinterpret_cast<int32_t*>(c);
-    c += align256((size_t)n * 4);
+    c += align256(n1 * 4);
+    s.wc = reinterpret_cast<uint64_t*>(c);
+    c += align256(n1 * 8);
     s.counts = reinterpret_cast<int32_t*>(c);
-    c += align256((size_t)std::max<int64_t>(n, 1) * 4);
+    c += align256(n1 * 4);
+    s.cell_of = reinterpret_cast<int32_t*>(c);
+    c += align256(n1 * 4);
     s.pres = reinterpret_cast<uint8_t*>(c);
     c += align256(grid_region_bytes(n) / 32);
     s.tail = c;
@@ -199,7 +227,8 @@ PlanScratch carve_scratch(void* p, int64_t n) {
 //     cells are looked up once (a block number per cell in LDS).
 //   * otherwise (no grid, or a tile spread too wide): the table's 27 entries of each voxel,
 //     ranked by tile_plan_core.
-// With a grid tile q holds voxels order[512 q ..] of the cell walk; otherwise rows 512 q ...
+// With a grid tile q holds voxels order[512 q ..] of the cell walk (their coordinates in
+// wc[512 q ..]); otherwise rows 512 q ...
 constexpr int WIN_COLS = 1280;                                   // columns of a window
 constexpr int WIN_CELLS = HB_PLAN_SCRATCH - 7 * WIN_COLS;        // cells of a window's box
 
@@ -243,7 +272,7 @@ __device__ int scan_popcounts64(const uint64_t* words, int nw, int32_t* pre, int
 
 __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __restrict__ nbr, int64_t n,
                                                            const int32_t* __restrict__ order,
-                                                           const int32_t* __restrict__ coords,
+                                                           const uint64_t* __restrict__ wc,
                                                            const int32_t* __restrict__ dir,
                                                            const uint8_t* __restrict__ pres,
                                                            const GridHdr* __restrict__ hdr,
@@ -293,7 +322,8 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
     if (cells) {
         g = grid_ref(dir, hdr);
         if (i[0] >= 0) {
-            x = coords[3 * i[0]]; y = coords[3 * i[0] + 1]; z = coords[3 * i[0] + 2];
+            const uint64_t p = wc[q];
+            x = (int32_t)(p & 0x1fffff); y = (int32_t)((p >> 21) & 0x1fffff); z = (int32_t)((p >> 42) & 0x1fffff);
             valid = coords_ok(x, y, z);
         }
         int b[6] = {valid ? x : INT32_MAX, valid ? y : INT32_MAX, valid ? z : INT32_MAX,
@@ -391,7 +421,7 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
                 for (int k = sl - wPre[lo]; k > 0; --k) bits &= bits - 1ull;
                 const int cx = wx0 + lo / WY, cy = wy0 + lo % WY, cz = wz0 + __builtin_ctzll(bits);
                 const int32_t blk = wCell[((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ + ((cz >> 3) - oz)];
-                ro[sl] = g.blocks[(int64_t)blk * 512 + cell_local(cx, cy, cz)] - 1;
+                ro[sl] = g.blocks[(int64_t)blk * GRID_BLOCK_WORDS + cell_word(cx, cy, cz)] - 1;
             }
         }
         // taps and slots of this voxel: 3 z bits of each of its 9 neighbouring columns
@@ -537,37 +567,50 @@ size_t halo_plan_bytes(int64_t n) {
     return plan_tile_bytes(n_tiles) + plan_scratch_bytes(n);
 }
 
-// With coordinates: the cell grid, the cell walk, then the tiles (which fall back to row tiles and
-// the table on the device when the grid did not fit its space).
+// The cell walk and the tiles on a grid built from coords (dir = its region, tail = its tail).
+static int plan_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, const int32_t* dir,
+                        void* tail, hipStream_t s) {
+    const int64_t n_tiles = ceil_div(n, HB_M);
+    const PlanScratch ps = carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
+    const GridTail gt = carve_grid_tail(tail);
+    hipLaunchKernelGGL(k_walk_count, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
+                       ps.pres, gt.parts);
+    TSP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_walk_emit, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
+                       ps.pres, ps.cell_of, gt.parts, ps.order, ps.wc);
+    TSP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, ps.order, ps.wc,
+                       dir, ps.pres, gt.hdr, n_tiles, carve_plan(plan, n_tiles));
+    TSP_CHECK_LAUNCH();
+    return TSP_OK;
+}
+
+// With coordinates: the cell grid (in the plan's scratch), the cell walk, then the tiles (which
+// fall back to row tiles and the table on the device when the grid did not fit its space).
 int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     if (n_tiles == 0) return TSP_OK;
-    const int32_t* order = nullptr;
-    const int32_t* dir = nullptr;
-    const uint8_t* pres = nullptr;
-    const GridHdr* hdr = nullptr;
     if (coords) {
         const PlanScratch ps = carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
-        const GridTail gt = carve_grid_tail(ps.tail);
-        int st = grid_build(coords, n, ps.region, ps.region_bytes, ps.tail, nullptr, s);
+        const int st = grid_build(coords, n, ps.region, ps.region_bytes, ps.tail, nullptr, HashView{nullptr, 0},
+                                  ps.cell_of, s);
         if (st != TSP_OK) return st;
-        dir = static_cast<const int32_t*>(ps.region);
-        hipLaunchKernelGGL(k_walk_count, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
-                           ps.pres, gt.parts);
-        TSP_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_walk_top, dim3(1), dim3(GRID_PARTS), 0, s, gt.hdr, gt.parts);
-        TSP_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_walk_emit, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
-                           gt.parts, ps.order);
-        TSP_CHECK_LAUNCH();
-        order = ps.order;
-        pres = ps.pres;
-        hdr = gt.hdr;
+        return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(ps.region), ps.tail, s);
     }
-    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, order, coords,
-                       dir, pres, hdr, n_tiles, carve_plan(plan, n_tiles));
+    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, nullptr, nullptr,
+                       nullptr, nullptr, nullptr, n_tiles, carve_plan(plan, n_tiles));
     TSP_CHECK_LAUNCH();
     return TSP_OK;
+}
+
+int32_t* plan_cell_of(void* plan, int64_t n) {
+    return carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(std::max<int64_t>(1, ceil_div(n, HB_M))), n).cell_of;
+}
+
+int halo_plan_build_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan,
+                            const void* region, void* tail, hipStream_t s) {
+    if (n == 0) return TSP_OK;
+    return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(region), tail, s);
 }
 
 }  // namespace tsp
