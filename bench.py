@@ -334,7 +334,7 @@ def main():
             "n_voxels": w6.n, "active_pairs": r6["pairs"], "ms_per_step": r6["ms"],
             "voxels_per_s": w6.n / (r6["ms"] * 1e-3), "tflops": f6 / (r6["ms"] * 1e-3) / 1e12,
             "frac": f6 / (r6["ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[w6.dtype],
-            "rulebook_ms": r6["rulebook_ms"], "plan_ms": r6["plan_ms"]}
+            "rulebook_ms": r6["rulebook_ms"], "plan_ms": r6["plan_ms"], "table_plan_ms": r6["table_plan_ms"]}
         del r6
 
     cpu = None
@@ -368,6 +368,7 @@ def main():
         "tflops_dense27_equivalent": flops_dense / (ms * 1e-3) / 1e12,
         "rulebook_ms": r["rulebook_ms"],
         "plan_ms": r["plan_ms"],
+        "table_plan_ms": r["table_plan_ms"],
         "wall_s_timed_region": r["wall"],
         "gpu": torch.cuda.get_device_name(0),
         "roofline": roof,
@@ -426,12 +427,14 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
         feats = torch.from_numpy(w.feats).to(tdt).to(dev)
         weight = torch.from_numpy(w.weight).to(tdt).to(dev)
         bias = torch.from_numpy(w.bias).to(dev)
-        # neighbour table: built once, timed on its own
+        # neighbour table: built once (range-checked), then timed on its own with its buffers
+        # allocated once, as a decoder level reuses them
         nbr = pkg.rulebook_build(coords)
+        ws = torch.empty(pkg.lib().tsp_rulebook_workspace_bytes(w.n), dtype=torch.uint8, device=dev)
         torch.cuda.synchronize()
         ev[0].record(stream)
         for _ in range(5):
-            nbr = pkg.rulebook_build(coords, check=False)
+            pkg.rulebook_build(coords, check=False, nbr=nbr, workspace=ws)
         ev[1].record(stream)
         torch.cuda.synchronize()
         rulebook_ms = ev[0].elapsed_time(ev[1]) / 5
@@ -445,9 +448,10 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
     # (like the table, a plan serves every conv of a stage; weights are packed at model load).
     planned = (args.algo in ("auto", "mfma") and w.dtype in ("bf16", "f16")
                and w.ci % 16 == 0 and w.co % 64 == 0)
-    plan = packed = plan_ms = None
+    plan = packed = plan_ms = table_plan_ms = None
     if planned and reuse is not None:
         plan, packed, plan_ms = reuse["plan"], reuse["packed"], reuse["plan_ms"]
+        table_plan_ms = reuse["table_plan_ms"]
     elif planned:
         # tiles in the Morton order of the voxels' 8^3 cells (or, with --plan-order rows, runs of
         # consecutive rows)
@@ -457,10 +461,19 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
         torch.cuda.synchronize()
         ev[0].record(stream)
         for _ in range(5):
-            plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
+            pkg.conv_plan_build(nbr, w.n, coords=pcoords, plan=plan)
         ev[1].record(stream)
         torch.cuda.synchronize()
         plan_ms = ev[0].elapsed_time(ev[1]) / 5
+        if pcoords is not None:
+            # the table and the Morton plan in one call, on one cell grid (what a decoder level
+            # runs); the same table and plan as the two calls above
+            ev[0].record(stream)
+            for _ in range(5):
+                pkg.rulebook_build_planned(coords, check=False, nbr=nbr, workspace=ws, plan=plan)
+            ev[1].record(stream)
+            torch.cuda.synchronize()
+            table_plan_ms = ev[0].elapsed_time(ev[1]) / 5
     if planned:
         def step():
             pkg.subm_conv3x3_planned(feats, nbr, plan, packed, bias, w.co, out=out, out_dtype=out.dtype)
@@ -479,7 +492,8 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return {"ms": ev[0].elapsed_time(ev[1]) / steps, "wall": wall, "pairs": pairs, "planned": planned,
-            "rulebook_ms": rulebook_ms, "plan_ms": plan_ms, "coords": coords, "feats": feats,
+            "rulebook_ms": rulebook_ms, "plan_ms": plan_ms, "table_plan_ms": table_plan_ms,
+            "coords": coords, "feats": feats,
             "weight": weight, "bias": bias, "nbr": nbr, "plan": plan, "packed": packed}
 
 

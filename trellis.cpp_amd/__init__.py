@@ -190,18 +190,32 @@ def _require_cuda(*ts):
             raise ValueError("tensors must live on the GPU")
 
 
-def rulebook_build(coords, check: bool = True, stream=None):
-    """coords int32 [N,3] on the GPU -> tap-major int32 neighbour table [27*N] (sentinel N)."""
+def _table_buffers(c, n, nbr, workspace):
+    torch = _torch()
+    ws_bytes = lib().tsp_rulebook_workspace_bytes(n)
+    if nbr is None:
+        nbr = torch.empty(27 * n, dtype=torch.int32, device=c.device)
+    elif nbr.dtype != torch.int32 or nbr.numel() != 27 * n or not nbr.is_contiguous():
+        raise ValueError("nbr must be a contiguous int32 buffer of 27*N")
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c.device)
+    elif workspace.dtype != torch.uint8 or workspace.numel() < ws_bytes:
+        raise ValueError("workspace must be a uint8 buffer of tsp_rulebook_workspace_bytes(N)")
+    return nbr, workspace, ws_bytes
+
+
+def rulebook_build(coords, check: bool = True, nbr=None, workspace=None, stream=None):
+    """coords int32 [N,3] on the GPU -> tap-major int32 neighbour table [27*N] (sentinel N).
+    nbr and workspace (uint8, tsp_rulebook_workspace_bytes(N)) may be given to reuse buffers;
+    check=False skips the range check's read-back."""
     torch = _torch()
     _require_cuda(coords)
     c = coords.contiguous()
     if c.dtype != torch.int32 or c.dim() != 2 or c.shape[1] != 3:
         raise ValueError("coords must be int32 [N, 3]")
     n = c.shape[0]
-    nbr = torch.empty(27 * n, dtype=torch.int32, device=c.device)
-    ws_bytes = lib().tsp_rulebook_workspace_bytes(n)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c.device)
-    status = torch.zeros(1, dtype=torch.int32, device=c.device)
+    nbr, ws, ws_bytes = _table_buffers(c, n, nbr, workspace)
+    status = torch.zeros(1, dtype=torch.int32, device=c.device) if check else None
     _check("tsp_rulebook_build",
            lib().tsp_rulebook_build(_ptr(c), n, _ptr(nbr), _ptr(ws), ws_bytes, _ptr(status),
                                     _stream(stream)))
@@ -221,16 +235,8 @@ def rulebook_build_planned(coords, check: bool = True, nbr=None, workspace=None,
     if c.dtype != torch.int32 or c.dim() != 2 or c.shape[1] != 3:
         raise ValueError("coords must be int32 [N, 3]")
     n = c.shape[0]
-    ws_bytes = lib().tsp_rulebook_workspace_bytes(n)
+    nbr, workspace, ws_bytes = _table_buffers(c, n, nbr, workspace)
     nb = lib().tsp_conv_plan_bytes(n)
-    if nbr is None:
-        nbr = torch.empty(27 * n, dtype=torch.int32, device=c.device)
-    elif nbr.dtype != torch.int32 or nbr.numel() != 27 * n or not nbr.is_contiguous():
-        raise ValueError("nbr must be a contiguous int32 buffer of 27*N")
-    if workspace is None:
-        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c.device)
-    elif workspace.dtype != torch.uint8 or workspace.numel() < ws_bytes:
-        raise ValueError("workspace must be a uint8 buffer of tsp_rulebook_workspace_bytes(N)")
     if plan is None:
         plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=c.device)
     elif plan.dtype != torch.uint8 or plan.numel() < nb:
@@ -238,7 +244,7 @@ def rulebook_build_planned(coords, check: bool = True, nbr=None, workspace=None,
     status = torch.zeros(1, dtype=torch.int32, device=c.device) if check else None
     _check("tsp_rulebook_build_planned",
            lib().tsp_rulebook_build_planned(_ptr(c), n, _ptr(nbr), _ptr(workspace), ws_bytes,
-                                            _ptr(status) if check else None, _ptr(plan), nb,
+                                            _ptr(status), _ptr(plan), nb,
                                             _stream(stream)))
     if check and n and int(status.item()) != 0:
         raise TspError("tsp_rulebook_build_planned", 3, "coordinate outside [0, 2^21-3]")
@@ -308,15 +314,19 @@ def subm_conv3x3(feats, nbr, weight, bias, out_dtype=None, algo: str = "auto", o
     return out
 
 
-def conv_plan_build(nbr, n: int, coords=None, stream=None):
-    """Plan of neighbour table nbr (int32 [27*N]) for the planned convs -> uint8 buffer. With
-    coords (int32 [N, 3], the coordinates the table was built from) tiles follow the Morton order
-    of the voxels' 8^3 cells; without, tiles are consecutive rows."""
+def conv_plan_build(nbr, n: int, coords=None, plan=None, stream=None):
+    """Plan of neighbour table nbr (int32 [27*N]) for the planned convs -> uint8 buffer (plan, of
+    tsp_conv_plan_bytes(N), may be given to reuse it). With coords (int32 [N, 3], the coordinates
+    the table was built from) tiles follow the Morton order of the voxels' 8^3 cells; without,
+    tiles are consecutive rows."""
     torch = _torch()
     _require_cuda(nbr, coords)
     _check_nbr(nbr, n, nbr.device)
     nb = lib().tsp_conv_plan_bytes(n)
-    plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=nbr.device)
+    if plan is None:
+        plan = torch.empty(max(nb, 1), dtype=torch.uint8, device=nbr.device)
+    elif plan.dtype != torch.uint8 or plan.numel() < nb:
+        raise ValueError("plan must be a uint8 buffer of tsp_conv_plan_bytes(N)")
     if coords is None:
         _check("tsp_conv_plan_build",
                lib().tsp_conv_plan_build(_ptr(nbr), n, _ptr(plan), nb, _stream(stream)))

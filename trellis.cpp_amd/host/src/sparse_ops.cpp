@@ -158,9 +158,18 @@ void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, in
     if (n == 0) return;
     DeviceBuffer ws(tsp_rulebook_workspace_bytes(n), s), status(d_status ? 0 : 4, s);
     if (!d_status) hip_check(hipMemsetAsync(status.get(), 0, 4, s), "rulebook");
-    lib(tsp_rulebook_build(d_coords, n, t.nbr.as<int32_t>(), ws.get(), ws.size(),
-                           d_status ? d_status : status.as<int32_t>(), s),
-        "rulebook");
+    if (morton_plan) {
+        // the table and its Morton-ordered plan from one cell grid
+        const size_t bytes = tsp_conv_plan_bytes(n);
+        t.plan = DeviceBuffer(bytes, s);
+        lib(tsp_rulebook_build_planned(d_coords, n, t.nbr.as<int32_t>(), ws.get(), ws.size(),
+                                       d_status ? d_status : status.as<int32_t>(), t.plan.get(), bytes, s),
+            "rulebook");
+    } else {
+        lib(tsp_rulebook_build(d_coords, n, t.nbr.as<int32_t>(), ws.get(), ws.size(),
+                               d_status ? d_status : status.as<int32_t>(), s),
+            "rulebook");
+    }
     if (d_status) return;
     int32_t st = 0;
     hip_check(hipMemcpyAsync(&st, status.get(), 4, hipMemcpyDeviceToHost, s), "rulebook");

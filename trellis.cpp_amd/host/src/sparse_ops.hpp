@@ -75,19 +75,17 @@ size_t convnext_scratch(const ConvNext& a, int xdt);
 struct Table {
     int64_t n = 0;
     tgr::DeviceBuffer nbr;    // int32 [27 n]
-    tgr::DeviceBuffer plan;   // empty until ensure_plan
-    // Set to the coordinates the table was built from (the caller's buffer, alive until the plan
-    // is built) for a plan whose tiles follow their Morton order: 6-8 % off each conv against
-    // tiles of consecutive rows, for a build about 0.1 ms longer per million voxels. Null: row
-    // tiles.
+    tgr::DeviceBuffer plan;   // built with the table (Morton tiles) or by ensure_plan (row tiles)
+    // The coordinates the table was built from when its plan has Morton-ordered tiles (6-8 % off
+    // each conv against tiles of consecutive rows); null: row tiles.
     const int32_t* coords = nullptr;
     void ensure_plan(hipStream_t s);
 };
 // Builds the table of d_coords [n][3] (its buffers stream-ordered on s). Without d_status it
 // waits for the build and throws for coordinates outside [0, 2^21-3]; with d_status (a device
 // int32 the caller zeroed) it ORs the range check into it and returns without waiting. With
-// morton_plan the table's plan will be built from d_coords, which must then stay alive until
-// ensure_plan has run.
+// morton_plan the table's Morton-ordered plan is built in the same call, on the same cell grid
+// (tsp_rulebook_build_planned).
 void build_table(const int32_t* d_coords, int64_t n, Table& t, hipStream_t s, int32_t* d_status = nullptr,
                  bool morton_plan = false);
 
