@@ -94,10 +94,11 @@ __global__ __launch_bounds__(WK_NT) void k_walk_emit(const int32_t* __restrict__
                                                      const int32_t* __restrict__ counts, const uint8_t* __restrict__ pres,
                                                      const int32_t* __restrict__ cell_of,
                                                      const int32_t* __restrict__ parts, int32_t* __restrict__ order,
-                                                     uint64_t* __restrict__ wc) {
+                                                     uint64_t* __restrict__ wc, int32_t* __restrict__ list_n) {
     __shared__ int sW[WK_NT / 64];
     __shared__ int sS[3][WK_NT / 64];
     __shared__ int sStart[WK_NT];
+    if (blockIdx.x == 0 && threadIdx.x == 0) *list_n = 0;   // the plan kernels' list of table tiles
     if (hdr->mode != GRID_MODE_CELLS) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const GridRef g = grid_ref(dir, hdr);
@@ -216,21 +217,27 @@ PlanScratch carve_scratch(void* p, int64_t n) {
 // then the 16 blocks are dealt to the 4 row groups (one per SIMD) so that the groups' MFMA counts
 // stay close.
 //
-// Distinct rows and slots, two ways:
-//   * window (cell grid, the tile's voxels within a box of at most WIN_COLS columns of <= 64
-//     voxels in z, with a voxel of margin): a bitmap over the box, one 64-bit word of z bits per
-//     (x, y) column. The tile's voxels are marked (one LDS OR each), dilated by one voxel along
+// Distinct rows and slots, two kernels:
+//   * k_plan_window (cell grid, the tile's voxels within a box of at most WIN_COLS columns of
+//     <= 64 voxels in z, with a voxel of margin): a bitmap over the box, one 64-bit word of z bits
+//     per (x, y) column. The tile's voxels are marked (one LDS OR each), dilated by one voxel along
 //     every axis with word shifts and ORs of the neighbouring columns, and ANDed with the grid's
 //     presence bits: the set bits are exactly the distinct rows the tile's taps reference. Their
 //     ranks in (x, y, z) order are the slots -- row order for coordinate-sorted sets -- and a
 //     voxel's 27 taps are 9 column reads (3 z bits each). No table entries are read; the box's
-//     cells are looked up once (a block number per cell in LDS).
-//   * otherwise (no grid, or a tile spread too wide): the table's 27 entries of each voxel,
-//     ranked by tile_plan_core.
+//     cells are looked up once (a block number per cell in LDS). Its LDS (~42 KiB) lets three
+//     workgroups share a CU, which hides the grid reads' latency.
+//   * k_plan_table (no grid, or the tiles k_plan_window listed as spread too wide): the table's 27
+//     entries of each voxel, ranked by tile_plan_core.
 // With a grid tile q holds voxels order[512 q ..] of the cell walk (their coordinates in
 // wc[512 q ..]); otherwise rows 512 q ...
-constexpr int WIN_COLS = 1280;                                   // columns of a window
-constexpr int WIN_CELLS = HB_PLAN_SCRATCH - 7 * WIN_COLS;        // cells of a window's box
+constexpr int WIN_COLS = 1280;     // columns of a window
+constexpr int WIN_CELLS = 1536;    // cells of a window's box
+constexpr int WIN_SEGS = 4;        // windows a tile may take
+constexpr int PL_NB = HB_M / 32;   // MFMA row blocks of a tile
+constexpr int PL_NW = HB_PLAN_NT / 64;
+constexpr int PL_ND = 257;         // digits: corner sets 0..255, 256 = no voxel
+constexpr int PL_ORDER_WORDS = PL_NW * PL_ND + PL_ND + 64 + HB_M + HB_M / 2 + HB_M / 2;
 
 // Exclusive scan of the popcounts of the 64-bit words[0..nw) (nw <= WIN_COLS) into pre[];
 // returns the total. sRed: NT / 64 ints.
@@ -270,192 +277,24 @@ __device__ int scan_popcounts64(const uint64_t* words, int nw, int32_t* pre, int
     return total;
 }
 
-__global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __restrict__ nbr, int64_t n,
-                                                           const int32_t* __restrict__ order,
-                                                           const uint64_t* __restrict__ wc,
-                                                           const int32_t* __restrict__ dir,
-                                                           const uint8_t* __restrict__ pres,
-                                                           const GridHdr* __restrict__ hdr,
-                                                           int64_t n_tiles, PlanView plan) {
-    static_assert(HB_PLAN_NT == HB_M, "one thread per tile position");
-    constexpr int NB = HB_M / 32;                 // MFMA row blocks of a tile
-    constexpr int NW = HB_PLAN_NT / 64;
-    constexpr int ND = 257;                       // digits: corner sets 0..255, 256 = no voxel
-    __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
-    __shared__ __attribute__((aligned(16))) int32_t sRowOf[HB_SLOTS];
-    __shared__ __attribute__((aligned(16))) uint32_t sScratch[HB_PLAN_SCRATCH];
-    __shared__ int sRed[2 * HB_PLAN_NT / 64];
-    __shared__ int sBox[6][NW];                   // the tile's coordinate box, per wave
-    __shared__ uint32_t sBlk[NB];                 // present taps of each sorted block
-    __shared__ int sBase[NB];                     // first position of each sorted block
-    __shared__ uint32_t sAct[4 * HB_ACT_WORDS];   // the tile's act words
-    // Until the slots are ranked (tile_plan_core), sRowOf holds the taps and the thread of each
-    // sorted index and the position of each thread, and the scratch the sort's counts; the
-    // window's bitmaps use the scratch before the sort.
-    static_assert(HB_SLOTS * 4 >= HB_M * 4 + HB_M * 2 + HB_M * 2, "sort records fit the row list");
-    static_assert(HB_PLAN_SCRATCH >= NW * ND + ND + 64, "sort counts fit the scratch");
-    static_assert(WIN_CELLS >= 512, "window bitmaps and cells fit the scratch");
-    uint32_t* sTaps = reinterpret_cast<uint32_t*>(sRowOf);
-    uint16_t* sTid = reinterpret_cast<uint16_t*>(sTaps + HB_M);
-    uint16_t* sPos = sTid + HB_M;
-    int* sCnt = reinterpret_cast<int*>(sScratch);            // [NW][ND]: count, then first rank
+// The tile's positions (see above) from each voxel's 27-bit tap set; writes the tile's act words
+// and its vox record and returns this thread's position. `lds`: PL_ORDER_WORDS words; sBlk, sBase,
+// sAct: PL_NB, PL_NB, 4 HB_ACT_WORDS. Every thread calls it.
+__device__ int tile_positions(uint32_t taps, int64_t i, int64_t tile, uint32_t* lds, uint32_t* sBlk, int* sBase,
+                              uint32_t* sAct, PlanView plan) {
+    constexpr int NW = PL_NW, ND = PL_ND, NB = PL_NB;
+    int* sCnt = reinterpret_cast<int*>(lds);                  // [NW][ND]: count, then first rank
     int* sDig = sCnt + NW * ND;                               // [ND]: first sorted index of a digit
     int* sWsum = sDig + ND;                                   // scan of the digit totals
-    uint64_t* wT = reinterpret_cast<uint64_t*>(sScratch);                   // window: the tile's voxels
-    uint64_t* wP = wT + WIN_COLS;                                            //   referenced and present
-    uint64_t* wPres = wP + WIN_COLS;                                         //   present voxels
-    int32_t* wPre = reinterpret_cast<int32_t*>(wPres + WIN_COLS);            //   slot of a column's first bit
-    int32_t* wCell = wPre + WIN_COLS;                                        //   block of each cell of the box
-
-    const int64_t tile = blockIdx.x;
+    uint32_t* sTaps = reinterpret_cast<uint32_t*>(sWsum + 64);   // taps of each sorted index
+    uint16_t* sTid = reinterpret_cast<uint16_t*>(sTaps + HB_M);  // thread of each sorted index
+    uint16_t* sPos = sTid + HB_M;                                // position of each thread
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int64_t q = tile * HB_M + tid;
-    const bool cells = hdr != nullptr && hdr->mode == GRID_MODE_CELLS;
-    int64_t i[1] = {q < n ? (cells ? (int64_t)order[q] : q) : -1};
-
-    // the window, when the grid is there and the tile's box fits
-    GridRef g{};
-    int32_t x = 0, y = 0, z = 0;
-    bool valid = false, win = false;
-    int wx0 = 0, wy0 = 0, wz0 = 0, WY = 1, ncol = 0;
-    int ox = 0, oy = 0, oz = 0, CY = 1, CZ = 1;   // the box's first cell and cells along y, z
-    if (cells) {
-        g = grid_ref(dir, hdr);
-        if (i[0] >= 0) {
-            const uint64_t p = wc[q];
-            x = (int32_t)(p & 0x1fffff); y = (int32_t)((p >> 21) & 0x1fffff); z = (int32_t)((p >> 42) & 0x1fffff);
-            valid = coords_ok(x, y, z);
-        }
-        int b[6] = {valid ? x : INT32_MAX, valid ? y : INT32_MAX, valid ? z : INT32_MAX,
-                    valid ? x : -1, valid ? y : -1, valid ? z : -1};
-#pragma unroll
-        for (int a = 0; a < 6; ++a) {
-            b[a] = a < 3 ? wave_min(b[a]) : wave_max(b[a]);
-            if (lane == 0) sBox[a][wave] = b[a];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int a = 0; a < 6; ++a) {
-            int v = sBox[a][0];
-            for (int w = 1; w < NW; ++w) v = a < 3 ? min(v, sBox[a][w]) : max(v, sBox[a][w]);
-            b[a] = v;
-        }
-        if (b[3] >= 0) {
-            wx0 = b[0] - 1; wy0 = b[1] - 1; wz0 = b[2] - 1;
-            const int64_t WX = (int64_t)b[3] - b[0] + 3, WYl = (int64_t)b[4] - b[1] + 3, WZ = (int64_t)b[5] - b[2] + 3;
-            ox = wx0 >> 3; oy = wy0 >> 3; oz = wz0 >> 3;
-            const int64_t CX = ((wx0 + WX - 1) >> 3) - ox + 1, CYl = ((wy0 + WYl - 1) >> 3) - oy + 1,
-                          CZl = ((wz0 + WZ - 1) >> 3) - oz + 1;
-            win = WZ <= 64 && WX * WYl <= WIN_COLS && CX * CYl * CZl <= WIN_CELLS;
-            if (win) {
-                WY = (int)WYl;
-                CY = (int)CYl;
-                CZ = (int)CZl;
-                ncol = (int)(WX * WYl);
-                const int ncell = (int)(CX * CYl * CZl);
-                // the block of every cell of the box
-                for (int k = tid; k < ncell; k += HB_PLAN_NT)
-                    wCell[k] = grid_block(g, ox + k / (CY * CZ), oy + (k / CZ) % CY, oz + k % CZ);
-                __syncthreads();
-                // presence words of the columns, from the blocks' presence bytes
-                const uint64_t zmask = WZ == 64 ? ~0ull : ((1ull << WZ) - 1ull);
-                for (int c = tid; c < ncol; c += HB_PLAN_NT) {
-                    const int cx = wx0 + c / WY, cy = wy0 + c % WY;
-                    const int32_t* cc = wCell + ((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ;
-                    const int po = (cx & 7) * 8 + (cy & 7);
-                    uint64_t word = 0;
-#pragma unroll
-                    for (int k = 0; k < 9; ++k) {
-                        if (k >= CZ) break;
-                        const int32_t blk = cc[k];
-                        const uint64_t byte = blk >= 0 ? pres[(int64_t)blk * 64 + po] : 0u;
-                        const int sh = (oz + k) * 8 - wz0;
-                        word |= sh >= 0 ? byte << sh : byte >> -sh;
-                    }
-                    wPres[c] = word & zmask;
-                    wT[c] = 0ull;
-                }
-                __syncthreads();
-                if (valid)
-                    atomicOr(reinterpret_cast<unsigned long long*>(&wT[(x - wx0) * WY + (y - wy0)]), 1ull << (z - wz0));
-                __syncthreads();
-                // dilate by one voxel, keep the present ones
-                for (int c = tid; c < ncol; c += HB_PLAN_NT) {
-                    const int cx = c / WY, cy = c % WY;
-                    uint64_t d = 0;
-#pragma unroll
-                    for (int dx = -1; dx <= 1; ++dx)
-#pragma unroll
-                        for (int dy = -1; dy <= 1; ++dy) {
-                            const int ax = cx + dx, ay = cy + dy;
-                            if (ax < 0 || ay < 0 || ax >= (int)WX || ay >= WY) continue;
-                            const uint64_t t = wT[ax * WY + ay];
-                            d |= t | (t << 1) | (t >> 1);
-                        }
-                    wP[c] = d & wPres[c];
-                }
-                __syncthreads();
-            }
-        }
-    }
-    // window and direct are uniform over the workgroup from here on
-    int H = 0;
-    bool direct = false;
-    uint32_t taps = 0;
-    uint16_t wsl[kTaps];
-    int32_t nv[kTaps][1];
-    if (win) {
-        H = scan_popcounts64<HB_PLAN_NT>(wP, ncol, wPre, sRed);
-        direct = H > HB_ZERO;
-        if (!direct) {
-            // the row of every slot s: column = the last one whose first slot is <= s, then the
-            // (s - first)-th set bit of its word
-            int32_t* ro = plan.rowof + tile * HB_SLOTS;
-            for (int sl = tid; sl < H; sl += HB_PLAN_NT) {
-                int lo = 0, hi = ncol - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (wPre[mid] <= sl) lo = mid; else hi = mid - 1;
-                }
-                uint64_t bits = wP[lo];
-                for (int k = sl - wPre[lo]; k > 0; --k) bits &= bits - 1ull;
-                const int cx = wx0 + lo / WY, cy = wy0 + lo % WY, cz = wz0 + __builtin_ctzll(bits);
-                const int32_t blk = wCell[((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ + ((cz >> 3) - oz)];
-                ro[sl] = g.blocks[(int64_t)blk * GRID_BLOCK_WORDS + cell_word(cx, cy, cz)] - 1;
-            }
-        }
-        // taps and slots of this voxel: 3 z bits of each of its 9 neighbouring columns
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t) wsl[t] = HB_ZERO;
-        if (valid) {
-            const int zz = z - wz0;   // in [1, WZ - 2]
-#pragma unroll
-            for (int dx = 0; dx < 3; ++dx)
-#pragma unroll
-                for (int dy = 0; dy < 3; ++dy) {
-                    const int c = (x - wx0 + dx - 1) * WY + (y - wy0 + dy - 1);
-                    const uint64_t w = wP[c];
-                    const uint32_t b3 = (uint32_t)(w >> (zz - 1)) & 7u;
-                    const int base = wPre[c] + __popcll(w & ((1ull << (zz - 1)) - 1ull));
-                    const int t0 = dx * 9 + dy * 3;
-                    taps |= b3 << t0;
-                    const int b0 = b3 & 1u, b1 = (b3 >> 1) & 1u;
-                    if (b3 & 1u) wsl[t0] = (uint16_t)base;
-                    if (b3 & 2u) wsl[t0 + 1] = (uint16_t)(base + b0);
-                    if (b3 & 4u) wsl[t0 + 2] = (uint16_t)(base + b0 + b1);
-                }
-        }
-        __syncthreads();   // the scratch is the sort's from here on
-    } else {
-        load_entries<1>(nbr, n, i, nv);
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t) taps |= (nv[t][0] >= 0 ? 1u : 0u) << t;
-    }
     constexpr int kCorner[8] = {0, 2, 6, 8, 18, 20, 24, 26};   // taps (+-1, +-1, +-1)
     int d = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) d |= ((taps >> kCorner[k]) & 1u) << k;
-    if (i[0] < 0) d = ND - 1;                     // empty positions sort last
+    if (i < 0) d = ND - 1;                        // empty positions sort last
     for (int k = tid; k < NW * ND; k += HB_PLAN_NT) sCnt[k] = 0;
     if (tid < 4 * HB_ACT_WORDS) sAct[tid] = 0u;
     // rank among this wave's lanes with the same digit (lanes in order)
@@ -495,7 +334,7 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
     }
     __syncthreads();
     const int sidx = sDig[d] + sCnt[wave * ND + d] + rank;   // this voxel's sorted index
-    sTaps[sidx] = i[0] >= 0 ? taps : 0u;
+    sTaps[sidx] = i >= 0 ? taps : 0u;
     sTid[sidx] = (uint16_t)tid;
     __syncthreads();
     // thread tid now stands for sorted index tid: the present taps of its 32-row block
@@ -532,32 +371,263 @@ __global__ __launch_bounds__(HB_PLAN_NT) void k_plan_build(const int32_t* __rest
     if (tid < 4 * HB_ACT_WORDS) plan.act[tile * 4 * HB_ACT_WORDS + tid] = sAct[tid];
     sPos[sTid[tid]] = (uint16_t)(sBase[tid >> 5] + (tid & 31));
     __syncthreads();
-    int pos[1] = {sPos[tid]};
-    plan.vox[tile * HB_M + pos[0]] = (int32_t)i[0];
-    __syncthreads();   // sRowOf and the scratch are the planner's from here on
+    const int pos = sPos[tid];
+    plan.vox[tile * HB_M + pos] = (int32_t)i;
+    __syncthreads();   // the LDS is the caller's again
+    return pos;
+}
 
-    if (win) {
-        if (!direct) {
-            const int rr = pos[0];
+// Tiles of the cell walk, in windows; tiles of more than WIN_SEGS windows are appended to list
+// (count in *list_n) for k_plan_table, and every tile is when the grid fell back.
+// (three workgroups a CU, as their LDS allows: at most 80 registers)
+__global__ __launch_bounds__(HB_PLAN_NT) __attribute__((amdgpu_waves_per_eu(6))) void k_plan_window(int64_t n, const int32_t* __restrict__ order,
+                                                            const uint64_t* __restrict__ wc,
+                                                            const int32_t* __restrict__ dir,
+                                                            const uint8_t* __restrict__ pres,
+                                                            const GridHdr* __restrict__ hdr, PlanView plan,
+                                                            int32_t* __restrict__ list, int32_t* __restrict__ list_n) {
+    static_assert(HB_PLAN_NT == HB_M, "one thread per tile position");
+    static_assert(2 * 2 * WIN_COLS >= PL_ORDER_WORDS, "the order step's records fit the dead bitmaps");
+    constexpr int NW = PL_NW;
+    __shared__ __attribute__((aligned(16))) uint64_t sA[2 * WIN_COLS];   // wT, wPres; then the order step
+    __shared__ __attribute__((aligned(16))) uint64_t wP[WIN_COLS];       // referenced and present
+    __shared__ int32_t wPre[WIN_COLS];                                    // slot of a column's first bit
+    __shared__ int32_t wCell[WIN_CELLS];                                  // block of each cell of the box
+    __shared__ int sRed[2 * NW];
+    __shared__ int sBox[6][NW];
+    __shared__ int sSeg[6];
+    __shared__ int sEnd;
+    __shared__ uint32_t sBlk[PL_NB];
+    __shared__ int sBase[PL_NB];
+    __shared__ uint32_t sAct[4 * HB_ACT_WORDS];
+    uint64_t* wT = sA;
+    uint64_t* wPres = sA + WIN_COLS;
+
+    const int64_t tile = blockIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (hdr->mode != GRID_MODE_CELLS) {
+        if (tid == 0) list[atomicAdd(list_n, 1)] = (int32_t)tile;
+        return;
+    }
+    const int64_t q = tile * HB_M + tid;
+    const int64_t i = q < n ? (int64_t)order[q] : -1;
+    const GridRef g = grid_ref(dir, hdr);
+    int32_t x = 0, y = 0, z = 0;
+    bool valid = false;
+    if (i >= 0) {
+        const uint64_t p = wc[q];
+        x = (int32_t)(p & 0x1fffff); y = (int32_t)((p >> 21) & 0x1fffff); z = (int32_t)((p >> 42) & 0x1fffff);
+        valid = coords_ok(x, y, z);
+    }
+    // The tile's voxels (walk order) in segments: runs whose box fits a window, found with a prefix
+    // box over the positions. Each segment's window ranks its own dilated set; the slots of later
+    // segments follow those of earlier ones (a row two segments reference gets a slot in each,
+    // which only stages it twice). A tile of more than WIN_SEGS segments goes to k_plan_table.
+    uint32_t taps = 0;
+    // the voxel's 27 slots, two 16-bit slots a register (tap 2 k low, 2 k + 1 high)
+    uint32_t wsl[(kTaps + 1) / 2];
 #pragma unroll
-            for (int t = 0; t < kTaps; ++t) sL[t][rr >> 7][rr & 31][(rr >> 5) & 3] = wsl[t];
+    for (int k = 0; k < (kTaps + 1) / 2; ++k) wsl[k] = HB_ZERO | (HB_ZERO << 16);
+    auto set_slot = [&](int t, int v) {
+        wsl[t >> 1] = (t & 1) ? ((wsl[t >> 1] & 0xffffu) | ((uint32_t)v << 16)) : ((wsl[t >> 1] & 0xffff0000u) | (uint32_t)v);
+    };
+    int H = 0, seg0 = 0, nseg = 0;
+    while (seg0 < HB_M) {
+        // inclusive prefix box over positions seg0 .. tid (lo xyz by min, hi xyz by max)
+        const bool in = valid && tid >= seg0;
+        int b[6] = {in ? x : INT32_MAX, in ? y : INT32_MAX, in ? z : INT32_MAX, in ? x : -1, in ? y : -1, in ? z : -1};
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+            for (int a = 0; a < 6; ++a) {
+                const int u = __shfl_up(b[a], off, 64);
+                if (lane >= off) b[a] = a < 3 ? min(b[a], u) : max(b[a], u);
+            }
+        }
+        if (lane == 63) {
+#pragma unroll
+            for (int a = 0; a < 6; ++a) sBox[a][wave] = b[a];
+        }
+        if (tid == 0) sEnd = HB_M;
+        __syncthreads();
+        for (int w = 0; w < wave; ++w) {
+#pragma unroll
+            for (int a = 0; a < 6; ++a) b[a] = a < 3 ? min(b[a], sBox[a][w]) : max(b[a], sBox[a][w]);
+        }
+        // the segment ends at the first position whose prefix box does not fit
+        bool fits = true;
+        if (b[3] >= 0) {
+            const int64_t WX = (int64_t)b[3] - b[0] + 3, WYl = (int64_t)b[4] - b[1] + 3, WZ = (int64_t)b[5] - b[2] + 3;
+            const int64_t CX = ((b[3] + 1) >> 3) - ((b[0] - 1) >> 3) + 1, CYl = ((b[4] + 1) >> 3) - ((b[1] - 1) >> 3) + 1,
+                          CZl = ((b[5] + 1) >> 3) - ((b[2] - 1) >> 3) + 1;
+            fits = WZ <= 64 && WX * WYl <= WIN_COLS && CX * CYl * CZl <= WIN_CELLS;
+        }
+        const uint64_t bad = __ballot(tid >= seg0 && !fits);
+        if (lane == 0 && bad) atomicMin(&sEnd, wave * 64 + (int)__builtin_ctzll(bad));
+        __syncthreads();
+        const int end = sEnd;   // > seg0: a box of one voxel always fits
+        if (tid == end - 1) {
+#pragma unroll
+            for (int a = 0; a < 6; ++a) sSeg[a] = b[a];
         }
         __syncthreads();
-    } else {
-        tile_plan_core<HB_PLAN_NT, 1>(nv, pos, sL, sRowOf, sScratch, sRed, H, direct);
+        int sb[6];
+#pragma unroll
+        for (int a = 0; a < 6; ++a) sb[a] = sSeg[a];
+        const bool member = valid && tid >= seg0 && tid < end;
+        if (sb[3] >= 0) {
+            const int wx0 = sb[0] - 1, wy0 = sb[1] - 1, wz0 = sb[2] - 1;
+            const int WX = sb[3] - sb[0] + 3, WY = sb[4] - sb[1] + 3, WZ = sb[5] - sb[2] + 3;
+            const int ox = wx0 >> 3, oy = wy0 >> 3, oz = wz0 >> 3;
+            const int CY = ((wy0 + WY - 1) >> 3) - oy + 1, CZ = ((wz0 + WZ - 1) >> 3) - oz + 1;
+            const int ncol = WX * WY, ncell = (((wx0 + WX - 1) >> 3) - ox + 1) * CY * CZ;
+            // the block of every cell of the box
+            for (int k = tid; k < ncell; k += HB_PLAN_NT)
+                wCell[k] = grid_block(g, ox + k / (CY * CZ), oy + (k / CZ) % CY, oz + k % CZ);
+            __syncthreads();
+            // presence words of the columns, from the blocks' presence bytes
+            const uint64_t zmask = WZ == 64 ? ~0ull : ((1ull << WZ) - 1ull);
+            for (int c = tid; c < ncol; c += HB_PLAN_NT) {
+                const int cx = wx0 + c / WY, cy = wy0 + c % WY;
+                const int32_t* cc = wCell + ((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ;
+                const int po = (cx & 7) * 8 + (cy & 7);
+                uint64_t word = 0;
+#pragma unroll
+                for (int k = 0; k < 9; ++k) {
+                    if (k >= CZ) break;
+                    const int32_t blk = cc[k];
+                    const uint64_t byte = blk >= 0 ? pres[(int64_t)blk * 64 + po] : 0u;
+                    const int sh = (oz + k) * 8 - wz0;
+                    word |= sh >= 0 ? byte << sh : byte >> -sh;
+                }
+                wPres[c] = word & zmask;
+                wT[c] = 0ull;
+            }
+            __syncthreads();
+            if (member)
+                atomicOr(reinterpret_cast<unsigned long long*>(&wT[(x - wx0) * WY + (y - wy0)]), 1ull << (z - wz0));
+            __syncthreads();
+            // dilate by one voxel, keep the present ones
+            for (int c = tid; c < ncol; c += HB_PLAN_NT) {
+                const int cx = c / WY, cy = c % WY;
+                uint64_t d = 0;
+#pragma unroll
+                for (int dx = -1; dx <= 1; ++dx)
+#pragma unroll
+                    for (int dy = -1; dy <= 1; ++dy) {
+                        const int ax = cx + dx, ay = cy + dy;
+                        if (ax < 0 || ay < 0 || ax >= WX || ay >= WY) continue;
+                        const uint64_t t = wT[ax * WY + ay];
+                        d |= t | (t << 1) | (t >> 1);
+                    }
+                wP[c] = d & wPres[c];
+            }
+            __syncthreads();
+            const int Hs = scan_popcounts64<HB_PLAN_NT>(wP, ncol, wPre, sRed);
+            // the row of every slot H + s of the segment: column = the last one whose first slot is
+            // <= s, then the (s - first)-th set bit of its word
+            int32_t* ro = plan.rowof + tile * HB_SLOTS;
+            for (int sl = tid; sl < Hs && H + sl < HB_SLOTS; sl += HB_PLAN_NT) {
+                int lo = 0, hi = ncol - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (wPre[mid] <= sl) lo = mid; else hi = mid - 1;
+                }
+                uint64_t bits = wP[lo];
+                for (int k = sl - wPre[lo]; k > 0; --k) bits &= bits - 1ull;
+                const int cx = wx0 + lo / WY, cy = wy0 + lo % WY, cz = wz0 + __builtin_ctzll(bits);
+                const int32_t blk = wCell[((cx >> 3) - ox) * CY * CZ + ((cy >> 3) - oy) * CZ + ((cz >> 3) - oz)];
+                ro[H + sl] = g.blocks[(int64_t)blk * GRID_BLOCK_WORDS + cell_word(cx, cy, cz)] - 1;
+            }
+            // taps and slots of the segment's voxels: 3 z bits of each of the 9 neighbouring columns
+            if (member) {
+                const int zz = z - wz0;   // in [1, WZ - 2]
+#pragma unroll
+                for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+                    for (int dy = 0; dy < 3; ++dy) {
+                        const int c = (x - wx0 + dx - 1) * WY + (y - wy0 + dy - 1);
+                        const uint64_t w = wP[c];
+                        const uint32_t b3 = (uint32_t)(w >> (zz - 1)) & 7u;
+                        const int base = H + wPre[c] + __popcll(w & ((1ull << (zz - 1)) - 1ull));
+                        const int t0 = dx * 9 + dy * 3;
+                        taps |= b3 << t0;
+                        const int b0 = b3 & 1u, b1 = (b3 >> 1) & 1u;
+                        if (b3 & 1u) set_slot(t0, base);
+                        if (b3 & 2u) set_slot(t0 + 1, base + b0);
+                        if (b3 & 4u) set_slot(t0 + 2, base + b0 + b1);
+                    }
+            }
+            H += Hs;
+            __syncthreads();   // the window's arrays are the next segment's
+        }
+        seg0 = end;
+        if (++nseg == WIN_SEGS && seg0 < HB_M) {
+            if (tid == 0) list[atomicAdd(list_n, 1)] = (int32_t)tile;
+            return;
+        }
     }
+    const bool direct = H > HB_ZERO;
+    __syncthreads();   // the bitmaps are dead: sA is the order step's
+    const int pos = tile_positions(taps, i, tile, reinterpret_cast<uint32_t*>(sA), sBlk, sBase, sAct, plan);
     if (tid == 0) {
         int32_t* h = plan.hdr + tile * 4;
         h[0] = H; h[1] = direct ? 1 : 0; h[2] = 0; h[3] = 0;
     }
     if (direct) return;
-    if (!win) {
-        int32_t* ro = plan.rowof + tile * HB_SLOTS;
-        for (int s = tid; s < H; s += HB_PLAN_NT) ro[s] = sRowOf[s];
+    // slot table [tap][position / 128][position % 32][position / 32 % 4], straight to memory
+    uint16_t* sl = plan.slots + tile * HB_SLOT_TABLE + (pos >> 7) * 128 + (pos & 31) * 4 + ((pos >> 5) & 3);
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) sl[t * HB_M] = (uint16_t)(wsl[t >> 1] >> (16 * (t & 1)));
+}
+
+// Tiles ranked from the table's entries: tiles list[0 .. *list_n) (cell walk order when the grid is
+// in cell mode), or, without a list, tiles 0 .. n_tiles of consecutive rows. A workgroup takes
+// tiles blockIdx.x, + gridDim.x, ...
+// (two workgroups a CU, as their LDS allows: at most 128 registers)
+__global__ __launch_bounds__(HB_PLAN_NT) __attribute__((amdgpu_waves_per_eu(4))) void k_plan_table(const int32_t* __restrict__ nbr, int64_t n,
+                                                           const int32_t* __restrict__ order,
+                                                           const GridHdr* __restrict__ hdr,
+                                                           const int32_t* __restrict__ list,
+                                                           const int32_t* __restrict__ list_n, int64_t n_tiles,
+                                                           PlanView plan) {
+    static_assert(HB_PLAN_SCRATCH >= PL_ORDER_WORDS, "the order step fits the scratch");
+    __shared__ __attribute__((aligned(16))) uint16_t sL[kTaps][4][32][4];
+    __shared__ __attribute__((aligned(16))) int32_t sRowOf[HB_SLOTS];
+    __shared__ __attribute__((aligned(16))) uint32_t sScratch[HB_PLAN_SCRATCH];
+    __shared__ int sRed[2 * PL_NW];
+    __shared__ uint32_t sBlk[PL_NB];
+    __shared__ int sBase[PL_NB];
+    __shared__ uint32_t sAct[4 * HB_ACT_WORDS];
+    const int tid = threadIdx.x;
+    const bool walk = order != nullptr && hdr->mode == GRID_MODE_CELLS;
+    const int64_t count = list ? (int64_t)*list_n : n_tiles;
+    for (int64_t k = blockIdx.x; k < count; k += gridDim.x) {
+        const int64_t tile = list ? (int64_t)list[k] : k;
+        const int64_t q = tile * HB_M + tid;
+        int64_t i[1] = {q < n ? (walk ? (int64_t)order[q] : q) : -1};
+        int32_t nv[kTaps][1];
+        load_entries<1>(nbr, n, i, nv);
+        uint32_t taps = 0;
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) taps |= (nv[t][0] >= 0 ? 1u : 0u) << t;
+        int pos[1] = {tile_positions(taps, i[0], tile, sScratch, sBlk, sBase, sAct, plan)};
+        int H;
+        bool direct;
+        tile_plan_core<HB_PLAN_NT, 1>(nv, pos, sL, sRowOf, sScratch, sRed, H, direct);
+        if (tid == 0) {
+            int32_t* h = plan.hdr + tile * 4;
+            h[0] = H; h[1] = direct ? 1 : 0; h[2] = 0; h[3] = 0;
+        }
+        if (!direct) {
+            int32_t* ro = plan.rowof + tile * HB_SLOTS;
+            for (int s = tid; s < H; s += HB_PLAN_NT) ro[s] = sRowOf[s];
+            const u32x4_t* src = reinterpret_cast<const u32x4_t*>(&sL[0][0][0][0]);
+            u32x4_t* dst = reinterpret_cast<u32x4_t*>(plan.slots + tile * HB_SLOT_TABLE);
+            for (int p = tid; p < HB_SLOT_TABLE / 8; p += HB_PLAN_NT) dst[p] = src[p];
+        }
+        __syncthreads();   // the LDS is the next tile's
     }
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(&sL[0][0][0][0]);
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(plan.slots + tile * HB_SLOT_TABLE);
-    for (int p = tid; p < HB_SLOT_TABLE / 8; p += HB_PLAN_NT) dst[p] = src[p];
 }
 
 }  // namespace
@@ -573,14 +643,21 @@ static int plan_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, vo
     const int64_t n_tiles = ceil_div(n, HB_M);
     const PlanScratch ps = carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
     const GridTail gt = carve_grid_tail(tail);
+    int32_t* list_n = gt.parts + 5 * GRID_PARTS;   // zeroed by k_walk_emit
+    int32_t* list = ps.counts;                     // free once k_walk_emit has read the counts
+    const PlanView pv = carve_plan(plan, n_tiles);
     hipLaunchKernelGGL(k_walk_count, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
                        ps.pres, gt.parts);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_walk_emit, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
-                       ps.pres, ps.cell_of, gt.parts, ps.order, ps.wc);
+                       ps.pres, ps.cell_of, gt.parts, ps.order, ps.wc, list_n);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, ps.order, ps.wc,
-                       dir, ps.pres, gt.hdr, n_tiles, carve_plan(plan, n_tiles));
+    hipLaunchKernelGGL(k_plan_window, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, n, ps.order, ps.wc, dir,
+                       ps.pres, gt.hdr, pv, list, list_n);
+    TSP_CHECK_LAUNCH();
+    const unsigned grid = (unsigned)std::min<int64_t>(n_tiles, 512);
+    hipLaunchKernelGGL(k_plan_table, dim3(grid), dim3(HB_PLAN_NT), 0, s, nbr, n, ps.order, gt.hdr, list, list_n,
+                       n_tiles, pv);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
@@ -597,8 +674,8 @@ int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* 
         if (st != TSP_OK) return st;
         return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(ps.region), ps.tail, s);
     }
-    hipLaunchKernelGGL(k_plan_build, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, nullptr, nullptr,
-                       nullptr, nullptr, nullptr, n_tiles, carve_plan(plan, n_tiles));
+    hipLaunchKernelGGL(k_plan_table, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, nullptr, nullptr,
+                       nullptr, nullptr, n_tiles, carve_plan(plan, n_tiles));
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
