@@ -423,7 +423,7 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
     stream = torch.cuda.current_stream()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     if reuse is None:
-        coords = torch.from_numpy(w.coords).to(dev)
+        coords = torch.from_numpy(np.ascontiguousarray(w.coords, np.int32)).to(dev)
         feats = torch.from_numpy(w.feats).to(tdt).to(dev)
         weight = torch.from_numpy(w.weight).to(tdt).to(dev)
         bias = torch.from_numpy(w.bias).to(dev)
