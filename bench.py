@@ -417,6 +417,7 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
     conv plan are built and timed first, each on its own (reuse: the table and plan of an
     earlier call on the same workload); then `steps` convs between two HIP events on the
     stream the kernel runs on."""
+    import numpy as np
     import torch
     dev = torch.device("cuda:0")
     tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w.dtype]
