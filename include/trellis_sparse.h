@@ -327,10 +327,25 @@ size_t tsp_convnext_workspace_bytes(int64_t n, int c, int x_dtype, const tsp_con
 /* SparseConvNeXtBlock3d (replaces trellis::sparse_convnext, include/sparse.h:24-25,
  * src/sparse.cpp:94-137): out f32 [n][c] = x + mlp.2(SiLU(mlp.0(LN(conv(x)) * norm.weight +
  * norm.bias))), LN eps 1e-6. x f32, or 16-bit of the conv input's type; d_plan (of d_nbr) may be
- * NULL; out must not alias x. */
+ * NULL; out must not alias x. With f32 x, c = 128 and both MLP weights of the normalised input's
+ * 16-bit type, the MLP is one kernel (tsp_convnext_mlp): its weights and the workspace must then be
+ * 16-byte aligned. */
 int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, const int32_t* d_nbr,
                  const void* d_plan, const tsp_convnext_weights* w, float* d_out,
                  void* d_workspace, size_t workspace_bytes, int flags, void* stream);
+
+/* The ConvNeXt block's MLP in one kernel (sparse.cpp:126-134: mlp.0, SiLU, mlp.2, + x, in place of
+ * two mul_mats): out f32 [n][c] = x + b2 + W2 . silu(W0 . xn + b0), with the hidden layer kept on
+ * chip and rounded to xn's type as a stored hidden layer would be. The weights W0 [4c][c] and
+ * W2 [c][4c] (xn's 16-bit dtype) are packed first by tsp_convnext_mlp_pack into
+ * tsp_convnext_mlp_packed_bytes(c) bytes (at model load; no counterpart in the reference). xn
+ * [n][c] and the packed weights 16-byte aligned; x, out f32 [n][c] (out may be x); b0 [4c], b2 [c]
+ * f32 or NULL. c = 128 (else TSP_ERR_UNSUPPORTED: wider blocks keep the two library GEMMs, whose
+ * hidden-layer traffic is small beside their arithmetic). */
+size_t tsp_convnext_mlp_packed_bytes(int c);
+int tsp_convnext_mlp_pack(const void* d_w0, const void* d_w2, int dtype, int c, void* d_packed, void* stream);
+int tsp_convnext_mlp(const void* d_xn, int dtype, int64_t n, int c, const void* d_packed, const float* d_b0,
+                     const float* d_b2, const float* d_x, float* d_out, void* stream);
 
 typedef struct {
     const float* norm1_weight;  /* [Cin] */

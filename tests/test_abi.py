@@ -293,3 +293,24 @@ def test_composite_validation(pkg):
     assert L.tsp_c2s_workspace_bytes(500, 1200, 128, 64, ctypes.byref(c), 1, 0, 0) != cb
     assert cs(ws=cb - 1) == 5
     assert cs(m=0) == 0
+
+
+def test_convnext_mlp_validation(pkg):
+    """tsp_convnext_mlp / _pack: C = 128 only (wider blocks keep the library GEMMs), 16-bit dtypes,
+    null and misaligned pointers, an output aliasing xn -- all refused before any launch; n = 0
+    is a no-op."""
+    L = pkg.lib()
+    assert L.tsp_convnext_mlp_packed_bytes(128) == 2 * 4 * 128 * 128 * 2
+    assert L.tsp_convnext_mlp_pack(FAKE, FAKE, 2, 256, FAKE, NULL) == 4 and "C=256" in _err(pkg)
+    assert L.tsp_convnext_mlp_pack(FAKE, FAKE, 0, 128, FAKE, NULL) == 4      # f32 weights
+    assert L.tsp_convnext_mlp_pack(FAKE, ctypes.c_void_p(0x1008), 2, 128, FAKE, NULL) == 1
+    mlp = lambda **kw: L.tsp_convnext_mlp(kw.get("xn", FAKE), kw.get("dt", 2), kw.get("n", 1000), kw.get("c", 128),
+                                          kw.get("packed", FAKE), NULL, NULL, FAKE, kw.get("out", ctypes.c_void_p(0x2000)),
+                                          NULL)
+    assert mlp(c=256) == 4 and mlp(c=64) == 4
+    assert mlp(dt=0) == 4
+    assert mlp(n=-1) == 1
+    assert mlp(packed=NULL) == 1
+    assert mlp(xn=ctypes.c_void_p(0x1008)) == 1 and "aligned" in _err(pkg)
+    assert mlp(out=FAKE) == 1 and "alias" in _err(pkg)
+    assert mlp(n=0, packed=NULL) == 0

@@ -24,6 +24,7 @@ STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "RANGE", 4: "UNSUPPORTED", 5: "WOR
 EXPORTS = (
     "tsp_last_error", "tsp_version",
     "tsp_rulebook_workspace_bytes", "tsp_rulebook_build", "tsp_rulebook_build_planned", "tsp_rulebook_count_pairs",
+    "tsp_convnext_mlp_packed_bytes", "tsp_convnext_mlp_pack", "tsp_convnext_mlp",
     "tsp_subm_conv3x3", "tsp_subm_conv3x3_ex",
     "tsp_conv_plan_bytes", "tsp_conv_plan_build", "tsp_conv_plan_build_ordered",
     "tsp_conv_weight_pack", "tsp_conv_weight_packed_bytes", "tsp_subm_conv3x3_planned_ln",
@@ -86,6 +87,12 @@ def lib() -> ctypes.CDLL:
     L.tsp_rulebook_workspace_bytes.argtypes = [c_i64]
     L.tsp_rulebook_build.restype = c_int
     L.tsp_rulebook_build.argtypes = [c_vp, c_i64, c_vp, c_vp, c_sz, c_vp, c_vp]
+    L.tsp_convnext_mlp_packed_bytes.restype = c_sz
+    L.tsp_convnext_mlp_packed_bytes.argtypes = [c_int]
+    L.tsp_convnext_mlp_pack.restype = c_int
+    L.tsp_convnext_mlp_pack.argtypes = [c_vp, c_vp, c_int, c_int, c_vp, c_vp]
+    L.tsp_convnext_mlp.restype = c_int
+    L.tsp_convnext_mlp.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
     L.tsp_rulebook_build_planned.restype = c_int
     L.tsp_rulebook_build_planned.argtypes = [c_vp, c_i64, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp]
     L.tsp_rulebook_count_pairs.restype = c_int
@@ -249,6 +256,46 @@ def rulebook_build_planned(coords, check: bool = True, nbr=None, workspace=None,
     if check and n and int(status.item()) != 0:
         raise TspError("tsp_rulebook_build_planned", 3, "coordinate outside [0, 2^21-3]")
     return nbr, plan
+
+
+def convnext_mlp_pack(w0, w2, stream=None):
+    """w0 [4C, C], w2 [C, 4C] of one 16-bit dtype -> the packed buffer tsp_convnext_mlp reads."""
+    torch = _torch()
+    _require_cuda(w0, w2)
+    c = w0.shape[1]
+    if w2.dtype != w0.dtype or tuple(w0.shape) != (4 * c, c) or tuple(w2.shape) != (c, 4 * c):
+        raise ValueError("w0 [4C, C] and w2 [C, 4C] of one dtype")
+    w0, w2 = w0.contiguous(), w2.contiguous()
+    packed = torch.empty(lib().tsp_convnext_mlp_packed_bytes(c) // 2, dtype=w0.dtype, device=w0.device)
+    _check("tsp_convnext_mlp_pack",
+           lib().tsp_convnext_mlp_pack(_ptr(w0), _ptr(w2), dtype_code(w0.dtype), c, _ptr(packed), _stream(stream)))
+    return packed
+
+
+def convnext_mlp(xn, packed, b0, b2, x, out=None, stream=None):
+    """The ConvNeXt MLP in one kernel: out f32 [N, C] = x + b2 + w2 . silu(w0 . xn + b0) for xn
+    [N, C] (16-bit), the weights packed by convnext_mlp_pack, x f32 [N, C], C = 128; out may be x."""
+    torch = _torch()
+    _require_cuda(xn, packed, x)
+    n, c = xn.shape
+    if packed.dtype != xn.dtype or packed.numel() * 2 != lib().tsp_convnext_mlp_packed_bytes(c):
+        raise ValueError("packed must come from convnext_mlp_pack with xn's dtype and C")
+    if x.dtype != torch.float32 or tuple(x.shape) != (n, c):
+        raise ValueError("x must be float32 [N, C]")
+    for name, b, size in (("b0", b0, 4 * c), ("b2", b2, c)):
+        if b is not None and (b.dtype != torch.float32 or b.numel() != size or not b.is_contiguous()
+                              or b.device != xn.device):
+            raise ValueError(f"{name} must be a contiguous float32 vector of {size} on xn's device")
+    if out is None:
+        out = torch.empty((n, c), dtype=torch.float32, device=xn.device)
+    elif (out.dtype != torch.float32 or tuple(out.shape) != (n, c) or not out.is_contiguous()
+          or out.device != xn.device):
+        raise ValueError("out must be a contiguous float32 [N, C] tensor on xn's device")
+    xn, x = xn.contiguous(), x.contiguous()
+    _check("tsp_convnext_mlp",
+           lib().tsp_convnext_mlp(_ptr(xn), dtype_code(xn.dtype), n, c, _ptr(packed), _ptr(b0), _ptr(b2),
+                                  _ptr(x), _ptr(out), _stream(stream)))
+    return out
 
 
 def count_pairs(nbr, n: int, stream=None) -> int:

@@ -119,10 +119,14 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
         xc = p;
     }
     const bool fuse = ln_fused(cdt, adt0, c, plan);
+    // the MLP in one kernel, its 16-bit hidden layer never stored (C = 128, one 16-bit dtype)
+    const bool mlp1 = is16(adt0) && adt2 == adt0 && w.mlp0_dtype == adt0 && w.mlp2_dtype == adt0 &&
+                      xdt == TSP_F32 && c == 128;
     float* h = fuse ? nullptr : static_cast<float*>(ws.take((size_t)n * c * 4));
     void* hn = ws.take((size_t)n * c * dtype_size(adt0));
-    float* hid = static_cast<float*>(ws.take((size_t)chunk * 4 * c * 4));
-    void* hid_in = adt2 == TSP_F32 ? hid : ws.take((size_t)chunk * 4 * c * 2);
+    void* mlp_packed = mlp1 ? ws.take(mlp_packed_bytes(c)) : nullptr;
+    float* hid = mlp1 ? nullptr : static_cast<float*>(ws.take((size_t)chunk * 4 * c * 4));
+    void* hid_in = mlp1 || adt2 == TSP_F32 ? hid : ws.take((size_t)chunk * 4 * c * 2);
     const float* row0 = xdt == TSP_F32 && cdt != TSP_F32 ? static_cast<const float*>(x) : nullptr;
     if (fuse) {
         if (int st = run_conv_ln(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed, w.conv_bias,
@@ -135,6 +139,14 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
             return st;
         if (!ws.base) return TSP_OK;
         if (int st = tsp_layer_norm(h, TSP_F32, n, c, w.norm_weight, w.norm_bias, 1e-6f, 0, hn, adt0, s)) return st;
+    }
+    if (mlp1) {
+        auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        TSP_REQUIRE(al(w.mlp0_weight) && al(w.mlp2_weight) &&
+                        mlp_fused_eligible(adt0, c, hn, mlp_packed, static_cast<const float*>(x), out),
+                    TSP_ERR_INVALID, "tsp_convnext: the MLP weights and the workspace must be 16-byte aligned");
+        if (int st = mlp_pack(w.mlp0_weight, w.mlp2_weight, c, mlp_packed, s)) return st;
+        return mlp_fused(hn, adt0, n, c, mlp_packed, w.mlp0_bias, w.mlp2_bias, static_cast<const float*>(x), out, s);
     }
     const size_t aes = dtype_size(adt0), xes = dtype_size(xdt);
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {

@@ -42,6 +42,14 @@ bool blaslt_eligible(int x_dtype, int weight_dtype, int out_dtype, int ci, int c
                      const void* w, const void* out);
 int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
                   int co, int act, const float* residual, void* out, int odt, hipStream_t s);
+// The ConvNeXt MLP in one kernel (mlp.hip): y = x + b2 + W2 . silu(W0 . xn + b0) for 16-bit xn and
+// weights of one dtype dt, C = 128 or 256, the weights packed by mlp_pack (mlp_packed_bytes(c)
+// bytes: W0 then W2 in MFMA operand order), 16-byte aligned xn and packed (mlp_fused_eligible).
+size_t mlp_packed_bytes(int c);
+int mlp_pack(const void* w0, const void* w2, int c, void* packed, hipStream_t s);
+bool mlp_fused_eligible(int dt, int c, const void* xn, const void* packed, const float* x, const float* y);
+int mlp_fused(const void* xn, int dt, int64_t n, int c, const void* packed, const float* b0, const float* b2,
+              const float* x, float* y, hipStream_t s);
 // Builds the plan of neighbour table `nbr` into `plan`: tiles in the Morton order of the voxels'
 // 8^3 cells when `coords` is given, else tiles of consecutive rows.
 int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s);

@@ -8,6 +8,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
+#include <algorithm>
 #include <mutex>
 #include <tuple>
 
@@ -65,8 +66,28 @@ bool blaslt_eligible(int x_dtype, int weight_dtype, int out_dtype, int ci, int c
              reinterpret_cast<uintptr_t>(out) % 16);
 }
 
+static int blaslt_linear_rows(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
+                              int co, int act, const float* residual, void* out, int odt, hipStream_t s);
+
+// Row chunks of at most 2^31 - 1 bytes in every operand (x, out, residual): one library call
+// never addresses more than that (the composite blocks already bound their hidden layers so).
 int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
                   int co, int act, const float* residual, void* out, int odt, hipStream_t s) {
+    const int64_t row_bytes = std::max<int64_t>({(int64_t)ci * (int64_t)dtype_size(xdt), (int64_t)co * (int64_t)dtype_size(odt),
+                                                 residual ? (int64_t)co * 4 : 0});
+    const int64_t rows = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / row_bytes / 256 * 256);
+    for (int64_t r0 = 0; r0 < n; r0 += rows) {
+        const int64_t nr = std::min(rows, n - r0);
+        const int st = blaslt_linear_rows(static_cast<const char*>(x) + r0 * ci * (int64_t)dtype_size(xdt), xdt, nr,
+                                          ci, w, bias, co, act, residual ? residual + r0 * co : nullptr,
+                                          static_cast<char*>(out) + r0 * co * (int64_t)dtype_size(odt), odt, s);
+        if (st != TSP_OK) return st;
+    }
+    return TSP_OK;
+}
+
+static int blaslt_linear_rows(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
+                              int co, int act, const float* residual, void* out, int odt, hipStream_t s) {
     int dev = 0;
     TSP_CHECK_HIP(hipGetDevice(&dev));
     TSP_REQUIRE(dev >= 0 && dev < kMaxDevices, TSP_ERR_INVALID, "linear: device %d out of range", dev);
