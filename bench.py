@@ -267,6 +267,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (the known-size kernel "
                          "that scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--mlp-rows", type=int, default=0, metavar="N",
+                    help="only time the fused ConvNeXt MLP (tsp_convnext_mlp, C = 128, bf16) on N rows "
+                         "of random data and print its line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -290,6 +293,9 @@ def main():
         return
 
     pkg = load_package()
+    if args.mlp_rows:
+        print(json.dumps(mlp_bench(pkg, torch, args.mlp_rows, args.steps, args.warmup)))
+        return
     import trellis_cpp_amd.shells as shells
     pkg.lib()
     torch.cuda.set_device(torch.device("cuda:0"))
@@ -318,6 +324,13 @@ def main():
             roof["traffic_note"] = "profile predates the current kernel sources; re-measure"
     roof["algorithmic_flops_per_launch"] = flops
     roof["compulsory_bytes_per_launch"] = compulsory
+    # the peaks this box reaches with library code, as a second denominator beside the datasheet's
+    mp = measured_peaks(torch, w.dtype)
+    roof["measured_peaks"] = mp
+    if roof["bound"] == "mfma" and mp.get("gemm_tflops"):
+        roof["frac_of_measured_gemm"] = roof["achieved"] / mp["gemm_tflops"]
+    elif roof["bound"] == "hbm" and mp.get("copy_gb_s"):
+        roof["frac_of_measured_copy"] = roof["achieved"] / mp["copy_gb_s"]
 
     # the same conv with f32 output (what the decoders and the parity tests read), and for the
     # 256^3 C=128 configuration the same shells at ~640K voxels (the size the target names)
@@ -376,6 +389,76 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))
+
+
+def mlp_bench(pkg, torch, n: int, steps: int, warmup: int) -> dict:
+    """The ConvNeXt MLP kernel alone: y = x + b2 + W2 . silu(W0 . xn + b0) at C = 128 on n rows
+    (xn bf16, x and y f32, weights bf16 ~ N(0, 1/sqrt(fan-in)), biases ~ N(0, 0.1))."""
+    c = 128
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    xn = torch.randn(n, c, device=dev, generator=g).to(torch.bfloat16)
+    w0 = (torch.randn(4 * c, c, device=dev, generator=g) / c ** 0.5).to(torch.bfloat16)
+    w2 = (torch.randn(c, 4 * c, device=dev, generator=g) / (4 * c) ** 0.5).to(torch.bfloat16)
+    b0 = torch.randn(4 * c, device=dev, generator=g) * 0.1
+    b2 = torch.randn(c, device=dev, generator=g) * 0.1
+    x = torch.randn(n, c, device=dev, generator=g)
+    y = torch.empty_like(x)
+    packed = pkg.convnext_mlp_pack(w0, w2)
+    step = lambda: pkg.convnext_mlp(xn, packed, b0, b2, x, out=y)
+    for _ in range(warmup):
+        step()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(steps):
+        step()
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 16.0 * n * c * c
+    nbytes = n * c * (2 + 4 + 4)
+    return {"kernel": "k_mlp_ws", "rows": n, "c": c, "dtype": "bf16", "ms": ms,
+            "tflops": flops / (ms * 1e-3) / 1e12, "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"],
+            "compulsory_gb_s": nbytes / (ms * 1e-3) / 1e9}
+
+
+def measured_peaks(torch, dtype: str) -> dict:
+    """Achievable peaks on this box: a dense 8192^3 GEMM in the conv's 16-bit type (torch.mm,
+    which runs hipBLASLt) and a 1 GiB device-to-device copy (read + write bytes counted), each the
+    median of 20 timed calls after 5 warm-up calls."""
+    def med(fn, it=20):
+        ts = []
+        for _ in range(5):
+            fn()
+        for _ in range(it):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return sorted(ts)[len(ts) // 2]
+    out = {}
+    if dtype in ("bf16", "f16"):
+        tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+        m = 8192
+        a = torch.randn(m, m, device="cuda").to(tdt)
+        b = torch.randn(m, m, device="cuda").to(tdt)
+        c = torch.empty(m, m, device="cuda", dtype=tdt)
+        t = med(lambda: torch.mm(a, b, out=c))
+        out["gemm_tflops"] = 2.0 * m ** 3 / (t * 1e-3) / 1e12
+        out["gemm"] = f"{m}x{m}x{m} {dtype} torch.mm"
+        del a, b, c
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    t = med(lambda: dst.copy_(src))
+    out["copy_gb_s"] = 2.0 * src.numel() * 4 / (t * 1e-3) / 1e9
+    out["copy"] = "1 GiB device-to-device, read + write"
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
 
 
 def kernel_sources_sha() -> str:
