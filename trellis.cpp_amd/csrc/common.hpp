@@ -122,11 +122,11 @@ __device__ __forceinline__ float dpp_move(float v) {
 }
 template <int L>
 __device__ __forceinline__ float group_sum(float v) {
-    static_assert(L == 16 || L == 32 || L == 64, "group of 16, 32 or 64 lanes");
+    static_assert(L == 8 || L == 16 || L == 32 || L == 64, "group of 8, 16, 32 or 64 lanes");
     v += dpp_move<0xB1>(v);    // quad_perm [1, 0, 3, 2]
     v += dpp_move<0x4E>(v);    // quad_perm [2, 3, 0, 1]
     v += dpp_move<0x141>(v);   // row_half_mirror
-    v += dpp_move<0x140>(v);   // row_mirror
+    if constexpr (L >= 16) v += dpp_move<0x140>(v);   // row_mirror
     if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
     if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
     return v;

@@ -194,9 +194,12 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
     // when each skip element spans a multiple of 4 channels, otherwise the skip pass does
     const bool octants = cp1.planned && cout % 64 == 0;
     const bool skip_in_stores = cp2.planned && (cout / (cin / 8)) % 4 == 0;
+    // at Cout = 64 (a wave's channels: a whole child row) conv1's stores also do norm2 + SiLU and
+    // write conv2's 16-bit input directly
+    const bool norm_in_stores = octants && cout == 64 && is16(in1) && in2 == in1;
     void* h0 = ws.take((size_t)n * cin * dtype_size(in1));
     float* h1 = octants ? nullptr : static_cast<float*>(ws.take((size_t)n * 8 * cout * 4));
-    float* g = static_cast<float*>(ws.take((size_t)m * cout * 4));
+    float* g = norm_in_stores ? nullptr : static_cast<float*>(ws.take((size_t)m * cout * 4));
     void* h2 = ws.take((size_t)m * cout * dtype_size(in2));
     void* pk1 = cp1.pack_here ? ws.take(tsp_conv_weight_packed_bytes(cin, 8 * cout)) : nullptr;
     void* pk2 = cp2.pack_here ? ws.take(tsp_conv_weight_packed_bytes(cout, cout)) : nullptr;
@@ -208,7 +211,17 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
         if ((st = tsp_conv_weight_pack(w.conv1_weight, w.conv1_dtype, cin, 8 * cout, pk1, s))) return st;
         p1 = pk1;
     }
-    if (octants) {
+    if (norm_in_stores) {
+        TSP_REQUIRE((reinterpret_cast<uintptr_t>(p1) & 15) == 0 && (reinterpret_cast<uintptr_t>(mask) & 7) == 0,
+                    TSP_ERR_INVALID, "tsp_c2s: packed conv1 weights must be 16-byte aligned, the mask 8-byte");
+        OctantScatter osc;
+        osc.mask = mask;
+        osc.mstart = mstart;
+        osc.cout = cout;
+        osc.norm_silu = true;
+        osc.norm_eps = 1e-6f;
+        st = halo_conv_launch(in1, in2, h0, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h2, s, osc);
+    } else if (octants) {
         st = tsp_subm_conv3x3_planned_octants(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, cout, mask, mstart, g, s);
     } else {
         if (cp1.planned)
@@ -221,7 +234,8 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
         if (!st) st = tsp_c2s_gather(h1, TSP_F32, gidx, m, cout, g, s);
     }
     if (st) return st;
-    if ((st = tsp_layer_norm(g, TSP_F32, m, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s))) return st;
+    if (!norm_in_stores && (st = tsp_layer_norm(g, TSP_F32, m, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s)))
+        return st;
     const void* p2 = w.conv2_packed;
     if (pk2) {
         if ((st = tsp_conv_weight_pack(w.conv2_weight, w.conv2_dtype, cout, cout, pk2, s))) return st;

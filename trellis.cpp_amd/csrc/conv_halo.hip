@@ -63,6 +63,11 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                   "(co=%d cout=%d)", bn128 ? 64 : 32, co, osc.cout);
         return TSP_ERR_UNSUPPORTED;
     }
+    if (osc.norm_silu && (!bn128 || osc.cout != 64 || odt != fdt)) {
+        set_error("MFMA conv: octant stores with the child norm need cout = 64, co %% 128 == 0 and "
+                  "output in the feature type (co=%d cout=%d)", co, osc.cout);
+        return TSP_ERR_UNSUPPORTED;
+    }
     if (skip.cin && (!planned || skip.cin % 8 != 0 || co % (skip.cin / 8) != 0 || (co / (skip.cin / 8)) % 4 != 0)) {
         set_error("MFMA conv: a skip add needs a plan, cin %% 8 == 0 and co / (cin / 8) a multiple of 4 "
                   "(cin=%d co=%d)", skip.cin, co);

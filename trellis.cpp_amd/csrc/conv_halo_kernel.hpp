@@ -138,6 +138,19 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_
         RowNorm{});
 }
 
+// The same octant stores with each child row normalised (no affine) and passed through SiLU, in
+// the feature type (stored plan, cout == the channels of one wave).
+template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
+__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_octants_norm(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
+    PadRow pad) {
+    conv_grid<BF16, BN, BF16 ? TSP_BF16 : TSP_F16, true, RB, CB, PD, SP, STG, 4>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{}, pad,
+        RowNorm{});
+}
+
 // The same conv with f32 output and the C2S skip added by its stores (stored plan).
 template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_skip(
@@ -193,8 +206,8 @@ __device__ __forceinline__ void conv_tiles(
     int rg = wave % NRG;                     // row group: voxels [32 RB rg, +32 RB)
     const int c0 = (int)(lin0 % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
     // with an octant scatter, the wave's channels lie in octant oct, from column ocol of a child
-    const int oct = EPI == 1 ? c0 / osc.cout : 0;
-    const int ocol = EPI == 1 ? c0 - oct * osc.cout : 0;
+    const int oct = EPI == 1 || EPI == 4 ? c0 / osc.cout : 0;
+    const int ocol = EPI == 1 || EPI == 4 ? c0 - oct * osc.cout : 0;
     const int nkc = ci / HB_KC;
     // The reference's absent taps read the padding row 0 * feats[0] (submconv_pad,
     // sparse.cpp:81-85), zeros here. Where row 0 holds an Inf or a NaN that row is NaN in those
@@ -367,7 +380,7 @@ __device__ __forceinline__ void conv_tiles(
         // Octant stores: the child row of octant oct of each of the wave's rows, or -1, looked up
         // once per tile for the lane's two positions and shuffled the same way.
         int child2[2] = {-1, -1};
-        if constexpr (EPI == 1) {
+        if constexpr (EPI == 1 || EPI == 4) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int64_t i = vrow[k];
@@ -445,7 +458,34 @@ __device__ __forceinline__ void conv_tiles(
                             for (int e = 0; e < CH / 4; ++e) vs[q][e] = f32x4_t{NAN, NAN, NAN, NAN};
                         }
                     }
-                    if constexpr (EPI == 1) {
+                    if constexpr (EPI == 4) {
+                        // the child row's norm (its WN channels: the WN / CH lanes of this row) + SiLU
+                        static_assert(EPI != 4 || (ODT != TSP_F32 && WN / CH == 8), "one row per 8 lanes");
+                        float sum = 0.f;
+#pragma unroll
+                        for (int e = 0; e < CH / 4; ++e)
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) sum += vs[q][e][k];
+                        const float mean = group_sum<WN / CH>(sum) / (float)WN;
+                        float sq = 0.f;
+#pragma unroll
+                        for (int e = 0; e < CH / 4; ++e)
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const float d = vs[q][e][k] - mean;
+                                sq += d * d;
+                            }
+                        const float rstd = 1.0f / sqrtf(group_sum<WN / CH>(sq) / (float)WN + osc.norm_eps);
+#pragma unroll
+                        for (int e = 0; e < CH / 4; ++e)
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                // (hardware exp and reciprocal: the value is rounded to 16 bits next)
+                                const float y = (vs[q][e][k] - mean) * rstd;
+                                vs[q][e][k] = y * __builtin_amdgcn_rcpf(1.0f + __expf(-y));
+                            }
+                    }
+                    if constexpr (EPI == 1 || EPI == 4) {
                         // parent row lr of the wave: its child of octant oct (or -1)
                         const int lr = 32 * rb + NR * h + r;
                         const int a = __shfl(child2[0], lr >> 1, 64), b = __shfl(child2[1], lr >> 1, 64);
@@ -883,6 +923,14 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
         }
     }
     if constexpr (PLANNED && ODT == (BF16 ? TSP_BF16 : TSP_F16)) {
+        if constexpr (CB == 2) {
+            if (osc.cout && osc.norm_silu) {
+                hipLaunchKernelGGL((k_conv_halo_octants_norm<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
+                                   f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, pad);
+                TSP_CHECK_LAUNCH();
+                return TSP_OK;
+            }
+        }
         if (ln.w) {
             hipLaunchKernelGGL((k_conv_halo_ln<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
                                f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, pad, ln);
