@@ -3,7 +3,9 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
+#include <unordered_map>
 
 #include "sparse.h"
 
@@ -40,6 +42,34 @@ const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s) {
         hip_check(tgr::launch_convert(t->data, tgr::tsp_dtype_of(t->type), p, TSP_F32, ggml_nelements(t), s),
                   "parameter conversion");
     return static_cast<const float*>(p);
+}
+
+// ---- packed conv weights -----------------------------------------------------------------------
+// A matrix-core conv's weights are packed once per weight buffer and kept until Model::free
+// (forget_packed_weights): decodes after the first pack nothing. In a sizing pass (where only
+// null or not matters to the workspace sizes) a stand-in pointer.
+namespace {
+std::mutex g_packed_mu;
+std::unordered_map<const void*, void*> g_packed;   // weight data -> its packed copy
+}  // namespace
+
+const void* packed_weights(const Conv& c, Carve& sc, hipStream_t s) {
+    if (!c.mfma) return nullptr;
+    if (!sc.running()) return reinterpret_cast<const void*>(uintptr_t(256));
+    std::lock_guard<std::mutex> lock(g_packed_mu);
+    auto it = g_packed.find(c.w->data);
+    if (it != g_packed.end()) return it->second;
+    void* p = nullptr;
+    hip_check(hipMalloc(&p, tsp_conv_weight_packed_bytes(c.ci, c.co)), "packed conv weights");
+    lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, p, s), "weight pack");
+    g_packed.emplace(c.w->data, p);
+    return p;
+}
+
+void forget_packed_weights() {
+    std::lock_guard<std::mutex> lock(g_packed_mu);
+    for (auto& e : g_packed) (void)hipFree(e.second);
+    g_packed.clear();
 }
 
 int act_dtype(int wdt, bool conv_weight) {
@@ -80,10 +110,9 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
         xr = p;
     }
     if (c.mfma) {
-        void* packed = sc.take(tsp_conv_weight_packed_bytes(c.ci, c.co));
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
-        lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, packed, s), "weight pack");
+        const void* packed = packed_weights(c, sc, s);
         lib(tsp_subm_conv3x3_planned_ex(xr, c.xdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, 0, row0, s),
             "sparse conv");
     } else {
@@ -124,6 +153,7 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
     w.conv_weight = a.conv.w->data;
     w.conv_dtype = a.conv.wdt;
     w.conv_bias = f32_param(a.conv.b, sc, s);
+    w.conv_packed = packed_weights(a.conv, sc, s);
     w.norm_weight = f32_param(a.nw, sc, s);
     w.norm_bias = f32_param(a.nb, sc, s);
     w.mlp0_weight = a.w0->data;
@@ -284,6 +314,8 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     w.conv2_weight = conv2.w->data;
     w.conv2_dtype = conv2.wdt;
     w.conv2_bias = f32_param(c2b, scp, s);
+    w.conv1_packed = packed_weights(conv1, scp, s);
+    w.conv2_packed = packed_weights(conv2, scp, s);
     const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
     const size_t nb = tsp_c2s_workspace_bytes(n, mm, cin, cout, &w, conv1.mfma, conv2.mfma, flags);
     DeviceBuffer work(nb, s);

@@ -51,6 +51,10 @@ struct Conv {
     bool mfma = false;   // matrix-core kernel (16-bit xdt, Ci % 16 == 0, Co % 64 == 0)
 };
 Conv conv_of(const Model& m, const std::string& prefix);
+// c's weights packed for the matrix-core kernel (null when !c.mfma), packed on first use and
+// cached per weight buffer; forget_packed_weights frees every cached copy (Model::free calls it).
+const void* packed_weights(const Conv& c, Carve& sc, hipStream_t s);
+void forget_packed_weights();
 // out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
               float* out, Carve& sc, hipStream_t s);

@@ -23,6 +23,7 @@
 #include "ggml-backend.h"
 #include "ggml.h"
 #include "gguf.h"
+#include "sparse_ops.hpp"
 
 namespace trellis {
 namespace {
@@ -227,6 +228,7 @@ size_t Model::total_bytes() const {
 }
 
 void Model::free() {
+    ops::forget_packed_weights();   // packed copies of this model's conv weights
     tensors.clear();
     if (auto* b = std::exchange(buffer, nullptr)) ggml_backend_buffer_free(b);
     if (auto* be = std::exchange(backend, nullptr)) ggml_backend_free(be);
