@@ -45,31 +45,43 @@ const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s) {
 }
 
 // ---- packed conv weights -----------------------------------------------------------------------
-// A matrix-core conv's weights are packed once per weight buffer and kept until Model::free
-// (forget_packed_weights): decodes after the first pack nothing. In a sizing pass (where only
-// null or not matters to the workspace sizes) a stand-in pointer.
+// The weights of a loaded Model (registered by Model::load, dropped by Model::free) are packed
+// for the matrix-core kernel on first use and kept: decodes after the first pack nothing. Other
+// weight tensors (a caller's own buffers, which may be freed and their memory reused) are not
+// cached. In a sizing pass (where only null or not matters to the workspace sizes) a stand-in.
 namespace {
 std::mutex g_packed_mu;
-std::unordered_map<const void*, void*> g_packed;   // weight data -> its packed copy
+std::unordered_map<const void*, void*> g_packed;   // a model tensor's data -> its packed copy or null
 }  // namespace
 
-const void* packed_weights(const Conv& c, Carve& sc, hipStream_t s) {
-    if (!c.mfma) return nullptr;
-    if (!sc.running()) return reinterpret_cast<const void*>(uintptr_t(256));
+void register_model_weights(const std::vector<const void*>& data) {
     std::lock_guard<std::mutex> lock(g_packed_mu);
-    auto it = g_packed.find(c.w->data);
-    if (it != g_packed.end()) return it->second;
-    void* p = nullptr;
-    hip_check(hipMalloc(&p, tsp_conv_weight_packed_bytes(c.ci, c.co)), "packed conv weights");
-    lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, p, s), "weight pack");
-    g_packed.emplace(c.w->data, p);
-    return p;
+    for (const void* d : data) g_packed.emplace(d, nullptr);
 }
 
-void forget_packed_weights() {
+void forget_model_weights(const std::vector<const void*>& data) {
     std::lock_guard<std::mutex> lock(g_packed_mu);
-    for (auto& e : g_packed) (void)hipFree(e.second);
-    g_packed.clear();
+    for (const void* d : data) {
+        auto it = g_packed.find(d);
+        if (it == g_packed.end()) continue;
+        if (it->second) (void)hipFree(it->second);
+        g_packed.erase(it);
+    }
+}
+
+const void* packed_weights(const Conv& c, bool running, hipStream_t s) {
+    if (!c.mfma) return nullptr;
+    std::lock_guard<std::mutex> lock(g_packed_mu);
+    auto it = g_packed.find(c.w->data);
+    if (it == g_packed.end()) return nullptr;
+    if (!running) return reinterpret_cast<const void*>(uintptr_t(256));
+    if (!it->second) {
+        void* p = nullptr;
+        hip_check(hipMalloc(&p, tsp_conv_weight_packed_bytes(c.ci, c.co)), "packed conv weights");
+        lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, p, s), "weight pack");
+        it->second = p;
+    }
+    return it->second;
 }
 
 int act_dtype(int wdt, bool conv_weight) {
@@ -110,9 +122,14 @@ void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* n
         xr = p;
     }
     if (c.mfma) {
+        const void* packed = packed_weights(c, sc.running(), s);
+        void* own = packed ? nullptr : sc.take(tsp_conv_weight_packed_bytes(c.ci, c.co));
         if (!sc.running()) return;
         if (!plan) fail("sparse conv: the matrix-core path needs a conv plan");
-        const void* packed = packed_weights(c, sc, s);
+        if (own) {
+            lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, own, s), "weight pack");
+            packed = own;
+        }
         lib(tsp_subm_conv3x3_planned_ex(xr, c.xdt, n, c.ci, nbr, plan, packed, bias, c.co, out, TSP_F32, 0, row0, s),
             "sparse conv");
     } else {
@@ -153,7 +170,7 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
     w.conv_weight = a.conv.w->data;
     w.conv_dtype = a.conv.wdt;
     w.conv_bias = f32_param(a.conv.b, sc, s);
-    w.conv_packed = packed_weights(a.conv, sc, s);
+    w.conv_packed = packed_weights(a.conv, sc.running(), s);
     w.norm_weight = f32_param(a.nw, sc, s);
     w.norm_bias = f32_param(a.nb, sc, s);
     w.mlp0_weight = a.w0->data;
@@ -314,8 +331,8 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     w.conv2_weight = conv2.w->data;
     w.conv2_dtype = conv2.wdt;
     w.conv2_bias = f32_param(c2b, scp, s);
-    w.conv1_packed = packed_weights(conv1, scp, s);
-    w.conv2_packed = packed_weights(conv2, scp, s);
+    w.conv1_packed = packed_weights(conv1, true, s);
+    w.conv2_packed = packed_weights(conv2, true, s);
     const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
     const size_t nb = tsp_c2s_workspace_bytes(n, mm, cin, cout, &w, conv1.mfma, conv2.mfma, flags);
     DeviceBuffer work(nb, s);

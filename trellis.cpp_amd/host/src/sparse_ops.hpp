@@ -51,10 +51,13 @@ struct Conv {
     bool mfma = false;   // matrix-core kernel (16-bit xdt, Ci % 16 == 0, Co % 64 == 0)
 };
 Conv conv_of(const Model& m, const std::string& prefix);
-// c's weights packed for the matrix-core kernel (null when !c.mfma), packed on first use and
-// cached per weight buffer; forget_packed_weights frees every cached copy (Model::free calls it).
-const void* packed_weights(const Conv& c, Carve& sc, hipStream_t s);
-void forget_packed_weights();
+// c's weights packed for the matrix-core kernel, packed on first use and cached when they are a
+// loaded model's (register_model_weights, by Model::load; forget_model_weights, by Model::free,
+// frees the copies); null when !c.mfma or the weights are not a model's. With running false
+// (a sizing pass) a non-null stand-in where a copy would be returned.
+const void* packed_weights(const Conv& c, bool running, hipStream_t s);
+void register_model_weights(const std::vector<const void*>& data);
+void forget_model_weights(const std::vector<const void*>& data);
 // out [n][co] f32 = conv(x [n][ci] of dtype xdt); plan may be null unless c.mfma.
 void run_conv(const Conv& c, const void* x, int xdt, int64_t n, const int32_t* nbr, const void* plan,
               float* out, Carve& sc, hipStream_t s);

@@ -206,6 +206,9 @@ Model Model::load(const std::string& path, int gpu) {
         m.free();
         throw;
     }
+    std::vector<const void*> data;
+    for (const auto& e : m.tensors) data.push_back(e.second->data);
+    ops::register_model_weights(data);
     return m;
 }
 
@@ -228,7 +231,9 @@ size_t Model::total_bytes() const {
 }
 
 void Model::free() {
-    ops::forget_packed_weights();   // packed copies of this model's conv weights
+    std::vector<const void*> data;   // the packed copies of these weights go too
+    for (const auto& e : tensors) data.push_back(e.second->data);
+    ops::forget_model_weights(data);
     tensors.clear();
     if (auto* b = std::exchange(buffer, nullptr)) ggml_backend_buffer_free(b);
     if (auto* be = std::exchange(backend, nullptr)) ggml_backend_free(be);
