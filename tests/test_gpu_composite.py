@@ -107,10 +107,14 @@ def test_convnext_mlp(gpu_lib, c, dt, n):
 
 
 @pytest.mark.parametrize("cin,cout,wtype,planned", [(128, 64, "bf16", True), (128, 64, "bf16", False),
-                                                    (64, 32, "f16", True), (32, 16, "f32", False)])
+                                                    (64, 32, "f16", True), (32, 16, "f32", False),
+                                                    (64, 64, "f16", True), (256, 128, "bf16", True),
+                                                    (128, 128, "f16", True)])
 def test_c2s(gpu_lib, orc, shells, cin, cout, wtype, planned):
     """After the caller's subdivision (mask, subdivide, the children's table): octant stores and
-    skip stores on the planned path at (128, 64); gather and skip passes elsewhere."""
+    skip stores on the planned path at Cout = 64 and 128, where conv1's stores also normalise the
+    children and apply SiLU (one wave, or both column waves of a workgroup, holding whole child
+    rows); gather and skip passes elsewhere."""
     import torch
     _case(f"c2s {cin}->{cout} {wtype} planned={planned}")
     rng = np.random.default_rng(cin + cout)
@@ -138,4 +142,4 @@ def test_c2s(gpu_lib, orc, shells, cin, cout, wtype, planned):
     assert np.array_equal(child.cpu().numpy(), rchild)
     err = orc.rel_err(out.cpu().numpy(), ref)
     print(f"c2s rel={err:.3e}", flush=True)
-    assert err < TOL_BLOCK
+    assert err < (TOL_BLOCK_BF16 if wtype == "bf16" else TOL_BLOCK)

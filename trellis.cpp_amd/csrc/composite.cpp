@@ -194,9 +194,9 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
     // when each skip element spans a multiple of 4 channels, otherwise the skip pass does
     const bool octants = cp1.planned && cout % 64 == 0;
     const bool skip_in_stores = cp2.planned && (cout / (cin / 8)) % 4 == 0;
-    // at Cout = 64 (a wave's channels: a whole child row) conv1's stores also do norm2 + SiLU and
-    // write conv2's 16-bit input directly
-    const bool norm_in_stores = octants && cout == 64 && is16(in1) && in2 == in1;
+    // at Cout = 64 / 128 (a wave's / a workgroup's channels: whole child rows) conv1's stores also
+    // do norm2 + SiLU and write conv2's 16-bit input directly
+    const bool norm_in_stores = octants && (cout == 64 || cout == 128) && is16(in1) && in2 == in1;
     void* h0 = ws.take((size_t)n * cin * dtype_size(in1));
     float* h1 = octants ? nullptr : static_cast<float*>(ws.take((size_t)n * 8 * cout * 4));
     float* g = norm_in_stores ? nullptr : static_cast<float*>(ws.take((size_t)m * cout * 4));

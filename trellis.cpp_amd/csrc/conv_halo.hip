@@ -63,8 +63,8 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                   "(co=%d cout=%d)", bn128 ? 64 : 32, co, osc.cout);
         return TSP_ERR_UNSUPPORTED;
     }
-    if (osc.norm_silu && (!bn128 || osc.cout != 64 || odt != fdt)) {
-        set_error("MFMA conv: octant stores with the child norm need cout = 64, co %% 128 == 0 and "
+    if (osc.norm_silu && (!bn128 || (osc.cout != 64 && osc.cout != 128) || odt != fdt)) {
+        set_error("MFMA conv: octant stores with the child norm need cout = 64 or 128, co %% 128 == 0 and "
                   "output in the feature type (co=%d cout=%d)", co, osc.cout);
         return TSP_ERR_UNSUPPORTED;
     }

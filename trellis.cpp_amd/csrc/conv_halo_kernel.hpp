@@ -151,6 +151,19 @@ __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_
         RowNorm{});
 }
 
+// The same with cout == BN: each child row normalised across the workgroup's two column waves
+// (as k_conv_halo_ln, no affine) and passed through SiLU.
+template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
+__global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_octants_rownorm(
+    const uint16_t* __restrict__ feats, int64_t n, int ci, const int32_t* __restrict__ nbr,
+    PlanView plan, const uint16_t* __restrict__ weight, const float* __restrict__ bias, int co,
+    void* __restrict__ out, int64_t n_tiles, int n_ctiles, int64_t per_xcd, OctantScatter osc,
+    PadRow pad) {
+    conv_grid<BF16, BN, BF16 ? TSP_BF16 : TSP_F16, true, RB, CB, PD, SP, STG, 5>(
+        feats, n, ci, nbr, plan, weight, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, SkipAdd{}, pad,
+        RowNorm{});
+}
+
 // The same conv with f32 output and the C2S skip added by its stores (stored plan).
 template <bool BF16, int BN, int RB, int CB, int PD, int SP, int STG>
 __global__ __launch_bounds__((hb_waves<BN, RB, CB>() * 64), 1) void k_conv_halo_skip(
@@ -206,8 +219,8 @@ __device__ __forceinline__ void conv_tiles(
     int rg = wave % NRG;                     // row group: voxels [32 RB rg, +32 RB)
     const int c0 = (int)(lin0 % n_ctiles) * BN + (wave / NRG) * WN;   // first channel of wave
     // with an octant scatter, the wave's channels lie in octant oct, from column ocol of a child
-    const int oct = EPI == 1 || EPI == 4 ? c0 / osc.cout : 0;
-    const int ocol = EPI == 1 || EPI == 4 ? c0 - oct * osc.cout : 0;
+    const int oct = EPI == 1 || EPI == 4 || EPI == 5 ? c0 / osc.cout : 0;
+    const int ocol = EPI == 1 || EPI == 4 || EPI == 5 ? c0 - oct * osc.cout : 0;
     const int nkc = ci / HB_KC;
     // The reference's absent taps read the padding row 0 * feats[0] (submconv_pad,
     // sparse.cpp:81-85), zeros here. Where row 0 holds an Inf or a NaN that row is NaN in those
@@ -532,8 +545,9 @@ __device__ __forceinline__ void conv_tiles(
         constexpr int RR = 16;                   // rows per round and row group
         constexpr int RSW = BN * 4 + 16;         // staged row stride in bytes
         constexpr int CPL = BN / 16;             // channels per lane
-        static_assert(EPI != 3 || (NCG == 2 && RB == 4 && NRG * RR * RSW <= (int)sizeof(sH1)), "row-norm staging");
-        static_assert(EPI != 3 || ODT == TSP_BF16 || ODT == TSP_F16, "row norm stores 16-bit rows");
+        constexpr bool RN = EPI == 3 || EPI == 5;
+        static_assert(!RN || (NCG == 2 && RB == 4 && NRG * RR * RSW <= (int)sizeof(sH1)), "row-norm staging");
+        static_assert(!RN || ODT == TSP_BF16 || ODT == TSP_F16, "row norm stores 16-bit rows");
         char* stage = reinterpret_cast<char*>(&sH1[0][0][0]) + rg * RR * RSW;
         const int cg = wave / NRG;
         int vrow[2];
@@ -547,8 +561,8 @@ __device__ __forceinline__ void conv_tiles(
         float gw[CPL], gb[CPL];
 #pragma unroll
         for (int e = 0; e < CPL; ++e) {
-            gw[e] = ln.w[lc + e];
-            gb[e] = ln.b[lc + e];
+            gw[e] = EPI == 5 ? 1.f : ln.w[lc + e];   // (EPI 5: no affine)
+            gb[e] = EPI == 5 ? 0.f : ln.b[lc + e];
         }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -584,11 +598,27 @@ __device__ __forceinline__ void conv_tiles(
                         const float d = v[e] - mean;
                         sq += d * d;
                     }
-                    const float rstd = 1.0f / sqrtf(group_sum<16>(sq) / (float)BN + ln.eps);
+                    const float rstd = 1.0f / sqrtf(group_sum<16>(sq) / (float)BN + (EPI == 5 ? osc.norm_eps : ln.eps));
                     float y[CPL];
 #pragma unroll
                     for (int e = 0; e < CPL; ++e) y[e] = (v[e] - mean) * rstd * gw[e] + gb[e];
+                    if constexpr (EPI == 5) {
+#pragma unroll
+                        for (int e = 0; e < CPL; ++e) y[e] = y[e] * __builtin_amdgcn_rcpf(1.0f + __expf(-y[e]));
+                    }
                     const int64_t i = row_at(32 * rb + 16 * h + r);
+                    // the stored row: i, or (EPI 5) the child of octant oct of parent i, or none
+                    int64_t drow = i;
+                    if constexpr (EPI == 5) {
+                        drow = -1;
+                        if (i >= 0) {
+                            constexpr uint64_t kLow7 = 0x7f7f7f7f7f7f7f7full;
+                            const uint64_t mw = *reinterpret_cast<const uint64_t*>(osc.mask + 8 * i);
+                            const uint64_t kept = (((mw & kLow7) + kLow7) | mw) & ~kLow7;
+                            if ((kept >> (8 * oct + 7)) & 1)
+                                drow = osc.mstart[i] + __popcll(kept & ((1ull << (8 * oct)) - 1));
+                        }
+                    }
                     if (row0_bad && i >= 0) {
                         bool absent = false;
                         for (int t = 0; t < kTaps; ++t) absent |= nbr[(int64_t)t * n + i] == (int32_t)n;
@@ -597,14 +627,14 @@ __device__ __forceinline__ void conv_tiles(
                             for (int e = 0; e < CPL; ++e) y[e] = NAN;
                         }
                     }
-                    if (i >= 0) {
+                    if (drow >= 0) {
                         uint32_t wd[CPL / 2];
 #pragma unroll
                         for (int e = 0; e < CPL / 2; ++e)
                             wd[e] = (ODT == TSP_BF16) ? f32x2_to_bf16x2_bits(y[2 * e], y[2 * e + 1])
                                                       : f32_to_f16_bits(y[2 * e]) |
                                                             ((uint32_t)f32_to_f16_bits(y[2 * e + 1]) << 16);
-                        uint16_t* dst = reinterpret_cast<uint16_t*>(out) + i * co + lc;
+                        uint16_t* dst = reinterpret_cast<uint16_t*>(out) + drow * (EPI == 5 ? osc.cout : co) + lc;
                         if constexpr (CPL == 8)
                             *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
                         else
@@ -616,7 +646,7 @@ __device__ __forceinline__ void conv_tiles(
         }
     };
     auto finish = [&](auto nr_c, f32x16_t (&acc)[RB][CB], int64_t tile) {
-        if constexpr (EPI == 3) epilogue_ln(acc, tile);
+        if constexpr (EPI == 3 || EPI == 5) epilogue_ln(acc, tile);
         else epilogue(nr_c, acc, tile);
     };
 
@@ -924,8 +954,14 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
     }
     if constexpr (PLANNED && ODT == (BF16 ? TSP_BF16 : TSP_F16)) {
         if constexpr (CB == 2) {
-            if (osc.cout && osc.norm_silu) {
+            if (osc.cout && osc.norm_silu && osc.cout == 32 * CB) {
                 hipLaunchKernelGGL((k_conv_halo_octants_norm<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
+                                   f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, pad);
+                TSP_CHECK_LAUNCH();
+                return TSP_OK;
+            }
+            if (osc.cout && osc.norm_silu && osc.cout == BN) {
+                hipLaunchKernelGGL((k_conv_halo_octants_rownorm<BF16, BN, RB, CB, PD, SP, STG>), grid, block, 0, s,
                                    f16, n, ci, nbr, pv, w16, bias, co, out, n_tiles, n_ctiles, per_xcd, osc, pad);
                 TSP_CHECK_LAUNCH();
                 return TSP_OK;

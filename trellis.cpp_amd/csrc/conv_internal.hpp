@@ -70,7 +70,8 @@ int halo_weight_pack(const void* w, int wdt, int ci, int co, void* packed, hipSt
 // channel c = o * cout + k of row i goes to row mstart[i] + (octants of parent i kept before o)
 // of an [M][cout] output when mask[8 i + o] != 0, and nowhere otherwise (the octant gather of
 // sparse.cpp:263-291 done by the conv's stores). mask must be 8-byte aligned. With norm_silu
-// set (cout == the 64 channels one wave owns, 16-bit output of the feature type) each child row
+// set (cout == 64 or 128: the channels of a wave or of a workgroup; 16-bit output of the feature
+// type) each child row
 // is stored as silu((y - mean(y)) / sqrt(var(y) + norm_eps)) instead: the C2S block's norm2 + SiLU
 // (no affine, sparse.cpp:293) done by the stores, its f32 input never written.
 struct OctantScatter {
