@@ -370,7 +370,7 @@ size_t tsp_c2s_workspace_bytes(int64_t n, int64_t m, int cin, int cout, const ts
  * conv2(SiLU(LN(gather(conv1(SiLU(LN(x) * norm1.weight + norm1.bias))))), absent taps of conv2
  * reading an exact zero row) + the repeat-interleaved skip of x. d_plan (of d_nbr, for conv1)
  * and d_child_plan (of d_child_nbr, for conv2) may each be NULL. out must not alias x. With
- * d_plan, cout = 64 and both convs' weights of one 16-bit type, conv1's stores also do the
+ * d_plan, cout = 64 or 128 and both convs' weights of one 16-bit type, conv1's stores also do the
  * children's LN + SiLU (the gathered f32 rows are never written; the packed conv1 weights must
  * then be 16-byte aligned and the mask 8-byte aligned). */
 int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
