@@ -115,7 +115,12 @@ void k_mlp_ws(const uint16_t* __restrict__ xn, int64_t n, const uint16_t* __rest
         const int64_t nxt = rb + gridDim.x;
         const int span = block_rows(rb) * MLP_C * 4;   // bytes of x and y in this block
         const u32x4_t xr = load_x(nxt);                  // the next block's rows
-        __builtin_amdgcn_sched_barrier(0);               // (issued here, a whole block ahead of its use)
+        // this block's inputs to add (needed last)
+        const __amdgpu_buffer_rsrc_t xres = span_rsrc(x + rb * 32 * MLP_C, span);
+        float xv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xres, out_off(e), 0, 0));
+        __builtin_amdgcn_sched_barrier(0);               // (issued here, a whole block ahead of their use)
         // xn^T as B operands: lane l holds row r32, channels 16 ks + 8 g .. + 7
         u32x4_t xf[8];
 #pragma unroll
@@ -143,11 +148,6 @@ void k_mlp_ws(const uint16_t* __restrict__ xn, int64_t n, const uint16_t* __rest
 #pragma unroll
             for (int h = 0; h < 8; ++h)
                 hf[hb][h >> 2][h & 3] = pack16x2<BF16>(silu(a1[hb][2 * h]), silu(a1[hb][2 * h + 1]));
-        // this block's inputs to add (needed last)
-        const __amdgpu_buffer_rsrc_t xres = span_rsrc(x + rb * 32 * MLP_C, span);
-        float xv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xres, out_off(e), 0, 0));
         // Y_w = H_w . W2_w^T, two column blocks at a time
         f32x16_t acc[2];
         __syncthreads();   // every wave has summed the previous block's partial products
