@@ -274,6 +274,13 @@ int tsp_linear_ex(const void* d_x, int x_dtype, int64_t n, int ci, const void* d
                   int weight_dtype, const float* d_bias, int co, int act, const float* d_residual,
                   void* d_out, int out_dtype, void* stream);
 
+/* Rows of x that tsp_linear and tsp_linear_ex hand hipBLASLt per library call: they cut n into
+ * chunks of this many rows so that no operand of one call (x, out, residual) spans 2^31 bytes or
+ * more (the counterpart of the reference's mul_mat_rows, sparse.cpp:41-59, which cuts at
+ * 1,000,000 rows for a Vulkan grid limit). A multiple of 256 where 256 rows fit; 0 for invalid
+ * arguments or a row of 2 GiB. Host arithmetic only (no device call). */
+int64_t tsp_linear_rows_per_call(int ci, int co, int x_dtype, int out_dtype, int has_residual);
+
 /* Row LayerNorm over c channels with biased variance and eps (ggml_norm, sparse.cpp:124,
  * 259, 293), then * gamma + beta when those are not NULL, then x * sigmoid(x) when silu != 0.
  * d_out may equal d_x. */
@@ -319,17 +326,19 @@ typedef struct {
     const void* mlp2_weight;   /* [C][4C] */
     int mlp2_dtype;
     const float* mlp2_bias;    /* [C] */
+    const void* mlp_packed;    /* optional: mlp.0 and mlp.2 packed by tsp_convnext_mlp_pack (used where
+                                  the MLP is one kernel; NULL packs them into the workspace per call) */
 } tsp_convnext_weights;
 
-/* Workspace tsp_convnext needs (only the dtypes and conv_packed of w are read). */
+/* Workspace tsp_convnext needs (only the dtypes, conv_packed and mlp_packed of w are read). */
 size_t tsp_convnext_workspace_bytes(int64_t n, int c, int x_dtype, const tsp_convnext_weights* w,
                                     int has_plan, int flags);
 /* SparseConvNeXtBlock3d (replaces trellis::sparse_convnext, include/sparse.h:24-25,
  * src/sparse.cpp:94-137): out f32 [n][c] = x + mlp.2(SiLU(mlp.0(LN(conv(x)) * norm.weight +
  * norm.bias))), LN eps 1e-6. x f32, or 16-bit of the conv input's type; d_plan (of d_nbr) may be
  * NULL; out must not alias x. With f32 x, c = 128 and both MLP weights of the normalised input's
- * 16-bit type, the MLP is one kernel (tsp_convnext_mlp): its weights and the workspace must then be
- * 16-byte aligned. */
+ * 16-bit type, the MLP is one kernel (tsp_convnext_mlp): its weights (or mlp_packed) and the
+ * workspace must then be 16-byte aligned. Arguments are checked before any work is enqueued. */
 int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, const int32_t* d_nbr,
                  const void* d_plan, const tsp_convnext_weights* w, float* d_out,
                  void* d_workspace, size_t workspace_bytes, int flags, void* stream);

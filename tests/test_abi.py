@@ -164,6 +164,44 @@ def test_linear_ex_validation(pkg):
     assert "residual" in _err(pkg)
 
 
+def test_linear_row_split(pkg):
+    """tsp_linear_rows_per_call: the rows tsp_linear / tsp_linear_ex hand hipBLASLt per call. For
+    every dtype pair, residual or not, and widths up to 4096 (plus 2^20 and 2^29 to reach the
+    one-row and no-row ends), no operand of one call -- x [rows][ci], out [rows][co], the f32
+    residual [rows][co] -- spans 2^31 bytes or more; the chunk is a multiple of 256 rows wherever
+    256 rows fit, and as large as that allows (one more block of 256 rows would break the bound).
+    The chunk walk over n = INT32_MAX - 1 rows covers every row exactly once."""
+    L = pkg.lib()
+    size = {0: 4, 1: 2, 2: 2}
+    limit = 2 ** 31
+    widths = [8, 16, 64, 128, 256, 512, 1000, 1024, 2048, 4096, 1 << 20, 1 << 29]
+    for xdt in (0, 1, 2):
+        for odt in (0, 1, 2):
+            for res in (0, 1):
+                for ci in widths:
+                    for co in widths:
+                        rows = L.tsp_linear_rows_per_call(ci, co, xdt, odt, res)
+                        row_bytes = max(ci * size[xdt], co * size[odt], co * 4 if res else 0)
+                        if row_bytes >= limit:
+                            assert rows == 0
+                            continue
+                        assert rows >= 1
+                        assert rows * row_bytes < limit, (ci, co, xdt, odt, res)
+                        if rows >= 256:
+                            assert rows % 256 == 0 and (rows + 256) * row_bytes >= limit
+                        else:
+                            assert (rows + 1) * row_bytes >= limit
+    assert L.tsp_linear_rows_per_call(0, 64, 2, 2, 0) == 0 and L.tsp_linear_rows_per_call(64, 64, 9, 2, 0) == 0
+    # the decoder's widest hidden layer: 2.45 M rows of 4 x 128 f32 channels (2.5 GB) take 3 calls
+    rows = L.tsp_linear_rows_per_call(128, 512, 2, 0, 0)
+    n = 2_445_586
+    assert rows == 1_048_320 and -(-n // rows) == 3
+    n = 2 ** 31 - 2
+    rows = L.tsp_linear_rows_per_call(4096, 4096, 2, 0, 1)
+    covered = sum(min(rows, n - r0) for r0 in range(0, n, rows))
+    assert covered == n
+
+
 def test_planned_octants_validation(pkg):
     """tsp_subm_conv3x3_planned_octants: argument checks before any device work -- range and dtype
     (1 / 4), cout not a multiple of 64 and ci not a multiple of 16 (4), the empty case (0), null,

@@ -77,6 +77,38 @@ def test_linear_ex(gpu_lib, orc, n, ci, co):
     with pytest.raises(gpu_lib.TspError, match="UNSUPPORTED"):
         gpu_lib.linear_ex(_t(np.ones((4, 32), np.float32)), _t(np.ones((64, 32), np.float32)))
 
+
+def test_linear_ex_chunked_over_2gib(gpu_lib, orc):
+    """tsp_linear_ex where one operand spans more than 2 GiB: the decoder's last-stage ConvNeXt
+    hidden layer, 2,445,586 rows x (128 -> 512) bf16 with f32 output (5.0 GB), which the library
+    cuts into calls of tsp_linear_rows_per_call rows (3 here) so that no operand of one hipBLASLt
+    call reaches 2^31 bytes. Sampled rows -- both chunk boundaries, the first and last rows and a
+    random sample -- against the fp64 oracle: the SiLU output and the residual output."""
+    import torch
+    n, ci, co = 2_445_586, 128, 512
+    L = gpu_lib.lib()
+    rows = L.tsp_linear_rows_per_call(ci, co, 2, 0, 0)
+    assert rows * co * 4 < 2 ** 31 and n * co * 4 > 2 ** 31 and -(-n // rows) == 3
+    _case(f"linear_ex chunked n={n} ci={ci} co={co} rows/call={rows}")
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((n, ci), generator=g, device="cuda").to(torch.bfloat16)
+    rng = np.random.default_rng(7)
+    w = _t((rng.standard_normal((co, ci)) / np.sqrt(ci)).astype(np.float32)).to(torch.bfloat16)
+    b = rng.standard_normal(co).astype(np.float32)
+    edges = [0, 1, rows - 1, rows, rows + 1, 2 * rows - 1, 2 * rows, n - 2, n - 1]
+    sample = np.unique(np.concatenate([edges, rng.integers(0, n, 3000)]))
+    xs = x[torch.from_numpy(sample).cuda()].float().cpu().numpy()
+    pre = orc.linear(xs, w.float().cpu().numpy(), b)
+    h = gpu_lib.linear_ex(x, w, _t(b), act="silu", out_dtype=torch.float32)
+    hs = h[torch.from_numpy(sample).cuda()].cpu().numpy()
+    del h
+    assert orc.rel_err(hs, orc.silu(pre)) < 1e-4
+    res = torch.randn((n, co), generator=g, device="cuda")
+    y = gpu_lib.linear_ex(x, w, _t(b), residual=res, out_dtype=torch.float32)
+    idx = torch.from_numpy(sample).cuda()
+    ys, rs = y[idx].cpu().numpy(), res[idx].cpu().numpy()
+    assert orc.rel_err(ys, pre + rs) < TOL_32
+
 @pytest.mark.parametrize("c", [7, 64, 128, 256, 512, 1024, 2048, 4096])
 def test_layer_norm(gpu_lib, orc, c):
     _case(f"layer_norm c={c}")

@@ -747,6 +747,80 @@ def test_ordered_plan_fallback(gpu_lib, shells, kind):
             assert np.array_equal(a["slots"][t], b["slots"][t])
 
 
+def _grid_blocks(coords):
+    """Blocks of the plan's cell grid for coords (8^3 cells; a cell above or below a voxel at the
+    top or bottom of its cell also gets one, inside the directory's power-of-two box)."""
+    c = np.asarray(coords, np.int64)
+    cell = c >> 3
+    lo = cell.min(0)
+    side = 1 << int(np.ceil(np.log2(max(int((cell.max(0) - lo).max()) + 1, 1))))
+    keys = {tuple(v) for v in cell.tolist()}
+    for v, z in zip(cell.tolist(), c[:, 2].tolist()):
+        for dz, hit in ((-1, z & 7 == 0), (1, z & 7 == 7)):
+            if hit and 0 <= v[2] + dz - lo[2] < side:
+                keys.add((v[0], v[1], v[2] + dz))
+    return len(keys)
+
+
+@pytest.mark.parametrize("n,box", [(2000, 256), (5000, 400)])
+def test_ordered_plan_scattered_more_blocks_than_voxels(gpu_lib, orc, shells, n, box):
+    """Scattered voxels whose cell grid has more blocks than voxels (a voxel can add a halo-only
+    block), which the plan's per-block scratch must hold: the conv on the Morton plan equals the
+    conv on the row plan and without a plan bit for bit, and the oracle within TOL_16; the table
+    and plan built in one call give the same conv."""
+    import torch
+    rng = np.random.default_rng(n)
+    coords = np.ascontiguousarray(rng.integers(0, box, size=(n, 3)), np.int32)
+    nb = _grid_blocks(coords)
+    assert nb > n, (nb, n)   # the case the scratch was once too small for
+    _case(f"ordered plan, scattered n={n} in [0,{box})^3: {nb} grid blocks")
+    ci = co = 64
+    feats = shells.round_to(rng.standard_normal((n, ci)).astype(np.float32), "bf16")
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32), "bf16")
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    f, w, b = _dev(feats, torch.bfloat16), _dev(weight, torch.bfloat16), _dev(bias, torch.float32)
+    pw = gpu_lib.conv_weight_pack(w)
+    outs = {}
+    for name, pc in (("morton", c), ("rows", None)):
+        plan = gpu_lib.conv_plan_build(nbr, n, coords=pc)
+        outs[name] = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, co, out_dtype=torch.float32)
+    nbr1, plan1 = gpu_lib.rulebook_build_planned(c)
+    outs["one-call"] = gpu_lib.subm_conv3x3_planned(f, nbr1, plan1, pw, b, co, out_dtype=torch.float32)
+    outs["none"] = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(nbr1, nbr)
+    for k in ("morton", "rows", "one-call"):
+        assert torch.equal(outs[k], outs["none"]), k
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    assert orc.rel_err(outs["morton"].cpu().numpy(), ref) < TOL_16
+
+
+def test_table_and_plan_dense_random_blocks(gpu_lib, shells):
+    """2,000,000 random voxels in [0,295)^3 (~40 per occupied 8^3 cell): the neighbour table's
+    workspace holds their cell grid, whose presence bitmaps (64 bytes a block) the plan built in
+    the same call must hold too. The one-call table equals tsp_rulebook_build's, and the conv on its
+    plan equals the conv without a plan bit for bit."""
+    import torch
+    rng = np.random.default_rng(295)
+    n = 2_000_000
+    coords = np.ascontiguousarray(rng.integers(0, 295, size=(n, 3)), np.int32)
+    _case(f"table + plan in one call: {n} random voxels in [0,295)^3")
+    c = torch.from_numpy(coords).cuda()
+    nbr1, plan1 = gpu_lib.rulebook_build_planned(c)
+    nbr = gpu_lib.rulebook_build(c)
+    assert torch.equal(nbr1, nbr)
+    ci = co = 64
+    f = (torch.randn((n, ci), device="cuda")).to(torch.bfloat16)
+    w = (torch.randn((co, 27, ci), device="cuda") / 40).to(torch.bfloat16)
+    b = torch.zeros(co, device="cuda")
+    out = gpu_lib.subm_conv3x3_planned(f, nbr1, plan1, gpu_lib.conv_weight_pack(w), b, co, out_dtype=torch.float32)
+    ref = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("ci,co", [(128, 128), (64, 64), (256, 64)])
 def test_ordered_plan_results(gpu_lib, orc, shells, ci, co):
     """The planned conv on Morton tiles, on row tiles and without a plan: the same bits, and the

@@ -31,7 +31,7 @@ EXPORTS = (
     "tsp_subm_conv3x3_planned", "tsp_subm_conv3x3_planned_ex", "tsp_subm_conv3x3_planned_octants",
     "tsp_subm_conv3x3_planned_skip",
     "tsp_subdivide_workspace_bytes", "tsp_subdivide", "tsp_subdivide_noalloc",
-    "tsp_linear", "tsp_linear_ex", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
+    "tsp_linear", "tsp_linear_ex", "tsp_linear_rows_per_call", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
     "tsp_convnext_workspace_bytes", "tsp_convnext", "tsp_c2s_workspace_bytes", "tsp_c2s",
 )
@@ -45,7 +45,7 @@ class ConvNextWeights(ctypes.Structure):
                 ("conv_packed", ctypes.c_void_p), ("norm_weight", ctypes.c_void_p),
                 ("norm_bias", ctypes.c_void_p), ("mlp0_weight", ctypes.c_void_p), ("mlp0_dtype", ctypes.c_int),
                 ("mlp0_bias", ctypes.c_void_p), ("mlp2_weight", ctypes.c_void_p), ("mlp2_dtype", ctypes.c_int),
-                ("mlp2_bias", ctypes.c_void_p)]
+                ("mlp2_bias", ctypes.c_void_p), ("mlp_packed", ctypes.c_void_p)]
 
 
 class C2SWeights(ctypes.Structure):
@@ -134,6 +134,8 @@ def lib() -> ctypes.CDLL:
     L.tsp_linear_ex.restype = c_int
     L.tsp_linear_ex.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_int, c_vp, c_int, c_int, c_vp,
                                 c_vp, c_int, c_vp]
+    L.tsp_linear_rows_per_call.restype = c_i64
+    L.tsp_linear_rows_per_call.argtypes = [c_int, c_int, c_int, c_int, c_int]
     L.tsp_layer_norm.restype = c_int
     L.tsp_layer_norm.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, ctypes.c_float, c_int,
                                  c_vp, c_int, c_vp]
@@ -663,7 +665,8 @@ def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None):
     """SparseConvNeXtBlock3d through tsp_convnext: x [N, C] (f32, or 16-bit of the conv input's
     type), p the block's tensors by their reference names without the prefix ("conv.weight"
     [C,27,C], "conv.bias", "norm.weight", "norm.bias", "mlp.0.weight" [4C,C], "mlp.0.bias",
-    "mlp.2.weight" [C,4C], "mlp.2.bias"); optional "conv.packed". -> f32 [N, C]."""
+    "mlp.2.weight" [C,4C], "mlp.2.bias"); optional "conv.packed" (conv_weight_pack) and
+    "mlp.packed" (convnext_mlp_pack of mlp.0 and mlp.2). -> f32 [N, C]."""
     torch = _torch()
     n, c = x.shape
     _check_nbr(nbr, n, x.device)
@@ -675,13 +678,16 @@ def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None):
     packed = p.get("conv.packed")
     if packed is not None and (packed.numel() * packed.element_size() != lib().tsp_conv_weight_packed_bytes(c, c)):
         raise ValueError("conv.packed must be conv.weight packed by conv_weight_pack")
+    mpacked = p.get("mlp.packed")
+    if mpacked is not None and mpacked.numel() * mpacked.element_size() != lib().tsp_convnext_mlp_packed_bytes(c):
+        raise ValueError("mlp.packed must be mlp.0 and mlp.2 packed by convnext_mlp_pack")
     if plan is not None and (plan.dtype != torch.uint8 or plan.numel() < lib().tsp_conv_plan_bytes(n)):
         raise ValueError("plan must be a uint8 buffer of tsp_conv_plan_bytes(N)")
-    _require_cuda(x, nbr, plan, packed, *t.values())
+    _require_cuda(x, nbr, plan, packed, mpacked, *t.values())
     w = ConvNextWeights(_ptr(t["conv.weight"]), dtype_code(t["conv.weight"].dtype), _ptr(t["conv.bias"]),
                         _ptr(packed), _ptr(t["norm.weight"]), _ptr(t["norm.bias"]), _ptr(t["mlp.0.weight"]),
                         dtype_code(t["mlp.0.weight"].dtype), _ptr(t["mlp.0.bias"]), _ptr(t["mlp.2.weight"]),
-                        dtype_code(t["mlp.2.weight"].dtype), _ptr(t["mlp.2.bias"]))
+                        dtype_code(t["mlp.2.weight"].dtype), _ptr(t["mlp.2.bias"]), _ptr(mpacked))
     flags = BLOCK_CAST_F32 if cast_f32 else 0
     xc = x.contiguous()
     out = torch.empty((n, c), dtype=torch.float32, device=x.device)

@@ -110,24 +110,38 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
     const int cdt = act_dtype(w.conv_dtype, true, flags);
     const int adt0 = act_dtype(w.mlp0_dtype, false, flags), adt2 = act_dtype(w.mlp2_dtype, false, flags);
     const int64_t chunk = mlp_chunk(n, c);
-    // conv input rounded (when x is f32 and the conv takes 16-bit input)
-    const void* xc = x;
-    if (xdt != cdt) {   // x is f32 here (the entry point rejects other mixes)
-        void* p = ws.take((size_t)n * c * dtype_size(cdt));
-        if (ws.base)
-            if (int st = f32_to(static_cast<const float*>(x), n * c, p, cdt, false, s)) return st;
-        xc = p;
-    }
+    // conv input rounded (when x is f32 and the conv takes 16-bit input; x is f32 there, the entry
+    // point rejects other mixes)
+    void* xr16 = xdt != cdt ? ws.take((size_t)n * c * dtype_size(cdt)) : nullptr;
+    const void* xc = xr16 ? xr16 : x;
     const bool fuse = ln_fused(cdt, adt0, c, plan);
     // the MLP in one kernel, its 16-bit hidden layer never stored (C = 128, one 16-bit dtype)
     const bool mlp1 = is16(adt0) && adt2 == adt0 && w.mlp0_dtype == adt0 && w.mlp2_dtype == adt0 &&
                       xdt == TSP_F32 && c == 128;
     float* h = fuse ? nullptr : static_cast<float*>(ws.take((size_t)n * c * 4));
     void* hn = ws.take((size_t)n * c * dtype_size(adt0));
-    void* mlp_packed = mlp1 ? ws.take(mlp_packed_bytes(c)) : nullptr;
+    void* mlp_packed = mlp1 && !w.mlp_packed ? ws.take(mlp_packed_bytes(c)) : nullptr;
     float* hid = mlp1 ? nullptr : static_cast<float*>(ws.take((size_t)chunk * 4 * c * 4));
     void* hid_in = mlp1 || adt2 == TSP_F32 ? hid : ws.take((size_t)chunk * 4 * c * 2);
     const float* row0 = xdt == TSP_F32 && cdt != TSP_F32 ? static_cast<const float*>(x) : nullptr;
+    if (!ws.base) {
+        // the conv's own pieces (packed weights) are sized by the same walk
+        if (fuse) return run_conv_ln(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed,
+                                     w.conv_bias, w.norm_weight, w.norm_bias, row0, hn, ws, s);
+        return run_conv(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed, w.conv_bias, c, h, 0,
+                        row0, ws, s);
+    }
+    // every check before the first launch, so that an error leaves no work behind
+    if (mlp1) {
+        auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        TSP_REQUIRE(w.mlp_packed ? al(w.mlp_packed) : al(w.mlp0_weight) && al(w.mlp2_weight), TSP_ERR_INVALID,
+                    "tsp_convnext: the MLP weights (or mlp_packed) must be 16-byte aligned");
+        TSP_REQUIRE(mlp_fused_eligible(adt0, c, hn, w.mlp_packed ? w.mlp_packed : mlp_packed,
+                                       static_cast<const float*>(x), out),
+                    TSP_ERR_INVALID, "tsp_convnext: the workspace must be 16-byte aligned");
+    }
+    if (xr16)
+        if (int st = f32_to(static_cast<const float*>(x), n * c, xr16, cdt, false, s)) return st;
     if (fuse) {
         if (int st = run_conv_ln(xc, cdt, n, c, nbr, plan, w.conv_weight, w.conv_dtype, w.conv_packed, w.conv_bias,
                                  w.norm_weight, w.norm_bias, row0, hn, ws, s))
@@ -141,12 +155,12 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
         if (int st = tsp_layer_norm(h, TSP_F32, n, c, w.norm_weight, w.norm_bias, 1e-6f, 0, hn, adt0, s)) return st;
     }
     if (mlp1) {
-        auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-        TSP_REQUIRE(al(w.mlp0_weight) && al(w.mlp2_weight) &&
-                        mlp_fused_eligible(adt0, c, hn, mlp_packed, static_cast<const float*>(x), out),
-                    TSP_ERR_INVALID, "tsp_convnext: the MLP weights and the workspace must be 16-byte aligned");
-        if (int st = mlp_pack(w.mlp0_weight, w.mlp2_weight, c, mlp_packed, s)) return st;
-        return mlp_fused(hn, adt0, n, c, mlp_packed, w.mlp0_bias, w.mlp2_bias, static_cast<const float*>(x), out, s);
+        const void* mp = w.mlp_packed;
+        if (!mp) {
+            if (int st = mlp_pack(w.mlp0_weight, w.mlp2_weight, c, mlp_packed, s)) return st;
+            mp = mlp_packed;
+        }
+        return mlp_fused(hn, adt0, n, c, mp, w.mlp0_bias, w.mlp2_bias, static_cast<const float*>(x), out, s);
     }
     const size_t aes = dtype_size(adt0), xes = dtype_size(xdt);
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {

@@ -483,8 +483,8 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
         if (st != TSP_ERR_UNSUPPORTED || algo == TSP_ALGO_THIN) {
             TSP_REQUIRE(st != TSP_ERR_UNSUPPORTED, TSP_ERR_UNSUPPORTED,
                         "tsp_subm_conv3x3: the thin kernel needs co in {4, 8, 16, 32}, ci %% 4 == 0, "
-                        "ci * co <= 512, 16-byte aligned feats and a dtype pair of the VALU kernel "
-                        "(got ci=%d co=%d)", ci, co);
+                        "ci * co <= 512, n * ci < 2^32, 16-byte aligned feats and a dtype pair of the "
+                        "VALU kernel (got ci=%d co=%d)", ci, co);
             return st;
         }
     }

@@ -56,6 +56,9 @@ int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* 
 // The same Morton-ordered plan on a cell grid already built from `coords` (region and tail of
 // grid_build, with cell_of = plan_cell_of(plan, n)), e.g. the neighbour table's.
 int32_t* plan_cell_of(void* plan, int64_t n);
+// The most grid blocks the plan's per-block scratch holds (grid_build's block_cap for a grid whose
+// blocks the plan walks).
+int64_t plan_block_cap(int64_t n);
 int halo_plan_build_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan,
                             const void* region, void* tail, hipStream_t s);
 // Packed weights: the [co][27][ci] 16-bit values in the MFMA operand order, then a trailer of

@@ -178,6 +178,8 @@ bool thin_fits(int ci, int co) {
 int thin_conv_launch(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad) {
     if (!thin_fits(ci, co) || !nbr) return TSP_ERR_UNSUPPORTED;
+    // the kernel's feature offsets (row * ci) are 32-bit
+    if ((uint64_t)n * (uint64_t)ci >= ((uint64_t)1 << 32)) return TSP_ERR_UNSUPPORTED;
     if (reinterpret_cast<uintptr_t>(feats) % 16) return TSP_ERR_UNSUPPORTED;
     if (fdt == TSP_F32 && wdt == TSP_F32) return thin_out<TSP_F32, TSP_F32>(odt, co, feats, n, ci, nbr, weight, bias, out, s, pad);
     if (fdt == TSP_F32 && wdt == TSP_F16) return thin_out<TSP_F32, TSP_F16>(odt, co, feats, n, ci, nbr, weight, bias, out, s, pad);

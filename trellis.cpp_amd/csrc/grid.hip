@@ -156,13 +156,14 @@ __global__ __launch_bounds__(GB_NT) void k_grid_scan(const GridHdr* __restrict__
 }
 
 // Every workgroup sums the GRID_PARTS partials for its own prefix and the block count, and
-// decides whether the blocks fit (the same answer in each; workgroup 0 records it). Then: block
+// decides whether the blocks fit the region and the caller's block_cap (the same answer in each;
+// workgroup 0 records it). Then: block
 // numbers into the directory (Morton order; cell_of, when given, gets each block's directory
 // index) and the blocks cleared; or, when the grid does not fit and a hash is given, the hash's
 // buckets cleared.
 __global__ __launch_bounds__(GB_NT) void k_grid_apply(GridHdr* __restrict__ hdr, int32_t* __restrict__ dir,
                                                       const int32_t* __restrict__ parts, HashView hash,
-                                                      int32_t* __restrict__ cell_of) {
+                                                      int32_t* __restrict__ cell_of, int64_t block_cap) {
     constexpr int PPT = GRID_PARTS / GB_NT;
     __shared__ int sW[2][GB_NT / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(GB_NT) void k_grid_apply(GridHdr* __restrict__ hdr,
         for (int w = 0; w < GB_NT / 64; ++w) { tot += sW[0][w]; run += sW[1][w]; }
         __syncthreads();   // sW is reused by the numbering below
         nblocks = tot;
-        cells = nblocks * GRID_BLOCK_WORDS < ((int64_t)1 << 31) &&
+        cells = nblocks <= block_cap && nblocks * GRID_BLOCK_WORDS < ((int64_t)1 << 31) &&
                 hdr->blocks_off + nblocks * GRID_BLOCK_WORDS <= hdr->region_words;
         if (blockIdx.x == 0 && tid == 0) {
             hdr->nblocks = (int32_t)nblocks;
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(GB_NT) void k_grid_fix(const int32_t* __restrict__ 
 }  // namespace
 
 int grid_build(const int32_t* coords, int64_t n, void* region, size_t region_bytes, void* tail,
-               int32_t* status, HashView hash, int32_t* cell_of, hipStream_t s) {
+               int32_t* status, HashView hash, int32_t* cell_of, int64_t block_cap, hipStream_t s) {
     const GridTail gt = carve_grid_tail(tail);
     int32_t* dir = static_cast<int32_t*>(region);
     const unsigned nvb = (unsigned)std::max<int64_t>(1, ceil_div(n, GB_NT));
@@ -300,7 +301,8 @@ int grid_build(const int32_t* coords, int64_t n, void* region, size_t region_byt
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_grid_scan, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir, gt.parts);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_apply, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir, gt.parts, hash, cell_of);
+    hipLaunchKernelGGL(k_grid_apply, dim3(GRID_PARTS), dim3(GB_NT), 0, s, gt.hdr, dir, gt.parts, hash, cell_of,
+                       block_cap);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_grid_insert, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir, hash);
     TSP_CHECK_LAUNCH();

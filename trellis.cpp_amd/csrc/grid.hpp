@@ -170,7 +170,9 @@ struct HashView {
 // buckets are `region`), the hash. Coordinates outside [0, kCoordMax] are left out and set bit 0
 // of *status when status is given. Returns a tsp_status of the launches.
 // cell_of (optional, one int per block): each block's directory index (its cell's Morton code).
+// block_cap: the most blocks the caller's per-block arrays (cell_of and the like) hold; a grid
+// with more blocks is not built (the mode says fallback), as when the region is too small.
 int grid_build(const int32_t* coords, int64_t n, void* region, size_t region_bytes, void* tail,
-               int32_t* status, HashView hash, int32_t* cell_of, hipStream_t s);
+               int32_t* status, HashView hash, int32_t* cell_of, int64_t block_cap, hipStream_t s);
 
 }  // namespace tsp

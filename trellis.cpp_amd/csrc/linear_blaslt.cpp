@@ -69,13 +69,22 @@ bool blaslt_eligible(int x_dtype, int weight_dtype, int out_dtype, int ci, int c
 static int blaslt_linear_rows(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
                               int co, int act, const float* residual, void* out, int odt, hipStream_t s);
 
-// Row chunks of at most 2^31 - 1 bytes in every operand (x, out, residual): one library call
-// never addresses more than that (the composite blocks already bound their hidden layers so).
-int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
-                  int co, int act, const float* residual, void* out, int odt, hipStream_t s) {
+// Rows of one library call: no operand (x, out, residual) of a call spans 2^31 bytes or more (a
+// multiple of 256 rows where one fits; 0 when not even one row does).
+int64_t blaslt_rows_per_call(int ci, int co, int xdt, int odt, bool residual) {
+    if (ci <= 0 || co <= 0 || !dtype_valid(xdt) || !dtype_valid(odt)) return 0;
     const int64_t row_bytes = std::max<int64_t>({(int64_t)ci * (int64_t)dtype_size(xdt), (int64_t)co * (int64_t)dtype_size(odt),
                                                  residual ? (int64_t)co * 4 : 0});
-    const int64_t rows = std::max<int64_t>(256, (((int64_t)1 << 31) - 1) / row_bytes / 256 * 256);
+    const int64_t rows = ((((int64_t)1) << 31) - 1) / row_bytes;
+    return rows >= 256 ? rows / 256 * 256 : rows;
+}
+
+// Row chunks of blaslt_rows_per_call rows: one library call never addresses 2^31 bytes or more
+// in an operand (the composite blocks already bound their hidden layers to 1 GiB).
+int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
+                  int co, int act, const float* residual, void* out, int odt, hipStream_t s) {
+    const int64_t rows = blaslt_rows_per_call(ci, co, xdt, odt, residual != nullptr);
+    TSP_REQUIRE(rows > 0, TSP_ERR_UNSUPPORTED, "linear: a row of ci=%d co=%d spans 2 GiB", ci, co);
     for (int64_t r0 = 0; r0 < n; r0 += rows) {
         const int64_t nr = std::min(rows, n - r0);
         const int st = blaslt_linear_rows(static_cast<const char*>(x) + r0 * ci * (int64_t)dtype_size(xdt), xdt, nr,
@@ -156,6 +165,10 @@ static int blaslt_linear_rows(const void* x, int xdt, int64_t n, int ci, const v
 }  // namespace tsp
 
 using namespace tsp;
+
+extern "C" int64_t tsp_linear_rows_per_call(int ci, int co, int x_dtype, int out_dtype, int has_residual) {
+    return blaslt_rows_per_call(ci, co, x_dtype, out_dtype, has_residual != 0);
+}
 
 extern "C" int tsp_linear_ex(const void* d_x, int x_dtype, int64_t n, int ci, const void* d_weight,
                              int weight_dtype, const float* d_bias, int co, int act,

@@ -68,7 +68,7 @@ template <bool BF16>
 __global__ __launch_bounds__(MLP_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_mlp_ws(const uint16_t* __restrict__ xn, int64_t n, const uint16_t* __restrict__ pw0,
               const float* __restrict__ b0, const uint16_t* __restrict__ pw2, const float* __restrict__ b2,
-              const float* __restrict__ x, float* __restrict__ y) {
+              const float* x, float* y) {   // (y may be x: not restrict)
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][32 * MLP_XS];   // staged rows, two blocks
     __shared__ f32x4_t sY[MLP_W * 4 * 4 * 64];                              // [wave][col block][j][lane]
     __shared__ __attribute__((aligned(16))) float sB0[MLP_H];

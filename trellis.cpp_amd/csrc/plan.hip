@@ -14,6 +14,7 @@
 // skipped absent tap would only have added exact zeros).
 #include <algorithm>
 
+#include "brick_hash.hpp"
 #include "grid.hpp"
 #include "tile_plan.hpp"
 
@@ -181,16 +182,29 @@ struct PlanScratch {
     void* region;
     size_t region_bytes;
 };
-// the grid may use 32 bytes per voxel + 16 MiB (surface-like sets need ~25-30 bytes per voxel);
-// presence bitmaps take 64 bytes per block of 2.5 KiB
+// the grid may use 32 bytes per voxel + 16 MiB (surface-like sets need ~25-30 bytes per voxel)
 size_t grid_region_bytes(int64_t n) { return align256((size_t)n * 32 + ((size_t)16 << 20)); }
+}  // namespace
+
+// Blocks the per-block scratch (counts, cell_of: 4 bytes each; presence bitmaps: 64 bytes each)
+// holds: every block that fits the larger of the plan's own grid region and the neighbour
+// table's workspace (whose grid the planned table build shares), and at least one entry per tile
+// (counts is reused as the list of table tiles). A grid with more blocks is not built
+// (grid_build's block_cap), so no block index runs past these arrays.
+int64_t plan_block_cap(int64_t n) {
+    const size_t region = std::max(grid_region_bytes(n), (size_t)table_capacity(n) * kBucketWords * 4);
+    return std::max<int64_t>(std::max<int64_t>(ceil_div(n, HB_M), 1),
+                             (int64_t)(region / (4 * GRID_BLOCK_WORDS)) + 1);
+}
+
+namespace {
 size_t plan_scratch_bytes(int64_t n) {
-    const size_t n1 = (size_t)std::max<int64_t>(n, 1);
-    return align256(n1 * 4) + align256(n1 * 8) + 2 * align256(n1 * 4) + align256(grid_region_bytes(n) / 32) +
+    const size_t n1 = (size_t)std::max<int64_t>(n, 1), cap = (size_t)plan_block_cap(n);
+    return align256(n1 * 4) + align256(n1 * 8) + 2 * align256(cap * 4) + align256(cap * 64) +
            GRID_TAIL + grid_region_bytes(n);
 }
 PlanScratch carve_scratch(void* p, int64_t n) {
-    const size_t n1 = (size_t)std::max<int64_t>(n, 1);
+    const size_t n1 = (size_t)std::max<int64_t>(n, 1), cap = (size_t)plan_block_cap(n);
     char* c = static_cast<char*>(p);
     PlanScratch s;
     s.order = reinterpret_cast<int32_t*>(c);
@@ -198,11 +212,11 @@ PlanScratch carve_scratch(void* p, int64_t n) {
     s.wc = reinterpret_cast<uint64_t*>(c);
     c += align256(n1 * 8);
     s.counts = reinterpret_cast<int32_t*>(c);
-    c += align256(n1 * 4);
+    c += align256(cap * 4);
     s.cell_of = reinterpret_cast<int32_t*>(c);
-    c += align256(n1 * 4);
+    c += align256(cap * 4);
     s.pres = reinterpret_cast<uint8_t*>(c);
-    c += align256(grid_region_bytes(n) / 32);
+    c += align256(cap * 64);
     s.tail = c;
     c += GRID_TAIL;
     s.region = c;
@@ -670,7 +684,7 @@ int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* 
     if (coords) {
         const PlanScratch ps = carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
         const int st = grid_build(coords, n, ps.region, ps.region_bytes, ps.tail, nullptr, HashView{nullptr, 0},
-                                  ps.cell_of, s);
+                                  ps.cell_of, plan_block_cap(n), s);
         if (st != TSP_OK) return st;
         return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(ps.region), ps.tail, s);
     }

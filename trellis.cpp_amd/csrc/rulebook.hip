@@ -116,7 +116,8 @@ static int rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d_nbr, vo
     void* tail = static_cast<char*>(d_workspace) + region;
     const GridHdr* hdr = carve_grid_tail(tail).hdr;
     const int st = grid_build(d_coords, n, d_workspace, region, tail, d_status, h,
-                              d_plan ? plan_cell_of(d_plan, n) : nullptr, s);
+                              d_plan ? plan_cell_of(d_plan, n) : nullptr,
+                              d_plan ? plan_block_cap(n) : INT64_MAX, s);
     if (st != TSP_OK) return st;
     hipLaunchKernelGGL(k_table_probe, dim3((unsigned)ceil_div(n, kProbeThreads)), dim3(kProbeThreads), 0, s,
                        d_coords, n, static_cast<const int32_t*>(d_workspace), hdr, h, d_nbr);

@@ -44,14 +44,36 @@ const float* f32_param(const ggml_tensor* t, Carve& sc, hipStream_t s) {
     return static_cast<const float*>(p);
 }
 
-// ---- packed conv weights -----------------------------------------------------------------------
+// ---- packed weights ------------------------------------------------------------------------------
 // The weights of a loaded Model (registered by Model::load, dropped by Model::free) are packed
-// for the matrix-core kernel on first use and kept: decodes after the first pack nothing. Other
+// on first use and kept: a conv weight for the matrix-core kernel, a ConvNeXt block's mlp.0 and
+// mlp.2 (keyed by mlp.0) for the one-kernel MLP. Decodes after the first pack nothing. Other
 // weight tensors (a caller's own buffers, which may be freed and their memory reused) are not
 // cached. In a sizing pass (where only null or not matters to the workspace sizes) a stand-in.
+// A pack runs on the first caller's stream, which is synchronised before the copy is published,
+// so that a caller on another stream never reads it unfinished.
 namespace {
 std::mutex g_packed_mu;
-std::unordered_map<const void*, void*> g_packed;   // a model tensor's data -> its packed copy or null
+std::unordered_map<const void*, void*> g_packed;       // a model tensor's data -> its packed copy or null
+std::unordered_map<const void*, void*> g_packed_mlp;   // a block's mlp.0 data -> its packed MLP
+
+// The cached copy of `key` in `cache` (a registered model tensor), packed by pack(p, s) into
+// `bytes` on first use; null when key is no model tensor. Called with g_packed_mu held.
+template <class Pack>
+const void* cached_pack(std::unordered_map<const void*, void*>& cache, const void* key, size_t bytes,
+                        bool running, hipStream_t s, Pack pack) {
+    if (g_packed.find(key) == g_packed.end()) return nullptr;
+    if (!running) return reinterpret_cast<const void*>(uintptr_t(256));
+    void*& slot = cache[key];
+    if (!slot) {
+        void* p = nullptr;
+        hip_check(hipMalloc(&p, bytes), "packed weights");
+        pack(p, s);
+        hip_check(hipStreamSynchronize(s), "weight pack");
+        slot = p;
+    }
+    return slot;
+}
 }  // namespace
 
 void register_model_weights(const std::vector<const void*>& data) {
@@ -62,26 +84,34 @@ void register_model_weights(const std::vector<const void*>& data) {
 void forget_model_weights(const std::vector<const void*>& data) {
     std::lock_guard<std::mutex> lock(g_packed_mu);
     for (const void* d : data) {
-        auto it = g_packed.find(d);
-        if (it == g_packed.end()) continue;
-        if (it->second) (void)hipFree(it->second);
-        g_packed.erase(it);
+        for (auto* cache : {&g_packed, &g_packed_mlp}) {
+            auto it = cache->find(d);
+            if (it == cache->end()) continue;
+            if (it->second) (void)hipFree(it->second);
+            cache->erase(it);
+        }
     }
 }
 
 const void* packed_weights(const Conv& c, bool running, hipStream_t s) {
     if (!c.mfma) return nullptr;
     std::lock_guard<std::mutex> lock(g_packed_mu);
-    auto it = g_packed.find(c.w->data);
-    if (it == g_packed.end()) return nullptr;
-    if (!running) return reinterpret_cast<const void*>(uintptr_t(256));
-    if (!it->second) {
-        void* p = nullptr;
-        hip_check(hipMalloc(&p, tsp_conv_weight_packed_bytes(c.ci, c.co)), "packed conv weights");
-        lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, p, s), "weight pack");
-        it->second = p;
-    }
-    return it->second;
+    return cached_pack(g_packed, c.w->data, tsp_conv_weight_packed_bytes(c.ci, c.co), running, s,
+                       [&](void* p, hipStream_t st) {
+                           lib(tsp_conv_weight_pack(c.w->data, c.wdt, c.ci, c.co, p, st), "weight pack");
+                       });
+}
+
+const void* packed_mlp(const ConvNext& a, bool running, hipStream_t s) {
+    const int dt = tgr::tsp_dtype_of(a.w0->type);
+    // the shapes and types of the one-kernel MLP (tsp_convnext_mlp_pack)
+    if (a.c != 128 || (dt != TSP_F16 && dt != TSP_BF16) || tgr::tsp_dtype_of(a.w2->type) != dt) return nullptr;
+    std::lock_guard<std::mutex> lock(g_packed_mu);
+    if (g_packed.find(a.w2->data) == g_packed.end()) return nullptr;
+    return cached_pack(g_packed_mlp, a.w0->data, tsp_convnext_mlp_packed_bytes(a.c), running, s,
+                       [&](void* p, hipStream_t st) {
+                           lib(tsp_convnext_mlp_pack(a.w0->data, a.w2->data, dt, a.c, p, st), "MLP pack");
+                       });
 }
 
 int act_dtype(int wdt, bool conv_weight) {
@@ -179,6 +209,7 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
     w.mlp2_weight = a.w2->data;
     w.mlp2_dtype = tgr::tsp_dtype_of(a.w2->type);
     w.mlp2_bias = f32_param(a.b2, sc, s);
+    w.mlp_packed = packed_mlp(a, sc.running(), s);
     const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
     // a plan comes with every matrix-core conv (the callers build it where conv.mfma)
     const size_t nb = tsp_convnext_workspace_bytes(a.n, a.c, xdt, &w, a.conv.mfma, flags);
