@@ -258,7 +258,7 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather", "thin"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the ~640K-voxel variant of the C=128 set")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other conv configurations")
     ap.add_argument("--plan-order", default="morton", choices=["morton", "rows"],
                     help="conv plan tiles: Morton order of 8^3 cells, or consecutive rows")
     ap.add_argument("--prepare-only", default="", metavar="DIR",
@@ -340,15 +340,23 @@ def main():
         extra["f32_out"] = {"ms_per_step": rf["ms"], "tflops": flops / (rf["ms"] * 1e-3) / 1e12,
                             "frac": flops / (rf["ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[w.dtype]}
     if w.name == "shells256-c128-bf16" and not args.no_extra:
-        w6 = shells.workload("shells600k-c128-bf16")
-        r6 = time_conv(pkg, w6, args, max(5, args.steps // 2), 2)
-        f6 = 2.0 * w6.ci * w6.co * r6["pairs"]
-        extra["shells600k-c128-bf16"] = {
-            "n_voxels": w6.n, "active_pairs": r6["pairs"], "ms_per_step": r6["ms"],
-            "voxels_per_s": w6.n / (r6["ms"] * 1e-3), "tflops": f6 / (r6["ms"] * 1e-3) / 1e12,
-            "frac": f6 / (r6["ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[w6.dtype],
-            "rulebook_ms": r6["rulebook_ms"], "plan_ms": r6["plan_ms"], "table_plan_ms": r6["table_plan_ms"]}
-        del r6
+        # every other conv configuration, timed the same way: the same shells at ~640K voxels
+        # (the size the target names), 128^3 ellipsoids at C = 256, the 512^3 band at C = 64, the
+        # fp32 64^3 shell (the CPU-reference configuration) and a thin C = 8 layer
+        for name in EXTRA_WORKLOADS:
+            we = shells.workload(name)
+            re_ = time_conv(pkg, we, args, max(5, args.steps // 2), 2)
+            fe = 2.0 * we.ci * we.co * re_["pairs"]
+            mfma_e = we.dtype in ("bf16", "f16") and we.co % 64 == 0 and we.ci % 16 == 0
+            roof_e = roofline(we, fe, compulsory_bytes(we), re_["ms"], valu=not mfma_e)
+            extra[name] = {
+                "n_voxels": we.n, "active_pairs": re_["pairs"], "c_in": we.ci, "c_out": we.co,
+                "dtype": we.dtype, "algo": "mfma-planned" if re_["planned"] else "auto",
+                "ms_per_step": re_["ms"], "voxels_per_s": we.n / (re_["ms"] * 1e-3),
+                "tflops": fe / (re_["ms"] * 1e-3) / 1e12, "frac": roof_e["frac"], "roofline": roof_e,
+                "rulebook_ms": re_["rulebook_ms"], "plan_ms": re_["plan_ms"],
+                "table_plan_ms": re_["table_plan_ms"]}
+            del re_
 
     cpu = None
     if not args.no_cpu:
@@ -471,6 +479,10 @@ def kernel_sources_sha() -> str:
         with open(os.path.join(ROOT, "trellis.cpp_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()
+
+
+EXTRA_WORKLOADS = ("shells600k-c128-bf16", "ellipsoids128-c256-bf16", "band512-c64-bf16", "shell64-c64-f32",
+                   "shells256-c8-bf16")
 
 
 def compulsory_bytes(w) -> float:

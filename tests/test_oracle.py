@@ -458,3 +458,51 @@ def test_rounding_noise_floor_helper(orc, shells):
     assert 0 < floor < 1e-2
     _, none = rounding_noise_floor(orc, lambda: orc.convnext_block(x, nbr, p, "blk"), rel=1e-4)
     assert none == 0
+
+
+@pytest.mark.parametrize("wtype", ["bf16", "f16"])
+def test_block_bar_catches_planted_mistakes(orc, shells, wtype):
+    """The block tests' bar, max(2e-4, 1.5 x the rounding noise floor), on the ConvNeXt block at
+    C = 128 (the composite test's case): the floor itself stays below the bar, while plausible
+    mistakes in the rounding of the product inputs -- none at all, the other 16-bit type,
+    truncation instead of round-to-nearest-even, or a systematic relative error of 3e-4 in every
+    product input -- move the block by more than the bar."""
+    from host_cases import rounding_noise_floor
+    c = 128
+    rng = np.random.default_rng(c + len(wtype))
+    coords = np.ascontiguousarray(shells.sphere_shell(20, 10.0, 6.0, 7.5), np.int32)
+    x = rng.standard_normal((len(coords), c)).astype(np.float32)
+    shapes = {"conv.weight": ((c, 27, c), 1 / np.sqrt(27 * c), 0), "conv.bias": ((c,), 0.1, 0),
+              "norm.weight": ((c,), 0.1, 1), "norm.bias": ((c,), 0.1, 0),
+              "mlp.0.weight": ((4 * c, c), 1 / np.sqrt(c), 0), "mlp.0.bias": ((4 * c,), 0.1, 0),
+              "mlp.2.weight": ((c, 4 * c), 1 / np.sqrt(4 * c), 0), "mlp.2.bias": ((c,), 0.1, 0)}
+    q, wt = {}, {}
+    for k, (shape, scale, off) in shapes.items():
+        v = (rng.standard_normal(shape) * scale + off).astype(np.float32)
+        q["blk." + k] = shells.round_to(v, wtype) if len(shape) >= 2 else v
+        wt["blk." + k] = wtype if len(shape) >= 2 else "f32"
+    tab = orc.neighbor_table(coords)
+    ref, floor = rounding_noise_floor(orc, lambda: orc.convnext_block(x, tab, q, "blk", wt), runs=3)
+    bar = max(2e-4, 1.5 * floor)
+    assert 0 < floor < bar
+    exact = orc.act_round
+    other = "f16" if wtype == "bf16" else "bf16"
+    keep = 16 if wtype == "bf16" else 13   # mantissa bits dropped by truncation to the 16-bit type
+
+    def truncate(v, wtype_, conv_weight=False, cast_f32=False):
+        u = np.asarray(v, np.float32).view(np.uint32) & np.uint32((0xffffffff >> keep) << keep)
+        return exact(u.view(np.float32), wtype_, conv_weight, cast_f32)
+
+    planted = {
+        "no rounding": lambda v, w_, cw=False, cf=False: np.asarray(v, np.float64),
+        "other type": lambda v, w_, cw=False, cf=False: exact(v, other if w_ == wtype else w_, cw, cf),
+        "truncation": truncate,
+        "relative 3e-4": lambda v, w_, cw=False, cf=False: exact(np.asarray(v, np.float64) * (1 + 3e-4), w_, cw, cf),
+    }
+    for name, fn in planted.items():
+        orc.act_round = fn
+        try:
+            moved = orc.rel_err(orc.convnext_block(x, tab, q, "blk", wt), ref)
+        finally:
+            orc.act_round = exact
+        assert moved > bar, (name, moved, bar)
