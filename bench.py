@@ -255,7 +255,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="shells256-c128-bf16")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather", "thin"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather", "thin", "thin_mfma"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other conv configurations")
@@ -306,10 +306,8 @@ def main():
     flops = 2.0 * w.ci * w.co * pairs
     flops_dense = 2.0 * w.ci * w.co * 27 * w.n
     compulsory = compulsory_bytes(w)
-    # the matrix-core kernels take 16-bit features with Ci % 16 (planned) / 32 and Co % 64 == 0;
-    # everything else runs on a VALU kernel (the thin one for Co <= 32)
-    mfma_shape = w.dtype in ("bf16", "f16") and w.co % 64 == 0 and w.ci % 16 == 0
-    roof = roofline(w, flops, compulsory, ms, valu=not mfma_shape)
+    path = conv_path(w, args.algo, planned)
+    roof = roofline(w, flops, compulsory, ms, valu=path in ("thin", "narrow"))
     # HBM bytes per launch of the conv kernel, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
     # passes scaled by a copy kernel of known size (profiles/traffic_<workload>.md); used only
     # while the kernel's sources are the ones that profile measured
@@ -347,11 +345,11 @@ def main():
             we = shells.workload(name)
             re_ = time_conv(pkg, we, args, max(5, args.steps // 2), 2)
             fe = 2.0 * we.ci * we.co * re_["pairs"]
-            mfma_e = we.dtype in ("bf16", "f16") and we.co % 64 == 0 and we.ci % 16 == 0
-            roof_e = roofline(we, fe, compulsory_bytes(we), re_["ms"], valu=not mfma_e)
+            path_e = conv_path(we, args.algo, re_["planned"])
+            roof_e = roofline(we, fe, compulsory_bytes(we), re_["ms"], valu=path_e in ("thin", "narrow"))
             extra[name] = {
                 "n_voxels": we.n, "active_pairs": re_["pairs"], "c_in": we.ci, "c_out": we.co,
-                "dtype": we.dtype, "algo": "mfma-planned" if re_["planned"] else "auto",
+                "dtype": we.dtype, "algo": path_e,
                 "ms_per_step": re_["ms"], "voxels_per_s": we.n / (re_["ms"] * 1e-3),
                 "tflops": fe / (re_["ms"] * 1e-3) / 1e12, "frac": roof_e["frac"], "roofline": roof_e,
                 "rulebook_ms": re_["rulebook_ms"], "plan_ms": re_["plan_ms"],
@@ -379,9 +377,7 @@ def main():
             "workload": w.name, "grid": w.grid, "n_voxels": w.n, "active_pairs": pairs,
             "pairs_per_voxel": pairs / max(w.n, 1), "c_in": w.ci, "c_out": w.co,
             "accumulate": "f32", "out_dtype": w.dtype,
-            "algo": "mfma-planned" if planned else (
-                "thin" if args.algo in ("auto", "thin") and w.co in (4, 8, 16, 32) and w.ci % 4 == 0
-                and w.ci * w.co <= 512 else args.algo),
+            "algo": path,
             "plan_order": args.plan_order if planned else None,
             "parallelism": "single-gpu",
         },
@@ -479,6 +475,22 @@ def kernel_sources_sha() -> str:
         with open(os.path.join(ROOT, "trellis.cpp_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()
+
+
+def conv_path(w, algo: str, planned: bool) -> str:
+    """The kernel the library runs for workload w under `algo` (tsp_subm_conv3x3's AUTO order:
+    matrix-core for 16-bit Ci % 32 / Co % 64 shapes -- here with a plan --, then the thin
+    matrix-core kernel, the thin VALU kernel, the tiled VALU kernel)."""
+    if planned:
+        return "mfma-planned"
+    if algo != "auto":
+        return algo
+    thin = w.co in (4, 8, 16, 32) and w.ci * w.co <= 512
+    if thin and w.dtype in ("bf16", "f16") and w.ci in (8, 16, 32):
+        return "thin_mfma"
+    if thin and w.ci % 4 == 0:
+        return "thin"
+    return "narrow"
 
 
 EXTRA_WORKLOADS = ("shells600k-c128-bf16", "ellipsoids128-c256-bf16", "band512-c64-bf16", "shell64-c64-f32",

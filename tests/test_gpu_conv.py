@@ -878,8 +878,9 @@ def test_nonfinite_weight_runs_every_tap(gpu_lib, shells, bad):
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16", "f32xf16"])
 def test_thin_vs_oracle(gpu_lib, orc, shells, ci, co, dt):
     """The thin-channel VALU kernel (one voxel's output row per thread) at every width it takes,
-    for f32, bf16, f16 and f32 features with f16 weights; chosen by AUTO for these shapes and
-    by algo="thin" explicitly (the same results)."""
+    for f32, bf16, f16 and f32 features with f16 weights, by algo="thin"; AUTO's choice for the
+    same shapes (the thin matrix-core kernel for 16-bit Ci in {8, 16, 32}, else this one) within
+    the same bar."""
     _case(f"thin ci={ci} co={co} {dt}")
     import torch
     rng = np.random.default_rng(ci * 7 + co)
@@ -893,18 +894,83 @@ def test_thin_vs_oracle(gpu_lib, orc, shells, ci, co, dt):
     tol = TOL_32 if fkey == "f32" and wkey == "f32" else (TOL_32 if fkey == "f32" else TOL_16)
     assert orc.rel_err(out, ref) < tol
     out2, _ = _run(gpu_lib, coords, feats, weight, bias, tdt[fkey], wdtype=tdt[wkey], algo="thin")
-    assert np.array_equal(out, out2)
+    assert orc.rel_err(out2, ref) < tol
+    if not (fkey == wkey and fkey != "f32" and ci in (8, 16, 32)):
+        assert np.array_equal(out, out2)   # AUTO took the VALU kernel
     if fkey != "f32":   # 16-bit output: one rounding more
         o16, _ = _run(gpu_lib, coords, feats, weight, bias, tdt[fkey], out_dtype=tdt[fkey], algo="thin")
         assert orc.rel_err(o16, ref) < TOL_16_OUT
 
 
+THIN_MFMA_SHAPES = [(8, 4), (8, 8), (8, 16), (8, 32), (16, 8), (16, 16), (16, 32), (32, 4), (32, 8), (32, 16)]
+
+
+@pytest.mark.parametrize("ci,co", THIN_MFMA_SHAPES)
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_thin_mfma_vs_oracle(gpu_lib, orc, shells, ci, co, dt):
+    """The thin matrix-core kernel (the 27 taps folded into K = 27 Ci of 16 x 16 x 32 steps, each
+    lane gathering its neighbour row piece straight into the operand) at every shape it takes, on
+    a ragged voxel count (not a multiple of its 16- or 32-voxel chunks), f32 and 16-bit output,
+    against the fp64 oracle; AUTO picks it for these shapes (the same bits)."""
+    _case(f"thin mfma ci={ci} co={co} {dt}")
+    import torch
+    rng = np.random.default_rng(ci * 11 + co)
+    coords, feats, weight, bias = _rand_case(shells, rng, 2999, ci, co, dt)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    out, _ = _run(gpu_lib, coords, feats, weight, bias, tdt, algo="thin_mfma")
+    assert orc.rel_err(out, ref) < TOL_16
+    auto, _ = _run(gpu_lib, coords, feats, weight, bias, tdt)
+    assert np.array_equal(out, auto)
+    o16, _ = _run(gpu_lib, coords, feats, weight, bias, tdt, out_dtype=tdt, algo="thin_mfma")
+    assert orc.rel_err(o16, ref) < TOL_16_OUT
+    # the 16-bit output is the f32 output rounded once
+    assert np.array_equal(o16, torch.from_numpy(out).to(tdt).float().numpy())
+
+
+def test_thin_mfma_full_size_shells256_c8(gpu_lib, orc, shells):
+    """The thin workload at full size (1,694,162 voxels, Ci = Co = 8, bf16): the thin matrix-core
+    kernel on every row against the thin VALU kernel, a deterministic row sample against the fp64
+    oracle, bitwise reproducibility, and the bf16 output equal to the f32 output rounded once."""
+    _case("thin mfma full size shells256-c8-bf16")
+    import torch
+    w = shells.workload("shells256-c8-bf16")
+    nbr = gpu_lib.rulebook_build(torch.from_numpy(w.coords).cuda())
+    f, wt, b = _dev(w.feats, torch.bfloat16), _dev(w.weight, torch.bfloat16), _dev(w.bias, torch.float32)
+    out = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="thin_mfma")
+    out2 = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="thin_mfma")
+    o16 = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.bfloat16, algo="thin_mfma")
+    outv = gpu_lib.subm_conv3x3(f, nbr, wt, b, out_dtype=torch.float32, algo="thin")
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    assert torch.equal(o16, out.to(torch.bfloat16))
+    got = out.cpu().numpy()
+    assert orc.rel_err(got, outv.cpu().numpy()) < TOL_16
+    rng = np.random.default_rng(8)
+    rows = np.unique(np.concatenate([np.arange(64), np.arange(w.n - 64, w.n), rng.integers(0, w.n, 4000)]))
+    ref = orc.subm_conv_f64_rows(w.feats, nbr.cpu().numpy(), w.weight, w.bias, rows)
+    assert orc.rel_err(got[rows], ref) < TOL_16
+
+
+def test_thin_mfma_rejects(gpu_lib, shells):
+    """algo="thin_mfma" outside its shapes: f32 features, Ci = 4 or 64, Co = 64, mixed dtypes."""
+    import torch
+    rng = np.random.default_rng(3)
+    for ci, co, fdt, wdt in ((8, 8, torch.float32, torch.float32), (4, 8, torch.bfloat16, torch.bfloat16),
+                             (64, 8, torch.bfloat16, torch.bfloat16), (8, 64, torch.bfloat16, torch.bfloat16),
+                             (8, 8, torch.float16, torch.bfloat16)):
+        coords, feats, weight, bias = _rand_case(shells, rng, 100, ci, co, "f32")
+        with pytest.raises(gpu_lib.TspError, match="UNSUPPORTED"):
+            _run(gpu_lib, coords, feats, weight, bias, fdt, wdtype=wdt, algo="thin_mfma")
+
+
+@pytest.mark.parametrize("algo", ["thin", "thin_mfma"])
 @pytest.mark.parametrize("mode", ["nan_row0", "zero_pad", "row0_source"])
-def test_thin_padding_row(gpu_lib, orc, shells, mode):
+def test_thin_padding_row(gpu_lib, orc, shells, mode, algo):
     """The thin kernel's padding row: a NaN in row 0 makes every row with an absent tap NaN;
     TSP_CONV_ZERO_PAD reads an exact zero row (only row 0's neighbours turn non-finite); an f32
     source row that is finite gives a zero padding row although its f16 rounding overflows."""
-    _case(f"thin padding {mode}")
+    _case(f"thin padding {mode} {algo}")
     import torch
     rng = np.random.default_rng(41)
     coords = np.ascontiguousarray(np.concatenate([shells.sphere_shell(24, 12.0, 7.0, 9.0),
@@ -923,7 +989,7 @@ def test_thin_padding_row(gpu_lib, orc, shells, mode):
     if mode == "nan_row0":
         feats[0, 3] = np.nan
         f16 = shells.round_to(feats, "f16")
-        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo="thin")
+        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo=algo)
         out = out.cpu().numpy()
         assert np.isnan(out[absent]).all()
         keep = ~absent & ~refs0
@@ -931,14 +997,14 @@ def test_thin_padding_row(gpu_lib, orc, shells, mode):
     elif mode == "zero_pad":
         feats[0, 3] = np.inf
         f16 = shells.round_to(feats, "f16")
-        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo="thin",
+        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo=algo,
                                    zero_pad=True).cpu().numpy()
         assert np.isfinite(out[~refs0]).all()
         _nan_aware(out, orc.subm_conv_f64(f16, nbr, weight, bias, zero_pad=True), TOL_16)
     else:
         feats[0, 3] = 1.0e5                         # finite, > 65504: rounds to Inf
         f16 = shells.round_to(feats, "f16")
-        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo="thin",
+        out = gpu_lib.subm_conv3x3(_dev(f16, torch.float16), nbr_d, w, b, out_dtype=torch.float32, algo=algo,
                                    row0=_dev(feats[0], torch.float32)).cpu().numpy()
         assert np.isfinite(out[~refs0]).all()
         _nan_aware(out, orc.subm_conv_f64(f16, nbr, weight, bias, row0=feats[0]), TOL_16)

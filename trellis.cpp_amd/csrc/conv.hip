@@ -448,7 +448,7 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
     TSP_CONV_COMMON_CHECKS("tsp_subm_conv3x3");
     TSP_REQUIRE(dtype_valid(feat_dtype) && dtype_valid(weight_dtype) && dtype_valid(out_dtype),
                 TSP_ERR_INVALID, "tsp_subm_conv3x3: bad dtype");
-    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_THIN, TSP_ERR_INVALID,
+    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_THIN_MFMA, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3: bad algo %d", algo);
     TSP_REQUIRE((flags & ~TSP_CONV_ZERO_PAD) == 0, TSP_ERR_INVALID, "tsp_subm_conv3x3: bad flags %d",
                 flags);
@@ -477,6 +477,17 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
     if (algo == TSP_ALGO_MFMA || (algo == TSP_ALGO_AUTO && eligible))
         return halo_conv_launch(feat_dtype, out_dtype, d_feats, n, ci, d_nbr, nullptr, d_weight,
                                 d_bias, co, d_out, s, OctantScatter{}, SkipAdd{}, pad);
+    if (algo == TSP_ALGO_THIN_MFMA || algo == TSP_ALGO_AUTO) {
+        const int st = thin_mfma_launch(feat_dtype, weight_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight,
+                                        d_bias, co, d_out, s, pad);
+        if (st != TSP_ERR_UNSUPPORTED || algo == TSP_ALGO_THIN_MFMA) {
+            TSP_REQUIRE(st != TSP_ERR_UNSUPPORTED, TSP_ERR_UNSUPPORTED,
+                        "tsp_subm_conv3x3: the thin matrix-core kernel needs f16/bf16 feats and weights of "
+                        "one dtype, ci in {8, 16, 32}, co in {4, 8, 16, 32}, ci * co <= 512, out f32 or the "
+                        "feats' dtype and 16-byte aligned feats and weights (got ci=%d co=%d)", ci, co);
+            return st;
+        }
+    }
     if (algo == TSP_ALGO_THIN || algo == TSP_ALGO_AUTO) {
         const int st = thin_conv_launch(feat_dtype, weight_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight,
                                         d_bias, co, d_out, s, pad);

@@ -124,6 +124,14 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                      hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {},
                      RowNorm ln = {});
 
+// The thin-channel matrix-core conv (conv_thin_mfma.hip): f16/bf16 features and weights of one
+// dtype, Ci in {8, 16, 32}, Co in {4, 8, 16, 32}, Ci * Co <= 512, a neighbour table, 16-byte
+// aligned features and weights (output 8-byte, f32 output 16-byte). Returns TSP_ERR_UNSUPPORTED
+// (with no message) for anything else.
+bool thin_mfma_fits(int fdt, int wdt, int ci, int co);
+int thin_mfma_launch(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+                     const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad);
+
 // The thin-channel VALU conv (conv_thin.hip): Co in {4, 8, 16, 32}, Ci % 4 == 0, Ci * Co <= 512,
 // a neighbour table, 16-byte aligned features. Returns TSP_ERR_UNSUPPORTED (with no message) for
 // anything else.
