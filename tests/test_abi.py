@@ -91,7 +91,8 @@ def test_conv_validation(pkg):
     assert f(n=-1) == 1
     assert f(ci=0) == 1 and f(co=-4) == 1
     assert f(fdt=7) == 1 and f(odt=9) == 1
-    assert f(algo=5) == 1
+    assert f(algo=6) == 1
+    assert f(algo=5) == 4 and "thin matrix-core" in _err(pkg)     # THIN_MFMA: ci=64 is not its shape
     assert f(nbr=NULL) == 1
     assert f(out=FAKE) == 1 and "alias" in _err(pkg)
     assert f(n=0) == 0                                              # empty: no-op
