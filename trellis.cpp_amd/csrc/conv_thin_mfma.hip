@@ -108,9 +108,15 @@ __global__ __launch_bounds__(TM_THREADS) void k_conv_thin_mfma(
                                                                          (int)(n * CI * 2), 0x00020000);
     // first byte past each buffer's range: a load there reads zeros and touches no memory
     const uint32_t tab_end = (uint32_t)(kTaps * n * 4), feat_end = (uint32_t)(n * CI * 2);
+    // XCD-aware order: workgroup ids go round-robin over the 8 XCDs, so each XCD takes one
+    // contiguous range of chunks, walked by its waves together -- the rows they gather (neighbours
+    // of nearby voxels) stay in that XCD's L2
     const int64_t nchunks = (n + CH - 1) / CH;
-    for (int64_t chunk = (int64_t)blockIdx.x * TM_WAVES + wave; chunk < nchunks;
-         chunk += (int64_t)gridDim.x * TM_WAVES) {
+    const int64_t per_xcd = (nchunks + 7) / 8;
+    const int64_t xlo = (int64_t)(blockIdx.x % 8) * per_xcd;
+    const int64_t xhi = xlo + per_xcd < nchunks ? xlo + per_xcd : nchunks;
+    for (int64_t chunk = xlo + (int64_t)(blockIdx.x / 8) * TM_WAVES + wave; chunk < xhi;
+         chunk += (int64_t)(gridDim.x / 8) * TM_WAVES) {
         // table entries of every (block, step) first, then the rows they name: all loads of the
         // chunk in flight together. Both go through buffer resources with 32-bit offsets (the
         // launch checks that the table and the features span less than 2 GiB): an entry of a
@@ -207,8 +213,10 @@ int launch_tm(const void* feats, int64_t n, const int32_t* nbr, const void* weig
     // 16-voxel blocks per chunk: two at Ci = 8, where a block's operands take 28 registers
     constexpr int RB = CI == 8 ? 2 : 1;
     const int64_t nchunks = ceil_div(n, 16 * RB);
-    const int64_t blocks = std::min<int64_t>(ceil_div(nchunks, TM_WAVES), (int64_t)cu_count_tm() * 4);
-    hipLaunchKernelGGL((k_conv_thin_mfma<BF16, ODT, CI, NCB, RB>), dim3((unsigned)std::max<int64_t>(blocks, 1)),
+    // a multiple of 8 workgroups (one range per XCD), at most 4 a CU
+    const int64_t blocks = std::max<int64_t>(
+        8, std::min<int64_t>(ceil_div(nchunks, TM_WAVES * 8) * 8, (int64_t)cu_count_tm() * 4 / 8 * 8));
+    hipLaunchKernelGGL((k_conv_thin_mfma<BF16, ODT, CI, NCB, RB>), dim3((unsigned)blocks),
                        dim3(TM_THREADS), 0, s, static_cast<const uint16_t*>(feats), n, nbr,
                        static_cast<const uint16_t*>(weight), bias, co,
                        static_cast<typename Elem<ODT>::storage*>(out), pad);
