@@ -324,16 +324,22 @@ def convnext_block(feats, nbr, p: dict, prefix: str, wt=None, cast_f32: bool = F
 
 
 def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None, wt=None,
-              cast_f32: bool = False):
+              cast_f32: bool = False, logits_out=None):
     """SparseResBlockC2S3d (sparse.cpp:172-336). wt rounds each product's input as in
-    convnext_block. Returns (out float64 [M,Cout], child_coords [M,3], mask_used uint8 [8N])."""
+    convnext_block. Returns (out float64 [M,Cout], child_coords [M,3], mask_used uint8 [8N]).
+    logits_out (a list), when given, receives the to_subdiv logits [N, 8] of this block's input,
+    also where ext_mask decides the mask (for checking a predicted mask against them)."""
     rd = _rounder(wt, cast_f32)
     x = np.asarray(feats, np.float32)
     n, cin = x.shape
     c = _coords(coords)
-    if ext_mask is None:
+    logits = None
+    if ext_mask is None or logits_out is not None:
         logits = linear(rd(x, prefix + ".to_subdiv.weight"), p[prefix + ".to_subdiv.weight"],
                         p[prefix + ".to_subdiv.bias"])
+        if logits_out is not None:
+            logits_out.append(logits)
+    if ext_mask is None:
         mask = (logits > 0).astype(np.uint8).reshape(-1)        # sparse.cpp:215
     else:
         mask = (np.asarray(ext_mask).reshape(-1) != 0).astype(np.uint8)
@@ -356,13 +362,14 @@ def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None, wt=
 
 
 def decode_unet(latent, coords, p: dict, stages, out_ch: int, guide=None, wt=None,
-                cast_f32: bool = False):
+                cast_f32: bool = False, logits_out=None):
     """SparseUnetVaeDecoder (shape_decoder.cpp:79-117): from_latent -> per stage, its ConvNeXt
     blocks on the stage's table then its C2S block (masks from `guide` when given, else
     predicted) -> LayerNorm(eps 1e-5, no affine, :116) -> output_layer. `stages` lists
     (block prefixes, (c2s prefix, cin, cout)); wt rounds each product's input as in
     convnext_block. The stream between blocks is float32 (ggml's F32 tensors). Returns (out
-    float64 [M, out_ch], coords [M,3], masks used per stage)."""
+    float64 [M, out_ch], coords [M,3], masks used per stage). logits_out as in c2s_block, one
+    entry per stage."""
     r = _rounder(wt, cast_f32)
     c = _coords(coords)
     h = linear(r(np.asarray(latent, np.float32), "from_latent.weight"), p["from_latent.weight"],
@@ -373,7 +380,7 @@ def decode_unet(latent, coords, p: dict, stages, out_ch: int, guide=None, wt=Non
         for b in blocks:
             h = convnext_block(h.astype(np.float32), nbr, p, b, wt, cast_f32)
         h, c, m = c2s_block(h.astype(np.float32), c, p, c2s, cout,
-                            None if guide is None else guide[si], wt, cast_f32)
+                            None if guide is None else guide[si], wt, cast_f32, logits_out)
         masks.append(m)
     h = layer_norm(h.astype(np.float32), None, None, 1e-5)
     out = linear(r(h, "output_layer.weight"), p["output_layer.weight"], p["output_layer.bias"])

@@ -102,14 +102,36 @@ def _decoder_case(tmp_path, orc, shells, out_ch, seed):
 
 
 def test_shape_decode_fp32(gpu, orc, shells, tmp_path):
-    """Predicted masks, fp32 paths: masks, children and output against the oracle decoder."""
+    """Predicted masks, fp32 paths: masks, children and output against the oracle decoder. A
+    predicted mask bit is the sign of a to_subdiv logit, computed after whole stages of float32
+    sums whose order differs from the oracle's (the device's differs from the fp64 oracle by
+    ~1e-5 of the logits' range by the third stage), so a logit that close to zero may land on
+    either side. The oracle therefore runs on the device's masks, recording its own logits: every
+    device bit must equal logit > 0 except where |logit| <= 1e-3 of the stage's largest |logit|,
+    and at most 1 in 10^4 bits of a stage may disagree (a systematic error flips far more); the
+    unguided oracle must reproduce the device's masks outright when no bit disagrees."""
     coords, latent, q, stages, wt = _decoder_case(tmp_path, orc, shells, 7, seed=11)
     _run([os.path.join(BIN, "decoder_check"), str(tmp_path / "model7.gguf"), str(tmp_path), "0", "--f32"])
+    dmasks = [np.load(tmp_path / f"subs_out_{s}.npy") for s in range(len(stages))]
+    logits = []
     (ref, rcoords, rmasks), floor = rounding_noise_floor(
-        orc, lambda: orc.decode_unet(latent, coords, q, stages, 7, wt=wt, cast_f32=True))
+        orc, lambda: orc.decode_unet(latent, coords, q, stages, 7, guide=dmasks, wt=wt, cast_f32=True,
+                                     logits_out=logits if not logits else None))
+    flips = 0
+    for s, (dm, lg) in enumerate(zip(dmasks, logits)):
+        lg = np.asarray(lg).reshape(-1)
+        diff = dm != (lg > 0).astype(np.uint8)
+        if diff.any():
+            rel = np.abs(lg[diff]).max() / np.abs(lg).max()
+            print(f"stage {s}: {int(diff.sum())} of {diff.size} mask bits on the other side of a logit "
+                  f"within {rel:.2e} of the largest |logit| from zero", flush=True)
+            assert rel <= 1e-3 and diff.sum() <= max(1, diff.size // 10000), s
+        flips += int(diff.sum())
+    if flips == 0:
+        (_, pcoords, pmasks) = orc.decode_unet(latent, coords, q, stages, 7, wt=wt, cast_f32=True)
+        assert all(np.array_equal(a, b) for a, b in zip(pmasks, dmasks))
+        assert np.array_equal(pcoords, rcoords)
     assert np.array_equal(np.load(tmp_path / "coords_out.npy"), rcoords)
-    for s, m in enumerate(rmasks):
-        assert np.array_equal(np.load(tmp_path / f"subs_out_{s}.npy"), m), s
     err = orc.rel_err(np.load(tmp_path / "out.npy"), ref)
     print(f"shape_decode fp32 rel={err:.3e} floor={floor:.3e} M={len(rcoords)}", flush=True)
     assert err < max(TOL_BLOCK_F16, 1.5 * floor)

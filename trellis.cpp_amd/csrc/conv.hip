@@ -32,17 +32,31 @@ constexpr int NB_M = 64, NB_N = 64, NB_K = 32, NB_THREADS = 256;
 
 // taps = 27 with a neighbour table is the conv; taps = 1 with nbr == nullptr (row i reads row
 // i) is a dense linear layer, weight [co][ci]. bias may be null.
-template <int FDT, int WDT, int ODT>
-__global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
+//
+// KG tap groups of NB_THREADS threads each: in round r, group g runs tap KG r + g of the tile
+// (with its own staging), and at the end the groups' partial sums are added in group order
+// through LDS -- a deterministic order. KG > 1 serves grids too small to fill the device (the
+// tile count is fixed by the voxels): KG times the waves on the same tiles, each with 1/KG of
+// the taps to walk.
+template <int FDT, int WDT, int ODT, int KG>
+__global__ __launch_bounds__(NB_THREADS * KG) void k_conv_narrow(
     const typename Elem<FDT>::storage* __restrict__ feats, int64_t n, int ci,
     const int32_t* __restrict__ nbr, int taps,
     const typename Elem<WDT>::storage* __restrict__ weight, const float* __restrict__ bias,
     int co, typename Elem<ODT>::storage* __restrict__ out, PadRow pad) {
-    __shared__ float sA[NB_K][NB_M + 4];
-    __shared__ float sB[NB_K][NB_N + 4];
-    __shared__ int32_t sRow[NB_M];
+    struct Stage {
+        float a[NB_K][NB_M + 4];
+        float b[NB_K][NB_N + 4];
+        int32_t row[NB_M];
+    };
+    static_assert(KG == 1 || (KG - 1) * NB_M * NB_N * 4 <= KG * (int)sizeof(Stage), "partials fit the staging");
+    __shared__ __attribute__((aligned(16))) Stage sStage[KG];
 
-    const int tid = threadIdx.x;
+    const int gid = threadIdx.x / NB_THREADS;      // tap group
+    const int tid = threadIdx.x % NB_THREADS;
+    float (*sA)[NB_M + 4] = sStage[gid].a;
+    float (*sB)[NB_N + 4] = sStage[gid].b;
+    int32_t* sRow = sStage[gid].row;
     const int ty = tid / 16, tx = tid % 16;
     const int64_t row0 = (int64_t)blockIdx.x * NB_M;
     const int co0 = blockIdx.y * NB_N;
@@ -51,7 +65,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
     // (an exact zero padding row, pad.zero, never does; with pad.row0 that f32 row is the source)
     bool row0_bad = false;
     if (nbr && !pad.zero)
-        for (int k = tid; k < ci; k += NB_THREADS)
+        for (int k = threadIdx.x; k < ci; k += NB_THREADS * KG)
             row0_bad |= !__builtin_isfinite(pad.row0 ? pad.row0[k] : Elem<FDT>::load(feats, k));
     row0_bad = __syncthreads_or(row0_bad);
 
@@ -61,15 +75,17 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = 0.f;
 
-    for (int t = 0; t < taps; ++t) {
+    for (int t0 = 0; t0 < taps; t0 += KG) {
+        const int t = t0 + gid;          // this group's tap; past the last one, a group adds nothing
+        const bool real = t < taps;
         int valid = 0;
         if (tid < NB_M) {
             const int64_t i = row0 + tid;
-            const int32_t r = (i < n) ? (nbr ? nbr[(int64_t)t * n + i] : (int32_t)i) : sentinel;
+            const int32_t r = (real && i < n) ? (nbr ? nbr[(int64_t)t * n + i] : (int32_t)i) : sentinel;
             sRow[tid] = r;
-            valid = r != sentinel;
+            valid = real && r != sentinel;
         }
-        // no voxel of the tile has this neighbour: skipped, unless the padding row is not zero
+        // no voxel of the tile has these neighbours: skipped, unless the padding row is not zero
         if (!__syncthreads_or(valid) && !row0_bad) continue;
 
         for (int kc = 0; kc < ci; kc += NB_K) {
@@ -82,7 +98,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
                     float v = 0.f;
                     // unsigned compare: the sentinel N (and any value outside [0,N)) reads the
                     // padding row 0 * feats[0] (sparse.cpp:81-85)
-                    if (k < ci) {
+                    if (k < ci && real) {
                         if ((uint32_t)src < (uint32_t)n) v = Elem<FDT>::load(feats, (int64_t)src * ci + k);
                         else if (row0_bad) v = 0.f * (pad.row0 ? pad.row0[k] : Elem<FDT>::load(feats, k));
                     }
@@ -96,7 +112,7 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
                 for (int j = 0; j < 8; ++j) {
                     const int k = kc + kk + j;
                     float v = 0.f;
-                    if (oc < co && k < ci)
+                    if (oc < co && k < ci && real)
                         v = Elem<WDT>::load(weight, ((int64_t)oc * taps + t) * ci + k);
                     sB[kk + j][c] = v;
                 }
@@ -117,6 +133,25 @@ __global__ __launch_bounds__(NB_THREADS) void k_conv_narrow(
         }
     }
 
+    if constexpr (KG > 1) {
+        // groups 1.. KG-1 leave their partial sums in LDS; group 0 adds them in group order
+        float* part = reinterpret_cast<float*>(&sStage[0]);
+        if (gid > 0) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    part[((gid - 1) * NB_M + ty * 4 + p) * NB_N + tx * 4 + q] = acc[p][q];
+        }
+        __syncthreads();
+        if (gid != 0) return;
+#pragma unroll
+        for (int g = 1; g < KG; ++g)
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[p][q] += part[((g - 1) * NB_M + ty * 4 + p) * NB_N + tx * 4 + q];
+    }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         const int64_t i = row0 + ty * 4 + p;
@@ -345,10 +380,21 @@ template <int FDT, int WDT, int ODT>
 int launch_narrow(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* weight,
                   const float* bias, int co, void* out, hipStream_t s, PadRow pad) {
     dim3 grid((unsigned)ceil_div(n, NB_M), (unsigned)ceil_div(co, NB_N));
-    hipLaunchKernelGGL((k_conv_narrow<FDT, WDT, ODT>), grid, dim3(NB_THREADS), 0, s,
-                       reinterpret_cast<const typename Elem<FDT>::storage*>(feats), n, ci, nbr,
-                       nbr ? kTaps : 1, reinterpret_cast<const typename Elem<WDT>::storage*>(weight),
-                       bias, co, reinterpret_cast<typename Elem<ODT>::storage*>(out), pad);
+    const auto* f = reinterpret_cast<const typename Elem<FDT>::storage*>(feats);
+    const auto* w = reinterpret_cast<const typename Elem<WDT>::storage*>(weight);
+    auto* o = reinterpret_cast<typename Elem<ODT>::storage*>(out);
+    // a conv whose tiles leave most of the device idle (fewer than two a CU, e.g. the 64^3 shell
+    // of ~15K voxels) splits each tile's taps over four groups of threads
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (nbr && (int64_t)grid.x * grid.y < 2 * (int64_t)cus)
+        hipLaunchKernelGGL((k_conv_narrow<FDT, WDT, ODT, 4>), grid, dim3(NB_THREADS * 4), 0, s, f, n, ci, nbr, kTaps,
+                           w, bias, co, o, pad);
+    else
+        hipLaunchKernelGGL((k_conv_narrow<FDT, WDT, ODT, 1>), grid, dim3(NB_THREADS), 0, s, f, n, ci, nbr,
+                           nbr ? kTaps : 1, w, bias, co, o, pad);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }
