@@ -385,3 +385,104 @@ def decode_unet(latent, coords, p: dict, stages, out_ch: int, guide=None, wt=Non
     h = layer_norm(h.astype(np.float32), None, None, 1e-5)
     out = linear(r(h, "output_layer.weight"), p["output_layer.weight"], p["output_layer.bias"])
     return out, c, masks
+
+
+def _lookup(coords):
+    """A row lookup for the voxels of coords: returns find(q [K,3]) -> rows [K] (-1 where absent;
+    the largest row for duplicated coordinates, as build_neighbor_table keeps the last insert)."""
+    c = _coords(coords).astype(np.int64)
+    n = c.shape[0]
+    key = lambda p: ((p[:, 0] + 1) << 42) | ((p[:, 1] + 1) << 21) | (p[:, 2] + 1)
+    k = key(c)
+    order = np.lexsort((np.arange(n), k))
+    ks = k[order]
+    last = np.ones(n, bool)
+    last[:-1] = ks[1:] != ks[:-1]
+    ks, rows = ks[last], order[last]
+
+    def find(q):
+        q = np.asarray(q, np.int64).reshape(-1, 3)
+        ok = (q >= 0).all(1)
+        kq = key(np.where(ok[:, None], q, 0))
+        pos = np.minimum(np.searchsorted(ks, kq), len(ks) - 1) if len(ks) else np.zeros(len(kq), np.int64)
+        hit = ok & (len(ks) > 0) & (ks[pos] == kq if len(ks) else False)
+        return np.where(hit, rows[pos] if len(ks) else -1, -1)
+    return find
+
+
+def _conv_rows(get, find, coords_rows, weight, bias, pad_row):
+    """fp64 submanifold conv of the voxels at coords_rows over the set `find` looks up: bias +
+    sum_t W_t . get(neighbour rows) (pad_row where a neighbour is absent) -> [K, Co]."""
+    w = np.asarray(weight, np.float64)                      # [Co, 27, Ci]
+    q = np.asarray(coords_rows, np.int64).reshape(-1, 3)
+    out = np.tile(np.asarray(bias, np.float64), (len(q), 1))
+    for t in range(27):
+        off = np.array([t // 9 - 1, (t // 3) % 3 - 1, t % 3 - 1])
+        r = find(q + off)
+        src = np.tile(pad_row[None, :], (len(q), 1))
+        if (r >= 0).any():
+            src[r >= 0] = get(r[r >= 0])
+        out += src @ w[:, t, :].T
+    return out
+
+
+def _compact(n, rows, values):
+    """get(r) over a few rows of an n-row array: values[i] is row rows[i]."""
+    pos = np.full(n, -1, np.int64)
+    pos[rows] = np.arange(len(rows))
+
+    def get(r):
+        i = pos[r]
+        assert (i >= 0).all(), "row outside the computed set"
+        return values[i]
+    return get
+
+
+def c2s_block_rows(feats, coords, p: dict, prefix: str, cout: int, mask, rows, wt=None,
+                   cast_f32: bool = False):
+    """c2s_block's output for the child rows `rows` only (same arithmetic and rounding, with the
+    mask given), for sets too large to run whole: conv2 of each child reads its neighbouring
+    children's conv1 octant slices, each from its parent's conv1 row, which reads the parent's
+    neighbours' normalised inputs. Returns (out float64 [len(rows), Cout], child_coords [M,3])."""
+    rd = _rounder(wt, cast_f32)
+    x = np.asarray(feats, np.float32)
+    n, cin = x.shape
+    c = _coords(coords)
+    mask = (np.asarray(mask).reshape(-1) != 0).astype(np.uint8)
+    child, gidx, _ = subdivide(mask, c)
+    m = len(child)
+    rows = np.asarray(rows, np.int64)
+    k = cin // 8
+    r = cout // k
+    offs = [np.array([t // 9 - 1, (t // 3) % 3 - 1, t % 3 - 1]) for t in range(27)]
+    find_p, find_c = _lookup(c), _lookup(child)
+    # children whose norm2 outputs the sampled rows read, and their parents' conv1 rows
+    need = np.stack([find_c(child[rows].astype(np.int64) + o) for o in offs], 1)
+    kids = np.unique(need[need >= 0])
+    parents = np.unique(gidx[kids] // 8)
+    # the normalised inputs of those parents' neighbours (and row 0, the padding row's source)
+    near = np.unique(np.concatenate([find_p(c[parents].astype(np.int64) + o) for o in offs] +
+                                    [np.zeros(1, np.int64)]))
+    near = near[near >= 0]
+    hn = silu(layer_norm(x[near], p[prefix + ".norm1.weight"], p[prefix + ".norm1.bias"], 1e-6))
+    xin = rd(hn.astype(np.float32), prefix + ".conv1.weight", True)
+    pad1 = 0.0 * hn[0].astype(np.float32).astype(np.float64)       # 0 * row 0 (near[0] == 0)
+    h1 = _conv_rows(_compact(n, near, xin), find_p, c[parents], p[prefix + ".conv1.weight"],
+                    p[prefix + ".conv1.bias"], pad1)
+    slot = _compact(n, parents, np.arange(len(parents)))
+    g = gidx[kids]
+    y = h1[slot(g // 8)[:, None], (g % 8)[:, None] * cout + np.arange(cout)[None, :]]
+    y = silu(layer_norm(y, None, None, 1e-6))
+    h2 = rd(y.astype(np.float32), prefix + ".conv2.weight", True)
+    out = _conv_rows(_compact(m, kids, h2), find_c, child[rows], p[prefix + ".conv2.weight"],
+                     p[prefix + ".conv2.bias"], np.zeros(cout))
+    xs = x.reshape(n * 8, k)[gidx[rows]].astype(np.float64)
+    return out + np.repeat(xs, r, axis=1), child
+
+
+def decoder_head_rows(h, p: dict, wt=None, cast_f32: bool = False):
+    """decode_unet's head on some rows: LayerNorm (eps 1e-5, no affine, shape_decoder.cpp:116),
+    then output_layer, its input rounded as the stored weight type says."""
+    r = _rounder(wt, cast_f32)
+    hn = layer_norm(np.asarray(h, np.float32), None, None, 1e-5)
+    return linear(r(hn, "output_layer.weight"), p["output_layer.weight"], p["output_layer.bias"])

@@ -225,3 +225,61 @@ def test_decoder_zero_weight_closed_form(gpu, shells, tmp_path):
     err = np.abs(out - ref).max() / np.abs(ref).max()
     print(f"zero-weight decoder rel={err:.3e} M={len(rc)}", flush=True)
     assert err < 1e-5
+
+
+def test_decoder_full_size_properties(gpu, orc, shells, tmp_path):
+    """The decoder stack at the benchmark's widths and size (decoder-shells64-c1024: 33,543 ->
+    9,881,361 voxels, 1024 -> 512 -> 256 -> 128 -> 64 channels, bf16 weights ~ N(0, 0.02)),
+    where the oracle cannot run whole: the coordinates of every level (read back through
+    TRELLIS_DECODER_DUMP) equal the oracle's chained subdivision of the input by the masks; the
+    output has one row per final voxel, all finite, and is the same bits on a repeat; and a row
+    sample of the output -- the first and last rows and random ones -- equals the oracle's last
+    C2S block (conv1 with its octant stores and child norm at Cout = 64, conv2 with the skip) and
+    head on those rows, fed the device's own input to that stage, within 1.5x the sample's rounding
+    noise floor (at least 2e-4)."""
+    import torch
+    from trellis_cpp_amd.gguf_writer import write as write_gguf
+    w = shells.decoder_workload("decoder-shells64-c1024")
+    p = shells.decoder_params(w.channels, w.blocks, w.latent.shape[1], w.out_ch, w.std, w.seed)
+    dtypes = {k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()}
+    write_gguf(str(tmp_path / "model.gguf"), p, dtypes=dtypes, arch="trellis2-tex-dec")
+    np.save(tmp_path / "latent.npy", w.latent)
+    np.save(tmp_path / "coords.npy", np.ascontiguousarray(w.coords, np.int32))
+    for s, m in enumerate(w.masks):
+        np.save(tmp_path / f"subs_{s}.npy", np.ascontiguousarray(m, np.uint8))
+    dump = tmp_path / "dump"
+    dump.mkdir()
+    env = dict(os.environ, TRELLIS_DECODER_DUMP=str(dump))
+    args = [os.path.join(BIN, "decoder_check"), str(tmp_path / "model.gguf"), str(tmp_path), "0", "--tex",
+            "--repeat", "2"]
+    print("[host] decoder_check full size, with the level dump", flush=True)
+    r = subprocess.run(args, capture_output=True, text=True, timeout=600, env=env)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    # every level's coordinates: the oracle's subdivision chain
+    c = np.ascontiguousarray(w.coords, np.int32)
+    nst = len(w.channels) - 1
+    for s in range(nst + 1):
+        got = np.load(dump / f"level{s}_coords.npy")
+        assert np.array_equal(got, c), s
+        if s < nst:
+            c, _, _ = orc.subdivide(w.masks[s], c)
+    out = np.load(tmp_path / "out.npy")
+    assert out.shape == (w.counts[-1], w.out_ch) and np.isfinite(out).all()
+    # the last stage and the head on sampled rows, from the device's input to that stage
+    x = np.load(dump / f"level{nst - 1}_in.npy")
+    pc = np.load(dump / f"level{nst - 1}_coords.npy")
+    assert x.shape == (w.counts[nst - 1], w.channels[nst - 1]) and np.isfinite(x).all()
+    q = {k: (shells.round_to(v, "bf16") if v.ndim >= 2 else v) for k, v in p.items()}
+    rng = np.random.default_rng(4)
+    m = w.counts[-1]
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m), rng.integers(0, m, 48)]))
+    pre = f"blocks.{nst - 1}.{w.blocks}"
+
+    def sample():
+        h, _ = orc.c2s_block_rows(x, pc, q, pre, w.channels[-1], w.masks[nst - 1], rows, wt=dtypes)
+        return orc.decoder_head_rows(h, q, wt=dtypes)
+    ref, floor = rounding_noise_floor(orc, sample, runs=2)
+    err = orc.rel_err(out[rows], ref)
+    print(f"decoder full size: M={m} sampled rows {len(rows)} rel={err:.3e} floor={floor:.3e}", flush=True)
+    assert err < max(2e-4, 1.5 * floor)

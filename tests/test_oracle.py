@@ -506,3 +506,42 @@ def test_block_bar_catches_planted_mistakes(orc, shells, wtype):
         finally:
             orc.act_round = exact
         assert moved > bar, (name, moved, bar)
+
+
+@pytest.mark.parametrize("wtype", ["bf16", "f32"])
+def test_c2s_block_rows_equals_block(orc, shells, wtype):
+    """c2s_block_rows (the C2S block on sampled child rows, for sets too large to run whole)
+    equals the whole block's rows exactly, including the first and last child and parents whose
+    octants are all pruned; decoder_head_rows equals decode_unet's head on a one-stage decoder."""
+    rng = np.random.default_rng(17)
+    coords = shells.sphere_shell(20, 10.0, 6.0, 7.5)
+    n, cin, cout = len(coords), 32, 16
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    rnd = (lambda v: shells.round_to(v, wtype)) if wtype != "f32" else (lambda v: v)
+    p = {"c.norm1.weight": (1 + 0.1 * rng.standard_normal(cin)).astype(np.float32),
+         "c.norm1.bias": (0.1 * rng.standard_normal(cin)).astype(np.float32),
+         "c.conv1.weight": rnd((rng.standard_normal((8 * cout, 27, cin)) / 30).astype(np.float32)),
+         "c.conv1.bias": (0.1 * rng.standard_normal(8 * cout)).astype(np.float32),
+         "c.conv2.weight": rnd((rng.standard_normal((cout, 27, cout)) / 20).astype(np.float32)),
+         "c.conv2.bias": (0.1 * rng.standard_normal(cout)).astype(np.float32)}
+    wt = {k: (wtype if v.ndim >= 2 else "f32") for k, v in p.items()}
+    mask = (rng.random(8 * n) < 0.4).astype(np.uint8)
+    mask[:8 * 5] = 0                                   # the first parents keep no child
+    full, child, _ = orc.c2s_block(x, coords, p, "c", cout, mask, wt)
+    rows = np.unique(np.concatenate([[0, 1, len(child) - 1], rng.integers(0, len(child), 60)]))
+    part, child2 = orc.c2s_block_rows(x, coords, p, "c", cout, mask, rows, wt)
+    assert np.array_equal(child, child2)
+    assert np.abs(part - full[rows]).max() <= 1e-12 * np.abs(full).max()
+    # the head: one stage of decode_unet with no ConvNeXt block
+    q = dict(p)
+    q.update({"from_latent.weight": rnd((rng.standard_normal((cin, 8)) / 3).astype(np.float32)),
+              "from_latent.bias": np.zeros(cin, np.float32),
+              "output_layer.weight": rnd((rng.standard_normal((6, cout)) / 4).astype(np.float32)),
+              "output_layer.bias": (0.1 * rng.standard_normal(6)).astype(np.float32)})
+    wq = {k: (wtype if v.ndim >= 2 else "f32") for k, v in q.items()}
+    latent = rng.standard_normal((n, 8)).astype(np.float32)
+    out, _, _ = orc.decode_unet(latent, coords, q, [([], ("c", cin, cout))], 6, [mask], wt=wq)
+    h0 = orc.linear(orc._rounder(wq, False)(latent, "from_latent.weight"), q["from_latent.weight"],
+                    q["from_latent.bias"])
+    last, _ = orc.c2s_block_rows(h0.astype(np.float32), coords, q, "c", cout, mask, rows, wq)
+    assert np.abs(orc.decoder_head_rows(last, q, wq) - out[rows]).max() <= 1e-12 * np.abs(out).max()

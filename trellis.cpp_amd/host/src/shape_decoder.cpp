@@ -11,10 +11,12 @@
 #include "shape_decoder.h"
 
 #include <cstdio>
+#include <cstdlib>
 #include <future>
 #include <string>
 
 #include "ggml.h"
+#include "npy_io.hpp"
 #include "runtime.hpp"
 #include "sparse_ops.hpp"
 #include "trellis_model.h"
@@ -59,6 +61,24 @@ std::vector<Stage> stages_of(const Model& m) {
     }
     if (st.empty()) fail("decoder: the model has no blocks.<stage>.<block> weights");
     return st;
+}
+
+// Debug output for checking a decode at sizes the checker cannot run whole: with
+// TRELLIS_DECODER_DUMP=<dir>, each level's voxel coordinates go to <dir>/level<s>_coords.npy
+// (int32 [N_s, 3]) and the last stage's input features to <dir>/level<S-1>_in.npy (f32
+// [N, C]). The copies synchronise the stream; without the variable nothing is read back.
+void dump_level(const char* dir, int level, const DeviceBuffer& dc, int64_t n, const DeviceBuffer* h, int c,
+                hipStream_t s) {
+    hip_check(hipStreamSynchronize(s), "decoder dump");
+    std::vector<int32_t> co((size_t)n * 3);
+    if (n) hip_check(hipMemcpy(co.data(), dc.get(), (size_t)n * 12, hipMemcpyDeviceToHost), "decoder dump");
+    const std::string base = std::string(dir) + "/level" + std::to_string(level);
+    npyio::save(base + "_coords.npy", "<i4", {n, 3}, co.data(), co.size() * 4);
+    if (h) {
+        std::vector<float> f((size_t)n * c);
+        if (n) hip_check(hipMemcpy(f.data(), h->get(), f.size() * 4, hipMemcpyDeviceToHost), "decoder dump");
+        npyio::save(base + "_in.npy", "<f4", {n, (int64_t)c}, f.data(), f.size() * 4);
+    }
 }
 
 // One decoder pass; coords is updated to the final voxel set.
@@ -112,6 +132,7 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
             for (size_t i = 0; i < ns; ++i) c[i] = ops::count_nonzero((*guide)[i].data(), (*guide)[i].size());
             return c;
         });
+    const char* dump_dir = std::getenv("TRELLIS_DECODER_DUMP");
     for (size_t si = 0; si < stages.size(); ++si) {
         const Stage& g = stages[si];
         for (const std::string& p : g.convnext) {   // ConvNeXt stage, ping-pong buffers
@@ -126,6 +147,7 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
             std::swap(h, h2);
         }
         if (g.cin != c) fail(g.c2s + ": expected " + std::to_string(c) + " input channels");
+        if (dump_dir) dump_level(dump_dir, (int)si, dc, n, si + 1 == stages.size() ? &h : nullptr, c, s);
         const std::vector<uint8_t>* ext = guide ? &(*guide)[si] : nullptr;
         if (guide && counts.empty()) {
             counts = guide_counts.get();
@@ -143,6 +165,7 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         if (!result_started && si + 1 == stages.size()) start_result(n);
     }
     if (!result_started) start_result(n);
+    if (dump_dir) dump_level(dump_dir, (int)stages.size(), dc, n, nullptr, c, s);
     int32_t st = 0;
     hip_check(hipMemcpyAsync(&st, status.get(), 4, hipMemcpyDeviceToHost, s), "decoder");
     hip_check(hipStreamSynchronize(s), "decoder");
