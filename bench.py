@@ -313,9 +313,9 @@ def main():
     # while the kernel's sources are the ones that profile measured
     roof["traffic"] = None
     tj = os.path.join(ROOT, "profiles", "traffic.json")
-    if planned and os.path.exists(tj):
+    if os.path.exists(tj):
         rec = json.load(open(tj)).get(w.name)
-        if rec and rec.get("sources_sha256") == kernel_sources_sha():
+        if rec and rec.get("path") == path and rec.get("sources_sha256") == kernel_sources_sha(rec["sources"]):
             roof["traffic"] = rec["bytes_per_launch"]
             roof["traffic_source"] = rec["source"]
         elif rec:
@@ -465,13 +465,12 @@ def measured_peaks(torch, dtype: str) -> dict:
     return out
 
 
-def kernel_sources_sha() -> str:
-    """sha256 over the conv kernel's sources: a traffic profile is valid for these only."""
+def kernel_sources_sha(files) -> str:
+    """sha256 over a conv kernel's sources (file names under trellis.cpp_amd/csrc): a traffic
+    profile is valid for these only."""
     import hashlib
     h = hashlib.sha256()
-    for f in ("conv_halo.hip", "conv_halo_kernel.hpp", "conv_halo_bf16_128.hip", "conv_halo_bf16_64.hip",
-              "conv_halo_f16_128.hip", "conv_halo_f16_64.hip", "tile_plan.hpp", "plan.hip",
-              "conv_internal.hpp", "common.hpp"):
+    for f in files:
         with open(os.path.join(ROOT, "trellis.cpp_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()

@@ -431,6 +431,56 @@ __device__ __forceinline__ void conv_tiles(
         };
         float sv_cur[NQ] = {}, sv_nxt[NQ] = {};
         if constexpr (EPI == 2) skip_vals(0, 0, sv_cur);
+        // a plain conv with 16-bit output stages the rounded values: half the LDS bytes, the same
+        // bits (the one rounding happens before the staging instead of after it)
+        constexpr bool S16 = EPI == 0 && ODT != TSP_F32;
+        constexpr int RS16 = WN * 2 + 16;
+        static_assert(!S16 || (RS16 % 16 == 0 && (NR == 32 ? WAVES / 2 : WAVES) * NR * RS16 <= (int)sizeof(sH0)),
+                      "16-bit staging");
+        if constexpr (S16) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+                for (int h = 0; h < 32 / NR; ++h) {
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                        for (int j = 16 * h * NR / 32; j < 16 * (h + 1) * NR / 32; j += 2) {
+                            const int r = 8 * (j / 4) + 4 * g + (j % 4) - NR * h;   // rows r, r + 1
+                            const float a = acc[rb][cb][j] + bv[cb], b = acc[rb][cb][j + 1] + bv[cb];
+                            const uint32_t pk = ODT == TSP_BF16 ? f32x2_to_bf16x2_bits(a, b)
+                                                                : f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+                            char* at = stage + r * RS16 + (cb * 32 + r32) * 2;
+                            *reinterpret_cast<uint16_t*>(at) = (uint16_t)(pk & 0xffffu);
+                            *reinterpret_cast<uint16_t*>(at + RS16) = (uint16_t)(pk >> 16);
+                        }
+                    constexpr int NQ16 = NR * (WN / 8) / 64;
+                    u32x4_t v16[NQ16];
+#pragma unroll
+                    for (int q = 0; q < NQ16; ++q) {
+                        const int c = q * 64 + lane;
+                        v16[q] = *reinterpret_cast<const u32x4_t*>(stage + (c / (WN / 8)) * RS16 + (c % (WN / 8)) * 16);
+                    }
+#pragma unroll
+                    for (int q = 0; q < NQ16; ++q) {
+                        const int c = q * 64 + lane;
+                        const int r = c / (WN / 8), cq = c % (WN / 8);
+                        const int64_t i = row_at(32 * rb + NR * h + r);
+                        if (i < 0) continue;
+                        if (row0_bad) {
+                            bool absent = false;
+                            for (int t = 0; t < kTaps; ++t) absent |= nbr[(int64_t)t * n + i] == (int32_t)n;
+                            if (absent) {
+                                constexpr uint32_t kNaN2 = ODT == TSP_BF16 ? 0x7FC07FC0u : 0x7E007E00u;
+                                v16[q] = u32x4_t{kNaN2, kNaN2, kNaN2, kNaN2};
+                            }
+                        }
+                        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + i * co + c0 + cq * 8) = v16[q];
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
