@@ -308,18 +308,7 @@ def main():
     compulsory = compulsory_bytes(w)
     path = conv_path(w, args.algo, planned)
     roof = roofline(w, flops, compulsory, ms, valu=path in ("thin", "narrow"))
-    # HBM bytes per launch of the conv kernel, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # passes scaled by a copy kernel of known size (profiles/traffic_<workload>.md); used only
-    # while the kernel's sources are the ones that profile measured
-    roof["traffic"] = None
-    tj = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tj):
-        rec = json.load(open(tj)).get(w.name)
-        if rec and rec.get("path") == path and rec.get("sources_sha256") == kernel_sources_sha(rec["sources"]):
-            roof["traffic"] = rec["bytes_per_launch"]
-            roof["traffic_source"] = rec["source"]
-        elif rec:
-            roof["traffic_note"] = "profile predates the current kernel sources; re-measure"
+    add_traffic(roof, w, path)
     roof["algorithmic_flops_per_launch"] = flops
     roof["compulsory_bytes_per_launch"] = compulsory
     # the peaks this box reaches with library code, as a second denominator beside the datasheet's
@@ -347,6 +336,7 @@ def main():
             fe = 2.0 * we.ci * we.co * re_["pairs"]
             path_e = conv_path(we, args.algo, re_["planned"])
             roof_e = roofline(we, fe, compulsory_bytes(we), re_["ms"], valu=path_e in ("thin", "narrow"))
+            add_traffic(roof_e, we, path_e)
             extra[name] = {
                 "n_voxels": we.n, "active_pairs": re_["pairs"], "c_in": we.ci, "c_out": we.co,
                 "dtype": we.dtype, "algo": path_e,
@@ -463,6 +453,22 @@ def measured_peaks(torch, dtype: str) -> dict:
     del src, dst
     torch.cuda.empty_cache()
     return out
+
+
+def add_traffic(roof: dict, w, path: str) -> None:
+    """roof["traffic"]: HBM bytes per launch of the conv kernel, measured with rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes scaled by a copy kernel of known size (profiles/traffic.json
+    and the summary it names); used only while the kernel's sources are the ones that profile
+    measured, else null."""
+    roof["traffic"] = None
+    tj = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tj):
+        rec = json.load(open(tj)).get(w.name)
+        if rec and rec.get("path") == path and rec.get("sources_sha256") == kernel_sources_sha(rec["sources"]):
+            roof["traffic"] = rec["bytes_per_launch"]
+            roof["traffic_source"] = rec["source"]
+        elif rec:
+            roof["traffic_note"] = "profile predates the current kernel sources; re-measure"
 
 
 def kernel_sources_sha(files) -> str:
