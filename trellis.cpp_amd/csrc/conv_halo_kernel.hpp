@@ -276,8 +276,7 @@ __device__ __forceinline__ void conv_tiles(
     int plane = lane & 1;
     auto piece_slot = [&](int j) { return 32 * (wave + WAVES * j); };
     // cross-tile pipelining needs slices in pairs and the slot table in the idle piece ring
-    const bool pipelined = PLANNED && WAVES == 8 && SLOT_BLOCKS <= NSTG && T_FREE < kTaps &&
-                           nkc % 2 == 0;
+    constexpr bool CAN_PIPE = PLANNED && WAVES == 8 && SLOT_BLOCKS <= NSTG && T_FREE < kTaps;
 
     // the bias of this lane's output channels (one column tile per workgroup)
     float bv[CB];
@@ -709,13 +708,18 @@ __device__ __forceinline__ void conv_tiles(
     static_assert(PIECES * SP <= kTaps, "slice pieces must fit in one slice's taps");
     static_assert((PIECES - 1) * SP + STG < kTaps, "every staged piece is written within its slice");
 
+    // The tile loop, once with cross-tile pipelining and once without: two loops rather than a
+    // branch per tile, so that the weight ring carried from one tile to the next is live only in
+    // the loop that carries it (across a per-tile branch the register allocator spilled it at
+    // every tile).
+    auto tile_loop = [&](auto pipe_c) {
+    constexpr bool PIPE = decltype(pipe_c)::value;
     // prologue state: the current tile's plan is in sL, its first slice in sH0 and the weights
     // of its first PD taps in the ring (set by the previous tile's last slice when pipelined)
     bool pre = false;
     int H = 0;
     bool direct = false;
     u32x4_t bR[PD + 1][CB];
-
 
     for (int64_t lin = lin0; lin < xhi; lin += stride) {
         asm volatile("" : "+v"(lane), "+v"(r32), "+v"(g), "+v"(rg), "+v"(plane));
@@ -864,7 +868,7 @@ __device__ __forceinline__ void conv_tiles(
             using I0 = std::integral_constant<int, 0>;
             using I1 = std::integral_constant<int, kTaps % (PD + 1)>;
             using NO = std::false_type;
-            if (pipelined) {
+            if constexpr (PIPE) {
                 f32x16_t acc[RB][CB];
                 zero(acc);
                 for (int kc = 0; kc + 2 < nkc; kc += 2) {
@@ -918,6 +922,11 @@ __device__ __forceinline__ void conv_tiles(
                 pre = false;
             }
         } else {
+            // the weight ring is dead here (the next tile's prologue reloads it)
+#pragma unroll
+            for (int q = 0; q <= PD; ++q)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) asm volatile("" : "=v"(bR[q][cb]));
             f32x16_t acc[RB][CB];
             zero(acc);
             // ---- direct path: A gathered from global memory
@@ -948,6 +957,14 @@ __device__ __forceinline__ void conv_tiles(
             pre = false;
         }
     }
+    };
+    if constexpr (CAN_PIPE) {
+        if (nkc % 2 == 0) {
+            tile_loop(std::true_type{});
+            return;
+        }
+    }
+    tile_loop(std::false_type{});
 }
 
 // Compute units of the current device (cached per device).
