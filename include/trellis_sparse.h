@@ -347,6 +347,17 @@ size_t tsp_convnext_workspace_bytes(int64_t n, int c, int x_dtype, const tsp_con
 int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, const int32_t* d_nbr,
                  const void* d_plan, const tsp_convnext_weights* w, float* d_out,
                  void* d_workspace, size_t workspace_bytes, int flags, void* stream);
+/* tsp_convnext with the 16-bit copies of a decoder's residual stream (no counterpart in the
+ * reference, where each conv rounds its f32 input itself; for callers that chain blocks):
+ * d_x16, optional with f32 x and a 16-bit conv input, is x already rounded to the conv input's
+ * type (as tsp_convnext would round it), so the block skips that pass; d_out16, optional, receives
+ * out rounded to out16_dtype (TSP_BF16 or TSP_F16, round to nearest even) -- written by the MLP
+ * kernel's stores where the MLP is one kernel, by a rounding pass otherwise. Both 16-byte aligned;
+ * d_out16 must not alias x, x16 or out. The workspace of tsp_convnext_workspace_bytes suffices. */
+int tsp_convnext_ex(const void* d_x, int x_dtype, const void* d_x16, int64_t n, int c,
+                    const int32_t* d_nbr, const void* d_plan, const tsp_convnext_weights* w,
+                    float* d_out, void* d_out16, int out16_dtype, void* d_workspace,
+                    size_t workspace_bytes, int flags, void* stream);
 
 /* The ConvNeXt block's MLP in one kernel (sparse.cpp:126-134: mlp.0, SiLU, mlp.2, + x, in place of
  * two mul_mats): out f32 [n][c] = x + b2 + W2 . silu(W0 . xn + b0), with the hidden layer kept on
@@ -392,6 +403,15 @@ int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const vo
             int cout, const int32_t* d_child_nbr, const void* d_child_plan,
             const tsp_c2s_weights* w, float* d_out, void* d_workspace, size_t workspace_bytes,
             int flags, void* stream);
+/* tsp_c2s with d_out16 (optional, 16-byte aligned, not aliasing x or out) receiving out rounded to
+ * out16_dtype (TSP_BF16 or TSP_F16): the next ConvNeXt conv's 16-bit input (tsp_convnext_ex's
+ * d_x16), written by conv2's stores where they add the skip, by a rounding pass otherwise (no
+ * counterpart in the reference). */
+int tsp_c2s_ex(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+               const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m,
+               int cout, const int32_t* d_child_nbr, const void* d_child_plan,
+               const tsp_c2s_weights* w, float* d_out, void* d_out16, int out16_dtype,
+               void* d_workspace, size_t workspace_bytes, int flags, void* stream);
 
 #ifdef __cplusplus
 }

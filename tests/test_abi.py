@@ -332,6 +332,20 @@ def test_composite_validation(pkg):
     assert L.tsp_c2s_workspace_bytes(500, 1200, 128, 64, ctypes.byref(c), 1, 0, 0) != cb
     assert cs(ws=cb - 1) == 5
     assert cs(m=0) == 0
+    # the rounded copies of the _ex forms: x16 only with f32 x, out16 bf16 or f16, 16-byte aligned,
+    # not aliasing the block's other buffers
+    cx = lambda **kw: L.tsp_convnext_ex(FAKE, kw.get("xdt", 0), kw.get("x16", None), 1000, 64, FAKE, FAKE,
+                                        ctypes.byref(w), ctypes.c_void_p(0x2000), kw.get("o16", None),
+                                        kw.get("o16dt", 2), FAKE, nb, 0, NULL)
+    assert cx(xdt=2, x16=FAKE) == 1 and "rounded copy of x" in _err(pkg)
+    assert cx(o16=ctypes.c_void_p(0x3000), o16dt=0) == 1
+    assert cx(x16=ctypes.c_void_p(0x3008)) == 1 and "aligned" in _err(pkg)
+    assert cx(o16=ctypes.c_void_p(0x2000)) == 1 and "alias" in _err(pkg)
+    cx2 = lambda **kw: L.tsp_c2s_ex(FAKE, 500, 128, FAKE, FAKE, FAKE, FAKE, FAKE, 1200, 64, FAKE, FAKE,
+                                    ctypes.byref(c), ctypes.c_void_p(0x2000), kw.get("o16", None),
+                                    kw.get("o16dt", 2), FAKE, cb, 0, NULL)
+    assert cx2(o16=ctypes.c_void_p(0x3000), o16dt=3) == 1
+    assert cx2(o16=ctypes.c_void_p(0x2000)) == 1 and "alias" in _err(pkg)
 
 
 def test_convnext_mlp_validation(pkg):

@@ -154,3 +154,68 @@ def test_c2s(gpu_lib, orc, shells, cin, cout, wtype, planned):
     err = orc.rel_err(out.cpu().numpy(), ref)
     print(f"c2s rel={err:.3e} floor={floor:.3e}", flush=True)
     assert err < _bar(floor)
+
+
+@pytest.mark.parametrize("c,wtype,planned,o16", [(128, "bf16", True, "bf16"), (128, "f16", True, "f16"),
+                                                 (128, "bf16", True, "f16"), (256, "bf16", True, "bf16"),
+                                                 (64, "bf16", False, "bf16")])
+def test_convnext_rounded_copies(gpu_lib, shells, c, wtype, planned, o16):
+    """tsp_convnext_ex: the rounded copy of out equals out rounded to nearest even, bit for bit (the
+    fused MLP's stores at C = 128, a rounding pass elsewhere); out itself is the same as without
+    the copy; and giving x's rounded copy (x16) leaves out unchanged, bit for bit."""
+    import torch
+    _case(f"convnext copies c={c} {wtype} planned={planned} out16={o16}")
+    rng = np.random.default_rng(7 * c + len(wtype))
+    coords = np.ascontiguousarray(shells.sphere_shell(20, 10.0, 6.0, 7.5), np.int32)
+    n = len(coords)
+    x = rng.standard_normal((n, c)).astype(np.float32)
+    P = _params(rng, {"conv.weight": ((c, 27, c), 1 / np.sqrt(27 * c), 0), "conv.bias": ((c,), 0.1, 0),
+                      "norm.weight": ((c,), 0.1, 1), "norm.bias": ((c,), 0.1, 0),
+                      "mlp.0.weight": ((4 * c, c), 1 / np.sqrt(c), 0), "mlp.0.bias": ((4 * c,), 0.1, 0),
+                      "mlp.2.weight": ((c, 4 * c), 1 / np.sqrt(4 * c), 0), "mlp.2.bias": ((c,), 0.1, 0)}, wtype)
+    p = {k: v[1] for k, v in P.items()}
+    nbr = gpu_lib.rulebook_build(_dev(coords))
+    plan = gpu_lib.conv_plan_build(nbr, n) if planned else None
+    xd = _dev(x)
+    t16 = getattr(torch, DT[o16])
+    base = gpu_lib.convnext(xd, nbr, p, plan=plan)
+    out, out16 = gpu_lib.convnext(xd, nbr, p, plan=plan, out16_dtype=t16)
+    with_x16 = gpu_lib.convnext(xd, nbr, p, plan=plan, x16=xd.to(getattr(torch, DT[wtype])))
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    assert torch.equal(out16.view(torch.int16), out.cpu().to(t16).cuda().view(torch.int16))
+    assert torch.equal(with_x16, base)
+
+
+@pytest.mark.parametrize("cin,cout,wtype,o16", [(256, 128, "bf16", "bf16"), (128, 64, "f16", "f16"),
+                                                (64, 32, "bf16", "bf16")])
+def test_c2s_rounded_copy(gpu_lib, shells, cin, cout, wtype, o16):
+    """tsp_c2s_ex: the rounded copy of out equals out rounded to nearest even, bit for bit -- from
+    conv2's skip stores (Cout / (Cin / 8) a multiple of 4) or from a rounding pass (64 -> 32) --
+    and out is the same as without the copy."""
+    import torch
+    _case(f"c2s copy {cin}->{cout} {wtype} out16={o16}")
+    rng = np.random.default_rng(cin + 3 * cout)
+    coords = np.ascontiguousarray(shells.sphere_shell(16, 8.0, 5.0, 6.5), np.int32)
+    n = len(coords)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    mask = (rng.random(8 * n) < 0.4).astype(np.uint8)
+    P = _params(rng, {"norm1.weight": ((cin,), 0.1, 1), "norm1.bias": ((cin,), 0.1, 0),
+                      "conv1.weight": ((8 * cout, 27, cin), 1 / np.sqrt(27 * cin), 0),
+                      "conv1.bias": ((8 * cout,), 0.1, 0),
+                      "conv2.weight": ((cout, 27, cout), 1 / np.sqrt(27 * cout), 0),
+                      "conv2.bias": ((cout,), 0.1, 0)}, wtype)
+    p = {k: v[1] for k, v in P.items()}
+    cc, mt = _dev(coords), _dev(mask)
+    nbr = gpu_lib.rulebook_build(cc)
+    child, gidx, mstart = gpu_lib.subdivide(mt, cc)
+    m = len(gidx)
+    cnbr = gpu_lib.rulebook_build(child)
+    plans = (gpu_lib.conv_plan_build(nbr, n), gpu_lib.conv_plan_build(cnbr, m))
+    t16 = getattr(torch, DT[o16])
+    base = gpu_lib.c2s(_dev(x), nbr, mt, mstart, gidx, m, cout, cnbr, p, plan=plans[0], child_plan=plans[1])
+    out, out16 = gpu_lib.c2s(_dev(x), nbr, mt, mstart, gidx, m, cout, cnbr, p, plan=plans[0], child_plan=plans[1],
+                             out16_dtype=t16)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    assert torch.equal(out16.view(torch.int16), out.cpu().to(t16).cuda().view(torch.int16))

@@ -33,7 +33,8 @@ EXPORTS = (
     "tsp_subdivide_workspace_bytes", "tsp_subdivide", "tsp_subdivide_noalloc",
     "tsp_linear", "tsp_linear_ex", "tsp_linear_rows_per_call", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
-    "tsp_convnext_workspace_bytes", "tsp_convnext", "tsp_c2s_workspace_bytes", "tsp_c2s",
+    "tsp_convnext_workspace_bytes", "tsp_convnext", "tsp_convnext_ex", "tsp_c2s_workspace_bytes", "tsp_c2s",
+    "tsp_c2s_ex",
 )
 
 BLOCK_CAST_F32 = 2
@@ -156,11 +157,17 @@ def lib() -> ctypes.CDLL:
     L.tsp_convnext_workspace_bytes.argtypes = [c_i64, c_int, c_int, cnw, c_int, c_int]
     L.tsp_convnext.restype = c_int
     L.tsp_convnext.argtypes = [c_vp, c_int, c_i64, c_int, c_vp, c_vp, cnw, c_vp, c_vp, c_sz, c_int, c_vp]
+    L.tsp_convnext_ex.restype = c_int
+    L.tsp_convnext_ex.argtypes = [c_vp, c_int, c_vp, c_i64, c_int, c_vp, c_vp, cnw, c_vp, c_vp, c_int, c_vp, c_sz,
+                                  c_int, c_vp]
     L.tsp_c2s_workspace_bytes.restype = c_sz
     L.tsp_c2s_workspace_bytes.argtypes = [c_i64, c_i64, c_int, c_int, c2w, c_int, c_int, c_int]
     L.tsp_c2s.restype = c_int
     L.tsp_c2s.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c2w,
                           c_vp, c_vp, c_sz, c_int, c_vp]
+    L.tsp_c2s_ex.restype = c_int
+    L.tsp_c2s_ex.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c2w,
+                             c_vp, c_vp, c_int, c_vp, c_sz, c_int, c_vp]
     _lib = L
     return L
 
@@ -661,12 +668,14 @@ def _mat(t, shape, name: str):
     return t.contiguous()
 
 
-def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None):
-    """SparseConvNeXtBlock3d through tsp_convnext: x [N, C] (f32, or 16-bit of the conv input's
+def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None, x16=None, out16_dtype=None):
+    """SparseConvNeXtBlock3d through tsp_convnext_ex: x [N, C] (f32, or 16-bit of the conv input's
     type), p the block's tensors by their reference names without the prefix ("conv.weight"
     [C,27,C], "conv.bias", "norm.weight", "norm.bias", "mlp.0.weight" [4C,C], "mlp.0.bias",
     "mlp.2.weight" [C,4C], "mlp.2.bias"); optional "conv.packed" (conv_weight_pack) and
-    "mlp.packed" (convnext_mlp_pack of mlp.0 and mlp.2). -> f32 [N, C]."""
+    "mlp.packed" (convnext_mlp_pack of mlp.0 and mlp.2). x16, optional with f32 x: x already
+    rounded to the conv input's 16-bit type. -> f32 [N, C], or (out, out rounded to out16_dtype)
+    when out16_dtype (torch.bfloat16 / torch.float16) is given."""
     torch = _torch()
     n, c = x.shape
     _check_nbr(nbr, n, x.device)
@@ -690,21 +699,29 @@ def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None):
                         dtype_code(t["mlp.2.weight"].dtype), _ptr(t["mlp.2.bias"]), _ptr(mpacked))
     flags = BLOCK_CAST_F32 if cast_f32 else 0
     xc = x.contiguous()
+    if x16 is not None:
+        x16 = x16.contiguous()
+        if tuple(x16.shape) != (n, c) or x16.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("x16 must be a 16-bit [N, C] tensor")
+        _require_cuda(x16)
     out = torch.empty((n, c), dtype=torch.float32, device=x.device)
+    out16 = None if out16_dtype is None else torch.empty((n, c), dtype=out16_dtype, device=x.device)
     nb = lib().tsp_convnext_workspace_bytes(n, c, dtype_code(xc.dtype), ctypes.byref(w), int(plan is not None), flags)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
-    _check("tsp_convnext", lib().tsp_convnext(_ptr(xc), dtype_code(xc.dtype), n, c, _ptr(nbr), _ptr(plan),
-                                              ctypes.byref(w), _ptr(out), _ptr(ws), nb, flags, _stream(stream)))
-    return out
+    _check("tsp_convnext_ex", lib().tsp_convnext_ex(
+        _ptr(xc), dtype_code(xc.dtype), _ptr(x16), n, c, _ptr(nbr), _ptr(plan), ctypes.byref(w), _ptr(out),
+        _ptr(out16), dtype_code(out16_dtype) if out16 is not None else 2, _ptr(ws), nb, flags, _stream(stream)))
+    return out if out16 is None else (out, out16)
 
 
 def c2s(x, nbr, mask, mstart, gidx, m: int, cout: int, child_nbr, p: dict, plan=None, child_plan=None,
-        cast_f32: bool = False, stream=None):
-    """The C2S block's features through tsp_c2s, after its subdivision (mask uint8 [8N], mstart
+        cast_f32: bool = False, stream=None, out16_dtype=None):
+    """The C2S block's features through tsp_c2s_ex, after its subdivision (mask uint8 [8N], mstart
     and gidx from subdivide, child_nbr the children's table): x f32 [N, Cin], p by reference
     names without the prefix ("norm1.weight", "norm1.bias", "conv1.weight" [8 Cout,27,Cin],
     "conv1.bias", "conv2.weight" [Cout,27,Cout], "conv2.bias"; optional "conv1.packed",
-    "conv2.packed"). -> f32 [M, Cout]."""
+    "conv2.packed"). -> f32 [M, Cout], or (out, out rounded to out16_dtype) when out16_dtype is
+    given."""
     torch = _torch()
     n, cin = x.shape
     if x.dtype != torch.float32:
@@ -733,10 +750,12 @@ def c2s(x, nbr, mask, mstart, gidx, m: int, cout: int, child_nbr, p: dict, plan=
     flags = BLOCK_CAST_F32 if cast_f32 else 0
     xc = x.contiguous()
     out = torch.empty((m, cout), dtype=torch.float32, device=x.device)
+    out16 = None if out16_dtype is None else torch.empty((m, cout), dtype=out16_dtype, device=x.device)
     nb = lib().tsp_c2s_workspace_bytes(n, m, cin, cout, ctypes.byref(w), int(plan is not None),
                                        int(child_plan is not None), flags)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
-    _check("tsp_c2s", lib().tsp_c2s(_ptr(xc), n, cin, _ptr(nbr), _ptr(plan), _ptr(mask.reshape(-1).contiguous()),
-                                    _ptr(mstart), _ptr(gidx), m, cout, _ptr(child_nbr), _ptr(child_plan),
-                                    ctypes.byref(w), _ptr(out), _ptr(ws), nb, flags, _stream(stream)))
-    return out
+    _check("tsp_c2s_ex", lib().tsp_c2s_ex(
+        _ptr(xc), n, cin, _ptr(nbr), _ptr(plan), _ptr(mask.reshape(-1).contiguous()), _ptr(mstart), _ptr(gidx), m,
+        cout, _ptr(child_nbr), _ptr(child_plan), ctypes.byref(w), _ptr(out), _ptr(out16),
+        dtype_code(out16_dtype) if out16 is not None else 2, _ptr(ws), nb, flags, _stream(stream)))
+    return out if out16 is None else (out, out16)

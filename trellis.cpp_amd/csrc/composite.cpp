@@ -105,15 +105,18 @@ int64_t mlp_chunk(int64_t n, int c) {
     return std::max<int64_t>(1, std::min<int64_t>(n, (int64_t(1) << 30) / (16 * (int64_t)c)));
 }
 
-int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, const void* plan,
-                  const tsp_convnext_weights& w, float* out, int flags, Carve& ws, hipStream_t s) {
+// x16 (optional): x already rounded to the conv input's 16-bit type; out16 (optional): out rounded
+// to out16dt, written by the MLP kernel's stores where it runs, else by a rounding pass.
+int convnext_walk(const void* x, int xdt, const void* x16, int64_t n, int c, const int32_t* nbr, const void* plan,
+                  const tsp_convnext_weights& w, float* out, void* out16, int out16dt, int flags, Carve& ws,
+                  hipStream_t s) {
     const int cdt = act_dtype(w.conv_dtype, true, flags);
     const int adt0 = act_dtype(w.mlp0_dtype, false, flags), adt2 = act_dtype(w.mlp2_dtype, false, flags);
     const int64_t chunk = mlp_chunk(n, c);
     // conv input rounded (when x is f32 and the conv takes 16-bit input; x is f32 there, the entry
     // point rejects other mixes)
-    void* xr16 = xdt != cdt ? ws.take((size_t)n * c * dtype_size(cdt)) : nullptr;
-    const void* xc = xr16 ? xr16 : x;
+    void* xr16 = xdt != cdt && !x16 ? ws.take((size_t)n * c * dtype_size(cdt)) : nullptr;
+    const void* xc = x16 ? x16 : xr16 ? xr16 : x;
     const bool fuse = ln_fused(cdt, adt0, c, plan);
     // the MLP in one kernel, its 16-bit hidden layer never stored (C = 128, one 16-bit dtype)
     const bool mlp1 = is16(adt0) && adt2 == adt0 && w.mlp0_dtype == adt0 && w.mlp2_dtype == adt0 &&
@@ -160,7 +163,8 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
             if (int st = mlp_pack(w.mlp0_weight, w.mlp2_weight, c, mlp_packed, s)) return st;
             mp = mlp_packed;
         }
-        return mlp_fused(hn, adt0, n, c, mp, w.mlp0_bias, w.mlp2_bias, static_cast<const float*>(x), out, s);
+        return mlp_fused(hn, adt0, n, c, mp, w.mlp0_bias, w.mlp2_bias, static_cast<const float*>(x), out, s, out16,
+                         out16dt);
     }
     const size_t aes = dtype_size(adt0), xes = dtype_size(xdt);
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {
@@ -192,14 +196,15 @@ int convnext_walk(const void* x, int xdt, int64_t n, int c, const int32_t* nbr, 
         }
         if (st) return st;
     }
-    return TSP_OK;
+    return out16 ? f32_to(out, n * c, out16, out16dt, false, s) : TSP_OK;
 }
 
 // The C2S block after its subdivision (sparse.cpp:256-336): norm1 + SiLU -> conv1 (Cin -> 8 Cout)
 // -> octant gather -> norm2 (no affine) + SiLU -> conv2 (exact zero padding row) -> + skip.
 int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void* plan, const uint8_t* mask,
              const int32_t* mstart, const int32_t* gidx, int64_t m, int cout, const int32_t* cnbr,
-             const void* cplan, const tsp_c2s_weights& w, float* out, int flags, Carve& ws, hipStream_t s) {
+             const void* cplan, const tsp_c2s_weights& w, float* out, void* out16, int out16dt, int flags,
+             Carve& ws, hipStream_t s) {
     const int in1 = act_dtype(w.conv1_dtype, true, flags), in2 = act_dtype(w.conv2_dtype, true, flags);
     const ConvPlan cp1 = conv_plan(in1, cin, 8 * cout, plan, w.conv1_packed);
     const ConvPlan cp2 = conv_plan(in2, cout, cout, cplan, w.conv2_packed);
@@ -256,8 +261,7 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
         p2 = pk2;
     }
     if (skip_in_stores)
-        return tsp_subm_conv3x3_planned_skip(h2, in2, m, cout, cnbr, cplan, p2, w.conv2_bias, cout, x, cin, gidx, out,
-                                             s);
+        return planned_skip(h2, in2, m, cout, cnbr, cplan, p2, w.conv2_bias, cout, x, cin, gidx, out, out16, out16dt, s);
     if (cp2.planned)
         st = tsp_subm_conv3x3_planned_ex(h2, in2, m, cout, cnbr, cplan, p2, w.conv2_bias, cout, out, TSP_F32,
                                          TSP_CONV_ZERO_PAD, nullptr, s);
@@ -266,7 +270,8 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
                                  TSP_F32, TSP_ALGO_AUTO,
                                  TSP_CONV_ZERO_PAD, nullptr, s);
     if (st) return st;
-    return tsp_c2s_skip_add(x, TSP_F32, gidx, m, cin, cout, out, TSP_F32, s);
+    if ((st = tsp_c2s_skip_add(x, TSP_F32, gidx, m, cin, cout, out, TSP_F32, s))) return st;
+    return out16 ? f32_to(out, m * cout, out16, out16dt, false, s) : TSP_OK;
 }
 
 // a non-null stand-in for the plan when sizing (sizing never dereferences it)
@@ -281,13 +286,15 @@ extern "C" size_t tsp_convnext_workspace_bytes(int64_t n, int c, int x_dtype, co
                                                int has_plan, int flags) {
     if (n <= 0 || c <= 0 || !w) return 0;
     Carve ws(nullptr);
-    convnext_walk(nullptr, x_dtype, n, c, nullptr, plan_flag(has_plan), *w, nullptr, flags, ws, nullptr);
+    convnext_walk(nullptr, x_dtype, nullptr, n, c, nullptr, plan_flag(has_plan), *w, nullptr, nullptr, TSP_BF16, flags, ws,
+                  nullptr);
     return ws.off;
 }
 
-extern "C" int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, const int32_t* d_nbr,
-                            const void* d_plan, const tsp_convnext_weights* w, float* d_out,
-                            void* d_workspace, size_t workspace_bytes, int flags, void* stream) {
+extern "C" int tsp_convnext_ex(const void* d_x, int x_dtype, const void* d_x16, int64_t n, int c,
+                               const int32_t* d_nbr, const void* d_plan, const tsp_convnext_weights* w,
+                               float* d_out, void* d_out16, int out16_dtype, void* d_workspace,
+                               size_t workspace_bytes, int flags, void* stream) {
     clear_error();
     TSP_REQUIRE(w, TSP_ERR_INVALID, "tsp_convnext: null weights");
     TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && c > 0, TSP_ERR_INVALID, "tsp_convnext: n=%lld c=%d",
@@ -298,16 +305,32 @@ extern "C" int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, cons
     const int cdt = act_dtype(w->conv_dtype, true, flags);
     TSP_REQUIRE(x_dtype == TSP_F32 || x_dtype == cdt, TSP_ERR_UNSUPPORTED,
                 "tsp_convnext: 16-bit x must have the conv input's type (%d), got %d", cdt, x_dtype);
+    TSP_REQUIRE(!d_x16 || (x_dtype == TSP_F32 && is16(cdt)), TSP_ERR_INVALID,
+                "tsp_convnext: a rounded copy of x goes with f32 x and a 16-bit conv input");
+    TSP_REQUIRE(!d_out16 || out16_dtype == TSP_BF16 || out16_dtype == TSP_F16, TSP_ERR_INVALID,
+                "tsp_convnext: the rounded copy of out is bf16 or f16, not dtype %d", out16_dtype);
     if (n == 0) return TSP_OK;
     TSP_REQUIRE(d_x && d_nbr && d_out && w->conv_weight && w->conv_bias && w->norm_weight && w->norm_bias &&
                     w->mlp0_weight && w->mlp0_bias && w->mlp2_weight && w->mlp2_bias,
                 TSP_ERR_INVALID, "tsp_convnext: null pointer");
     TSP_REQUIRE(static_cast<const void*>(d_out) != d_x, TSP_ERR_INVALID, "tsp_convnext: out aliases x");
+    TSP_REQUIRE(!d_out16 || (d_out16 != d_x && d_out16 != d_out && d_out16 != d_x16), TSP_ERR_INVALID,
+                "tsp_convnext: the rounded copy of out aliases another buffer");
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    TSP_REQUIRE(al16(d_x16) && al16(d_out16), TSP_ERR_INVALID, "tsp_convnext: the rounded copies must be 16-byte aligned");
     const size_t need = tsp_convnext_workspace_bytes(n, c, x_dtype, w, d_plan != nullptr, flags);
     TSP_REQUIRE(d_workspace && workspace_bytes >= need, TSP_ERR_WORKSPACE,
                 "tsp_convnext: workspace %zu < %zu bytes", workspace_bytes, need);
     Carve ws(d_workspace);
-    return convnext_walk(d_x, x_dtype, n, c, d_nbr, d_plan, *w, d_out, flags, ws, as_stream(stream));
+    return convnext_walk(d_x, x_dtype, d_x16, n, c, d_nbr, d_plan, *w, d_out, d_out16, out16_dtype, flags, ws,
+                         as_stream(stream));
+}
+
+extern "C" int tsp_convnext(const void* d_x, int x_dtype, int64_t n, int c, const int32_t* d_nbr,
+                            const void* d_plan, const tsp_convnext_weights* w, float* d_out,
+                            void* d_workspace, size_t workspace_bytes, int flags, void* stream) {
+    return tsp_convnext_ex(d_x, x_dtype, nullptr, n, c, d_nbr, d_plan, w, d_out, nullptr, TSP_BF16, d_workspace,
+                           workspace_bytes, flags, stream);
 }
 
 extern "C" size_t tsp_c2s_workspace_bytes(int64_t n, int64_t m, int cin, int cout, const tsp_c2s_weights* w,
@@ -315,14 +338,15 @@ extern "C" size_t tsp_c2s_workspace_bytes(int64_t n, int64_t m, int cin, int cou
     if (n <= 0 || m < 0 || cin <= 0 || cout <= 0 || !w) return 0;
     Carve ws(nullptr);
     c2s_walk(nullptr, n, cin, nullptr, plan_flag(has_plan), nullptr, nullptr, nullptr, m, cout, nullptr,
-             plan_flag(has_child_plan), *w, nullptr, flags, ws, nullptr);
+             plan_flag(has_child_plan), *w, nullptr, nullptr, TSP_BF16, flags, ws, nullptr);
     return ws.off;
 }
 
-extern "C" int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
-                       const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m, int cout,
-                       const int32_t* d_child_nbr, const void* d_child_plan, const tsp_c2s_weights* w,
-                       float* d_out, void* d_workspace, size_t workspace_bytes, int flags, void* stream) {
+extern "C" int tsp_c2s_ex(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+                          const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m, int cout,
+                          const int32_t* d_child_nbr, const void* d_child_plan, const tsp_c2s_weights* w,
+                          float* d_out, void* d_out16, int out16_dtype, void* d_workspace, size_t workspace_bytes,
+                          int flags, void* stream) {
     clear_error();
     TSP_REQUIRE(w, TSP_ERR_INVALID, "tsp_c2s: null weights");
     TSP_REQUIRE(n >= 0 && 8 * n < (int64_t)INT32_MAX && m >= 0 && m <= 8 * n, TSP_ERR_INVALID,
@@ -331,15 +355,29 @@ extern "C" int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nb
                 "tsp_c2s: needs Cin %% 8 == 0 and Cout %% (Cin/8) == 0 (Cin=%d Cout=%d)", cin, cout);
     TSP_REQUIRE((flags & ~TSP_BLOCK_CAST_F32) == 0, TSP_ERR_INVALID, "tsp_c2s: bad flags %d", flags);
     TSP_REQUIRE(dtype_valid(w->conv1_dtype) && dtype_valid(w->conv2_dtype), TSP_ERR_INVALID, "tsp_c2s: bad dtype");
+    TSP_REQUIRE(!d_out16 || out16_dtype == TSP_BF16 || out16_dtype == TSP_F16, TSP_ERR_INVALID,
+                "tsp_c2s: the rounded copy of out is bf16 or f16, not dtype %d", out16_dtype);
     if (m == 0) return TSP_OK;
     TSP_REQUIRE(d_x && d_nbr && d_mask && d_mstart && d_gidx && d_child_nbr && d_out && w->norm1_weight &&
                     w->norm1_bias && w->conv1_weight && w->conv1_bias && w->conv2_weight && w->conv2_bias,
                 TSP_ERR_INVALID, "tsp_c2s: null pointer");
     TSP_REQUIRE(d_out != d_x, TSP_ERR_INVALID, "tsp_c2s: out aliases x");
+    TSP_REQUIRE(!d_out16 || (d_out16 != static_cast<const void*>(d_x) && d_out16 != static_cast<void*>(d_out)),
+                TSP_ERR_INVALID, "tsp_c2s: the rounded copy of out aliases another buffer");
+    TSP_REQUIRE((reinterpret_cast<uintptr_t>(d_out16) & 15) == 0, TSP_ERR_INVALID,
+                "tsp_c2s: the rounded copy of out must be 16-byte aligned");
     const size_t need = tsp_c2s_workspace_bytes(n, m, cin, cout, w, d_plan != nullptr, d_child_plan != nullptr, flags);
     TSP_REQUIRE(d_workspace && workspace_bytes >= need, TSP_ERR_WORKSPACE, "tsp_c2s: workspace %zu < %zu bytes",
                 workspace_bytes, need);
     Carve ws(d_workspace);
     return c2s_walk(d_x, n, cin, d_nbr, d_plan, d_mask, d_mstart, d_gidx, m, cout, d_child_nbr, d_child_plan, *w,
-                    d_out, flags, ws, as_stream(stream));
+                    d_out, d_out16, out16_dtype, flags, ws, as_stream(stream));
+}
+
+extern "C" int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+                       const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m, int cout,
+                       const int32_t* d_child_nbr, const void* d_child_plan, const tsp_c2s_weights* w,
+                       float* d_out, void* d_workspace, size_t workspace_bytes, int flags, void* stream) {
+    return tsp_c2s_ex(d_x, n, cin, d_nbr, d_plan, d_mask, d_mstart, d_gidx, m, cout, d_child_nbr, d_child_plan, w,
+                      d_out, nullptr, TSP_BF16, d_workspace, workspace_bytes, flags, stream);
 }

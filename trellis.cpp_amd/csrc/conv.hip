@@ -688,12 +688,9 @@ extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, 
                             co, d_out, as_stream(stream), osc);
 }
 
-extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int ci,
-                                             const int32_t* d_nbr, const void* d_plan,
-                                             const void* d_packed_weight, const float* d_bias, int co,
-                                             const float* d_x, int cin, const int32_t* d_gidx,
-                                             float* d_out, void* stream) {
-    clear_error();
+int tsp::planned_skip(const void* d_feats, int dtype, int64_t n, int ci, const int32_t* d_nbr, const void* d_plan,
+                      const void* d_packed_weight, const float* d_bias, int co, const float* d_x, int cin,
+                      const int32_t* d_gidx, float* d_out, void* d_out16, int out16_dtype, hipStream_t s) {
     TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && ci > 0 && co > 0 && cin > 0, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3_planned_skip: n=%lld ci=%d co=%d cin=%d", (long long)n, ci, co, cin);
     TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
@@ -706,6 +703,8 @@ extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int
                 "(cin=%d co=%d)", cin, co);
     TSP_REQUIRE((int64_t)kTaps * ci * co * 2 < ((int64_t)1 << 32), TSP_ERR_UNSUPPORTED,
                 "tsp_subm_conv3x3_planned_skip: weight of 4 GiB or more");
+    TSP_REQUIRE(!d_out16 || out16_dtype == TSP_BF16 || out16_dtype == TSP_F16, TSP_ERR_INVALID,
+                "tsp_subm_conv3x3_planned_skip: the 16-bit copy is bf16 or f16, not dtype %d", out16_dtype);
     if (n == 0) return TSP_OK;
     TSP_REQUIRE(d_feats && d_nbr && d_plan && d_packed_weight && d_bias && d_x && d_gidx && d_out,
                 TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_skip: null pointer");
@@ -713,17 +712,30 @@ extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int
                 "tsp_subm_conv3x3_planned_skip: out aliases feats or x");
     TSP_REQUIRE(reinterpret_cast<uintptr_t>(d_feats) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(d_packed_weight) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(d_out) % 16 == 0,
-                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_skip: buffers must be 16-byte aligned");
+                    reinterpret_cast<uintptr_t>(d_out) % 16 == 0 && reinterpret_cast<uintptr_t>(d_out16) % 8 == 0,
+                TSP_ERR_INVALID, "tsp_subm_conv3x3_planned_skip: buffers must be 16-byte aligned (the 16-bit "
+                "copy 8-byte)");
     SkipAdd skip;
     skip.x = d_x;
     skip.gidx = d_gidx;
     skip.cin = cin;
+    skip.out16 = d_out16;
+    skip.out16_bf16 = out16_dtype == TSP_BF16;
     // the C2S conv2 reads an exact zero padding column (sparse.cpp:289-306)
     PadRow pad;
     pad.zero = true;
     return halo_conv_launch(dtype, TSP_F32, d_feats, n, ci, d_nbr, d_plan, d_packed_weight, d_bias, co,
-                            d_out, as_stream(stream), OctantScatter{}, skip, pad);
+                            d_out, s, OctantScatter{}, skip, pad);
+}
+
+extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int ci,
+                                             const int32_t* d_nbr, const void* d_plan,
+                                             const void* d_packed_weight, const float* d_bias, int co,
+                                             const float* d_x, int cin, const int32_t* d_gidx,
+                                             float* d_out, void* stream) {
+    clear_error();
+    return planned_skip(d_feats, dtype, n, ci, d_nbr, d_plan, d_packed_weight, d_bias, co, d_x, cin, d_gidx, d_out,
+                        nullptr, TSP_BF16, as_stream(stream));
 }
 
 extern "C" int tsp_subm_conv3x3_planned_ln(const void* d_feats, int dtype, int64_t n, int ci,

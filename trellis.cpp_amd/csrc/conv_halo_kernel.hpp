@@ -563,6 +563,16 @@ __device__ __forceinline__ void conv_tiles(
                     if (keep) {
                         if constexpr (ODT == TSP_F32) {
                             *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(out) + o) = vs[q][0];
+                            if constexpr (EPI == 2) {
+                                if (skip.out16) {
+                                    const f32x4_t v = vs[q][0];
+                                    const uint2 w16 = skip.out16_bf16
+                                        ? uint2{f32x2_to_bf16x2_bits(v[0], v[1]), f32x2_to_bf16x2_bits(v[2], v[3])}
+                                        : uint2{f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16),
+                                                f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16)};
+                                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(skip.out16) + o) = w16;
+                                }
+                            }
                         } else {
                             uint32_t w[4];
 #pragma unroll

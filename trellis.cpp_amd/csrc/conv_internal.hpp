@@ -43,13 +43,14 @@ bool blaslt_eligible(int x_dtype, int weight_dtype, int out_dtype, int ci, int c
 int blaslt_linear(const void* x, int xdt, int64_t n, int ci, const void* w, const float* bias,
                   int co, int act, const float* residual, void* out, int odt, hipStream_t s);
 // The ConvNeXt MLP in one kernel (mlp.hip): y = x + b2 + W2 . silu(W0 . xn + b0) for 16-bit xn and
-// weights of one dtype dt, C = 128 or 256, the weights packed by mlp_pack (mlp_packed_bytes(c)
-// bytes: W0 then W2 in MFMA operand order), 16-byte aligned xn and packed (mlp_fused_eligible).
+// weights of one dtype dt, C = 128, the weights packed by mlp_pack (mlp_packed_bytes(c) bytes: W0
+// then W2 in MFMA operand order), 16-byte aligned xn and packed (mlp_fused_eligible). With y16
+// set, y is also stored rounded to y16_dtype (TSP_BF16 or TSP_F16) in y16 [n][c].
 size_t mlp_packed_bytes(int c);
 int mlp_pack(const void* w0, const void* w2, int c, void* packed, hipStream_t s);
 bool mlp_fused_eligible(int dt, int c, const void* xn, const void* packed, const float* x, const float* y);
 int mlp_fused(const void* xn, int dt, int64_t n, int c, const void* packed, const float* b0, const float* b2,
-              const float* x, float* y, hipStream_t s);
+              const float* x, float* y, hipStream_t s, void* y16 = nullptr, int y16_dtype = TSP_BF16);
 // Builds the plan of neighbour table `nbr` into `plan`: tiles in the Morton order of the voxels'
 // 8^3 cells when `coords` is given, else tiles of consecutive rows.
 int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, hipStream_t s);
@@ -87,11 +88,15 @@ struct OctantScatter {
 
 // The C2S skip added by the conv's stores (sparse.cpp:302-323): with cin > 0, output row m
 // channel c gets x[gidx[m] / 8][(gidx[m] % 8) * K + c / R] added, K = cin / 8, R = co / K
-// (R % 4 == 0), x f32 [N][cin].
+// (R % 4 == 0), x f32 [N][cin]. With out16 set, the stores also write each output value rounded
+// to bf16 (out16_bf16) or f16 into out16 [M][co]: the next conv's 16-bit input, without a
+// rounding pass over the output.
 struct SkipAdd {
     const float* x = nullptr;
     const int32_t* gidx = nullptr;
     int cin = 0;
+    void* out16 = nullptr;
+    bool out16_bf16 = true;
 };
 
 // The padding row that absent taps read. The reference's is 0 * feats[0] (submconv_pad,
@@ -123,6 +128,12 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                      const void* plan, const void* weight, const float* bias, int co, void* out,
                      hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {},
                      RowNorm ln = {});
+
+// tsp_subm_conv3x3_planned_skip with, when out16 is not null, out also rounded to out16_dtype
+// (TSP_BF16 or TSP_F16) in out16 [n][co] by the same stores.
+int planned_skip(const void* feats, int dtype, int64_t n, int ci, const int32_t* nbr, const void* plan,
+                 const void* packed, const float* bias, int co, const float* x, int cin, const int32_t* gidx,
+                 float* out, void* out16, int out16_dtype, hipStream_t s);
 
 // The thin-channel matrix-core conv (conv_thin_mfma.hip): f16/bf16 features and weights of one
 // dtype, Ci in {8, 16, 32}, Co in {4, 8, 16, 32}, Ci * Co <= 512, a neighbour table, 16-byte

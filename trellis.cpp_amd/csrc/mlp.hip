@@ -68,7 +68,7 @@ template <bool BF16>
 __global__ __launch_bounds__(MLP_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_mlp_ws(const uint16_t* __restrict__ xn, int64_t n, const uint16_t* __restrict__ pw0,
               const float* __restrict__ b0, const uint16_t* __restrict__ pw2, const float* __restrict__ b2,
-              const float* x, float* y) {   // (y may be x: not restrict)
+              const float* x, float* y, uint16_t* y16, bool y16_bf16) {   // (y may be x: not restrict)
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][32 * MLP_XS];   // staged rows, two blocks
     __shared__ f32x4_t sY[MLP_W * 4 * 4 * 64];                              // [wave][col block][j][lane]
     __shared__ __attribute__((aligned(16))) float sB0[MLP_H];
@@ -190,6 +190,15 @@ void k_mlp_ws(const uint16_t* __restrict__ xn, int64_t n, const uint16_t* __rest
         const __amdgpu_buffer_rsrc_t yres = span_rsrc(y + rb * 32 * MLP_C, span);
 #pragma unroll
         for (int e = 0; e < 8; ++e) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv[e]), yres, out_off(e), 0, 0);
+        if (y16) {
+            // the next conv's 16-bit input: y rounded as a rounding pass over it would
+            const __amdgpu_buffer_rsrc_t hres = span_rsrc(y16 + rb * 32 * MLP_C, span / 2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t h = y16_bf16 ? f32_to_bf16_bits(yv[e]) : f32_to_f16_bits(yv[e]);
+                __builtin_amdgcn_raw_buffer_store_b16(h, hres, out_off(e) / 2, 0, 0);
+            }
+        }
     }
 }
 
@@ -215,7 +224,7 @@ bool mlp_fused_eligible(int dt, int c, const void* xn, const void* packed, const
 }
 
 int mlp_fused(const void* xn, int dt, int64_t n, int c, const void* packed, const float* b0, const float* b2,
-              const float* x, float* y, hipStream_t s) {
+              const float* x, float* y, hipStream_t s, void* y16, int y16_dtype) {
     if (n == 0) return TSP_OK;
     if (c != MLP_C) return TSP_ERR_UNSUPPORTED;
     // one workgroup per CU (the staged rows and partial products fill its LDS), each walking row
@@ -231,9 +240,11 @@ int mlp_fused(const void* xn, int dt, int64_t n, int c, const void* packed, cons
     const auto* p0 = static_cast<const uint16_t*>(packed);
     const auto* p2 = p0 + (size_t)4 * c * c;
     if (dt == TSP_BF16)
-        hipLaunchKernelGGL(k_mlp_ws<true>, dim3(grid), dim3(MLP_NT), 0, s, a, n, p0, b0, p2, b2, x, y);
+        hipLaunchKernelGGL(k_mlp_ws<true>, dim3(grid), dim3(MLP_NT), 0, s, a, n, p0, b0, p2, b2, x, y,
+                           static_cast<uint16_t*>(y16), y16_dtype == TSP_BF16);
     else
-        hipLaunchKernelGGL(k_mlp_ws<false>, dim3(grid), dim3(MLP_NT), 0, s, a, n, p0, b0, p2, b2, x, y);
+        hipLaunchKernelGGL(k_mlp_ws<false>, dim3(grid), dim3(MLP_NT), 0, s, a, n, p0, b0, p2, b2, x, y,
+                           static_cast<uint16_t*>(y16), y16_dtype == TSP_BF16);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }

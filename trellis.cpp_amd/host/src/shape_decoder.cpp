@@ -112,6 +112,14 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     // Morton-ordered plans: dc holds each level's coordinates until that level's plans are built
     ops::build_table(dc.as<int32_t>(), n, table, s, status.as<int32_t>(), /*morton_plan=*/true);
     DeviceBuffer scratch, h2;
+    // h rounded to h16dt, the input type of the next ConvNeXt conv (-1: none): written by the
+    // stores of the block or C2S that produced h, so that conv needs no rounding pass of its own
+    DeviceBuffer h16, h16b;
+    int h16dt = -1;
+    auto conv_input16 = [&](const std::string& block) {
+        const ops::Conv nc = ops::conv_of(m, block + ".conv");
+        return nc.xdt != TSP_F32 ? nc.xdt : -1;
+    };
     // The result's host memory is touched on threads of their own while the device works: from
     // the start when the masks fix the final voxel count, else once the last subdivision is known.
     tgr::HostVector<float> result;
@@ -135,16 +143,23 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     const char* dump_dir = std::getenv("TRELLIS_DECODER_DUMP");
     for (size_t si = 0; si < stages.size(); ++si) {
         const Stage& g = stages[si];
-        for (const std::string& p : g.convnext) {   // ConvNeXt stage, ping-pong buffers
+        for (size_t j = 0; j < g.convnext.size(); ++j) {   // ConvNeXt stage, ping-pong buffers
+            const std::string& p = g.convnext[j];
             ops::ConvNext a = ops::convnext_of(m, p, n);
             if (a.c != c) fail(p + ": expected " + std::to_string(c) + " channels");
             if (a.conv.mfma) table.ensure_plan(s);
             const size_t need = ops::convnext_scratch(a, TSP_F32);
             if (scratch.size() < need) scratch = DeviceBuffer(need, s);
             if (h2.size() < (size_t)n * c * 4) h2 = DeviceBuffer((size_t)n * c * 4, s);
+            const int next16 = j + 1 < g.convnext.size() ? conv_input16(g.convnext[j + 1]) : -1;
+            if (next16 >= 0 && h16b.size() < (size_t)n * c * 2) h16b = DeviceBuffer((size_t)n * c * 2, s);
+            const void* x16 = h16dt >= 0 && h16dt == a.conv.xdt ? h16.get() : nullptr;
             ops::Carve sc(scratch.get());
-            ops::run_convnext(a, h.get(), TSP_F32, table.nbr.as<int32_t>(), table.plan.get(), h2.as<float>(), sc, s);
+            ops::run_convnext(a, h.get(), TSP_F32, table.nbr.as<int32_t>(), table.plan.get(), h2.as<float>(), sc, s,
+                              x16, next16 >= 0 ? h16b.get() : nullptr, next16 >= 0 ? next16 : TSP_BF16);
             std::swap(h, h2);
+            std::swap(h16, h16b);
+            h16dt = next16;
         }
         if (g.cin != c) fail(g.c2s + ": expected " + std::to_string(c) + " input channels");
         if (dump_dir) dump_level(dump_dir, (int)si, dc, n, si + 1 == stages.size() ? &h : nullptr, c, s);
@@ -153,10 +168,14 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
             counts = guide_counts.get();
             start_result(counts.back());
         }
+        const int c2s16 = si + 1 < stages.size() && !stages[si + 1].convnext.empty()
+                              ? conv_input16(stages[si + 1].convnext[0]) : -1;
         ops::C2SOut o = ops::run_c2s(m, g.c2s, h.as<float>(), dc.as<int32_t>(), table, g.cin, g.cout, ext, s,
-                                     status.as<int32_t>(), subs_out != nullptr, guide ? counts[si] : -1);
+                                     status.as<int32_t>(), subs_out != nullptr, guide ? counts[si] : -1, c2s16);
         if (subs_out) subs_out->push_back(std::move(o.mask));
         h = std::move(o.feats);
+        h16 = std::move(o.feats16);
+        h16dt = c2s16;
         dc = std::move(o.coords);
         table = std::move(o.table);
         if (table.n != o.m) ops::build_table(dc.as<int32_t>(), o.m, table, s, status.as<int32_t>(), true);

@@ -195,7 +195,7 @@ ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n) {
 
 // The block is one tsp_convnext call; 16-bit vectors are converted to f32 in the scratch first.
 void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr, const void* plan,
-                  float* out, Carve& sc, hipStream_t s) {
+                  float* out, Carve& sc, hipStream_t s, const void* x16, void* out16, int out16_dtype) {
     tsp_convnext_weights w{};
     w.conv_weight = a.conv.w->data;
     w.conv_dtype = a.conv.wdt;
@@ -216,7 +216,8 @@ void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr,
     void* ws = sc.take(nb);
     if (!sc.running()) return;
     if (a.conv.mfma && !plan) fail("sparse_convnext: the matrix-core path needs a conv plan");
-    lib(tsp_convnext(x, xdt, a.n, a.c, nbr, a.conv.mfma ? plan : nullptr, &w, out, ws, nb, flags, s),
+    lib(tsp_convnext_ex(x, xdt, x16, a.n, a.c, nbr, a.conv.mfma ? plan : nullptr, &w, out, out16, out16_dtype, ws, nb,
+                        flags, s),
         "sparse_convnext");
 }
 
@@ -283,7 +284,7 @@ int64_t count_nonzero(const uint8_t* p, size_t n) {
 
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
                Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
-               int32_t* d_status, bool want_mask, int64_t ext_count) {
+               int32_t* d_status, bool want_mask, int64_t ext_count, int out16_dtype) {
     const int64_t n = parent.n;
     if (cin <= 0 || cin % 8 != 0 || cout <= 0 || cout % (cin / 8) != 0)
         fail(prefix + ": C2S needs Cin % 8 == 0 and Cout % (Cin/8) == 0");
@@ -339,6 +340,7 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     r.m = mm;
     r.coords = DeviceBuffer((size_t)mm * 12, s);
     r.feats = DeviceBuffer((size_t)mm * cout * 4, s);
+    if (out16_dtype >= 0) r.feats16 = DeviceBuffer((size_t)mm * cout * 2, s);
     if (mm == 0) return r;
     hip_check(hipMemcpyAsync(r.coords.get(), d_child.get(), (size_t)mm * 12, hipMemcpyDeviceToDevice, s),
               "c2s");
@@ -367,9 +369,11 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
     const size_t nb = tsp_c2s_workspace_bytes(n, mm, cin, cout, &w, conv1.mfma, conv2.mfma, flags);
     DeviceBuffer work(nb, s);
-    lib(tsp_c2s(d_x, n, cin, parent.nbr.as<int32_t>(), conv1.mfma ? parent.plan.get() : nullptr, d_mask.as<uint8_t>(),
-                d_mstart.as<int32_t>(), d_gidx.as<int32_t>(), mm, cout, r.table.nbr.as<int32_t>(),
-                conv2.mfma ? r.table.plan.get() : nullptr, &w, r.feats.as<float>(), work.get(), nb, flags, s),
+    lib(tsp_c2s_ex(d_x, n, cin, parent.nbr.as<int32_t>(), conv1.mfma ? parent.plan.get() : nullptr,
+                   d_mask.as<uint8_t>(), d_mstart.as<int32_t>(), d_gidx.as<int32_t>(), mm, cout, r.table.nbr.as<int32_t>(),
+                   conv2.mfma ? r.table.plan.get() : nullptr, &w, r.feats.as<float>(),
+                   out16_dtype >= 0 ? r.feats16.get() : nullptr, out16_dtype >= 0 ? out16_dtype : TSP_BF16, work.get(),
+                   nb, flags, s),
         prefix);
     return r;
 }

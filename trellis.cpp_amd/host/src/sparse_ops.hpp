@@ -72,10 +72,12 @@ struct ConvNext {
     int c = 0;
 };
 ConvNext convnext_of(const Model& m, const std::string& prefix, int64_t n);
-// out [n][c] f32 = block(x [n][c]) by tsp_convnext (plan needed where conv.mfma); out must not
-// alias x.
+// out [n][c] f32 = block(x [n][c]) by tsp_convnext_ex (plan needed where conv.mfma); out must not
+// alias x. x16 (optional, with f32 x): x rounded to a.conv.xdt; out16 (optional): receives out
+// rounded to out16_dtype, for the next block's x16.
 void run_convnext(const ConvNext& a, const void* x, int xdt, const int32_t* nbr, const void* plan,
-                  float* out, Carve& sc, hipStream_t s);
+                  float* out, Carve& sc, hipStream_t s, const void* x16 = nullptr, void* out16 = nullptr,
+                  int out16_dtype = TSP_BF16);
 size_t convnext_scratch(const ConvNext& a, int xdt);
 
 // A voxel set on the device with its neighbour table and (optionally) conv plan.
@@ -107,12 +109,14 @@ int64_t count_nonzero(const uint8_t* p, size_t n);
 struct C2SOut {
     int64_t m = 0;
     tgr::DeviceBuffer feats, coords;
+    tgr::DeviceBuffer feats16;   // feats rounded to out16_dtype (run_c2s's, when >= 0)
     Table table;
     std::vector<uint8_t> mask;
 };
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
                Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
-               int32_t* d_status = nullptr, bool want_mask = true, int64_t ext_count = -1);
+               int32_t* d_status = nullptr, bool want_mask = true, int64_t ext_count = -1,
+               int out16_dtype = -1);
 
 // out [n][co] f32 = (optionally LN(eps, no affine) of) x [n][ci] . W^T + b for `prefix.weight`
 // ggml [ci, co]; the input (the LN's output) is rounded to act_dtype of the weight.
