@@ -8,7 +8,9 @@ Prints one JSON line. `value` is active voxels per second; `roofline` prices the
 average launch time (HIP events over the timed region, on the stream the kernel runs on)
 against MI355X's dense bf16 MFMA peak; `cpu_baseline` is the CPU oracle (a C restatement of
 the reference's tap-sequential fp32 algorithm) timed on this host's cores over a bounded row
-sample of the same workload.
+sample of the same workload. The table, plan and extra-configuration timings each follow
+SETTLE_MS of untimed calls of the same kind (the shader clock ramps up over the first tens of
+milliseconds of activity; the headline conv follows those builds and its own warm-up steps).
 
     python bench.py [--steps 50] [--warmup 5] [--workload shells256-c128-bf16]
 
@@ -323,7 +325,8 @@ def main():
     # 256^3 C=128 configuration the same shells at ~640K voxels (the size the target names)
     extra = {}
     if w.dtype != "f32" and planned:
-        rf = time_conv(pkg, w, args, max(5, args.steps // 2), 2, out_dtype=torch.float32, reuse=r)
+        rf = time_conv(pkg, w, args, max(5, args.steps // 2), 2, out_dtype=torch.float32, reuse=r,
+                       settle_ms=SETTLE_MS)
         extra["f32_out"] = {"ms_per_step": rf["ms"], "tflops": flops / (rf["ms"] * 1e-3) / 1e12,
                             "frac": flops / (rf["ms"] * 1e-3) / 1e12 / PEAK_TFLOPS[w.dtype]}
     if w.name == "shells256-c128-bf16" and not args.no_extra:
@@ -332,7 +335,7 @@ def main():
         # fp32 64^3 shell (the CPU-reference configuration) and a thin C = 8 layer
         for name in EXTRA_WORKLOADS:
             we = shells.workload(name)
-            re_ = time_conv(pkg, we, args, max(5, args.steps // 2), 2)
+            re_ = time_conv(pkg, we, args, max(5, args.steps // 2), 2, settle_ms=SETTLE_MS)
             fe = 2.0 * we.ci * we.co * re_["pairs"]
             path_e = conv_path(we, args.algo, re_["planned"])
             roof_e = roofline(we, fe, compulsory_bytes(we), re_["ms"], valu=path_e in ("thin", "narrow"))
@@ -340,7 +343,8 @@ def main():
             extra[name] = {
                 "n_voxels": we.n, "active_pairs": re_["pairs"], "c_in": we.ci, "c_out": we.co,
                 "dtype": we.dtype, "algo": path_e,
-                "ms_per_step": re_["ms"], "voxels_per_s": we.n / (re_["ms"] * 1e-3),
+                "ms_per_step": re_["ms"], "steps": max(5, args.steps // 2), "warmup_steps": re_["warmup_steps"],
+                "voxels_per_s": we.n / (re_["ms"] * 1e-3),
                 "tflops": fe / (re_["ms"] * 1e-3) / 1e12, "frac": roof_e["frac"], "roofline": roof_e,
                 "rulebook_ms": re_["rulebook_ms"], "plan_ms": re_["plan_ms"],
                 "table_plan_ms": re_["table_plan_ms"]}
@@ -524,11 +528,29 @@ def roofline(w, flops: float, compulsory: float, ms: float, valu: bool = False) 
     return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}
 
 
-def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None) -> dict:
+SETTLE_MS = 100.0   # untimed calls before a timed loop of short calls: the clock ramps over tens of ms
+
+
+def settle(fn, ms: float = SETTLE_MS) -> int:
+    """Calls fn until `ms` of wall time have passed (at least once), synchronising every few
+    calls so that the time is the device's; returns the number of calls."""
+    import torch
+    t0, k = time.perf_counter(), 0
+    while True:
+        fn()
+        k += 1
+        if k % 4 == 0 or k == 1:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= ms:
+                return k
+
+
+def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None, settle_ms: float = 0.0) -> dict:
     """Times one conv of workload w: the neighbour table and (16-bit, matrix-core shapes) the
-    conv plan are built and timed first, each on its own (reuse: the table and plan of an
-    earlier call on the same workload); then `steps` convs between two HIP events on the
-    stream the kernel runs on."""
+    conv plan are built and timed first, each on its own after SETTLE_MS of untimed calls
+    (reuse: the table and plan of an earlier call on the same workload); then `warmup` untimed
+    convs (and, with settle_ms, more until that much time has passed), then `steps` convs
+    between two HIP events on the stream the kernel runs on."""
     import numpy as np
     import torch
     dev = torch.device("cuda:0")
@@ -544,6 +566,7 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
         # allocated once, as a decoder level reuses them
         nbr = pkg.rulebook_build(coords)
         ws = torch.empty(pkg.lib().tsp_rulebook_workspace_bytes(w.n), dtype=torch.uint8, device=dev)
+        settle(lambda: pkg.rulebook_build(coords, check=False, nbr=nbr, workspace=ws))
         torch.cuda.synchronize()
         ev[0].record(stream)
         for _ in range(5):
@@ -571,6 +594,7 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
         pcoords = coords if args.plan_order == "morton" else None
         plan = pkg.conv_plan_build(nbr, w.n, coords=pcoords)
         packed = pkg.conv_weight_pack(weight)
+        settle(lambda: pkg.conv_plan_build(nbr, w.n, coords=pcoords, plan=plan))
         torch.cuda.synchronize()
         ev[0].record(stream)
         for _ in range(5):
@@ -581,6 +605,8 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
         if pcoords is not None:
             # the table and the Morton plan in one call, on one cell grid (what a decoder level
             # runs); the same table and plan as the two calls above
+            settle(lambda: pkg.rulebook_build_planned(coords, check=False, nbr=nbr, workspace=ws, plan=plan))
+            torch.cuda.synchronize()
             ev[0].record(stream)
             for _ in range(5):
                 pkg.rulebook_build_planned(coords, check=False, nbr=nbr, workspace=ws, plan=plan)
@@ -596,6 +622,7 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
 
     for _ in range(warmup):
         step()
+    extra_warmup = settle(step, settle_ms) if settle_ms > 0 else 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev[0].record(stream)
@@ -605,6 +632,7 @@ def time_conv(pkg, w, args, steps: int, warmup: int, out_dtype=None, reuse=None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return {"ms": ev[0].elapsed_time(ev[1]) / steps, "wall": wall, "pairs": pairs, "planned": planned,
+            "warmup_steps": warmup + extra_warmup,
             "rulebook_ms": rulebook_ms, "plan_ms": plan_ms, "table_plan_ms": table_plan_ms,
             "coords": coords, "feats": feats,
             "weight": weight, "bias": bias, "nbr": nbr, "plan": plan, "packed": packed}
