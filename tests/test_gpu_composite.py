@@ -219,3 +219,85 @@ def test_c2s_rounded_copy(gpu_lib, shells, cin, cout, wtype, o16):
     torch.cuda.synchronize()
     assert torch.equal(out, base)
     assert torch.equal(out16.view(torch.int16), out.cpu().to(t16).cuda().view(torch.int16))
+
+
+def _region_mask(coords, rng, p_keep=0.5):
+    """A subdivision mask whose kept octants depend on the parent's 8^3 region, so that whole
+    32-parent blocks of a tile keep none of some octants (those blocks' conv1 MFMAs for that
+    octant are skipped)."""
+    reg = (coords[:, 0] >> 3) * 73 + (coords[:, 1] >> 3) * 31 + (coords[:, 2] >> 3) * 7
+    keep_reg = np.stack([(np.random.default_rng(o).random(reg.max() + 1) < p_keep)[reg] for o in range(8)], 1)
+    return (keep_reg & (rng.random((len(coords), 8)) < 0.8)).astype(np.uint8).reshape(-1)
+
+
+@pytest.mark.parametrize("cin,cout,wtype", [(256, 256, "bf16"), (512, 256, "f16")])
+def test_c2s_octant_skip_bitexact(gpu_lib, shells, cin, cout, wtype):
+    """tsp_c2s at Cout >= 256 (conv1 with octant stores, no child norm) skips conv1's MFMAs for
+    row blocks whose parents keep none of a wave's octant; its output equals, bit for bit, the
+    same block composed from the single entry points (norm1 + SiLU, the octant conv without the
+    skip, norm2 + SiLU, the skip conv), on a mask that empties whole blocks' octants."""
+    import torch
+    _case(f"c2s octant skip {cin}->{cout} {wtype}")
+    rng = np.random.default_rng(cin + cout + 1)
+    coords = np.ascontiguousarray(shells.sphere_shell(40, 20.0, 12.0, 15.0), np.int32)
+    n = len(coords)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    mask = _region_mask(coords, rng)
+    P = _params(rng, {"norm1.weight": ((cin,), 0.1, 1), "norm1.bias": ((cin,), 0.1, 0),
+                      "conv1.weight": ((8 * cout, 27, cin), 1 / np.sqrt(27 * cin), 0),
+                      "conv1.bias": ((8 * cout,), 0.1, 0),
+                      "conv2.weight": ((cout, 27, cout), 1 / np.sqrt(27 * cout), 0),
+                      "conv2.bias": ((cout,), 0.1, 0)}, wtype)
+    p = {k: v[1] for k, v in P.items()}
+    cc, mt = _dev(coords), _dev(mask)
+    nbr = gpu_lib.rulebook_build(cc)
+    child, gidx, mstart = gpu_lib.subdivide(mt, cc)
+    m = len(gidx)
+    cnbr = gpu_lib.rulebook_build(child)
+    plan, cplan = gpu_lib.conv_plan_build(nbr, n, coords=cc), gpu_lib.conv_plan_build(cnbr, m, coords=child)
+    xd = _dev(x)
+    out = gpu_lib.c2s(xd, nbr, mt, mstart, gidx, m, cout, cnbr, p, plan=plan, child_plan=cplan)
+    t16 = getattr(torch, DT[wtype])
+    h0 = gpu_lib.layer_norm(xd, p["norm1.weight"], p["norm1.bias"], 1e-6, silu=True, out_dtype=t16)
+    g = gpu_lib.subm_conv3x3_planned_octants(h0, nbr, plan, gpu_lib.conv_weight_pack(p["conv1.weight"]),
+                                             p["conv1.bias"], cout, mt, mstart, m)
+    h2 = gpu_lib.layer_norm(g, None, None, 1e-6, silu=True, out_dtype=t16)
+    ref = gpu_lib.subm_conv3x3_planned_skip(h2, cnbr, cplan, gpu_lib.conv_weight_pack(p["conv2.weight"]),
+                                            p["conv2.bias"], cout, xd, gidx)
+    torch.cuda.synchronize()
+    assert m > 0 and torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("cin,cout,wtype", [(128, 64, "bf16"), (256, 128, "f16"), (512, 256, "bf16")])
+def test_c2s_octant_skip_vs_oracle(gpu_lib, orc, shells, cin, cout, wtype):
+    """The same skip in the norm-in-stores kernels (Cout = 64, 128) and the plain octant stores,
+    against the oracle's block, on masks that empty whole blocks' octants."""
+    import torch
+    _case(f"c2s octant skip oracle {cin}->{cout} {wtype}")
+    rng = np.random.default_rng(cin + 5 * cout)
+    coords = np.ascontiguousarray(shells.sphere_shell(24, 12.0, 7.0, 9.0), np.int32)
+    n = len(coords)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    mask = _region_mask(coords, rng)
+    P = _params(rng, {"norm1.weight": ((cin,), 0.1, 1), "norm1.bias": ((cin,), 0.1, 0),
+                      "conv1.weight": ((8 * cout, 27, cin), 1 / np.sqrt(27 * cin), 0),
+                      "conv1.bias": ((8 * cout,), 0.1, 0),
+                      "conv2.weight": ((cout, 27, cout), 1 / np.sqrt(27 * cout), 0),
+                      "conv2.bias": ((cout,), 0.1, 0)}, wtype)
+    cc, mt = _dev(coords), _dev(mask)
+    nbr = gpu_lib.rulebook_build(cc)
+    child, gidx, mstart = gpu_lib.subdivide(mt, cc)
+    m = len(gidx)
+    cnbr = gpu_lib.rulebook_build(child)
+    plans = (gpu_lib.conv_plan_build(nbr, n, coords=cc), gpu_lib.conv_plan_build(cnbr, m, coords=child))
+    out = gpu_lib.c2s(_dev(x), nbr, mt, mstart, gidx, m, cout, cnbr, {k: v[1] for k, v in P.items()},
+                      plan=plans[0], child_plan=plans[1])
+    torch.cuda.synchronize()
+    q = {"c2s." + k: v[0] for k, v in P.items()}
+    wt = {"c2s." + k: (wtype if v[0].ndim >= 2 else "f32") for k, v in P.items()}
+    (ref, rchild, _), floor = rounding_noise_floor(orc, lambda: orc.c2s_block(x, coords, q, "c2s", cout, mask, wt),
+                                                   runs=3)
+    assert np.array_equal(child.cpu().numpy(), rchild)
+    err = orc.rel_err(out.cpu().numpy(), ref)
+    print(f"c2s skip rel={err:.3e} floor={floor:.3e}", flush=True)
+    assert err < _bar(floor)

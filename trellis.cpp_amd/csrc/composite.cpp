@@ -222,6 +222,9 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
     void* h2 = ws.take((size_t)m * cout * dtype_size(in2));
     void* pk1 = cp1.pack_here ? ws.take(tsp_conv_weight_packed_bytes(cin, 8 * cout)) : nullptr;
     void* pk2 = cp2.pack_here ? ws.take(tsp_conv_weight_packed_bytes(cout, cout)) : nullptr;
+    // with octant stores: which of conv1's row blocks hold a parent keeping each octant (the
+    // others' MFMAs for that octant's channels are skipped; their outputs are never stored)
+    auto* blocks = octants ? static_cast<uint32_t*>(ws.take((size_t)ceil_div(n, HB_M) * 4 * 4)) : nullptr;
     if (!ws.base) return TSP_OK;
     int st;
     if ((st = tsp_layer_norm(x, TSP_F32, n, cin, w.norm1_weight, w.norm1_bias, 1e-6f, 1, h0, in1, s))) return st;
@@ -230,6 +233,7 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
         if ((st = tsp_conv_weight_pack(w.conv1_weight, w.conv1_dtype, cin, 8 * cout, pk1, s))) return st;
         p1 = pk1;
     }
+    if (octants && (st = octant_blocks(plan, n, mask, blocks, s))) return st;
     if (norm_in_stores) {
         TSP_REQUIRE((reinterpret_cast<uintptr_t>(p1) & 15) == 0 && (reinterpret_cast<uintptr_t>(mask) & 7) == 0,
                     TSP_ERR_INVALID, "tsp_c2s: packed conv1 weights must be 16-byte aligned, the mask 8-byte");
@@ -239,9 +243,10 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
         osc.cout = cout;
         osc.norm_silu = true;
         osc.norm_eps = 1e-6f;
+        osc.blocks = blocks;
         st = halo_conv_launch(in1, in2, h0, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h2, s, osc);
     } else if (octants) {
-        st = tsp_subm_conv3x3_planned_octants(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, cout, mask, mstart, g, s);
+        st = planned_octants(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, cout, mask, mstart, g, blocks, s);
     } else {
         if (cp1.planned)
             st = tsp_subm_conv3x3_planned_ex(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h1, TSP_F32, 0,

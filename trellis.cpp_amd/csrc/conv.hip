@@ -651,13 +651,9 @@ extern "C" int tsp_subm_conv3x3_planned(const void* d_feats, int dtype, int64_t 
                                        co, d_out, out_dtype, 0, nullptr, stream);
 }
 
-extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, int64_t n, int ci,
-                                                const int32_t* d_nbr, const void* d_plan,
-                                                const void* d_packed_weight, const float* d_bias,
-                                                int cout, const uint8_t* d_mask,
-                                                const int32_t* d_mstart, float* d_out,
-                                                void* stream) {
-    clear_error();
+int tsp::planned_octants(const void* d_feats, int dtype, int64_t n, int ci, const int32_t* d_nbr, const void* d_plan,
+                         const void* d_packed_weight, const float* d_bias, int cout, const uint8_t* d_mask,
+                         const int32_t* d_mstart, float* d_out, const uint32_t* d_blocks, hipStream_t s) {
     TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && ci > 0 && cout > 0, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3_planned_octants: n=%lld ci=%d cout=%d", (long long)n, ci, cout);
     TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
@@ -684,8 +680,20 @@ extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, 
     osc.mask = d_mask;
     osc.mstart = d_mstart;
     osc.cout = cout;
+    osc.blocks = d_blocks;
     return halo_conv_launch(dtype, TSP_F32, d_feats, n, ci, d_nbr, d_plan, d_packed_weight, d_bias,
-                            co, d_out, as_stream(stream), osc);
+                            co, d_out, s, osc);
+}
+
+extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, int64_t n, int ci,
+                                                const int32_t* d_nbr, const void* d_plan,
+                                                const void* d_packed_weight, const float* d_bias,
+                                                int cout, const uint8_t* d_mask,
+                                                const int32_t* d_mstart, float* d_out,
+                                                void* stream) {
+    clear_error();
+    return planned_octants(d_feats, dtype, n, ci, d_nbr, d_plan, d_packed_weight, d_bias, cout, d_mask, d_mstart,
+                           d_out, nullptr, as_stream(stream));
 }
 
 int tsp::planned_skip(const void* d_feats, int dtype, int64_t n, int ci, const int32_t* d_nbr, const void* d_plan,

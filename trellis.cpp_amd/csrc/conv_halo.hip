@@ -31,7 +31,46 @@ __global__ void k_pack_trailer_clear(uint32_t* __restrict__ trailer) {
     trailer[threadIdx.x] = 0u;
 }
 
+// One workgroup per tile, one thread per position: the octants each position's parent keeps
+// (mask bytes != 0), ORed over each 32-position block (a wave's ballot covers two) into the word
+// of its row group: bit 4 o + b for block b (0..3) of the 128 positions of row group p / 128.
+__global__ __launch_bounds__(HB_M) void k_octant_blocks(const int32_t* __restrict__ vox, int64_t n,
+                                                       const uint8_t* __restrict__ mask,
+                                                       uint32_t* __restrict__ out) {
+    __shared__ uint32_t sw[HB_M / 128];
+    const int64_t tile = blockIdx.x;
+    const int p = threadIdx.x, lane = p & 63, wave = p >> 6;
+    if (p < HB_M / 128) sw[p] = 0u;
+    __syncthreads();
+    const int32_t v = vox[tile * HB_M + p];
+    uint32_t kept = 0;
+    if (v >= 0 && v < n) {
+#pragma unroll
+        for (int o = 0; o < 8; ++o) kept |= (mask[8 * (int64_t)v + o] != 0 ? 1u : 0u) << o;
+    }
+    uint32_t bits = 0;
+    const int b0 = (wave & 1) * 2;   // this wave's first block within its row group
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+        const uint64_t b = __ballot((kept >> o) & 1u);
+        bits |= ((uint32_t)(b & 0xffffffffull) != 0u ? 1u : 0u) << (4 * o + b0);
+        bits |= ((uint32_t)(b >> 32) != 0u ? 1u : 0u) << (4 * o + b0 + 1);
+    }
+    if (lane == 0 && bits) atomicOr(&sw[wave >> 1], bits);
+    __syncthreads();
+    if (p < HB_M / 128) out[tile * (HB_M / 128) + p] = sw[p];
+}
+
 }  // namespace
+
+int octant_blocks(const void* plan, int64_t n, const uint8_t* mask, uint32_t* out, hipStream_t s) {
+    const int64_t n_tiles = ceil_div(n, HB_M);
+    if (n_tiles == 0) return TSP_OK;
+    const PlanView pv = carve_plan(const_cast<void*>(plan), n_tiles);
+    hipLaunchKernelGGL(k_octant_blocks, dim3((unsigned)n_tiles), dim3(HB_M), 0, s, pv.vox, n, mask, out);
+    TSP_CHECK_LAUNCH();
+    return TSP_OK;
+}
 
 bool halo_fits(int64_t n, int ci) { return n * (int64_t)ci * 2 < ((int64_t)1 << 32); }
 

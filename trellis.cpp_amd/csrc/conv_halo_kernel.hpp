@@ -262,13 +262,27 @@ __device__ __forceinline__ void conv_tiles(
                                     (int)plan.act[(tl * 4 + rgs) * HB_ACT_WORDS + k])
                               : ~0u;
     };
+    // With octant stores: the wave's 4 blocks that hold a parent keeping the wave's octant
+    // (wave-uniform; all set when the caller gave no block words). Every tap's MFMAs of the other
+    // blocks are skipped, whatever the weights: their outputs are never stored.
+    uint32_t ob = 15u;
+    auto load_ob = [&](int64_t tl) -> uint32_t {
+        if constexpr (EPI == 1 || EPI == 4 || EPI == 5) {
+            if (osc.blocks) {
+                const int rgs = __builtin_amdgcn_readfirstlane(rg);
+                const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane((int)osc.blocks[tl * 4 + rgs]);
+                return (w >> (4 * __builtin_amdgcn_readfirstlane(oct))) & 15u;
+            }
+        }
+        return 15u;
+    };
     // the act bits of tap t for the wave's 4 blocks (t compile-time after unrolling). The empty
     // asm re-reads the word in a scalar register at each use: the tests stay scalar branches on
     // it, rather than 108 lane masks computed once and spilled.
     auto tap_bits = [&](int t) -> uint32_t {
         uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)ab[(4 * t) >> 5]);
         asm volatile("" : "+s"(v));
-        return (v >> ((4 * t) & 31)) & 15u;
+        return (v >> ((4 * t) & 31)) & ob;
     };
 
     // slice loads: wave w streams the 32-slot blocks w + WAVES j, lane pairs loading the two
@@ -758,6 +772,7 @@ __device__ __forceinline__ void conv_tiles(
                 H = h0;
                 direct = h1 != 0;
                 load_act(tile, ab);
+                ob = load_ob(tile);
             } else {
                 tile_plan<NT>(nbr, n, row0, sL, reinterpret_cast<int32_t*>(&sH0[0][0][0]),
                               reinterpret_cast<uint32_t*>(&sH1[0][0][0]), sRed, H, direct);
@@ -897,6 +912,7 @@ __device__ __forceinline__ void conv_tiles(
                 for (int j = 0; j < PIECES; ++j) nrow[j] = nro[piece_slot(j) + (lane >> 1)];
                 uint32_t nab[HB_ACT_WORDS];
                 load_act(ntile, nab);
+                const uint32_t nob = load_ob(ntile);
                 run_slice(acc, I0{}, NO{}, sH0, sH1, nkc - 2, nkc - 1, nullptr);
                 // the last slice streams the next tile's slice 0 (rows clamped to 0 where the
                 // plan holds none, e.g. a direct tile) and the first taps of its weights
@@ -917,6 +933,7 @@ __device__ __forceinline__ void conv_tiles(
                 direct = ndirect != 0;
 #pragma unroll
                 for (int k = 0; k < HB_ACT_WORDS; ++k) ab[k] = nab[k];
+                ob = nob;
             } else {
                 f32x16_t acc[RB][CB];
                 zero(acc);

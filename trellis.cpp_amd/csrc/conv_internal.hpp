@@ -84,7 +84,15 @@ struct OctantScatter {
     int cout = 0;
     bool norm_silu = false;
     float norm_eps = 0.f;
+    // Optional, from octant_blocks: word (tile * 4 + row group) has bit 4 o + b set when some
+    // parent of 32-row block b of that row group keeps octant o. The MFMAs of a block whose
+    // parents keep none of a wave's octant are skipped: those outputs are never stored.
+    const uint32_t* blocks = nullptr;
 };
+
+// The words OctantScatter::blocks reads, for a stored plan of n parents and their mask [8 n]:
+// out [n_tiles * 4].
+int octant_blocks(const void* plan, int64_t n, const uint8_t* mask, uint32_t* out, hipStream_t s);
 
 // The C2S skip added by the conv's stores (sparse.cpp:302-323): with cin > 0, output row m
 // channel c gets x[gidx[m] / 8][(gidx[m] % 8) * K + c / R] added, K = cin / 8, R = co / K
@@ -128,6 +136,12 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                      const void* plan, const void* weight, const float* bias, int co, void* out,
                      hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {},
                      RowNorm ln = {});
+
+// tsp_subm_conv3x3_planned_octants with, when blocks is not null, the MFMAs of row blocks whose
+// parents keep none of a wave's octant skipped (blocks from octant_blocks).
+int planned_octants(const void* feats, int dtype, int64_t n, int ci, const int32_t* nbr, const void* plan,
+                    const void* packed, const float* bias, int cout, const uint8_t* mask, const int32_t* mstart,
+                    float* out, const uint32_t* blocks, hipStream_t s);
 
 // tsp_subm_conv3x3_planned_skip with, when out16 is not null, out also rounded to out16_dtype
 // (TSP_BF16 or TSP_F16) in out16 [n][co] by the same stores.
