@@ -1088,3 +1088,44 @@ def test_planned_ln_nonfinite_row0(gpu_lib, orc, shells):
     keep = ~absent & ~refs0
     ref = orc.layer_norm(orc.subm_conv_f64(feats, nbr, weight, bias), nw, nb, 1e-6)
     assert orc.rel_err(out[keep], ref[keep]) < TOL_16_OUT
+
+
+@pytest.mark.parametrize("seed", list(range(12)))
+def test_planned_random_shapes(gpu_lib, orc, shells, seed):
+    """Seeded random shapes through the planned conv with a Morton plan: channel counts whose
+    slice count is odd (the tile loop without cross-tile pipelining) or even (with it), output
+    widths of one to five column tiles, band or scattered voxel sets of 1 to ~12 K voxels, bf16
+    and f16, f32 and 16-bit output. Against the fp64 oracle, and bit for bit against the
+    unplanned matrix-core conv (the same accumulation order per output, tiles of consecutive
+    rows built inside the kernel, which takes Ci % 32 == 0)."""
+    import torch
+    rng = np.random.default_rng(1000 + seed)
+    ci = int(rng.choice([16, 32, 48, 64, 80, 96, 112, 128, 144, 192, 256]))
+    co = int(rng.choice([64, 128, 192, 256, 320]))
+    key = "bf16" if seed % 2 == 0 else "f16"
+    dt = torch.bfloat16 if key == "bf16" else torch.float16
+    if seed % 3 == 2:
+        coords = shells.random_distinct_voxels(int(rng.integers(1, 6000)), 96, seed)
+    else:
+        shapes = shells.random_shapes(rng, 48, 2, 6.0, 16.0, boxes=seed % 3 == 1)
+        coords = shells.band_voxels(shapes, 48, 2.0)
+        coords = coords[: int(rng.integers(1, len(coords) + 1))]
+    coords = np.ascontiguousarray(coords, np.int32)
+    n = len(coords)
+    _case(f"planned random seed={seed} n={n} ci={ci} co={co} {key}")
+    feats = shells.round_to(rng.standard_normal((n, ci)).astype(np.float32), key)
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32), key)
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    f, b = _dev(feats, dt), _dev(bias, torch.float32)
+    pw = gpu_lib.conv_weight_pack(_dev(weight, dt))
+    odt = torch.float32 if seed % 4 < 2 else dt
+    out = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, co, out_dtype=odt)
+    unplanned = gpu_lib.subm_conv3x3(f, nbr, _dev(weight, dt), b, out_dtype=odt, algo="mfma") if ci % 32 == 0 \
+        else None
+    torch.cuda.synchronize()
+    ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
+    assert orc.rel_err(out.float().cpu().numpy(), ref) < (TOL_16 if odt == torch.float32 else TOL_16_OUT)
+    assert unplanned is None or torch.equal(out, unplanned)
