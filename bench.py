@@ -15,7 +15,8 @@ milliseconds of activity; the headline conv follows those builds and its own war
     python bench.py [--steps 50] [--warmup 5] [--workload shells256-c128-bf16]
 
 `--workload decoder-shells64-c1024` times the whole texture decoder stack instead (one decode
-per step, through the C++ host library): see trellis_cpp_amd.shells.decoder_workload.
+per step, through the C++ host library): see trellis_cpp_amd.shells.decoder_workload. The default
+line's `extra` holds the other conv configurations and 3 decodes of that stack.
 """
 from __future__ import annotations
 
@@ -44,6 +45,11 @@ def _load(name, path, pkg_dir=None):
     sys.modules[name] = mod
     spec.loader.exec_module(mod)
     return mod
+
+
+def progress(msg: str) -> None:
+    """A line on stderr as each part of the run ends (stdout holds only the JSON line)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
 def load_package():
@@ -212,6 +218,31 @@ def decoder_bench(args) -> dict:
     }
 
 
+DECODER_WORKLOAD = "decoder-shells64-c1024"
+
+
+def decoder_extra(args) -> dict:
+    """decoder_bench on the decoder workload with a short step count and no CPU leg, for the
+    default line's `extra`; a failure is reported in the entry, not raised."""
+    import torch
+    torch.cuda.empty_cache()
+    dargs = argparse.Namespace(**vars(args))
+    dargs.workload, dargs.steps, dargs.warmup = DECODER_WORKLOAD, 3, 1
+    dargs.no_cpu, dargs.prepare_only = True, ""
+    t0 = time.perf_counter()
+    try:
+        d = decoder_bench(dargs)
+    except (SystemExit, Exception) as e:    # decoder_bench raises SystemExit on a failed child
+        return {"error": str(e)[-2000:]}
+    return {"ms_per_step": d["ms_per_step"], "min_ms": d["min_ms"], "steps": dargs.steps,
+            "warmup_steps": dargs.warmup, "voxels_per_s": d["value"], "tflops": d["tflops"],
+            "frac": d["roofline"]["frac"], "device_gb_in_use": d["device_gb_in_use"],
+            "voxels_per_level": d["config"]["voxels_per_level"], "channels": d["config"]["channels"],
+            "wall_s": time.perf_counter() - t0,
+            "note": "one decode per step: host latent, coordinates and masks in, host features out "
+                    "(trellis::tex_decode, random-init bf16 weights)"}
+
+
 def decoder_cpu_baseline(w, flops_dense: float, budget_s: float) -> dict:
     """The CPU oracle's conv (the reference's dense-over-27-taps fp32 algorithm) timed on a row
     sample of the decoder's widest conv (stage 0: ch[0] -> ch[0] on the latent voxels), its
@@ -304,6 +335,7 @@ def main():
 
     w = shells.workload(args.workload)
     r = time_conv(pkg, w, args, args.steps, args.warmup)
+    progress(f"{w.name}: {r['ms']:.4f} ms per step")
     ms, pairs, planned = r["ms"], r["pairs"], r["planned"]
     flops = 2.0 * w.ci * w.co * pairs
     flops_dense = 2.0 * w.ci * w.co * 27 * w.n
@@ -348,11 +380,17 @@ def main():
                 "tflops": fe / (re_["ms"] * 1e-3) / 1e12, "frac": roof_e["frac"], "roofline": roof_e,
                 "rulebook_ms": re_["rulebook_ms"], "plan_ms": re_["plan_ms"],
                 "table_plan_ms": re_["table_plan_ms"]}
+            progress(f"{name}: {re_['ms']:.4f} ms per step")
             del re_
+        # the whole texture decoder stack (a few decodes through the C++ host library, in a
+        # child process), so that its time is in the same line
+        extra[DECODER_WORKLOAD] = decoder_extra(args)
+        progress(f"{DECODER_WORKLOAD}: {extra[DECODER_WORKLOAD].get('ms_per_step')} ms per decode")
 
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(w, r["nbr"].cpu().numpy(), args.cpu_seconds)
+        progress("cpu baseline done")
 
     res = {
         "metric": "active voxels/s & TFLOP/s per sparse conv layer; % MFMA/HBM roofline",
