@@ -288,7 +288,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="shells256-c128-bf16")
-    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather", "thin", "thin_mfma"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "mfma", "narrow", "mfma_gather", "thin", "thin_mfma", "f32_mfma"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other conv configurations")
@@ -527,7 +527,8 @@ def kernel_sources_sha(files) -> str:
 def conv_path(w, algo: str, planned: bool) -> str:
     """The kernel the library runs for workload w under `algo` (tsp_subm_conv3x3's AUTO order:
     matrix-core for 16-bit Ci % 32 / Co % 64 shapes -- here with a plan --, then the thin
-    matrix-core kernel, the thin VALU kernel, the tiled VALU kernel)."""
+    matrix-core kernel, the thin VALU kernel, the fp32 matrix-core kernel, the tiled VALU
+    kernel)."""
     if planned:
         return "mfma-planned"
     if algo != "auto":
@@ -537,6 +538,8 @@ def conv_path(w, algo: str, planned: bool) -> str:
         return "thin_mfma"
     if thin and w.ci % 4 == 0:
         return "thin"
+    if w.dtype == "f32" and w.ci % 16 == 0 and w.co % 32 == 0:
+        return "f32_mfma"
     return "narrow"
 
 

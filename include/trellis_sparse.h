@@ -41,7 +41,8 @@ typedef enum {
 typedef enum { TSP_F32 = 0, TSP_F16 = 1, TSP_BF16 = 2 } tsp_dtype;
 
 /* Conv kernel selection. AUTO picks MFMA for 16-bit features with Ci % 32 == 0 and
- * Co % 64 == 0, THIN_MFMA and then THIN where their shapes fit, and NARROW otherwise.
+ * Co % 64 == 0, THIN_MFMA and then THIN where their shapes fit, F32_MFMA where its shapes fit,
+ * and NARROW otherwise.
  *   MFMA         matrix-core kernel that stages each tile's distinct neighbour rows in LDS
  *   NARROW       VALU fp32-FMA kernel over 64 x 64 output tiles, any dtype mix and channel count
  *   MFMA_GATHER  matrix-core kernel that gathers neighbour rows straight from L2/HBM (no LDS
@@ -52,10 +53,14 @@ typedef enum { TSP_F32 = 0, TSP_F16 = 1, TSP_BF16 = 2 } tsp_dtype;
  *                contraction (K = 27 Ci) of 16 x 16 x 32 matrix-core steps, each lane gathering
  *                one 16-byte piece of a neighbour row per step straight into its operand; f16/bf16
  *                feats and weights of one dtype, Ci in {8, 16, 32}, Co in {4, 8, 16, 32},
- *                Ci * Co <= 512, out f32 or the feats' dtype, 16-byte aligned feats and weights */
+ *                Ci * Co <= 512, out f32 or the feats' dtype, 16-byte aligned feats and weights
+ *   F32_MFMA     fp32 matrix-core kernel (v_mfma_f32_32x32x2_f32) for f32 feats and weights (the
+ *                reference's cast-to-f32 mode, sparse.cpp:16-19): Ci % 16 == 0, Co % 32 == 0,
+ *                16-byte aligned feats and weights, any output dtype; operands gathered from L2,
+ *                the taps of small convs split over up to 8 waves a tile */
 typedef enum {
     TSP_ALGO_AUTO = 0, TSP_ALGO_MFMA = 1, TSP_ALGO_NARROW = 2, TSP_ALGO_MFMA_GATHER = 3,
-    TSP_ALGO_THIN = 4, TSP_ALGO_THIN_MFMA = 5
+    TSP_ALGO_THIN = 4, TSP_ALGO_THIN_MFMA = 5, TSP_ALGO_F32_MFMA = 6
 } tsp_algo;
 
 /* Thread-local message for the last failing call on this thread ("" if none). */

@@ -91,8 +91,12 @@ def test_conv_validation(pkg):
     assert f(n=-1) == 1
     assert f(ci=0) == 1 and f(co=-4) == 1
     assert f(fdt=7) == 1 and f(odt=9) == 1
-    assert f(algo=6) == 1
+    assert f(algo=7) == 1
     assert f(algo=5) == 4 and "thin matrix-core" in _err(pkg)     # THIN_MFMA: ci=64 is not its shape
+    assert f(algo=6) == 4 and "fp32 matrix-core" in _err(pkg)     # F32_MFMA: bf16 feats
+    assert f(algo=6, fdt=0, wdt=2) == 4                             # f32 feats, bf16 weights
+    assert f(algo=6, fdt=0, wdt=0, ci=40) == 4                      # ci % 16 != 0
+    assert f(algo=6, fdt=0, wdt=0, co=48) == 4                      # co % 32 != 0
     assert f(nbr=NULL) == 1
     assert f(out=FAKE) == 1 and "alias" in _err(pkg)
     assert f(n=0) == 0                                              # empty: no-op

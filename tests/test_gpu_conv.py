@@ -198,13 +198,14 @@ def test_planned_skip(gpu_lib, orc, shells, cin, ci, co, n, dtype_name):
 
 
 @pytest.mark.parametrize("bad", ["inf", "nan"])
-@pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "unsorted"])
+@pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "f32_narrow", "unsorted"])
 def test_nonfinite_row0(gpu_lib, orc, shells, path, bad):
     """Absent taps read the padding row 0 * feats[0] (sparse.cpp:81-85). With an Inf or a NaN in
     row 0 every output row that has an absent tap is NaN in every channel, on every kernel path
     (the LDS-staged kernel with and without a stored plan, its direct path on unsorted rows, the
-    gather kernel, the VALU kernel in 16 and 32 bits); rows whose 27 taps are all present keep
-    their finite values (checked against the oracle away from row 0's own neighbours)."""
+    gather kernel, the VALU kernel in 16 and 32 bits, the fp32 matrix-core kernel that AUTO takes
+    for f32); rows whose 27 taps are all present keep their finite values (checked against the
+    oracle away from row 0's own neighbours)."""
     _case(f"non-finite row 0 {path} {bad}")
     import torch
     rng = np.random.default_rng(23)
@@ -214,7 +215,7 @@ def test_nonfinite_row0(gpu_lib, orc, shells, path, bad):
         coords = np.concatenate([coords[:1], rng.permutation(coords[1:])])
     coords = np.ascontiguousarray(coords, np.int32)
     n, ci, co = len(coords), 32, 64
-    key = "f32" if path == "f32" else "bf16"
+    key = "f32" if path.startswith("f32") else "bf16"
     feats = rng.standard_normal((n, ci)).astype(np.float32)
     feats[0, 7] = np.inf if bad == "inf" else np.nan
     weight = (rng.standard_normal((co, 27, ci)) / 30).astype(np.float32)
@@ -228,7 +229,7 @@ def test_nonfinite_row0(gpu_lib, orc, shells, path, bad):
         out = _run_planned(gpu_lib, coords, feats, weight, bias, dt)
     else:
         algo = {"auto": "auto", "unsorted": "mfma", "mfma_gather": "mfma_gather", "narrow": "narrow",
-                "f32": "auto"}[path]
+                "f32": "auto", "f32_narrow": "narrow"}[path]
         out, _ = _run(gpu_lib, coords, feats, weight, bias, dt, algo=algo)
     t = nbr.reshape(27, n)
     absent = (t == n).any(axis=0)
@@ -308,7 +309,7 @@ def test_narrow_fp32_ragged(gpu_lib, orc, shells, ci, co):
     rng = np.random.default_rng(ci + 100 * co)
     coords, feats, weight, bias = _rand_case(shells, rng, 1500, ci, co, "f32")
     ref = orc.subm_conv_f64(feats, orc.neighbor_table(coords), weight, bias)
-    out, _ = _run(gpu_lib, coords, feats, weight, bias, torch.float32)
+    out, _ = _run(gpu_lib, coords, feats, weight, bias, torch.float32, algo="narrow")
     assert orc.rel_err(out, ref) < TOL_32
 
 
@@ -359,12 +360,79 @@ def test_isolated_voxels_and_empty(gpu_lib, orc):
 
 
 def test_shell64_fp32_workload(gpu_lib, orc, shells):
+    """The fp32 64^3 shell on AUTO's kernel (the fp32 matrix-core one) and on the VALU kernel."""
     _case("shell64-c64-f32")
     import torch
     w = shells.workload("shell64-c64-f32")
     ref = orc.subm_conv_f64(w.feats, orc.neighbor_table(w.coords), w.weight, w.bias)
-    out, _ = _run(gpu_lib, w.coords, w.feats, w.weight, w.bias, torch.float32)
-    assert orc.rel_err(out, ref) < TOL_32
+    for algo in ("auto", "f32_mfma", "narrow"):
+        out, _ = _run(gpu_lib, w.coords, w.feats, w.weight, w.bias, torch.float32, algo=algo)
+        assert orc.rel_err(out, ref) < TOL_32, algo
+
+
+@pytest.mark.parametrize("ci,co,n", [(16, 32, 1500), (64, 64, 0), (48, 96, 3000), (32, 128, 40000),
+                                     (64, 64, 380934), (128, 96, 200000)])
+def test_f32_mfma_vs_oracle(gpu_lib, orc, shells, ci, co, n):
+    """The fp32 matrix-core kernel (algo="f32_mfma", AUTO's choice for f32 layers with Ci % 16 == 0
+    and Co % 32 == 0, after the thin kernels' shapes) in both launch shapes it picks by size -- the
+    taps of 32-row tiles split over 4 waves (up to 40 K voxels here), one wave per 64-row tile
+    (200 K and 381 K voxels) -- with 32- and 64-channel column tiles, against the fp64 oracle
+    (every row, or 4000 sampled rows plus the first and last tiles at the larger sizes), against
+    the VALU kernel on every row, bitwise repeatable and equal to AUTO, and with bf16 and f16
+    outputs."""
+    _case(f"f32 mfma ci={ci} co={co} n={n}")
+    import torch
+    rng = np.random.default_rng(7 * ci + co)
+    if n > 6000:
+        coords = shells.sphere_shell(160, 70.0, 50.0, 60.0)[:n]
+    else:
+        coords = shells.sphere_shell(48, 24.0, 14.0, 16.0)[:n or None]
+    coords = np.ascontiguousarray(coords, np.int32)
+    n = len(coords)
+    feats = rng.standard_normal((n, ci)).astype(np.float32)
+    weight = (rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32)
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    f, w, b = _dev(feats, torch.float32), _dev(weight, torch.float32), _dev(bias, torch.float32)
+    out = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="f32_mfma")
+    out2 = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="f32_mfma")
+    auto = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="auto")
+    outn = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="narrow")
+    o16 = {dt: gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=dt, algo="f32_mfma")
+           for dt in (torch.bfloat16, torch.float16)}
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    if not (co <= 32 and ci * co <= 512):    # AUTO's choice unless the thin VALU kernel takes the shape
+        assert torch.equal(out, auto)
+    got = out.cpu().numpy()
+    nbr_h = nbr.cpu().numpy()
+    if n > 6000:
+        rows = np.unique(np.concatenate([np.arange(64), np.arange(n - 64, n), rng.integers(0, n, 4000)]))
+        ref = orc.subm_conv_f64_rows(feats, nbr_h, weight, bias, rows)
+    else:
+        rows = np.arange(n)
+        ref = orc.subm_conv_f64(feats, nbr_h, weight, bias)
+    assert orc.rel_err(got[rows], ref) < TOL_32
+    assert orc.rel_err(got, outn.cpu().numpy()) < TOL_32
+    for dt, o in o16.items():
+        assert orc.rel_err(o.float().cpu().numpy()[rows], ref) < TOL_16_OUT, dt
+
+
+def test_f32_mfma_rejects(gpu_lib, shells):
+    """algo="f32_mfma" outside its shapes: 16-bit features, mixed dtypes, Ci % 16 != 0, Co % 32 != 0."""
+    _case("f32 mfma rejects")
+    import torch
+    coords = np.ascontiguousarray(shells.sphere_shell(24, 12.0, 7.0, 9.0), np.int32)
+    n = len(coords)
+    nbr = gpu_lib.rulebook_build(torch.from_numpy(coords).cuda())
+    b = torch.zeros(64, dtype=torch.float32, device="cuda")
+    for fdt, wdt, ci, co in ((torch.bfloat16, torch.bfloat16, 64, 64), (torch.float32, torch.float16, 64, 64),
+                             (torch.float32, torch.float32, 40, 64), (torch.float32, torch.float32, 64, 48)):
+        f = torch.zeros((n, ci), dtype=fdt, device="cuda")
+        w = torch.zeros((co, 27, ci), dtype=wdt, device="cuda")
+        with pytest.raises(gpu_lib.TspError, match="fp32 matrix-core"):
+            gpu_lib.subm_conv3x3(f, nbr, w, b[:co], out_dtype=torch.float32, algo="f32_mfma")
 
 
 @pytest.mark.parametrize("name", ["ellipsoids128-c256-bf16", "shells256-c128-bf16"])
@@ -411,7 +479,8 @@ def _nan_aware(out, ref, tol):
 
 
 @pytest.mark.parametrize("bad", ["inf", "nan"])
-@pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "unsorted", "skip"])
+@pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "f32_narrow", "unsorted",
+                                  "skip"])
 def test_zero_padding_row(gpu_lib, orc, shells, path, bad):
     """TSP_CONV_ZERO_PAD: absent taps read an exact zero row, as the C2S conv2 reads hn's zero
     padding column (sparse.cpp:289-306). With an Inf or a NaN in feature row 0, only the rows
@@ -426,7 +495,7 @@ def test_zero_padding_row(gpu_lib, orc, shells, path, bad):
         coords = np.concatenate([coords[:1], rng.permutation(coords[1:])])
     coords = np.ascontiguousarray(coords, np.int32)
     n, ci, co = len(coords), 32, 64
-    key = "f32" if path == "f32" else "bf16"
+    key = "f32" if path.startswith("f32") else "bf16"
     feats = rng.standard_normal((n, ci)).astype(np.float32)
     feats[0, 5] = np.inf if bad == "inf" else np.nan
     weight = (rng.standard_normal((co, 27, ci)) / 30).astype(np.float32)
@@ -455,7 +524,7 @@ def test_zero_padding_row(gpu_lib, orc, shells, path, bad):
             ref = ref + np.repeat(x.reshape(-1, k)[np.arange(n)], co // k, axis=1)
     else:
         algo = {"auto": "auto", "unsorted": "mfma", "mfma_gather": "mfma_gather", "narrow": "narrow",
-                "f32": "auto"}[path]
+                "f32": "auto", "f32_narrow": "narrow"}[path]
         out = gpu_lib.subm_conv3x3(f, nbr_d, w, b, out_dtype=torch.float32, algo=algo, zero_pad=True)
     torch.cuda.synchronize()
     out = out.cpu().numpy()

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtrellis_sparse.so")
 
 TSP_F32, TSP_F16, TSP_BF16 = 0, 1, 2
-ALGO = {"auto": 0, "mfma": 1, "narrow": 2, "mfma_gather": 3, "thin": 4, "thin_mfma": 5}
+ALGO = {"auto": 0, "mfma": 1, "narrow": 2, "mfma_gather": 3, "thin": 4, "thin_mfma": 5, "f32_mfma": 6}
 STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "RANGE", 4: "UNSUPPORTED", 5: "WORKSPACE"}
 
 # Every extern "C" entry point the header declares (checked by the CPU test suite).

@@ -18,6 +18,9 @@
 //                     prefetching the next chunk while the current one multiplies.
 //   * k_conv_narrow -- VALU fp32 FMA, any dtype mix and any channel count. LDS-tiled 64 voxels
 //                     x 64 channels, each thread a 4x4 register block.
+// The entry point also dispatches to the thin kernels (conv_thin.hip, conv_thin_mfma.hip) and the
+// fp32 matrix-core kernel (conv_f32_mfma.hip), which AUTO takes for f32 features and weights with
+// Ci % 16 == 0 and Co % 32 == 0 before falling back to k_conv_narrow.
 #include <algorithm>
 
 #include "conv_internal.hpp"
@@ -494,7 +497,7 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
     TSP_CONV_COMMON_CHECKS("tsp_subm_conv3x3");
     TSP_REQUIRE(dtype_valid(feat_dtype) && dtype_valid(weight_dtype) && dtype_valid(out_dtype),
                 TSP_ERR_INVALID, "tsp_subm_conv3x3: bad dtype");
-    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_THIN_MFMA, TSP_ERR_INVALID,
+    TSP_REQUIRE(algo >= TSP_ALGO_AUTO && algo <= TSP_ALGO_F32_MFMA, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3: bad algo %d", algo);
     TSP_REQUIRE((flags & ~TSP_CONV_ZERO_PAD) == 0, TSP_ERR_INVALID, "tsp_subm_conv3x3: bad flags %d",
                 flags);
@@ -542,6 +545,16 @@ extern "C" int tsp_subm_conv3x3_ex(const void* d_feats, int feat_dtype, int64_t 
                         "tsp_subm_conv3x3: the thin kernel needs co in {4, 8, 16, 32}, ci %% 4 == 0, "
                         "ci * co <= 512, n * ci < 2^32, 16-byte aligned feats and a dtype pair of the "
                         "VALU kernel (got ci=%d co=%d)", ci, co);
+            return st;
+        }
+    }
+    if (algo == TSP_ALGO_F32_MFMA || algo == TSP_ALGO_AUTO) {
+        const int st = f32_mfma_launch(feat_dtype, weight_dtype, out_dtype, d_feats, n, ci, d_nbr, d_weight, d_bias,
+                                       co, d_out, s, pad);
+        if (st != TSP_ERR_UNSUPPORTED || algo == TSP_ALGO_F32_MFMA) {
+            TSP_REQUIRE(st != TSP_ERR_UNSUPPORTED, TSP_ERR_UNSUPPORTED,
+                        "tsp_subm_conv3x3: the fp32 matrix-core kernel needs f32 feats and weights, ci %% 16 == 0, "
+                        "co %% 32 == 0 and 16-byte aligned feats and weights (got ci=%d co=%d)", ci, co);
             return st;
         }
     }

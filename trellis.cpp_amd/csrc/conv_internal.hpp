@@ -157,6 +157,13 @@ bool thin_mfma_fits(int fdt, int wdt, int ci, int co);
 int thin_mfma_launch(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad);
 
+// The fp32 matrix-core conv (conv_f32_mfma.hip): f32 features and weights, Ci % 16 == 0,
+// Co % 32 == 0, a neighbour table, 16-byte aligned features and weights. Returns
+// TSP_ERR_UNSUPPORTED (with no message) for anything else.
+bool f32_mfma_fits(int fdt, int wdt, int ci, int co, const void* feats, const void* weight);
+int f32_mfma_launch(int fdt, int wdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
+                    const void* weight, const float* bias, int co, void* out, hipStream_t s, PadRow pad);
+
 // The thin-channel VALU conv (conv_thin.hip): Co in {4, 8, 16, 32}, Ci % 4 == 0, Ci * Co <= 512,
 // a neighbour table, 16-byte aligned features. Returns TSP_ERR_UNSUPPORTED (with no message) for
 // anything else.
