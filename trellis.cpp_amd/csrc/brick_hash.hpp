@@ -140,4 +140,39 @@ __device__ __forceinline__ void hash_neighbours(const HashView& h, int32_t x, in
                 r[qx * 9 + qy * 3 + q] = ez ? by3[qx][qy][q + 1] : by3[qx][qy][q];
 }
 
+// The neighbour-table column of voxel i (tap-major nbr [27][n]): the row of each of its 27
+// neighbours from the cell grid, or from the brick hash when the grid fell back; n where a
+// neighbour is absent, and in all 27 entries of a coordinate out of range.
+__device__ __forceinline__ void probe_voxel(const int32_t* __restrict__ coords, int64_t n, int64_t i,
+                                            const int32_t* __restrict__ dir, const GridHdr* __restrict__ hdr,
+                                            const HashView& hash, int32_t* __restrict__ nbr) {
+    const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+    const int32_t miss = (int32_t)n;
+    if (!coords_ok(x, y, z)) {
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = miss;
+        return;
+    }
+    if (hdr->mode == GRID_MODE_CELLS) {
+        const GridRef g = grid_ref(dir, hdr);
+        int32_t word[kTaps];
+        grid_neighbours(g, x, y, z, word);
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = word[t] ? word[t] - 1 : miss;
+    } else {
+        uint32_t r[kTaps];
+        hash_neighbours(hash, x, y, z, r);
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = r[t] ? (int32_t)(r[t] - 1) : miss;
+    }
+}
+
+// Voxels [v0, v1) of a table probe carried by extra workgroups of another launch (of 256
+// threads, one voxel a thread, after the launch's own workgroups).
+struct ProbeJob {
+    int32_t* nbr = nullptr;      // nullptr: no probe work
+    HashView hash{nullptr, 0};
+    int64_t v0 = 0, v1 = 0;
+};
+
 }  // namespace tsp

@@ -60,8 +60,11 @@ int32_t* plan_cell_of(void* plan, int64_t n);
 // The most grid blocks the plan's per-block scratch holds (grid_build's block_cap for a grid whose
 // blocks the plan walks).
 int64_t plan_block_cap(int64_t n);
+// With probe, the same launches also write the neighbour table nbr from that grid (probe->nbr,
+// the grid's brick hash for the fallback), which the plan then reads only after those launches.
+struct ProbeJob;
 int halo_plan_build_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan,
-                            const void* region, void* tail, hipStream_t s);
+                            const void* region, void* tail, hipStream_t s, const ProbeJob* probe = nullptr);
 // Packed weights: the [co][27][ci] 16-bit values in the MFMA operand order, then a trailer of
 // HB_PACK_TRAILER bytes whose first word is nonzero when some weight is an Inf or a NaN. With
 // finite weights the planned conv skips the MFMAs of taps absent from a whole 32-row block (their

@@ -90,15 +90,25 @@ __global__ __launch_bounds__(WK_NT) void k_walk_count(const int32_t* __restrict_
 // The stores of the walk: the row (order) and packed coordinates (wc) of every voxel -- block
 // voxels from their block's start, column by column, then the left-out voxels after all block
 // voxels. Every workgroup sums the partials before it (and all block partials) itself.
+// Workgroups from GRID_PARTS on carry the neighbour-table probe (pj), when asked for: the walk is
+// latency-bound and the probe bound by its table stores, so the two share the launch (2-3 % off
+// the table + plan call, against the probe as a launch of its own; a third of the probe on the
+// count launch instead measured the same).
 __global__ __launch_bounds__(WK_NT) void k_walk_emit(const int32_t* __restrict__ coords, int64_t n,
                                                      const int32_t* __restrict__ dir, const GridHdr* __restrict__ hdr,
                                                      const int32_t* __restrict__ counts, const uint8_t* __restrict__ pres,
                                                      const int32_t* __restrict__ cell_of,
                                                      const int32_t* __restrict__ parts, int32_t* __restrict__ order,
-                                                     uint64_t* __restrict__ wc, int32_t* __restrict__ list_n) {
+                                                     uint64_t* __restrict__ wc, int32_t* __restrict__ list_n,
+                                                     ProbeJob pj) {
     __shared__ int sW[WK_NT / 64];
     __shared__ int sS[3][WK_NT / 64];
     __shared__ int sStart[WK_NT];
+    if (blockIdx.x >= GRID_PARTS) {
+        const int64_t i = pj.v0 + (int64_t)(blockIdx.x - GRID_PARTS) * WK_NT + threadIdx.x;
+        if (i < pj.v1) probe_voxel(coords, n, i, dir, hdr, pj.hash, pj.nbr);
+        return;
+    }
     if (blockIdx.x == 0 && threadIdx.x == 0) *list_n = 0;   // the plan kernels' list of table tiles
     if (hdr->mode != GRID_MODE_CELLS) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -653,18 +663,27 @@ size_t halo_plan_bytes(int64_t n) {
 
 // The cell walk and the tiles on a grid built from coords (dir = its region, tail = its tail).
 static int plan_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan, const int32_t* dir,
-                        void* tail, hipStream_t s) {
+                        void* tail, hipStream_t s, const ProbeJob* probe) {
     const int64_t n_tiles = ceil_div(n, HB_M);
     const PlanScratch ps = carve_scratch(static_cast<char*>(plan) + plan_tile_bytes(n_tiles), n);
     const GridTail gt = carve_grid_tail(tail);
     int32_t* list_n = gt.parts + 5 * GRID_PARTS;   // zeroed by k_walk_emit
     int32_t* list = ps.counts;                     // free once k_walk_emit has read the counts
     const PlanView pv = carve_plan(plan, n_tiles);
+    // the table probe, when asked for, rides on the walk's emit launch
+    ProbeJob pj;
+    int64_t ge = GRID_PARTS;
+    if (probe && probe->nbr) {
+        pj = *probe;
+        pj.v0 = 0;
+        pj.v1 = n;
+        ge += ceil_div(n, WK_NT);
+    }
     hipLaunchKernelGGL(k_walk_count, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
                        ps.pres, gt.parts);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_walk_emit, dim3(GRID_PARTS), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
-                       ps.pres, ps.cell_of, gt.parts, ps.order, ps.wc, list_n);
+    hipLaunchKernelGGL(k_walk_emit, dim3((unsigned)ge), dim3(WK_NT), 0, s, coords, n, dir, gt.hdr, ps.counts,
+                       ps.pres, ps.cell_of, gt.parts, ps.order, ps.wc, list_n, pj);
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_plan_window, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, n, ps.order, ps.wc, dir,
                        ps.pres, gt.hdr, pv, list, list_n);
@@ -686,7 +705,7 @@ int halo_plan_build(const int32_t* nbr, const int32_t* coords, int64_t n, void* 
         const int st = grid_build(coords, n, ps.region, ps.region_bytes, ps.tail, nullptr, HashView{nullptr, 0},
                                   ps.cell_of, plan_block_cap(n), s);
         if (st != TSP_OK) return st;
-        return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(ps.region), ps.tail, s);
+        return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(ps.region), ps.tail, s, nullptr);
     }
     hipLaunchKernelGGL(k_plan_table, dim3((unsigned)n_tiles), dim3(HB_PLAN_NT), 0, s, nbr, n, nullptr, nullptr,
                        nullptr, nullptr, n_tiles, carve_plan(plan, n_tiles));
@@ -699,9 +718,9 @@ int32_t* plan_cell_of(void* plan, int64_t n) {
 }
 
 int halo_plan_build_on_grid(const int32_t* nbr, const int32_t* coords, int64_t n, void* plan,
-                            const void* region, void* tail, hipStream_t s) {
+                            const void* region, void* tail, hipStream_t s, const ProbeJob* probe) {
     if (n == 0) return TSP_OK;
-    return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(region), tail, s);
+    return plan_on_grid(nbr, coords, n, plan, static_cast<const int32_t*>(region), tail, s, probe);
 }
 
 }  // namespace tsp

@@ -29,26 +29,7 @@ __global__ __launch_bounds__(kProbeThreads) void k_table_probe(const int32_t* __
                                                                const GridHdr* __restrict__ hdr, HashView hash,
                                                                int32_t* __restrict__ nbr) {
     const int64_t i = blockIdx.x * (int64_t)kProbeThreads + threadIdx.x;
-    if (i >= n) return;
-    const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
-    const int32_t miss = (int32_t)n;
-    if (!coords_ok(x, y, z)) {
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = miss;
-        return;
-    }
-    if (hdr->mode == GRID_MODE_CELLS) {
-        const GridRef g = grid_ref(dir, hdr);
-        int32_t word[kTaps];
-        grid_neighbours(g, x, y, z, word);
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = word[t] ? word[t] - 1 : miss;
-    } else {
-        uint32_t r[kTaps];
-        hash_neighbours(hash, x, y, z, r);
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t) nbr[(int64_t)t * n + i] = r[t] ? (int32_t)(r[t] - 1) : miss;
-    }
+    if (i < n) probe_voxel(coords, n, i, dir, hdr, hash, nbr);
 }
 
 __global__ void k_count_pairs(const int32_t* __restrict__ nbr, int64_t total, int32_t sentinel,
@@ -119,10 +100,18 @@ static int rulebook_build(const int32_t* d_coords, int64_t n, int32_t* d_nbr, vo
                               d_plan ? plan_cell_of(d_plan, n) : nullptr,
                               d_plan ? plan_block_cap(n) : INT64_MAX, s);
     if (st != TSP_OK) return st;
+    if (d_plan) {
+        // the probe's workgroups ride on the plan's walk launches (the walk is latency-bound, the
+        // probe bound by its stores); the plan reads the table only after those launches
+        ProbeJob pj;
+        pj.nbr = d_nbr;
+        pj.hash = h;
+        pj.v1 = n;
+        return halo_plan_build_on_grid(d_nbr, d_coords, n, d_plan, d_workspace, tail, s, &pj);
+    }
     hipLaunchKernelGGL(k_table_probe, dim3((unsigned)ceil_div(n, kProbeThreads)), dim3(kProbeThreads), 0, s,
                        d_coords, n, static_cast<const int32_t*>(d_workspace), hdr, h, d_nbr);
     TSP_CHECK_LAUNCH();
-    if (d_plan) return halo_plan_build_on_grid(d_nbr, d_coords, n, d_plan, d_workspace, tail, s);
     return TSP_OK;
 }
 
