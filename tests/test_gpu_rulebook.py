@@ -44,6 +44,12 @@ def test_edge_cases(gpu_lib, orc, shells):
         "scattered-box": rng.integers(0, 400, size=(20000, 3)).astype(np.int32),
         # duplicates spread over many cells of the grid
         "shell-duplicates": np.concatenate([shells.sphere_shell(40, 20.0, 12.0, 14.0)] * 2)[::-1].copy(),
+        # rows in (x, y, z) order with repeats next to each other (the grid's duplicate fix is
+        # skipped only for strictly ascending rows): every row twice, and one repeat whose two rows
+        # fall in different workgroups of the ascending check
+        "sorted-repeats": np.repeat(shells.sphere_shell(40, 20.0, 12.0, 14.0), 2, axis=0),
+        "sorted-one-repeat": np.insert(shells.sphere_shell(40, 20.0, 12.0, 14.0), 256,
+                                       shells.sphere_shell(40, 20.0, 12.0, 14.0)[255], axis=0),
     }
     import torch
     for name, c in cases.items():

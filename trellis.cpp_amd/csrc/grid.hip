@@ -25,14 +25,19 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 }
 
 // Bounding box of the valid coordinates, one partial per workgroup: parts[6 p ..] = lo xyz, hi xyz
-// (lo = INT32_MAX, hi = -1 when the workgroup saw none).
+// (lo = INT32_MAX, hi = -1 when the workgroup saw none); parts[6 GRID_PARTS + p] = 1 when each
+// of the workgroup's rows i > 0 comes strictly after row i - 1 in (x, y, z) order.
 __global__ __launch_bounds__(GB_NT) void k_grid_bbox(const int32_t* __restrict__ coords, int64_t n,
                                                      int32_t* __restrict__ parts, int32_t* status) {
     __shared__ int sR[6][GB_NT / 64];
     int lo[3] = {INT32_MAX, INT32_MAX, INT32_MAX}, hi[3] = {-1, -1, -1};
-    bool bad = false;
+    bool bad = false, desc = false;
     for (int64_t i = blockIdx.x * (int64_t)GB_NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * GB_NT) {
         const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+        if (i > 0) {
+            const int32_t px = coords[3 * i - 3], py = coords[3 * i - 2], pz = coords[3 * i - 1];
+            desc |= x < px || (x == px && (y < py || (y == py && z <= pz)));
+        }
         if (!coords_ok(x, y, z)) {
             bad = true;
             continue;
@@ -41,6 +46,8 @@ __global__ __launch_bounds__(GB_NT) void k_grid_bbox(const int32_t* __restrict__
         hi[0] = max(hi[0], x); hi[1] = max(hi[1], y); hi[2] = max(hi[2], z);
     }
     if (status && __ballot(bad) != 0ull && (threadIdx.x & 63) == 0) atomicOr(status, 1);
+    const int asc = !__syncthreads_or(desc);
+    if (threadIdx.x == 0) parts[6 * GRID_PARTS + blockIdx.x] = asc;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
@@ -61,6 +68,7 @@ __global__ __launch_bounds__(GB_NT) void k_grid_bbox(const int32_t* __restrict__
 __global__ __launch_bounds__(GB_NT) void k_grid_clear(const int32_t* __restrict__ parts, GridHdr* __restrict__ hdr,
                                                       int32_t* __restrict__ dir, int64_t region_words) {
     static_assert(BBOX_PARTS % GB_NT == 0, "whole partials per thread");
+    static_assert(BBOX_PARTS == GRID_PARTS, "the ascending flags fill their partials");
     __shared__ int sR[6][GB_NT / 64];
     __shared__ GridHdr sH;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -74,7 +82,9 @@ __global__ __launch_bounds__(GB_NT) void k_grid_clear(const int32_t* __restrict_
         const int r = a < 3 ? wave_min_i(v) : wave_max_i(v);
         if (lane == 0) sR[a][wave] = r;
     }
-    __syncthreads();
+    bool desc = false;
+    for (int p = tid; p < BBOX_PARTS; p += GB_NT) desc |= parts[6 * GRID_PARTS + p] == 0;
+    const bool ascending = !__syncthreads_or(desc);
     if (tid == 0) {
         int lo[3], hi[3];
 #pragma unroll
@@ -85,6 +95,7 @@ __global__ __launch_bounds__(GB_NT) void k_grid_clear(const int32_t* __restrict_
         }
         GridHdr h{};
         h.mode = GRID_MODE_CELLS;
+        h.ascending = ascending ? 1 : 0;
         if (hi[0] < 0) {                  // no valid voxel: a one-cell directory that stays empty
             lo[0] = lo[1] = lo[2] = 0;
             hi[0] = hi[1] = hi[2] = 0;
@@ -270,19 +281,21 @@ __global__ __launch_bounds__(GB_NT) void k_grid_insert(const int32_t* __restrict
     if (k == 2) blocks[w[1]] = (int32_t)(i + 1);
 }
 
+// Duplicated coordinates: each word raised to the largest row that holds it. Rows strictly
+// ascending in (x, y, z) repeat no coordinate, and then the insert's stores are final.
 __global__ __launch_bounds__(GB_NT) void k_grid_fix(const int32_t* __restrict__ coords, int64_t n,
                                                     const GridHdr* __restrict__ hdr, int32_t* __restrict__ dir) {
-    if (hdr->mode != GRID_MODE_CELLS) return;
-    const int64_t i = blockIdx.x * (int64_t)GB_NT + threadIdx.x;
-    if (i >= n) return;
-    const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
-    if (!coords_ok(x, y, z)) return;
+    if (hdr->mode != GRID_MODE_CELLS || hdr->ascending) return;
     const GridRef g = grid_ref(dir, hdr);
-    int64_t w[2];
-    const int k = voxel_words(g, x, y, z, w);
     int32_t* blocks = dir + hdr->blocks_off;
-    for (int j = 0; j < k; ++j)
-        if (blocks[w[j]] < (int32_t)(i + 1)) atomicMax(&blocks[w[j]], (int32_t)(i + 1));
+    for (int64_t i = blockIdx.x * (int64_t)GB_NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * GB_NT) {
+        const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+        if (!coords_ok(x, y, z)) continue;
+        int64_t w[2];
+        const int k = voxel_words(g, x, y, z, w);
+        for (int j = 0; j < k; ++j)
+            if (blocks[w[j]] < (int32_t)(i + 1)) atomicMax(&blocks[w[j]], (int32_t)(i + 1));
+    }
 }
 
 }  // namespace
@@ -306,7 +319,7 @@ int grid_build(const int32_t* coords, int64_t n, void* region, size_t region_byt
     TSP_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_grid_insert, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir, hash);
     TSP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_grid_fix, dim3(nvb), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir);
+    hipLaunchKernelGGL(k_grid_fix, dim3(std::min(nvb, 4u * GRID_PARTS)), dim3(GB_NT), 0, s, coords, n, gt.hdr, dir);
     TSP_CHECK_LAUNCH();
     return TSP_OK;
 }

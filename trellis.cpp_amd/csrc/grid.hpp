@@ -24,7 +24,7 @@ namespace tsp {
 constexpr int32_t kCoordMax = (1 << 21) - 3;   // voxel coordinates in [0, kCoordMax]
 constexpr int GRID_PARTS = 1024;               // workgroups of the grid's scans
 constexpr int GRID_MAX_BITS = 10;              // directory of at most 2^30 cells
-constexpr size_t GRID_TAIL = 32768;            // bytes: header + GRID_PARTS * 6 partials
+constexpr size_t GRID_TAIL = 32768;            // bytes: header + GRID_PARTS * 7 partials
 constexpr int GRID_MODE_CELLS = 0, GRID_MODE_FALLBACK = 1;
 
 struct GridHdr {
@@ -32,14 +32,16 @@ struct GridHdr {
     int32_t bits;           // Morton bits per axis of the directory
     int32_t clo[3];         // first cell of the bounding box
     int32_t nblocks;        // occupied cells
-    int32_t pad0, pad1;
+    int32_t ascending;      // rows strictly ascending in (x, y, z): no coordinate repeats
+    int32_t pad1;
     int64_t dir_n;          // directory words: 8^bits
     int64_t blocks_off;     // words from the directory to the first block
     int64_t region_words;   // words available for directory + blocks
 };
 static_assert(sizeof(GridHdr) <= 256, "header fits its slot");
 
-// The tail (GRID_TAIL bytes, 16-byte aligned): the header, then int32 partials [6 GRID_PARTS].
+// The tail (GRID_TAIL bytes, 16-byte aligned): the header, then int32 partials [7 GRID_PARTS]
+// (the bounding-box pass's 6 per workgroup, then its ascending flags).
 struct GridTail {
     GridHdr* hdr;
     int32_t* parts;
@@ -48,7 +50,7 @@ inline GridTail carve_grid_tail(void* p) {
     char* c = static_cast<char*>(p);
     return GridTail{reinterpret_cast<GridHdr*>(c), reinterpret_cast<int32_t*>(c + 256)};
 }
-static_assert(256 + 4 * 6 * GRID_PARTS <= GRID_TAIL, "tail layout");
+static_assert(256 + 4 * 7 * GRID_PARTS <= GRID_TAIL, "tail layout");
 
 // Exclusive scan of one value per thread over a workgroup of NT threads; total = the sum.
 // sW: NT / 64 ints of LDS. Every thread must call it.
