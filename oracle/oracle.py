@@ -323,6 +323,21 @@ def convnext_block(feats, nbr, p: dict, prefix: str, wt=None, cast_f32: bool = F
     return h + x.astype(np.float64)
 
 
+def convnext_block_rows(feats, nbr, p: dict, prefix: str, rows, wt=None, cast_f32: bool = False):
+    """convnext_block for the listed output rows only -> float64 [len(rows), C]: the conv of those
+    rows, then the row-local rest (sparse.cpp:121-135)."""
+    r = _rounder(wt, cast_f32)
+    x = np.asarray(feats, np.float32)
+    rows = np.asarray(rows, np.int64)
+    xc = r(x, prefix + ".conv.weight", True).astype(np.float32)
+    h = subm_conv_f64_rows(xc, nbr, p[prefix + ".conv.weight"], p[prefix + ".conv.bias"], rows, row0=x[0])
+    h = layer_norm(h, p[prefix + ".norm.weight"], p[prefix + ".norm.bias"], 1e-6)
+    h = linear(r(h, prefix + ".mlp.0.weight"), p[prefix + ".mlp.0.weight"], p[prefix + ".mlp.0.bias"])
+    h = silu(h)
+    h = linear(r(h, prefix + ".mlp.2.weight"), p[prefix + ".mlp.2.weight"], p[prefix + ".mlp.2.bias"])
+    return h + x[rows].astype(np.float64)
+
+
 def c2s_block(feats, coords, p: dict, prefix: str, cout: int, ext_mask=None, wt=None,
               cast_f32: bool = False, logits_out=None):
     """SparseResBlockC2S3d (sparse.cpp:172-336). wt rounds each product's input as in

@@ -75,6 +75,69 @@ def test_convnext(gpu_lib, orc, shells, c, wtype, cast, planned):
     assert err < _bar(floor)
 
 
+def _tail_split_units(n, c, cus):
+    """The (tile, column tile) units the planned conv's tail split cuts into parts, for n voxels,
+    C = c and `cus` compute units (the library's arithmetic: 8 XCDs, each walking its share of the
+    units with cus / 8 workgroups rounded down to a multiple of the column tiles)."""
+    nct = c // 128 if c % 128 == 0 else c // 64
+    total = -(-n // 512) * nct
+    per_xcd = -(-total // 8)
+    g = min(per_xcd, max(1, cus // 8 // nct) * nct)
+    units = []
+    for x in range(8):
+        lo = x * per_xcd
+        p = min(per_xcd, total - lo)
+        if p <= 0:
+            continue
+        r, t = divmod(p, g)
+        if 0 < t and 2 * t <= g:
+            units += [lo + r * g + i for i in range(t)]
+    return units, nct
+
+
+@pytest.mark.skip(reason="the planned conv's tail split (the last, thin round of units cut by input-channel "
+                         "ranges over the idle CUs) made an illegal memory access on the GPU at C = 256, "
+                         "N = 70000 and its cause was not found; the split is not in the library")
+@pytest.mark.parametrize("c,n", [(1024, 16600), (256, 70000)])
+def test_convnext_tail_split(gpu_lib, orc, shells, c, n):
+    """The ConvNeXt conv on a stored plan at sizes whose last round of (tile, column tile) units is
+    thin, so that its units are cut by input-channel ranges over the idle CUs and their parts added
+    by a second pass (the decoder's 33.5 K-voxel level at C = 1024 is such a size): rows of every
+    split unit's tile and random rows against the oracle's block, at the block bar, and two runs
+    bit-identical."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    units, nct = _tail_split_units(n, c, cus)
+    _case(f"convnext tail split c={c} n={n}: {len(units)} split units on {cus} CUs")
+    assert units, "the size was chosen to split"
+    rng = np.random.default_rng(c + n)
+    coords = np.ascontiguousarray(shells.sphere_shell(140, 70.0, 40.0, 52.0)[:n], np.int32)
+    assert len(coords) == n
+    x = rng.standard_normal((n, c)).astype(np.float32)
+    P = _params(rng, {"conv.weight": ((c, 27, c), 1 / np.sqrt(27 * c), 0), "conv.bias": ((c,), 0.1, 0),
+                      "norm.weight": ((c,), 0.1, 1), "norm.bias": ((c,), 0.1, 0),
+                      "mlp.0.weight": ((4 * c, c), 1 / np.sqrt(c), 0), "mlp.0.bias": ((4 * c,), 0.1, 0),
+                      "mlp.2.weight": ((c, 4 * c), 1 / np.sqrt(4 * c), 0), "mlp.2.bias": ((c,), 0.1, 0)}, "bf16")
+    nbr = gpu_lib.rulebook_build(_dev(coords))
+    plan = gpu_lib.conv_plan_build(nbr, n)          # row tiles: tile t holds rows [512 t, 512 t + 512)
+    wd = {k: v[1] for k, v in P.items()}
+    out = gpu_lib.convnext(_dev(x), nbr, wd, plan=plan)
+    out2 = gpu_lib.convnext(_dev(x), nbr, wd, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    tiles = sorted({u // nct for u in units})
+    rows = np.unique(np.concatenate([np.concatenate([rng.choice(np.arange(512 * t, min(n, 512 * t + 512)), 24,
+                                                                replace=False) for t in tiles]),
+                                     rng.integers(0, n, 200)]))
+    q = {"blk." + k: v[0] for k, v in P.items()}
+    wt = {"blk." + k: ("bf16" if v[0].ndim >= 2 else "f32") for k, v in P.items()}
+    tab = orc.neighbor_table(coords)
+    ref, floor = rounding_noise_floor(orc, lambda: orc.convnext_block_rows(x, tab, q, "blk", rows, wt), runs=2)
+    err = orc.rel_err(out.cpu().numpy()[rows], ref)
+    print(f"tail split rel={err:.3e} floor={floor:.3e} rows={len(rows)}", flush=True)
+    assert err < _bar(floor)
+
+
 @pytest.mark.parametrize("c,dt,n", [(128, "bf16", 1), (128, "bf16", 5001), (128, "f16", 300),
                                     (128, "bf16", 40001), (128, "f16", 8192 + 33)])
 def test_convnext_mlp(gpu_lib, orc, c, dt, n):

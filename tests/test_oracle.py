@@ -322,6 +322,24 @@ def test_convnext_block_vs_torch(orc, shells):
     assert np.allclose(out, h.numpy(), atol=1e-10)
 
 
+def test_convnext_block_rows_vs_whole_block(orc, shells):
+    """convnext_block_rows equals the rows of convnext_block (a row's block output depends on its
+    conv row and its own input only), with and without product-input rounding; a planted mistake
+    (the rows' block read from the neighbouring rows) must differ."""
+    rng = np.random.default_rng(14)
+    coords = shells.random_distinct_voxels(300, 9, 14)
+    c = 16
+    x = rng.standard_normal((300, c)).astype(np.float32)
+    p = _block_params(rng, c)
+    nbr = orc.neighbor_table(coords)
+    rows = np.array([0, 1, 7, 150, 298, 299, 42])
+    for wt in (None, {k: ("bf16" if v.ndim >= 2 else "f32") for k, v in p.items()}):
+        whole = orc.convnext_block(x, nbr, p, "blk", wt)
+        part = orc.convnext_block_rows(x, nbr, p, "blk", rows, wt)
+        assert np.allclose(part, whole[rows], rtol=1e-12, atol=1e-12)
+        assert not np.allclose(part, whole[(rows + 1) % 300], rtol=1e-6, atol=1e-6)
+
+
 def test_c2s_block_vs_loops(orc, shells):
     """sparse.cpp:172-336 against a per-(parent, octant) loop statement of SparseResBlockC2S3d
     (the formulation of tools/ref_c2s.py:59-79)."""
