@@ -11,7 +11,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <functional>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <unordered_map>
 #include <unordered_set>
@@ -117,6 +119,75 @@ constexpr int kMaxDevices = 64;
 std::mutex g_stage_mu;
 void* g_stage[2] = {nullptr, nullptr};
 hipEvent_t g_stage_ev[kMaxDevices][2] = {};
+// copies of produced chunks: a stream of their own per device and the event they wait for
+hipStream_t g_copy_stream[kMaxDevices] = {};
+hipEvent_t g_prod_ev[kMaxDevices] = {};
+
+// Chunks of whole units (at most kStageChunk bytes) through the two staging buffers. With
+// produce, chunk i is first produced by produce(off, len) on s and copied on the device's copy
+// stream once that work is done, so that the copy of one chunk overlaps the production of the
+// next; the copies have all landed when this returns.
+void download_staged(const void* src, size_t bytes, size_t unit, hipStream_t s,
+                     const std::function<void(size_t, size_t)>* produce,
+                     const std::function<void(const void*, size_t)>& sink) {
+    if (!bytes) return;
+    if (!unit || unit > kStageChunk || bytes % unit) fail("download: bad unit");
+    std::lock_guard<std::mutex> lock(g_stage_mu);
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) fail("download: device out of range");
+    for (int k = 0; k < 2; ++k) {
+        if (!g_stage[k]) hip_check(hipHostMalloc(&g_stage[k], kStageChunk, hipHostMallocDefault), "hipHostMalloc");
+        if (!g_stage_ev[dev][k])
+            hip_check(hipEventCreateWithFlags(&g_stage_ev[dev][k], hipEventDisableTiming), "hipEventCreate");
+    }
+    hipStream_t cs = s;
+    if (produce) {
+        if (!g_copy_stream[dev])
+            hip_check(hipStreamCreateWithFlags(&g_copy_stream[dev], hipStreamNonBlocking), "hipStreamCreate");
+        if (!g_prod_ev[dev])
+            hip_check(hipEventCreateWithFlags(&g_prod_ev[dev], hipEventDisableTiming), "hipEventCreate");
+        cs = g_copy_stream[dev];
+    }
+    const size_t chunk = kStageChunk / unit * unit;
+    const size_t nchunk = (bytes + chunk - 1) / chunk;
+    auto issue = [&](size_t i) {
+        const size_t off = i * chunk, len = std::min(chunk, bytes - off);
+        if (produce) {
+            (*produce)(off, len);
+            hip_check(hipEventRecord(g_prod_ev[dev], s), "hipEventRecord");
+            hip_check(hipStreamWaitEvent(cs, g_prod_ev[dev], 0), "hipStreamWaitEvent");
+        }
+        hip_check(hipMemcpyAsync(g_stage[i % 2], static_cast<const char*>(src) + off, len,
+                                 hipMemcpyDeviceToHost, cs), "download");
+        hip_check(hipEventRecord(g_stage_ev[dev][i % 2], cs), "hipEventRecord");
+    };
+    issue(0);
+    for (size_t i = 0; i < nchunk; ++i) {
+        if (i + 1 < nchunk) issue(i + 1);   // the other buffer: its chunk i-1 was taken already
+        hip_check(hipEventSynchronize(g_stage_ev[dev][i % 2]), "download");
+        sink(g_stage[i % 2], std::min(chunk, bytes - i * chunk));
+    }
+}
+
+// a sink that copies each staged chunk to the next bytes of dst on several host threads
+std::function<void(const void*, size_t)> threaded_sink(void* dst) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const size_t nthr = std::max<size_t>(1, std::min<size_t>(8, hw ? hw : 1));
+    auto done = std::make_shared<size_t>(0);
+    char* out = static_cast<char*>(dst);
+    return [=](const void* p, size_t n) {
+        // each thread copies a 64-byte-aligned part of the chunk
+        const size_t part = (n / nthr + 63) / 64 * 64;
+        char* to = out + *done;
+        std::vector<std::thread> th;
+        for (size_t k = 1; k < nthr && k * part < n; ++k)
+            th.emplace_back([=] { memcpy(to + k * part, static_cast<const char*>(p) + k * part, std::min(part, n - k * part)); });
+        memcpy(to, p, std::min(part, n));
+        for (auto& t : th) t.join();
+        *done += n;
+    };
+}
 }  // namespace
 
 void advise_huge_pages(void* p, size_t bytes) {
@@ -128,48 +199,16 @@ void advise_huge_pages(void* p, size_t bytes) {
 
 void download_chunks(const void* src, size_t bytes, hipStream_t s,
                      const std::function<void(const void*, size_t)>& sink) {
-    if (!bytes) return;
-    std::lock_guard<std::mutex> lock(g_stage_mu);
-    int dev = 0;
-    hip_check(hipGetDevice(&dev), "hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices) fail("download: device out of range");
-    for (int k = 0; k < 2; ++k) {
-        if (!g_stage[k]) hip_check(hipHostMalloc(&g_stage[k], kStageChunk, hipHostMallocDefault), "hipHostMalloc");
-        if (!g_stage_ev[dev][k])
-            hip_check(hipEventCreateWithFlags(&g_stage_ev[dev][k], hipEventDisableTiming), "hipEventCreate");
-    }
-    const size_t nchunk = (bytes + kStageChunk - 1) / kStageChunk;
-    auto issue = [&](size_t i) {
-        const size_t off = i * kStageChunk, len = std::min(kStageChunk, bytes - off);
-        hip_check(hipMemcpyAsync(g_stage[i % 2], static_cast<const char*>(src) + off, len,
-                                 hipMemcpyDeviceToHost, s), "download");
-        hip_check(hipEventRecord(g_stage_ev[dev][i % 2], s), "hipEventRecord");
-    };
-    issue(0);
-    for (size_t i = 0; i < nchunk; ++i) {
-        if (i + 1 < nchunk) issue(i + 1);   // the other buffer: its chunk i-1 was taken already
-        hip_check(hipEventSynchronize(g_stage_ev[dev][i % 2]), "download");
-        sink(g_stage[i % 2], std::min(kStageChunk, bytes - i * kStageChunk));
-    }
+    download_staged(src, bytes, 1, s, nullptr, sink);
 }
 
 void download_into(void* dst, const void* src, size_t bytes, hipStream_t s) {
-    const unsigned hw = std::thread::hardware_concurrency();
-    const size_t nthr = std::max<size_t>(1, std::min<size_t>(8, hw ? hw : 1));
-    char* out = static_cast<char*>(dst);
-    size_t done = 0;
-    download_chunks(src, bytes, s, [&](const void* p, size_t n) {
-        // n is a multiple of 64 except for the last chunk; each thread copies a 64-byte-aligned part
-        const size_t part = (n / nthr + 63) / 64 * 64;
-        std::vector<std::thread> th;
-        for (size_t k = 1; k < nthr && k * part < n; ++k)
-            th.emplace_back([=] {
-                memcpy(out + done + k * part, static_cast<const char*>(p) + k * part, std::min(part, n - k * part));
-            });
-        memcpy(out + done, p, std::min(part, n));
-        for (auto& t : th) t.join();
-        done += n;
-    });
+    download_staged(src, bytes, 1, s, nullptr, threaded_sink(dst));
+}
+
+void download_produced(void* dst, const void* src, size_t bytes, size_t unit, hipStream_t s,
+                       const std::function<void(size_t, size_t)>& produce) {
+    download_staged(src, bytes, unit, s, &produce, threaded_sink(dst));
 }
 
 int tsp_dtype_of(enum ggml_type t) {

@@ -91,6 +91,12 @@ void advise_huge_pages(void* p, size_t bytes);
 // chunk is copied out by several host threads. dst should be touched memory (see HostVector).
 void download_into(void* dst, const void* src, size_t bytes, hipStream_t s);
 
+// download_into for a buffer whose contents are produced chunk by chunk: produce(off, len)
+// enqueues on s the work that writes bytes [off, off + len) of src (whole units of `unit` bytes,
+// in order), and each chunk is copied, on a stream of its own, while the next one is produced.
+void download_produced(void* dst, const void* src, size_t bytes, size_t unit, hipStream_t s,
+                       const std::function<void(size_t, size_t)>& produce);
+
 // A host vector of `count` value-initialised elements, made on a thread of its own: the first
 // touches of a large fresh buffer (page faults, the kernel zeroing the pages) then overlap with
 // device work queued before the result is needed. take() waits for the thread and hands the

@@ -199,10 +199,16 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     if (wo->ne[0] != c || wo->ne[1] != out_ch)
         fail("output_layer.weight: expected ggml shape [" + std::to_string(c) + ", " + std::to_string(out_ch) + "]");
     DeviceBuffer out((size_t)n * out_ch * 4, s);
-    if (n) ops::run_linear(m, "output_layer", h.as<float>(), n, c, out_ch, true, 1e-5f, out.as<float>(), s);
     std::vector<float> feats = result.take();
     if (feats.size() != (size_t)n * out_ch) fail("decoder: the masks' final voxel count is not the decoded one");
-    tgr::download_into(feats.data(), out.get(), feats.size() * 4, s);
+    // the output layer (a row-wise LayerNorm + linear) in row chunks, each chunk's rows copied to
+    // the host while the next chunk's are computed
+    const size_t row_bytes = (size_t)out_ch * 4;
+    tgr::download_produced(feats.data(), out.get(), feats.size() * 4, row_bytes, s, [&](size_t off, size_t len) {
+        const int64_t r0 = (int64_t)(off / row_bytes), nr = (int64_t)(len / row_bytes);
+        ops::run_linear(m, "output_layer", h.as<float>() + r0 * c, nr, c, out_ch, true, 1e-5f,
+                        out.as<float>() + r0 * out_ch, s);
+    });
     return feats;
 }
 
