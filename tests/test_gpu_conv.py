@@ -197,6 +197,83 @@ def test_planned_skip(gpu_lib, orc, shells, cin, ci, co, n, dtype_name):
 
 
 
+def _column_split_tiles(n_tiles, nct, cus):
+    """The tile where the planned conv at co = 128 nct hands the rest of its tiles to 64-channel
+    units (0: one launch): the whole rounds of its persistent grid (cus / 8 workgroups per XCD,
+    rounded down to a multiple of nct), when the tiles left fill at most one round of the
+    64-channel grid."""
+    g = 8 * max(1, cus // 8 // nct) * nct
+    rounds = n_tiles * nct // g
+    if rounds < 1:
+        return 0
+    t = rounds * (g // nct)
+    left = n_tiles - t
+    fit64 = max(1, cus // 8 // (2 * nct)) * (2 * nct)
+    return t if 0 < left and -(-left * 2 * nct // 8) <= fit64 else 0
+
+
+@pytest.mark.parametrize("kind,ci,co,shell,dtype_name,out16", [
+    ("plain", 64, 1024, (64, 32.0, 28.5, 31.5), "bfloat16", False),
+    ("plain", 64, 512, (64, 32.0, 28.5, 31.5), "float16", True),
+    ("plain", 128, 128, (112, 56.0, 49.0, 53.5), "bfloat16", True),
+    ("plain", 64, 256, (112, 56.0, 49.0, 53.5), "float16", False),
+    ("octants", 64, 1024, (64, 32.0, 28.5, 31.5), "bfloat16", False),
+    ("skip", 64, 256, (64, 32.0, 28.5, 31.5), "float16", False)])
+def test_planned_column_split(gpu_lib, shells, kind, ci, co, shell, dtype_name, out16):
+    """Planned convs whose 128-channel units leave a thin last round of the persistent grid run
+    that round's tiles as 64-channel units in a second launch: bit for bit the unplanned conv
+    (plain), the unplanned conv then the gather (C2S conv1's octant stores), the unplanned conv
+    then the skip pass (C2S conv2's skip stores), on Morton plans of shells sized so that the
+    split happens on this device."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    dt = getattr(torch, dtype_name)
+    key = "bf16" if dt == torch.bfloat16 else "f16"
+    rng = np.random.default_rng(ci + co + len(kind))
+    pcoords = np.ascontiguousarray(shells.sphere_shell(*shell), np.int32)
+    if kind == "skip":
+        mask = (rng.random(len(pcoords) * 8) < 0.5).astype(np.uint8)
+        _, gidx, _ = gpu_lib.subdivide(torch.from_numpy(mask).cuda(), torch.from_numpy(pcoords).cuda())
+        coords = np.ascontiguousarray(shells.children(mask, pcoords), np.int32)
+    else:
+        coords = pcoords
+    n = len(coords)
+    t_split = _column_split_tiles(-(-n // 512), co // 128, cus)
+    _case(f"column split {kind} ci={ci} co={co} n={n} {dtype_name} out16={out16}: tiles [0, {t_split}) "
+          f"at 128 channels, the rest at 64 ({cus} CUs)")
+    if cus == 256:
+        assert t_split > 0, "the shell was sized to split on 256 compute units"
+    feats = shells.round_to(rng.standard_normal((n, ci)).astype(np.float32), key)
+    weight = shells.round_to((rng.standard_normal((co, 27, ci)) / np.sqrt(27 * ci)).astype(np.float32), key)
+    bias = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    c = torch.from_numpy(coords).cuda()
+    nbr = gpu_lib.rulebook_build(c)
+    plan = gpu_lib.conv_plan_build(nbr, n, coords=c)
+    f, w, b = _dev(feats, dt), _dev(weight, dt), _dev(bias, torch.float32)
+    pw = gpu_lib.conv_weight_pack(w)
+    if kind == "plain":
+        odt = dt if out16 else torch.float32
+        out = gpu_lib.subm_conv3x3_planned(f, nbr, plan, pw, b, co, out_dtype=odt)
+        ref = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=odt, algo="mfma")
+    elif kind == "octants":
+        cout = co // 8
+        mask = np.where(rng.random((n, 8)) < 0.4, rng.integers(1, 256, (n, 8)), 0).astype(np.uint8)
+        mask_t = torch.from_numpy(mask.reshape(-1)).cuda()
+        _, g8, mstart = gpu_lib.subdivide(mask_t, c)
+        out = gpu_lib.subm_conv3x3_planned_octants(f, nbr, plan, pw, b, cout, mask_t, mstart, len(g8))
+        full = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+        ref = gpu_lib.c2s_gather(full, g8, cout)
+    else:
+        cin = 128
+        x = _dev(rng.standard_normal((len(pcoords), cin)).astype(np.float32), torch.float32)
+        out = gpu_lib.subm_conv3x3_planned_skip(f, nbr, plan, pw, b, co, x, gidx)
+        ref = gpu_lib.subm_conv3x3(f, nbr, w, b, out_dtype=torch.float32, algo="mfma")
+        gpu_lib.c2s_skip_add(x, gidx, ref)
+    torch.cuda.synchronize()
+    assert out.shape == ref.shape and bool(torch.isfinite(out.float()).all())
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("bad", ["inf", "nan"])
 @pytest.mark.parametrize("path", ["planned", "auto", "mfma_gather", "narrow", "f32", "f32_narrow", "unsorted"])
 def test_nonfinite_row0(gpu_lib, orc, shells, path, bad):

@@ -87,6 +87,23 @@ int halo_weight_pack(const void* w, int wdt, int ci, int co, void* packed, hipSt
     return TSP_OK;
 }
 
+int64_t column_split_tiles(int64_t n_tiles, int nct, int cus) {
+    if (n_tiles <= 0 || nct <= 0 || cus <= 0) return 0;
+    // the planned grid at 128 channels a unit: cus / 8 workgroups per XCD rounded down to a
+    // multiple of the nct column tiles, each XCD walking its contiguous share of the units a round
+    // at a time
+    const int64_t g128 = 8 * std::max<int64_t>(1, cus / 8 / nct) * nct;
+    const int64_t rounds = n_tiles * nct / g128;
+    if (rounds < 1) return 0;
+    const int64_t t_split = rounds * (g128 / nct);   // whole rounds of every workgroup
+    const int64_t left = n_tiles - t_split;
+    if (left <= 0) return 0;
+    // the last round's units as 64-channel units: worth it while they make one round of the
+    // 64-channel grid (each unit half the products, at 0.64-0.83 of a 128-channel unit's time)
+    const int64_t fit64 = std::max<int64_t>(1, cus / 8 / (2 * nct)) * (2 * nct);
+    return ceil_div(left * 2 * nct, 8) <= fit64 ? t_split : 0;
+}
+
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
                      hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
@@ -118,9 +135,21 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
                   "kernel addresses", (long long)(n * ci * 2));
         return TSP_ERR_UNSUPPORTED;
     }
-    auto* fn = fdt == TSP_BF16 ? (bn128 ? halo_launch_bf16_128 : halo_launch_bf16_64)
-                               : (bn128 ? halo_launch_f16_128 : halo_launch_f16_64);
-    return fn(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
+    auto* fn64 = fdt == TSP_BF16 ? halo_launch_bf16_64 : halo_launch_f16_64;
+    auto* fn = bn128 ? (fdt == TSP_BF16 ? halo_launch_bf16_128 : halo_launch_f16_128) : fn64;
+    // With a plan, whole rounds of 128-channel units and the tiles left over as 64-channel units
+    // (kernels where either width runs: not the row norms, which need whole rows in a workgroup)
+    if (planned && bn128 && !ln.w && !osc.norm_silu) {
+        const int64_t t_split = column_split_tiles(ceil_div(n, HB_M), co / 128, cu_count());
+        if (t_split > 0) {
+            if (int st = fn(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln,
+                            TileRange{0, t_split}))
+                return st;
+            return fn64(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln,
+                        TileRange{t_split, -1});
+        }
+    }
+    return fn(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln, TileRange{});
 }
 
 }  // namespace tsp

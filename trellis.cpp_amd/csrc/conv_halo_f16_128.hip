@@ -5,7 +5,7 @@ namespace tsp {
 
 int halo_launch_f16_128(TSP_HALO_LAUNCH_ARGS) {
     return launch_out<false, 128>(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s,
-                                     osc, skip, pad, ln);
+                                     osc, skip, pad, ln, tr);
 }
 
 }  // namespace tsp

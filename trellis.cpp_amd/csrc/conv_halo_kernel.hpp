@@ -1011,13 +1011,31 @@ int cu_count() {
 template <bool BF16, int BN, int ODT, bool PLANNED>
 int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void* plan,
            const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc,
-           SkipAdd skip, PadRow pad, RowNorm ln) {
-    const int64_t n_tiles = ceil_div(n, HB_M);
+           SkipAdd skip, PadRow pad, RowNorm ln, TileRange tr) {
+    const int64_t all_tiles = ceil_div(n, HB_M);
+    // a stored plan's tiles [t0, t0 + n_tiles): its per-tile arrays (and the octant block words)
+    // start at tile t0, and the kernel's tile indices count from there
+    const int64_t t0 = PLANNED ? tr.t0 : 0;
+    const int64_t n_tiles = PLANNED && tr.nt >= 0 ? tr.nt : all_tiles - t0;
+    if (t0 < 0 || n_tiles < 0 || t0 + n_tiles > all_tiles) {
+        set_error("MFMA conv: tiles [%lld, %lld) outside the plan's %lld", (long long)t0,
+                  (long long)(t0 + n_tiles), (long long)all_tiles);
+        return TSP_ERR_INVALID;
+    }
+    if (n_tiles == 0) return TSP_OK;
     const int n_ctiles = co / BN;
     const int64_t total = n_tiles * n_ctiles;
     const int64_t per_xcd = ceil_div(total, 8);
     PlanView pv{};
-    if (plan) pv = carve_plan(const_cast<void*>(plan), n_tiles);
+    if (plan) {
+        pv = carve_plan(const_cast<void*>(plan), all_tiles);
+        pv.hdr += t0 * 4;
+        pv.rowof += t0 * HB_SLOTS;
+        pv.slots += t0 * HB_SLOT_TABLE;
+        pv.vox += t0 * HB_M;
+        pv.act += t0 * 4 * HB_ACT_WORDS;
+    }
+    if (osc.blocks) osc.blocks += t0 * 4;
     // 8 waves of 128 voxels x BN/2 channels; weights 2 taps ahead (5 at BN = 64, whose waves
     // have the registers for it: 3 % faster there, while at BN = 128 the deeper ring spills);
     // a slice piece every other tap, written to LDS 6 taps after its load
@@ -1082,21 +1100,26 @@ int launch(const void* feats, int64_t n, int ci, const int32_t* nbr, const void*
 template <bool BF16, int BN, int ODT>
 int launch_planned(bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                    const void* plan, const void* weight, const float* bias, int co, void* out,
-                   hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
-    if (planned) return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
-    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip, pad, ln);
+                   hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln, TileRange tr) {
+    if (planned)
+        return launch<BF16, BN, ODT, true>(feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln, tr);
+    return launch<BF16, BN, ODT, false>(feats, n, ci, nbr, nullptr, weight, bias, co, out, s, osc, skip, pad, ln,
+                                        TileRange{});
 }
 
 template <bool BF16, int BN>
 int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr,
                const void* plan, const void* weight, const float* bias, int co, void* out,
-               hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
+               hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln, TileRange tr) {
     if (odt == TSP_F32)
-        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
+        return launch_planned<BF16, BN, TSP_F32>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip,
+                                                 pad, ln, tr);
     if (BF16 && odt == TSP_BF16)
-        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
+        return launch_planned<BF16, BN, TSP_BF16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc,
+                                                  skip, pad, ln, tr);
     if (!BF16 && odt == TSP_F16)
-        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln);
+        return launch_planned<BF16, BN, TSP_F16>(planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip,
+                                                 pad, ln, tr);
     set_error("MFMA conv writes f32 or the feature dtype, not %d", odt);
     return TSP_ERR_UNSUPPORTED;
 }
@@ -1107,7 +1130,7 @@ int launch_out(int odt, bool planned, const void* feats, int64_t n, int ci, cons
 // output dtype odt, octant or skip stores when given.
 #define TSP_HALO_LAUNCH_ARGS int odt, bool planned, const void* feats, int64_t n, int ci, const int32_t* nbr, \
     const void* plan, const void* weight, const float* bias, int co, void* out, hipStream_t s, OctantScatter osc, \
-    SkipAdd skip, PadRow pad, RowNorm ln
+    SkipAdd skip, PadRow pad, RowNorm ln, TileRange tr
 int halo_launch_bf16_128(TSP_HALO_LAUNCH_ARGS);
 int halo_launch_bf16_64(TSP_HALO_LAUNCH_ARGS);
 int halo_launch_f16_128(TSP_HALO_LAUNCH_ARGS);

@@ -135,6 +135,18 @@ struct RowNorm {
 // OctantScatter or a SkipAdd needs a plan and f32 output; an OctantScatter needs cout a multiple
 // of the channels one wave owns (64 when co % 128 == 0, else 32). A RowNorm needs a plan,
 // co == 64 or 128 (one workgroup holds whole rows) and odt == fdt.
+// Tiles [t0, t0 + nt) of a stored plan (nt < 0: every tile from t0): the planned launches run
+// the persistent grid over those tiles' units only.
+struct TileRange {
+    int64_t t0 = 0;
+    int64_t nt = -1;
+};
+
+// The planned convs at co % 128 == 0 (nct = co / 128 column tiles) run tiles [0, t) as 128-channel
+// units and the rest as 64-channel units when the 128-channel units leave a last round that the
+// 64-channel grid takes in one: returns that t, or 0 for one launch (cus: compute units).
+int64_t column_split_tiles(int64_t n_tiles, int nct, int cus);
+
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
                      hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {},
