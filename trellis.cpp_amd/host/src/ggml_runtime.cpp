@@ -162,11 +162,17 @@ void download_staged(const void* src, size_t bytes, size_t unit, hipStream_t s,
                                  hipMemcpyDeviceToHost, cs), "download");
         hip_check(hipEventRecord(g_stage_ev[dev][i % 2], cs), "hipEventRecord");
     };
-    issue(0);
-    for (size_t i = 0; i < nchunk; ++i) {
-        if (i + 1 < nchunk) issue(i + 1);   // the other buffer: its chunk i-1 was taken already
-        hip_check(hipEventSynchronize(g_stage_ev[dev][i % 2]), "download");
-        sink(g_stage[i % 2], std::min(chunk, bytes - i * chunk));
+    try {
+        issue(0);
+        for (size_t i = 0; i < nchunk; ++i) {
+            if (i + 1 < nchunk) issue(i + 1);   // the other buffer: its chunk i-1 was taken already
+            hip_check(hipEventSynchronize(g_stage_ev[dev][i % 2]), "download");
+            sink(g_stage[i % 2], std::min(chunk, bytes - i * chunk));
+        }
+    } catch (...) {
+        // copies still in flight must not land in the staging buffers under the next download
+        (void)hipStreamSynchronize(cs);
+        throw;
     }
 }
 
