@@ -218,7 +218,9 @@ def _column_split_tiles(n_tiles, nct, cus):
     ("plain", 128, 128, (112, 56.0, 49.0, 53.5), "bfloat16", True),
     ("plain", 64, 256, (112, 56.0, 49.0, 53.5), "float16", False),
     ("octants", 64, 1024, (64, 32.0, 28.5, 31.5), "bfloat16", False),
-    ("skip", 64, 256, (64, 32.0, 28.5, 31.5), "float16", False)])
+    ("octants", 32, 512, (64, 32.0, 28.5, 31.5), "float16", False),
+    ("skip", 64, 256, (64, 32.0, 28.5, 31.5), "float16", False),
+    ("skip", 128, 128, (64, 32.0, 28.5, 31.5), "bfloat16", False)])
 def test_planned_column_split(gpu_lib, shells, kind, ci, co, shell, dtype_name, out16):
     """Planned convs whose 128-channel units leave a thin last round of the persistent grid run
     that round's tiles as 64-channel units in a second launch: bit for bit the unplanned conv
