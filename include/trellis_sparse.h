@@ -417,6 +417,24 @@ int tsp_c2s_ex(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const
                int cout, const int32_t* d_child_nbr, const void* d_child_plan,
                const tsp_c2s_weights* w, float* d_out, void* d_out16, int out16_dtype,
                void* d_workspace, size_t workspace_bytes, int flags, void* stream);
+/* tsp_c2s_ex in two parts, for a caller that takes the output rows while conv2 still runs (no
+ * counterpart in the reference; the decoder's last block, whose rows go to the host): part
+ * TSP_C2S_PART_FRONT runs everything before conv2 (norm1, conv1, the gather, norm2: conv2's input
+ * stays in the workspace); then TSP_C2S_PART_CONV2, with the same arguments and workspace, runs
+ * conv2 and the skip over the child plan's tiles [t0, t0 + nt) (nt = -1: to the last tile), so
+ * that rows [512 t0, 512 (t0 + nt)) are final when the child plan was built without coordinates
+ * (tiles of consecutive rows). Both parts at once (t0 = 0, nt = -1) are tsp_c2s_ex. A tile range
+ * other than all tiles needs conv2 on the matrix cores with the skip in its stores (a child plan,
+ * conv2's input 16-bit, Cout % 64 == 0, Cout / (Cin / 8) % 4 == 0), else TSP_ERR_UNSUPPORTED; a
+ * range past the plan's tiles is TSP_ERR_INVALID. Conv2 parts over disjoint ranges write disjoint
+ * rows of d_out (and d_out16). */
+enum { TSP_C2S_PART_FRONT = 1, TSP_C2S_PART_CONV2 = 2 };
+int tsp_c2s_part(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+                 const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m,
+                 int cout, const int32_t* d_child_nbr, const void* d_child_plan,
+                 const tsp_c2s_weights* w, float* d_out, void* d_out16, int out16_dtype,
+                 void* d_workspace, size_t workspace_bytes, int flags, int part, int64_t t0, int64_t nt,
+                 void* stream);
 
 #ifdef __cplusplus
 }

@@ -350,6 +350,15 @@ def test_composite_validation(pkg):
                                     kw.get("o16dt", 2), FAKE, cb, 0, NULL)
     assert cx2(o16=ctypes.c_void_p(0x3000), o16dt=3) == 1
     assert cx2(o16=ctypes.c_void_p(0x2000)) == 1 and "alias" in _err(pkg)
+    # tsp_c2s_part: the part, and a tile range only for the conv2 part
+    cp = lambda **kw: L.tsp_c2s_part(FAKE, 500, 128, FAKE, FAKE, FAKE, FAKE, FAKE, 1200, 64, FAKE, FAKE,
+                                     ctypes.byref(c), ctypes.c_void_p(0x2000), None, 2, FAKE, kw.get("ws", cb), 0,
+                                     kw.get("part", 3), kw.get("t0", 0), kw.get("nt", -1), NULL)
+    assert cp(part=0) == 1 and "part" in _err(pkg)
+    assert cp(part=4) == 1
+    assert cp(part=2, t0=-1) == 1 and cp(part=2, nt=-2) == 1
+    assert cp(part=1, t0=3) == 1 and "conv2 part" in _err(pkg)
+    assert cp(part=2, t0=1, nt=2, ws=cb - 1) == 5
 
 
 def test_convnext_mlp_validation(pkg):

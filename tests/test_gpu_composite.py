@@ -219,6 +219,59 @@ def test_c2s(gpu_lib, orc, shells, cin, cout, wtype, planned):
     assert err < _bar(floor)
 
 
+@pytest.mark.parametrize("cin,cout,wtype,o16", [(128, 64, "bf16", None), (256, 128, "f16", "f16"),
+                                               (128, 64, "f16", "bf16")])
+def test_c2s_in_parts(gpu_lib, shells, cin, cout, wtype, o16):
+    """tsp_c2s_part: the front part once, then conv2 over ranges of the child plan's tiles (a plan
+    without coordinates: tile t holds children [512 t, 512 t + 512)), in an order other than
+    ascending and with an empty range, equals tsp_c2s_ex bit for bit (out and its rounded copy);
+    a range past the last tile is refused, and so is a conv2 range where conv2 does not store the
+    skip itself (Cout = 32: no matrix-core conv2)."""
+    import torch
+    _case(f"c2s in parts {cin}->{cout} {wtype} out16={o16}")
+    rng = np.random.default_rng(cin + 3 * cout)
+    coords = np.ascontiguousarray(shells.sphere_shell(40, 20.0, 15.0, 17.5), np.int32)
+    n = len(coords)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    mask = (rng.random(8 * n) < 0.45).astype(np.uint8)
+    P = _params(rng, {"norm1.weight": ((cin,), 0.1, 1), "norm1.bias": ((cin,), 0.1, 0),
+                      "conv1.weight": ((8 * cout, 27, cin), 1 / np.sqrt(27 * cin), 0),
+                      "conv1.bias": ((8 * cout,), 0.1, 0),
+                      "conv2.weight": ((cout, 27, cout), 1 / np.sqrt(27 * cout), 0),
+                      "conv2.bias": ((cout,), 0.1, 0)}, wtype)
+    p = {k: v[1] for k, v in P.items()}
+    cc, mt = _dev(coords), _dev(mask)
+    nbr = gpu_lib.rulebook_build(cc)
+    child, gidx, mstart = gpu_lib.subdivide(mt, cc)
+    m = len(gidx)
+    cnbr = gpu_lib.rulebook_build(child)
+    plan, cplan = gpu_lib.conv_plan_build(nbr, n, coords=cc), gpu_lib.conv_plan_build(cnbr, m)
+    t16 = None if o16 is None else getattr(torch, DT[o16])
+    xd = _dev(x)
+    args = (xd, nbr, mt, mstart, gidx, m, cout, cnbr, p)
+    whole = gpu_lib.c2s(*args, plan=plan, child_plan=cplan, out16_dtype=t16)
+    nt = -(-m // 512)
+    assert nt >= 6, "enough child tiles for several ranges"
+    ranges = [(nt // 2, nt - nt // 2), (0, 0), (3, nt // 2 - 3), (0, 3)]
+    parts = gpu_lib.c2s(*args, plan=plan, child_plan=cplan, out16_dtype=t16, conv2_tiles=ranges)
+    torch.cuda.synchronize()
+    if t16 is None:
+        assert torch.equal(parts, whole)
+    else:
+        assert torch.equal(parts[0], whole[0]) and torch.equal(parts[1].view(torch.int16), whole[1].view(torch.int16))
+    with pytest.raises(gpu_lib.TspError, match="tiles"):
+        gpu_lib.c2s(*args, plan=plan, child_plan=cplan, conv2_tiles=[(nt - 1, 2)])
+    P32 = _params(rng, {"norm1.weight": ((cin,), 0.1, 1), "norm1.bias": ((cin,), 0.1, 0),
+                        "conv1.weight": ((8 * 32, 27, cin), 1 / np.sqrt(27 * cin), 0),
+                        "conv1.bias": ((8 * 32,), 0.1, 0),
+                        "conv2.weight": ((32, 27, 32), 1 / np.sqrt(27 * 32), 0),
+                        "conv2.bias": ((32,), 0.1, 0)}, wtype)
+    with pytest.raises(gpu_lib.TspError, match="range of tiles"):
+        gpu_lib.c2s(xd, nbr, mt, mstart, gidx, m, 32, cnbr, {k: v[1] for k, v in P32.items()}, plan=plan,
+                    child_plan=cplan, conv2_tiles=[(0, 1)])
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("c,wtype,planned,o16", [(128, "bf16", True, "bf16"), (128, "f16", True, "f16"),
                                                  (128, "bf16", True, "f16"), (256, "bf16", True, "bf16"),
                                                  (64, "bf16", False, "bf16")])

@@ -34,7 +34,7 @@ EXPORTS = (
     "tsp_linear", "tsp_linear_ex", "tsp_linear_rows_per_call", "tsp_layer_norm", "tsp_c2s_gather", "tsp_c2s_skip_add",
     "tsp_mask_positive",
     "tsp_convnext_workspace_bytes", "tsp_convnext", "tsp_convnext_ex", "tsp_c2s_workspace_bytes", "tsp_c2s",
-    "tsp_c2s_ex",
+    "tsp_c2s_ex", "tsp_c2s_part",
 )
 
 BLOCK_CAST_F32 = 2
@@ -168,6 +168,9 @@ def lib() -> ctypes.CDLL:
     L.tsp_c2s_ex.restype = c_int
     L.tsp_c2s_ex.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c2w,
                              c_vp, c_vp, c_int, c_vp, c_sz, c_int, c_vp]
+    L.tsp_c2s_part.restype = c_int
+    L.tsp_c2s_part.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c2w,
+                               c_vp, c_vp, c_int, c_vp, c_sz, c_int, c_int, c_i64, c_i64, c_vp]
     _lib = L
     return L
 
@@ -715,13 +718,14 @@ def convnext(x, nbr, p: dict, plan=None, cast_f32: bool = False, stream=None, x1
 
 
 def c2s(x, nbr, mask, mstart, gidx, m: int, cout: int, child_nbr, p: dict, plan=None, child_plan=None,
-        cast_f32: bool = False, stream=None, out16_dtype=None):
+        cast_f32: bool = False, stream=None, out16_dtype=None, conv2_tiles=None):
     """The C2S block's features through tsp_c2s_ex, after its subdivision (mask uint8 [8N], mstart
     and gidx from subdivide, child_nbr the children's table): x f32 [N, Cin], p by reference
     names without the prefix ("norm1.weight", "norm1.bias", "conv1.weight" [8 Cout,27,Cin],
     "conv1.bias", "conv2.weight" [Cout,27,Cout], "conv2.bias"; optional "conv1.packed",
     "conv2.packed"). -> f32 [M, Cout], or (out, out rounded to out16_dtype) when out16_dtype is
-    given."""
+    given. conv2_tiles, a list of (t0, nt) child-plan tile ranges: through tsp_c2s_part instead,
+    the front part once, then conv2 over each range in turn."""
     torch = _torch()
     n, cin = x.shape
     if x.dtype != torch.float32:
@@ -754,8 +758,14 @@ def c2s(x, nbr, mask, mstart, gidx, m: int, cout: int, child_nbr, p: dict, plan=
     nb = lib().tsp_c2s_workspace_bytes(n, m, cin, cout, ctypes.byref(w), int(plan is not None),
                                        int(child_plan is not None), flags)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
-    _check("tsp_c2s_ex", lib().tsp_c2s_ex(
-        _ptr(xc), n, cin, _ptr(nbr), _ptr(plan), _ptr(mask.reshape(-1).contiguous()), _ptr(mstart), _ptr(gidx), m,
-        cout, _ptr(child_nbr), _ptr(child_plan), ctypes.byref(w), _ptr(out), _ptr(out16),
-        dtype_code(out16_dtype) if out16 is not None else 2, _ptr(ws), nb, flags, _stream(stream)))
+    mk = mask.reshape(-1).contiguous()
+    args = (_ptr(xc), n, cin, _ptr(nbr), _ptr(plan), _ptr(mk), _ptr(mstart), _ptr(gidx), m, cout, _ptr(child_nbr),
+            _ptr(child_plan), ctypes.byref(w), _ptr(out), _ptr(out16), dtype_code(out16_dtype) if out16 is not None
+            else 2, _ptr(ws), nb, flags)
+    if conv2_tiles is None:
+        _check("tsp_c2s_ex", lib().tsp_c2s_ex(*args, _stream(stream)))
+    else:
+        _check("tsp_c2s_part", lib().tsp_c2s_part(*args, 1, 0, -1, _stream(stream)))
+        for t0, nt in conv2_tiles:
+            _check("tsp_c2s_part", lib().tsp_c2s_part(*args, 2, t0, nt, _stream(stream)))
     return out if out16 is None else (out, out16)

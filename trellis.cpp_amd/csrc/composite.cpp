@@ -201,10 +201,12 @@ int convnext_walk(const void* x, int xdt, const void* x16, int64_t n, int c, con
 
 // The C2S block after its subdivision (sparse.cpp:256-336): norm1 + SiLU -> conv1 (Cin -> 8 Cout)
 // -> octant gather -> norm2 (no affine) + SiLU -> conv2 (exact zero padding row) -> + skip.
+// part: TSP_C2S_PART_FRONT runs everything before conv2 (its input stays in the workspace),
+// TSP_C2S_PART_CONV2 conv2 and the skip, over the child plan's tiles `tiles` (all by default).
 int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void* plan, const uint8_t* mask,
              const int32_t* mstart, const int32_t* gidx, int64_t m, int cout, const int32_t* cnbr,
              const void* cplan, const tsp_c2s_weights& w, float* out, void* out16, int out16dt, int flags,
-             Carve& ws, hipStream_t s) {
+             Carve& ws, hipStream_t s, int part = TSP_C2S_PART_FRONT | TSP_C2S_PART_CONV2, TileRange tiles = {}) {
     const int in1 = act_dtype(w.conv1_dtype, true, flags), in2 = act_dtype(w.conv2_dtype, true, flags);
     const ConvPlan cp1 = conv_plan(in1, cin, 8 * cout, plan, w.conv1_packed);
     const ConvPlan cp2 = conv_plan(in2, cout, cout, cplan, w.conv2_packed);
@@ -227,46 +229,50 @@ int c2s_walk(const float* x, int64_t n, int cin, const int32_t* nbr, const void*
     auto* blocks = octants ? static_cast<uint32_t*>(ws.take((size_t)ceil_div(n, HB_M) * 4 * 4)) : nullptr;
     if (!ws.base) return TSP_OK;
     int st;
-    if ((st = tsp_layer_norm(x, TSP_F32, n, cin, w.norm1_weight, w.norm1_bias, 1e-6f, 1, h0, in1, s))) return st;
-    const void* p1 = w.conv1_packed;
-    if (pk1) {
-        if ((st = tsp_conv_weight_pack(w.conv1_weight, w.conv1_dtype, cin, 8 * cout, pk1, s))) return st;
-        p1 = pk1;
+    const void* p2 = pk2 ? pk2 : w.conv2_packed;
+    if (part & TSP_C2S_PART_FRONT) {
+        if ((st = tsp_layer_norm(x, TSP_F32, n, cin, w.norm1_weight, w.norm1_bias, 1e-6f, 1, h0, in1, s))) return st;
+        const void* p1 = w.conv1_packed;
+        if (pk1) {
+            if ((st = tsp_conv_weight_pack(w.conv1_weight, w.conv1_dtype, cin, 8 * cout, pk1, s))) return st;
+            p1 = pk1;
+        }
+        if (octants && (st = octant_blocks(plan, n, mask, blocks, s))) return st;
+        if (norm_in_stores) {
+            TSP_REQUIRE((reinterpret_cast<uintptr_t>(p1) & 15) == 0 &&
+                            (reinterpret_cast<uintptr_t>(mask) & 7) == 0,
+                        TSP_ERR_INVALID, "tsp_c2s: packed conv1 weights must be 16-byte aligned, the mask 8-byte");
+            OctantScatter osc;
+            osc.mask = mask;
+            osc.mstart = mstart;
+            osc.cout = cout;
+            osc.norm_silu = true;
+            osc.norm_eps = 1e-6f;
+            osc.blocks = blocks;
+            st = halo_conv_launch(in1, in2, h0, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h2, s, osc);
+        } else if (octants) {
+            st = planned_octants(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, cout, mask, mstart, g, blocks, s);
+        } else {
+            if (cp1.planned)
+                st = tsp_subm_conv3x3_planned_ex(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h1,
+                                                 TSP_F32, 0, nullptr, s);
+            else
+                st = tsp_subm_conv3x3_ex(h0, in1, n, cin, nbr, w.conv1_weight, w.conv1_dtype, w.conv1_bias,
+                                         8 * cout, h1, TSP_F32, TSP_ALGO_AUTO, 0, nullptr, s);
+            if (!st) st = tsp_c2s_gather(h1, TSP_F32, gidx, m, cout, g, s);
+        }
+        if (st) return st;
+        if (!norm_in_stores && (st = tsp_layer_norm(g, TSP_F32, m, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s)))
+            return st;
+        if (pk2 && (st = tsp_conv_weight_pack(w.conv2_weight, w.conv2_dtype, cout, cout, pk2, s))) return st;
     }
-    if (octants && (st = octant_blocks(plan, n, mask, blocks, s))) return st;
-    if (norm_in_stores) {
-        TSP_REQUIRE((reinterpret_cast<uintptr_t>(p1) & 15) == 0 && (reinterpret_cast<uintptr_t>(mask) & 7) == 0,
-                    TSP_ERR_INVALID, "tsp_c2s: packed conv1 weights must be 16-byte aligned, the mask 8-byte");
-        OctantScatter osc;
-        osc.mask = mask;
-        osc.mstart = mstart;
-        osc.cout = cout;
-        osc.norm_silu = true;
-        osc.norm_eps = 1e-6f;
-        osc.blocks = blocks;
-        st = halo_conv_launch(in1, in2, h0, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h2, s, osc);
-    } else if (octants) {
-        st = planned_octants(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, cout, mask, mstart, g, blocks, s);
-    } else {
-        if (cp1.planned)
-            st = tsp_subm_conv3x3_planned_ex(h0, in1, n, cin, nbr, plan, p1, w.conv1_bias, 8 * cout, h1, TSP_F32, 0,
-                                             nullptr, s);
-        else
-            st = tsp_subm_conv3x3_ex(h0, in1, n, cin, nbr, w.conv1_weight, w.conv1_dtype, w.conv1_bias, 8 * cout, h1,
-                                     TSP_F32, TSP_ALGO_AUTO, 0,
-                                     nullptr, s);
-        if (!st) st = tsp_c2s_gather(h1, TSP_F32, gidx, m, cout, g, s);
-    }
-    if (st) return st;
-    if (!norm_in_stores && (st = tsp_layer_norm(g, TSP_F32, m, cout, nullptr, nullptr, 1e-6f, 1, h2, in2, s)))
-        return st;
-    const void* p2 = w.conv2_packed;
-    if (pk2) {
-        if ((st = tsp_conv_weight_pack(w.conv2_weight, w.conv2_dtype, cout, cout, pk2, s))) return st;
-        p2 = pk2;
-    }
+    if (!(part & TSP_C2S_PART_CONV2)) return TSP_OK;
     if (skip_in_stores)
-        return planned_skip(h2, in2, m, cout, cnbr, cplan, p2, w.conv2_bias, cout, x, cin, gidx, out, out16, out16dt, s);
+        return planned_skip(h2, in2, m, cout, cnbr, cplan, p2, w.conv2_bias, cout, x, cin, gidx, out, out16, out16dt, s,
+                            tiles);
+    TSP_REQUIRE(tiles.t0 == 0 && tiles.nt < 0, TSP_ERR_UNSUPPORTED,
+                "tsp_c2s_part: conv2 over a range of tiles needs it on the matrix cores with the skip in its "
+                "stores (a child plan, 16-bit weights, Cout %% 64 == 0, Cout / (Cin / 8) %% 4 == 0)");
     if (cp2.planned)
         st = tsp_subm_conv3x3_planned_ex(h2, in2, m, cout, cnbr, cplan, p2, w.conv2_bias, cout, out, TSP_F32,
                                          TSP_CONV_ZERO_PAD, nullptr, s);
@@ -347,12 +353,19 @@ extern "C" size_t tsp_c2s_workspace_bytes(int64_t n, int64_t m, int cin, int cou
     return ws.off;
 }
 
-extern "C" int tsp_c2s_ex(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
-                          const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m, int cout,
-                          const int32_t* d_child_nbr, const void* d_child_plan, const tsp_c2s_weights* w,
-                          float* d_out, void* d_out16, int out16_dtype, void* d_workspace, size_t workspace_bytes,
-                          int flags, void* stream) {
+extern "C" int tsp_c2s_part(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+                            const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m,
+                            int cout, const int32_t* d_child_nbr, const void* d_child_plan,
+                            const tsp_c2s_weights* w, float* d_out, void* d_out16, int out16_dtype,
+                            void* d_workspace, size_t workspace_bytes, int flags, int part, int64_t t0, int64_t nt,
+                            void* stream) {
     clear_error();
+    TSP_REQUIRE(part >= TSP_C2S_PART_FRONT && part <= (TSP_C2S_PART_FRONT | TSP_C2S_PART_CONV2), TSP_ERR_INVALID,
+                "tsp_c2s_part: bad part %d", part);
+    TSP_REQUIRE(t0 >= 0 && (nt >= 0 || nt == -1), TSP_ERR_INVALID, "tsp_c2s_part: bad tiles t0=%lld nt=%lld",
+                (long long)t0, (long long)nt);
+    TSP_REQUIRE((part & TSP_C2S_PART_CONV2) || (t0 == 0 && nt == -1), TSP_ERR_INVALID,
+                "tsp_c2s_part: a tile range is for the conv2 part");
     TSP_REQUIRE(w, TSP_ERR_INVALID, "tsp_c2s: null weights");
     TSP_REQUIRE(n >= 0 && 8 * n < (int64_t)INT32_MAX && m >= 0 && m <= 8 * n, TSP_ERR_INVALID,
                 "tsp_c2s: n=%lld m=%lld out of range", (long long)n, (long long)m);
@@ -376,7 +389,17 @@ extern "C" int tsp_c2s_ex(const float* d_x, int64_t n, int cin, const int32_t* d
                 workspace_bytes, need);
     Carve ws(d_workspace);
     return c2s_walk(d_x, n, cin, d_nbr, d_plan, d_mask, d_mstart, d_gidx, m, cout, d_child_nbr, d_child_plan, *w,
-                    d_out, d_out16, out16_dtype, flags, ws, as_stream(stream));
+                    d_out, d_out16, out16_dtype, flags, ws, as_stream(stream), part, TileRange{t0, nt});
+}
+
+extern "C" int tsp_c2s_ex(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,
+                          const uint8_t* d_mask, const int32_t* d_mstart, const int32_t* d_gidx, int64_t m, int cout,
+                          const int32_t* d_child_nbr, const void* d_child_plan, const tsp_c2s_weights* w,
+                          float* d_out, void* d_out16, int out16_dtype, void* d_workspace, size_t workspace_bytes,
+                          int flags, void* stream) {
+    return tsp_c2s_part(d_x, n, cin, d_nbr, d_plan, d_mask, d_mstart, d_gidx, m, cout, d_child_nbr, d_child_plan, w,
+                        d_out, d_out16, out16_dtype, d_workspace, workspace_bytes, flags,
+                        TSP_C2S_PART_FRONT | TSP_C2S_PART_CONV2, 0, -1, stream);
 }
 
 extern "C" int tsp_c2s(const float* d_x, int64_t n, int cin, const int32_t* d_nbr, const void* d_plan,

@@ -711,7 +711,8 @@ extern "C" int tsp_subm_conv3x3_planned_octants(const void* d_feats, int dtype, 
 
 int tsp::planned_skip(const void* d_feats, int dtype, int64_t n, int ci, const int32_t* d_nbr, const void* d_plan,
                       const void* d_packed_weight, const float* d_bias, int co, const float* d_x, int cin,
-                      const int32_t* d_gidx, float* d_out, void* d_out16, int out16_dtype, hipStream_t s) {
+                      const int32_t* d_gidx, float* d_out, void* d_out16, int out16_dtype, hipStream_t s,
+                      TileRange tr) {
     TSP_REQUIRE(n >= 0 && n < (int64_t)INT32_MAX && ci > 0 && co > 0 && cin > 0, TSP_ERR_INVALID,
                 "tsp_subm_conv3x3_planned_skip: n=%lld ci=%d co=%d cin=%d", (long long)n, ci, co, cin);
     TSP_REQUIRE(dtype == TSP_F16 || dtype == TSP_BF16, TSP_ERR_UNSUPPORTED,
@@ -746,7 +747,7 @@ int tsp::planned_skip(const void* d_feats, int dtype, int64_t n, int ci, const i
     PadRow pad;
     pad.zero = true;
     return halo_conv_launch(dtype, TSP_F32, d_feats, n, ci, d_nbr, d_plan, d_packed_weight, d_bias, co,
-                            d_out, s, OctantScatter{}, skip, pad);
+                            d_out, s, OctantScatter{}, skip, pad, RowNorm{}, tr);
 }
 
 extern "C" int tsp_subm_conv3x3_planned_skip(const void* d_feats, int dtype, int64_t n, int ci,

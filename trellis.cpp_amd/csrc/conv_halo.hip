@@ -106,8 +106,13 @@ int64_t column_split_tiles(int64_t n_tiles, int nct, int cus) {
 
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
-                     hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln) {
+                     hipStream_t s, OctantScatter osc, SkipAdd skip, PadRow pad, RowNorm ln, TileRange tr) {
     const bool planned = plan != nullptr;
+    const bool all_tiles = tr.t0 == 0 && tr.nt < 0;
+    if (!all_tiles && !planned) {
+        set_error("MFMA conv: a tile range needs a plan");
+        return TSP_ERR_INVALID;
+    }
     if (ln.w && (!planned || !(co == 64 || co == 128) || odt != fdt || osc.cout || skip.cin)) {
         set_error("MFMA conv: a row norm needs a plan, co = 64 or 128 and output in the feature type "
                   "(co=%d)", co);
@@ -139,6 +144,7 @@ int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, con
     auto* fn = bn128 ? (fdt == TSP_BF16 ? halo_launch_bf16_128 : halo_launch_f16_128) : fn64;
     // With a plan, whole rounds of 128-channel units and the tiles left over as 64-channel units
     // (kernels where either width runs: not the row norms, which need whole rows in a workgroup)
+    if (!all_tiles) return fn(odt, planned, feats, n, ci, nbr, plan, weight, bias, co, out, s, osc, skip, pad, ln, tr);
     if (planned && bn128 && !ln.w && !osc.norm_silu) {
         const int64_t t_split = column_split_tiles(ceil_div(n, HB_M), co / 128, cu_count());
         if (t_split > 0) {

@@ -147,10 +147,12 @@ struct TileRange {
 // 64-channel grid takes in one: returns that t, or 0 for one launch (cus: compute units).
 int64_t column_split_tiles(int64_t n_tiles, int nct, int cus);
 
+// tr (planned only): the plan's tiles to run, all of them by default; a narrower range runs in one
+// launch of its units.
 int halo_conv_launch(int fdt, int odt, const void* feats, int64_t n, int ci, const int32_t* nbr,
                      const void* plan, const void* weight, const float* bias, int co, void* out,
                      hipStream_t s, OctantScatter osc = {}, SkipAdd skip = {}, PadRow pad = {},
-                     RowNorm ln = {});
+                     RowNorm ln = {}, TileRange tr = {});
 
 // tsp_subm_conv3x3_planned_octants with, when blocks is not null, the MFMAs of row blocks whose
 // parents keep none of a wave's octant skipped (blocks from octant_blocks).
@@ -160,9 +162,10 @@ int planned_octants(const void* feats, int dtype, int64_t n, int ci, const int32
 
 // tsp_subm_conv3x3_planned_skip with, when out16 is not null, out also rounded to out16_dtype
 // (TSP_BF16 or TSP_F16) in out16 [n][co] by the same stores.
+// tr: the plan's tiles whose rows are computed (all by default).
 int planned_skip(const void* feats, int dtype, int64_t n, int ci, const int32_t* nbr, const void* plan,
                  const void* packed, const float* bias, int co, const float* x, int cin, const int32_t* gidx,
-                 float* out, void* out16, int out16_dtype, hipStream_t s);
+                 float* out, void* out16, int out16_dtype, hipStream_t s, TileRange tr = {});
 
 // The thin-channel matrix-core conv (conv_thin_mfma.hip): f16/bf16 features and weights of one
 // dtype, Ci in {8, 16, 32}, Co in {4, 8, 16, 32}, Ci * Co <= 512, a neighbour table, 16-byte

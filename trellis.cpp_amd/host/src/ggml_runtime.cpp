@@ -123,15 +123,15 @@ hipEvent_t g_stage_ev[kMaxDevices][2] = {};
 hipStream_t g_copy_stream[kMaxDevices] = {};
 hipEvent_t g_prod_ev[kMaxDevices] = {};
 
-// Chunks of whole units (at most kStageChunk bytes) through the two staging buffers. With
-// produce, chunk i is first produced by produce(off, len) on s and copied on the device's copy
-// stream once that work is done, so that the copy of one chunk overlaps the production of the
-// next; the copies have all landed when this returns.
+// Chunks of whole units (at most kStageChunk bytes; the last one what is left) through the two
+// staging buffers. With produce, chunk i is first produced by produce(off, len) on s and copied
+// on the device's copy stream once that work is done, so that the copy of one chunk overlaps the
+// production of the next; the copies have all landed when this returns.
 void download_staged(const void* src, size_t bytes, size_t unit, hipStream_t s,
                      const std::function<void(size_t, size_t)>* produce,
                      const std::function<void(const void*, size_t)>& sink) {
     if (!bytes) return;
-    if (!unit || unit > kStageChunk || bytes % unit) fail("download: bad unit");
+    if (!unit || unit > kStageChunk) fail("download: bad unit");
     std::lock_guard<std::mutex> lock(g_stage_mu);
     int dev = 0;
     hip_check(hipGetDevice(&dev), "hipGetDevice");

@@ -92,8 +92,9 @@ void advise_huge_pages(void* p, size_t bytes);
 void download_into(void* dst, const void* src, size_t bytes, hipStream_t s);
 
 // download_into for a buffer whose contents are produced chunk by chunk: produce(off, len)
-// enqueues on s the work that writes bytes [off, off + len) of src (whole units of `unit` bytes,
-// in order), and each chunk is copied, on a stream of its own, while the next one is produced.
+// enqueues on s the work that writes bytes [off, off + len) of src (in order; chunks of whole
+// units of `unit` bytes but the last), and each chunk is copied, on a stream of its own, while the
+// next one is produced.
 void download_produced(void* dst, const void* src, size_t bytes, size_t unit, hipStream_t s,
                        const std::function<void(size_t, size_t)>& produce);
 

@@ -12,6 +12,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <functional>
 #include <future>
 #include <string>
 
@@ -141,6 +142,8 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
             return c;
         });
     const char* dump_dir = std::getenv("TRELLIS_DECODER_DUMP");
+    DeviceBuffer last_x;
+    std::function<void(int64_t, int64_t)> conv2_rows;
     for (size_t si = 0; si < stages.size(); ++si) {
         const Stage& g = stages[si];
         for (size_t j = 0; j < g.convnext.size(); ++j) {   // ConvNeXt stage, ping-pong buffers
@@ -170,9 +173,17 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
         }
         const int c2s16 = si + 1 < stages.size() && !stages[si + 1].convnext.empty()
                               ? conv_input16(stages[si + 1].convnext[0]) : -1;
+        // the last block's conv2 runs by ranges of rows as the output layer and the readback take
+        // them (below), so that the copy to the host overlaps it
+        const bool defer = si + 1 == stages.size() && !dump_dir;
         ops::C2SOut o = ops::run_c2s(m, g.c2s, h.as<float>(), dc.as<int32_t>(), table, g.cin, g.cout, ext, s,
-                                     status.as<int32_t>(), subs_out != nullptr, guide ? counts[si] : -1, c2s16);
+                                     status.as<int32_t>(), subs_out != nullptr, guide ? counts[si] : -1, c2s16,
+                                     defer);
         if (subs_out) subs_out->push_back(std::move(o.mask));
+        if (defer) {
+            last_x = std::move(h);   // the deferred conv2's skip reads the block's input
+            conv2_rows = std::move(o.conv2_rows);
+        }
         h = std::move(o.feats);
         h16 = std::move(o.feats16);
         h16dt = c2s16;
@@ -201,11 +212,13 @@ std::vector<float> decode(const Model& m, const std::vector<float>& latent, int 
     DeviceBuffer out((size_t)n * out_ch * 4, s);
     std::vector<float> feats = result.take();
     if (feats.size() != (size_t)n * out_ch) fail("decoder: the masks' final voxel count is not the decoded one");
-    // the output layer (a row-wise LayerNorm + linear) in row chunks, each chunk's rows copied to
-    // the host while the next chunk's are computed
+    // the last block's conv2 (when deferred) and the output layer (a row-wise LayerNorm + linear) in
+    // chunks of whole 512-row tiles, each chunk's rows copied to the host while the next chunk's are
+    // computed
     const size_t row_bytes = (size_t)out_ch * 4;
-    tgr::download_produced(feats.data(), out.get(), feats.size() * 4, row_bytes, s, [&](size_t off, size_t len) {
+    tgr::download_produced(feats.data(), out.get(), feats.size() * 4, 512 * row_bytes, s, [&](size_t off, size_t len) {
         const int64_t r0 = (int64_t)(off / row_bytes), nr = (int64_t)(len / row_bytes);
+        if (conv2_rows) conv2_rows(r0, r0 + nr);
         ops::run_linear(m, "output_layer", h.as<float>() + r0 * c, nr, c, out_ch, true, 1e-5f,
                         out.as<float>() + r0 * out_ch, s);
     });

@@ -284,7 +284,7 @@ int64_t count_nonzero(const uint8_t* p, size_t n) {
 
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
                Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
-               int32_t* d_status, bool want_mask, int64_t ext_count, int out16_dtype) {
+               int32_t* d_status, bool want_mask, int64_t ext_count, int out16_dtype, bool defer_conv2) {
     const int64_t n = parent.n;
     if (cin <= 0 || cin % 8 != 0 || cout <= 0 || cout % (cin / 8) != 0)
         fail(prefix + ": C2S needs Cin % 8 == 0 and Cout % (Cin/8) == 0");
@@ -348,7 +348,8 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     // the children's table (and plans where a conv runs on the matrix cores), then the block's
     // features in one tsp_c2s call: norm1 + SiLU, conv1 with the octant gather, norm2 + SiLU,
     // conv2 (its absent taps read hn's zero padding column, sparse.cpp:289-306) with the skip
-    build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status, /*morton_plan=*/true);   // r.coords outlives it
+    // (a deferred conv2 takes tiles of consecutive rows: ranges of rows are then ranges of tiles)
+    build_table(r.coords.as<int32_t>(), mm, r.table, s, d_status, /*morton_plan=*/!defer_conv2);   // r.coords outlives it
     if (conv1.mfma) parent.ensure_plan(s);
     if (conv2.mfma) r.table.ensure_plan(s);
     const ggml_tensor* c1b = conv1.b;
@@ -369,12 +370,50 @@ C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, cons
     const int flags = g_sparse_cast_f32 ? TSP_BLOCK_CAST_F32 : 0;
     const size_t nb = tsp_c2s_workspace_bytes(n, mm, cin, cout, &w, conv1.mfma, conv2.mfma, flags);
     DeviceBuffer work(nb, s);
-    lib(tsp_c2s_ex(d_x, n, cin, parent.nbr.as<int32_t>(), conv1.mfma ? parent.plan.get() : nullptr,
-                   d_mask.as<uint8_t>(), d_mstart.as<int32_t>(), d_gidx.as<int32_t>(), mm, cout, r.table.nbr.as<int32_t>(),
-                   conv2.mfma ? r.table.plan.get() : nullptr, &w, r.feats.as<float>(),
-                   out16_dtype >= 0 ? r.feats16.get() : nullptr, out16_dtype >= 0 ? out16_dtype : TSP_BF16, work.get(),
-                   nb, flags, s),
-        prefix);
+    // the buffers a deferred conv2 still reads (stream-ordered: released after its last call)
+    struct Kept {
+        DeviceBuffer mask, mstart, gidx, params, work;
+        tsp_c2s_weights w;
+        bool whole = false;   // conv2 ran over every tile (its ranges are then done)
+    };
+    auto kept = std::make_shared<Kept>();
+    // (device pointers: the tables' and the outputs' buffers keep their addresses when moved)
+    const int32_t* pnbr = parent.nbr.as<int32_t>();
+    const void* pplan = conv1.mfma ? parent.plan.get() : nullptr;
+    const int32_t* cnbr = r.table.nbr.as<int32_t>();
+    const void* cplan = conv2.mfma ? r.table.plan.get() : nullptr;
+    float* feats = r.feats.as<float>();
+    void* feats16 = out16_dtype >= 0 ? r.feats16.get() : nullptr;
+    const int o16 = out16_dtype >= 0 ? out16_dtype : TSP_BF16;
+    auto part = [=](int p, int64_t t0, int64_t nt) {
+        return tsp_c2s_part(d_x, n, cin, pnbr, pplan, kept->mask.as<uint8_t>(), kept->mstart.as<int32_t>(),
+                            kept->gidx.as<int32_t>(), mm, cout, cnbr, cplan, &kept->w, feats, feats16, o16,
+                            kept->work.get(), nb, flags, p, t0, nt, s);
+    };
+    kept->mask = std::move(d_mask);
+    kept->mstart = std::move(d_mstart);
+    kept->gidx = std::move(d_gidx);
+    kept->params = std::move(pbuf);
+    kept->work = std::move(work);
+    kept->w = w;
+    if (!defer_conv2) {
+        lib(part(TSP_C2S_PART_FRONT | TSP_C2S_PART_CONV2, 0, -1), prefix);
+        return r;
+    }
+    lib(part(TSP_C2S_PART_FRONT, 0, -1), prefix);
+    r.conv2_rows = [kept, part, prefix, mm](int64_t r0, int64_t r1) {
+        if (kept->whole) return;
+        const int64_t t0 = r0 / 512, t1 = std::min((r1 + 511) / 512, (mm + 511) / 512);
+        const int st = part(TSP_C2S_PART_CONV2, t0, t1 - t0);
+        if (st != TSP_ERR_UNSUPPORTED) {
+            lib(st, prefix + " conv2");
+            return;
+        }
+        // conv2 that does not run by tiles (no matrix-core conv2 with the skip in its stores): all
+        // rows at once
+        lib(part(TSP_C2S_PART_CONV2, 0, -1), prefix + " conv2");
+        kept->whole = true;
+    };
     return r;
 }
 

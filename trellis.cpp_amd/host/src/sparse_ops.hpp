@@ -3,6 +3,7 @@
 // allocates its own temporaries unless a scratch Carve is passed in.
 #pragma once
 
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -112,11 +113,16 @@ struct C2SOut {
     tgr::DeviceBuffer feats16;   // feats rounded to out16_dtype (run_c2s's, when >= 0)
     Table table;
     std::vector<uint8_t> mask;
+    // With defer_conv2: conv2 (and the skip) over the child rows [r0, r1) on s, rows of feats being
+    // final only once a call covered them (the block's input x and `table` must still be alive).
+    std::function<void(int64_t r0, int64_t r1)> conv2_rows;
 };
+// defer_conv2: the block's conv2 waits for conv2_rows (the child plan then holds tiles of
+// consecutive rows, so that ranges of rows are ranges of tiles).
 C2SOut run_c2s(const Model& m, const std::string& prefix, const float* d_x, const int32_t* d_coords,
                Table& parent, int cin, int cout, const std::vector<uint8_t>* ext_mask, hipStream_t s,
                int32_t* d_status = nullptr, bool want_mask = true, int64_t ext_count = -1,
-               int out16_dtype = -1);
+               int out16_dtype = -1, bool defer_conv2 = false);
 
 // out [n][co] f32 = (optionally LN(eps, no affine) of) x [n][ci] . W^T + b for `prefix.weight`
 // ggml [ci, co]; the input (the LN's output) is rounded to act_dtype of the weight.
